@@ -1,0 +1,94 @@
+"""ctypes binding of libkadllm_hip.so (the C ABI declared in include/kadllm_hip.h).
+
+The library is built in-tree by ``kadllm_amd.csrc.build``.  torch is imported
+first so that the library binds to the HIP runtime torch already loaded (both
+carry the SONAME libamdhip64.so.7), giving one runtime, one set of streams and
+one device allocator per process.  There is no fallback: if the library is
+missing or fails to load, every operator raises.
+"""
+
+import ctypes
+import os
+import re
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkadllm_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                           "include", "kadllm_hip.h")
+
+KAD_OK = 0
+ERRORS = {-1: "invalid argument", -2: "unsupported", -3: "HIP error"}
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+_P, _L, _I, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+_CTYPES = {"p": _P, "l": _L, "i": _I, "f": _F, "s": _P}
+
+# argument signatures, one letter per parameter (p pointer, l int64, i int,
+# f float, s stream), in the order of include/kadllm_hip.h
+SIGNATURES = {
+    "kad_gdn_suffix_replay": "ppplli" "pipil" "pi" "pl" "iiiiiii" "f" "s",
+    "kad_causal_conv_suffix": "plll" "pllli" "pip" "plll" "iiiiii" "s",
+    "kad_selftest_mfma16": "ppps",
+    "kad_selftest_mfma32": "ppps",
+}
+
+_lib = None
+
+
+class KadLibraryError(RuntimeError):
+    """Raised when the HIP library is missing or an entry point fails."""
+
+
+def header_symbols():
+    """Entry points declared in include/kadllm_hip.h."""
+    with open(HEADER_PATH) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int)\s+(kad_\w+)\s*\(", text, re.M)))
+
+
+def load():
+    """Load the library (once) and declare argument types."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise KadLibraryError(
+            f"{LIB_PATH} is not built; run `python -m kadllm_amd.csrc.build` "
+            "(kadllm_amd has no non-HIP implementation)")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.kad_last_error.restype = ctypes.c_char_p
+    lib.kad_last_error.argtypes = []
+    lib.kad_abi_version.restype = ctypes.c_int
+    lib.kad_abi_version.argtypes = []
+    for name, sig in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [_CTYPES[c] for c in sig]
+    _lib = lib
+    return lib
+
+
+def stream_of(t):
+    """Raw hipStream_t of torch's current stream on ``t``'s device."""
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def call(name, *args):
+    """Invoke entry point ``name``; raise KadLibraryError on a nonzero code."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != KAD_OK:
+        msg = lib.kad_last_error().decode(errors="replace")
+        raise KadLibraryError(f"{name} failed ({ERRORS.get(rc, rc)}): {msg}")
+
+
+def dtype_code(dtype):
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}") from None
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)

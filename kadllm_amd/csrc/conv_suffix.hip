@@ -1,0 +1,164 @@
+// Depthwise causal short convolution over [shared prefix taps || beam suffix].
+//
+// Replaces src/kadllm/ops.py:166-226 and src/kadllm/kernels/causal_conv1d.py:10-78.
+// HBM-bound: each output element reads its input once; the request-sized
+// prefix taps (state[b, c, history-3 ..]) and the weights are read by every
+// beam of the request and stay in L2.  Rounding follows the reference torch
+// path: the convolution result is rounded to the tensor dtype, then SiLU is
+// applied and rounded again (for fp32 both roundings are exact).
+//
+// Two paths: a vectorised one when channels are contiguous in x and out
+// (8 channels per thread, 16-byte accesses; the [rows, T, C] layout produced by
+// the projection GEMM), and a scalar one for any other strides (the
+// reference's [BW, C, T] layout).
+
+#include "kad_common.h"
+
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p) { return Elem<T>::to_f(*p); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void conv_suffix_scalar(
+    const T* __restrict__ x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
+    const T* __restrict__ state, int64_t ss_b, int64_t ss_c, int64_t ss_t, int history,
+    const T* __restrict__ w, int width, const T* __restrict__ bias, T* __restrict__ out,
+    int64_t so_n, int64_t so_c, int64_t so_t, int W, int C, int T_, int64_t total, int silu) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int c = (int)(idx % C);
+  const int64_t n = idx / C;
+  const int64_t b = n / W;
+  float win[4] = {0.f, 0.f, 0.f, 0.f};  // win[3] is the newest tap
+  float wt[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < width; ++i) wt[4 - width + i] = ld(w + (int64_t)c * width + i);
+  for (int i = 0; i < width - 1; ++i)
+    win[4 - (width - 1) + i] = ld(state + b * ss_b + (int64_t)c * ss_c +
+                                  (int64_t)(history - (width - 1) + i) * ss_t);
+  const float bv = bias ? ld(bias + c) : 0.f;
+  for (int t = 0; t < T_; ++t) {
+    win[0] = win[1];
+    win[1] = win[2];
+    win[2] = win[3];
+    win[3] = ld(x + n * sx_n + (int64_t)c * sx_c + (int64_t)t * sx_t);
+    float acc = bv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc += wt[i] * win[i];
+    float y = round_to_dtype(acc, Elem<T>::code);
+    if (silu) y = silu_f(y);
+    out[n * so_n + (int64_t)c * so_c + (int64_t)t * so_t] = Elem<T>::from_f(y);
+  }
+}
+
+// 8 contiguous bf16 channels per thread; width 4 (3 taps), any T.
+__global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
+    const bf16_t* __restrict__ x, int64_t sx_n, int64_t sx_t, const bf16_t* __restrict__ state,
+    int64_t ss_b, int64_t ss_c, int64_t ss_t, int history, const bf16_t* __restrict__ w,
+    bf16_t* __restrict__ out, int64_t so_n, int64_t so_t, int W, int C, int T_, int64_t total,
+    int silu) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int C8 = C / 8;
+  const int c0 = (int)(idx % C8) * 8;
+  const int64_t n = idx / C8;
+  const int64_t b = n / W;
+  float wt[8][4];
+  {
+    const u32x4* wp = (const u32x4*)(w + (int64_t)c0 * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4 r = wp[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int flat = j * 8 + e * 2;  // channel c0 + flat/4, tap flat%4
+        wt[flat / 4][flat % 4] = __uint_as_float(r[e] << 16);
+        wt[(flat + 1) / 4][(flat + 1) % 4] = __uint_as_float(r[e] & 0xffff0000u);
+      }
+    }
+  }
+  float win[8][4];
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch) {
+    win[ch][0] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      win[ch][1 + i] = bf2f(state[b * ss_b + (int64_t)(c0 + ch) * ss_c +
+                                  (int64_t)(history - 3 + i) * ss_t]);
+  }
+  for (int t = 0; t < T_; ++t) {
+    u32x4 r = *(const u32x4*)(x + n * sx_n + (int64_t)t * sx_t + c0);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float xv[2] = {__uint_as_float(r[e] << 16), __uint_as_float(r[e] & 0xffff0000u)};
+      uint32_t packed = 0;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int ch = e * 2 + hh;
+        win[ch][0] = win[ch][1];
+        win[ch][1] = win[ch][2];
+        win[ch][2] = win[ch][3];
+        win[ch][3] = xv[hh];
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc += wt[ch][i] * win[ch][i];
+        float y = round_bf(acc);
+        if (silu) y = silu_f(y);
+        packed |= (uint32_t)f2bf(y) << (16 * hh);
+      }
+      o[e] = packed;
+    }
+    *(u32x4*)(out + n * so_n + (int64_t)t * so_t + c0) = o;
+  }
+}
+
+template <typename T>
+int launch_scalar(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx_t, const void* state,
+                  int64_t ss_b, int64_t ss_c, int64_t ss_t, int history, const void* w,
+                  int width, const void* bias, void* out, int64_t so_n, int64_t so_c,
+                  int64_t so_t, int B, int W, int C, int T_, int silu, hipStream_t s) {
+  const int64_t total = (int64_t)B * W * C;
+  hipLaunchKernelGGL((conv_suffix_scalar<T>), dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
+                     s, (const T*)x, sx_n, sx_c, sx_t, (const T*)state, ss_b, ss_c, ss_t,
+                     history, (const T*)w, width, (const T*)bias, (T*)out, so_n, so_c, so_t, W,
+                     C, T_, total, silu);
+  return kad_launch_status("conv_suffix_scalar");
+}
+
+}  // namespace
+
+extern "C" int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
+                                      const void* state, int64_t ss_b, int64_t ss_c,
+                                      int64_t ss_t, int history, const void* weight, int width,
+                                      const void* bias, void* out, int64_t so_n, int64_t so_c,
+                                      int64_t so_t, int B, int W, int C, int T, int dtype,
+                                      int activation_silu, kad_stream_t stream) {
+  KAD_REQUIRE(x && state && weight && out, "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0 && C > 0 && T > 0 && width > 0, "dimensions must be positive");
+  if (width > 4) KAD_UNSUPPORTED("causal conv supports width <= 4, got %d", width);
+  KAD_REQUIRE(history >= width - 1, "state history %d shorter than width-1", history);
+  KAD_REQUIRE((int64_t)B * W * C < ((int64_t)1 << 40), "problem too large");
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = dtype == KAD_DTYPE_BF16 && width == 4 && bias == nullptr && sx_c == 1 &&
+                   so_c == 1 && C % 8 == 0 && sx_n % 8 == 0 && sx_t % 8 == 0 && so_n % 8 == 0 &&
+                   so_t % 8 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 16) == 0 &&
+                   ((uintptr_t)weight % 16) == 0;
+  if (vec) {
+    const int64_t total = (int64_t)B * W * (C / 8);
+    hipLaunchKernelGGL(conv_suffix_vec_bf16, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0, s,
+                       (const bf16_t*)x, sx_n, sx_t, (const bf16_t*)state, ss_b, ss_c, ss_t,
+                       history, (const bf16_t*)weight, (bf16_t*)out, so_n, so_t, W, C, T, total,
+                       activation_silu);
+    return kad_launch_status("conv_suffix_vec_bf16");
+  }
+  if (dtype == KAD_DTYPE_BF16)
+    return launch_scalar<bf16_t>(x, sx_n, sx_c, sx_t, state, ss_b, ss_c, ss_t, history, weight,
+                                 width, bias, out, so_n, so_c, so_t, B, W, C, T,
+                                 activation_silu, s);
+  if (dtype == KAD_DTYPE_F32)
+    return launch_scalar<float>(x, sx_n, sx_c, sx_t, state, ss_b, ss_c, ss_t, history, weight,
+                                width, bias, out, so_n, so_c, so_t, B, W, C, T, activation_silu,
+                                s);
+  KAD_UNSUPPORTED("causal conv supports bf16 and fp32, got dtype %d", dtype);
+}

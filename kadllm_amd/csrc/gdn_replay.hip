@@ -1,0 +1,351 @@
+// Gated DeltaNet suffix replay from a request-shared prefix state (gfx950).
+//
+// Replaces the per-beam / grouped recurrences of the reference
+// (src/kadllm/ops.py:139-163, src/kadllm/kernels/gated_delta.py:14-142).
+//
+// Design.  One workgroup (4 waves) serves one (request b, value head hv) and a
+// block of beams.  The request state S0 = state[b,hv] ([K,V] fp32) is read
+// from HBM once per workgroup and kept for the whole kernel in registers as
+// bf16 hi/lo MFMA A-fragments of S0^T (S0 ~= hi + lo to 2^-16 relative); wave
+// w owns value rows [w*V/4, (w+1)*V/4).  Beams are the MFMA N dimension: for
+// 16 beams at a time the raw bf16 q_t and k_t rows are loaded straight into
+// B-fragments and v_mfma_f32_16x16x32_bf16 gives a_t = S0^T k_t and
+// b_t = S0^T q_t exactly up to fp32 accumulation (two passes, hi and lo).
+// No per-beam copy of S0 is ever formed.  The recurrence is then finished per
+// beam in registers with the factored form (gamma_t = prod_{i<=t} e^{g_i},
+// c_j(t) = gamma_t / gamma_j, hats = L2-normalised):
+//   recall_t = gamma_t a^_t + sum_{j<t} c_j(t) (k^_j.k^_t) u_j
+//   u_t      = beta_t (v_t - recall_t)
+//   o_t      = gamma_t b^_t + sum_{j<t} c_j(t) (k^_j.q^_t) u_j + (k^_t.q^_t) u_t
+// which is the reference recurrence S <- S e^g; u = beta (v - S^T k);
+// S <- S + k u^T; o = S^T q expanded over the suffix (the reference's grouped
+// kernel uses the t = T-1 row of the same identity, gated_delta.py:133-134).
+// Norms and the T x T Gram terms come from the same fragments with two
+// cross-lane reductions.
+
+#include "kad_common.h"
+
+namespace {
+
+constexpr int kTMax = 4;
+
+template <typename TIN>
+struct QKFrag;
+
+template <>
+struct QKFrag<bf16_t> {
+  bf16x8 hi;
+  __device__ __forceinline__ void load(const bf16_t* p, float* f) {
+    u32x4 raw = *(const u32x4*)p;
+    hi = as_bf16x8(raw);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)hi[i];
+  }
+};
+
+template <>
+struct QKFrag<float> {
+  bf16x8 hi, lo;
+  __device__ __forceinline__ void load(const float* p, float* f) {
+    f32x4 a = *(const f32x4*)p;
+    f32x4 b = *(const f32x4*)(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[i] = a[i];
+      f[4 + i] = b[i];
+    }
+    split8(f, hi, lo);
+  }
+};
+
+template <typename TIN>
+__device__ __forceinline__ void load4(const TIN* p, float* f);
+template <>
+__device__ __forceinline__ void load4<bf16_t>(const bf16_t* p, float* f) {
+  u32x2 r = *(const u32x2*)p;
+  f[0] = __uint_as_float(r[0] << 16);
+  f[1] = __uint_as_float(r[0] & 0xffff0000u);
+  f[2] = __uint_as_float(r[1] << 16);
+  f[3] = __uint_as_float(r[1] & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ void load4<float>(const float* p, float* f) {
+  f32x4 r = *(const f32x4*)p;
+  f[0] = r[0];
+  f[1] = r[1];
+  f[2] = r[2];
+  f[3] = r[3];
+}
+
+template <typename TIN>
+__device__ __forceinline__ void store4(TIN* p, const float* f);
+template <>
+__device__ __forceinline__ void store4<bf16_t>(bf16_t* p, const float* f) {
+  u32x2 r;
+  r[0] = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+  r[1] = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+  *(u32x2*)p = r;
+}
+template <>
+__device__ __forceinline__ void store4<float>(float* p, const float* f) {
+  f32x4 r = {f[0], f[1], f[2], f[3]};
+  *(f32x4*)p = r;
+}
+
+template <int KD, int VD, typename TIN>
+__global__ __launch_bounds__(256) void gdn_replay_kernel(
+    const TIN* __restrict__ q, const TIN* __restrict__ k, const TIN* __restrict__ v,
+    int64_t ld_qk, int64_t ld_v, const void* __restrict__ gdecay, int gate_dtype,
+    const void* __restrict__ beta, int beta_dtype, int64_t ld_gate,
+    const void* __restrict__ state, int state_dtype, TIN* __restrict__ out, int64_t ld_out,
+    int W, int T, int H, int HV, float scale, int beams_per_block, int nbb) {
+  constexpr int KSTEPS = KD / 32;
+  constexpr int VROWS = VD / 4;
+  constexpr int MT = VROWS / 16;
+  constexpr bool kSplitB = sizeof(TIN) == 4;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int bb = lid % nbb;
+  const int rh = lid / nbb;
+  const int hv = rh % HV;
+  const int b = rh / HV;
+  const int h = hv / (HV / H);
+  const int v0 = wave * VROWS;
+  const int col = lane & 15;   // beam within the 16-beam group (MFMA N index)
+  const int quad = lane >> 4;  // 0..3
+
+  // ---- S0^T fragments, hi/lo bf16, held in registers for the whole kernel
+  bf16x8 a_hi[MT][KSTEPS], a_lo[MT][KSTEPS];
+  {
+    const int64_t sbase = ((int64_t)b * HV + hv) * KD * VD;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int vrow = v0 + mt * 16 + col;
+        const int kc = ks * 32 + quad * 8;
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          x[i] = load_as_float(state, sbase + (int64_t)(kc + i) * VD + vrow, state_dtype);
+        split8(x, a_hi[mt][ks], a_lo[mt][ks]);
+      }
+    }
+  }
+
+  const int n_begin = bb * beams_per_block;
+  const int n_end = min(W, n_begin + beams_per_block);
+
+  for (int g0 = n_begin; g0 < n_end; g0 += 16) {
+    const int nl = g0 + col;
+    const bool valid = nl < n_end;
+    const int64_t n = (int64_t)b * W + (valid ? nl : n_begin);
+
+    f32x4 acc_q[kTMax][MT], acc_k[kTMax][MT];
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc_q[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc_k[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    float qq[kTMax], kk[kTMax], kkx[kTMax][kTMax], kqx[kTMax][kTMax];
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+      qq[t] = 0.f;
+      kk[t] = 0.f;
+#pragma unroll
+      for (int j = 0; j < kTMax; ++j) {
+        kkx[j][t] = 0.f;
+        kqx[j][t] = 0.f;
+      }
+    }
+
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      QKFrag<TIN> fq[kTMax], fk[kTMax];
+      float xq[kTMax][8], xk[kTMax][8];
+#pragma unroll
+      for (int t = 0; t < kTMax; ++t) {
+        if (t < T) {
+          const int64_t row = (n * T + t) * ld_qk + (int64_t)h * KD + ks * 32 + quad * 8;
+          fq[t].load(q + row, xq[t]);
+          fk[t].load(k + row, xk[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kTMax; ++t) {
+        if (t < T) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            qq[t] += xq[t][i] * xq[t][i];
+            kk[t] += xk[t][i] * xk[t][i];
+          }
+#pragma unroll
+          for (int j = 0; j <= t; ++j) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              kqx[j][t] += xk[j][i] * xq[t][i];
+              if (j < t) kkx[j][t] += xk[j][i] * xk[t][i];
+            }
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            acc_k[t][mt] = mfma16x16x32(a_hi[mt][ks], fk[t].hi, acc_k[t][mt]);
+            acc_k[t][mt] = mfma16x16x32(a_lo[mt][ks], fk[t].hi, acc_k[t][mt]);
+            acc_q[t][mt] = mfma16x16x32(a_hi[mt][ks], fq[t].hi, acc_q[t][mt]);
+            acc_q[t][mt] = mfma16x16x32(a_lo[mt][ks], fq[t].hi, acc_q[t][mt]);
+            if constexpr (kSplitB) {
+              acc_k[t][mt] = mfma16x16x32(a_hi[mt][ks], fk[t].lo, acc_k[t][mt]);
+              acc_q[t][mt] = mfma16x16x32(a_hi[mt][ks], fq[t].lo, acc_q[t][mt]);
+            }
+          }
+        }
+      }
+    }
+
+    // full 128-element dot products: sum the 4 lanes (quad 0..3) of each beam
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+      qq[t] += __shfl_xor(qq[t], 16, 64);
+      qq[t] += __shfl_xor(qq[t], 32, 64);
+      kk[t] += __shfl_xor(kk[t], 16, 64);
+      kk[t] += __shfl_xor(kk[t], 32, 64);
+#pragma unroll
+      for (int j = 0; j <= t; ++j) {
+        kqx[j][t] += __shfl_xor(kqx[j][t], 16, 64);
+        kqx[j][t] += __shfl_xor(kqx[j][t], 32, 64);
+        if (j < t) {
+          kkx[j][t] += __shfl_xor(kkx[j][t], 16, 64);
+          kkx[j][t] += __shfl_xor(kkx[j][t], 32, 64);
+        }
+      }
+    }
+
+    float rk[kTMax], rq[kTMax], et[kTMax], bt[kTMax];
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+      rk[t] = 1.0f / sqrtf(kk[t] + 1e-6f);
+      rq[t] = scale / sqrtf(qq[t] + 1e-6f);
+      if (t < T) {
+        const int64_t gi = (n * T + t) * ld_gate + hv;
+        et[t] = expf(load_as_float(gdecay, gi, gate_dtype));
+        bt[t] = load_as_float(beta, gi, beta_dtype);
+      } else {
+        et[t] = 1.f;
+        bt[t] = 0.f;
+      }
+    }
+
+    float u[kTMax][MT][4];
+    float c[kTMax];
+    float gam = 1.f;
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+      if (t < T) {
+        gam *= et[t];
+#pragma unroll
+        for (int j = 0; j < t; ++j) c[j] *= et[t];
+        const int64_t vrow_base = (n * T + t);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int vr = v0 + mt * 16 + quad * 4;
+          float vt[4], ov[4];
+          load4<TIN>(v + vrow_base * ld_v + (int64_t)hv * VD + vr, vt);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float recall = gam * (acc_k[t][mt][i] * rk[t]);
+#pragma unroll
+            for (int j = 0; j < t; ++j) recall += c[j] * (kkx[j][t] * rk[j] * rk[t]) * u[j][mt][i];
+            const float ut = bt[t] * (vt[i] - recall);
+            u[t][mt][i] = ut;
+            float o = gam * (acc_q[t][mt][i] * rq[t]);
+#pragma unroll
+            for (int j = 0; j < t; ++j) o += c[j] * (kqx[j][t] * rk[j] * rq[t]) * u[j][mt][i];
+            o += (kqx[t][t] * rk[t] * rq[t]) * ut;
+            ov[i] = o;
+          }
+          if (valid) store4<TIN>(out + vrow_base * ld_out + (int64_t)hv * VD + vr, ov);
+        }
+        c[t] = 1.f;
+      }
+    }
+  }
+}
+
+template <int KD, int VD, typename TIN>
+int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
+                  const void* g, int gdt, const void* beta, int bdt, int64_t ld_gate,
+                  const void* state, int sdt, void* out, int64_t ld_out, int B, int W,
+                  int T, int H, int HV, float scale, hipStream_t stream) {
+  int bpb = W >= 256 ? 128 : ((W + 15) / 16) * 16;
+  if (bpb > 128) bpb = 128;
+  const int nbb = (int)kad_cdiv(W, bpb);
+  const int64_t nblocks = (int64_t)B * HV * nbb;
+  if (nblocks > 0x7fffffff) {
+    kad_set_error("gdn replay grid too large");
+    return KAD_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((gdn_replay_kernel<KD, VD, TIN>), dim3((unsigned)nblocks), dim3(256), 0,
+                     stream, (const TIN*)q, (const TIN*)k, (const TIN*)v, ld_qk, ld_v, g, gdt,
+                     beta, bdt, ld_gate, state, sdt, (TIN*)out, ld_out, W, T, H, HV, scale,
+                     bpb, nbb);
+  return kad_launch_status("gdn_replay_kernel");
+}
+
+template <typename TIN>
+int dispatch_dims(int K, int V, const void* q, const void* k, const void* v, int64_t ld_qk,
+                  int64_t ld_v, const void* g, int gdt, const void* beta, int bdt,
+                  int64_t ld_gate, const void* state, int sdt, void* out, int64_t ld_out,
+                  int B, int W, int T, int H, int HV, float scale, hipStream_t s) {
+#define KAD_REPLAY(KK, VV)                                                                  \
+  if (K == KK && V == VV)                                                                   \
+    return launch_replay<KK, VV, TIN>(q, k, v, ld_qk, ld_v, g, gdt, beta, bdt, ld_gate,     \
+                                      state, sdt, out, ld_out, B, W, T, H, HV, scale, s);
+  KAD_REPLAY(128, 128)
+  KAD_REPLAY(64, 64)
+  KAD_REPLAY(128, 64)
+  KAD_REPLAY(64, 128)
+#undef KAD_REPLAY
+  KAD_UNSUPPORTED("gdn replay supports K, V in {64, 128}; got K=%d V=%d", K, V);
+}
+
+}  // namespace
+
+extern "C" int kad_gdn_suffix_replay(const void* q, const void* k, const void* v,
+                                     int64_t ld_qk, int64_t ld_v, int qkv_dtype,
+                                     const void* log_decay, int gate_dtype, const void* beta,
+                                     int beta_dtype, int64_t ld_gate, const void* state,
+                                     int state_dtype, void* out, int64_t ld_out, int B, int W,
+                                     int T, int H, int HV, int K, int V, float scale,
+                                     kad_stream_t stream) {
+  KAD_REQUIRE(q && k && v && log_decay && beta && state && out, "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0 && T > 0 && H > 0 && HV > 0 && K > 0 && V > 0,
+              "dimensions must be positive");
+  KAD_REQUIRE(HV % H == 0, "HV must be divisible by H");
+  KAD_REQUIRE(ld_qk >= (int64_t)H * K && ld_v >= (int64_t)HV * V && ld_out >= (int64_t)HV * V &&
+                  ld_gate >= HV,
+              "row strides smaller than a row");
+  KAD_REQUIRE(ld_qk % 8 == 0 && ld_v % 4 == 0 && ld_out % 4 == 0,
+              "q/k row stride must be a multiple of 8 and v/out of 4 elements");
+  KAD_REQUIRE(((uintptr_t)q | (uintptr_t)k) % 16 == 0 && ((uintptr_t)v | (uintptr_t)out) % 8 == 0,
+              "q/k must be 16-byte and v/out 8-byte aligned");
+  if (T > kTMax) KAD_UNSUPPORTED("gdn replay supports T <= %d suffix tokens, got %d", kTMax, T);
+  for (int dt : {gate_dtype, beta_dtype, state_dtype})
+    KAD_REQUIRE(dt == KAD_DTYPE_BF16 || dt == KAD_DTYPE_F16 || dt == KAD_DTYPE_F32,
+                "unknown dtype code %d", dt);
+  hipStream_t s = (hipStream_t)stream;
+  if (qkv_dtype == KAD_DTYPE_BF16)
+    return dispatch_dims<bf16_t>(K, V, q, k, v, ld_qk, ld_v, log_decay, gate_dtype, beta,
+                                 beta_dtype, ld_gate, state, state_dtype, out, ld_out, B, W, T,
+                                 H, HV, scale, s);
+  if (qkv_dtype == KAD_DTYPE_F32) {
+    KAD_REQUIRE(((uintptr_t)v | (uintptr_t)out) % 16 == 0, "fp32 v/out must be 16-byte aligned");
+    return dispatch_dims<float>(K, V, q, k, v, ld_qk, ld_v, log_decay, gate_dtype, beta,
+                                beta_dtype, ld_gate, state, state_dtype, out, ld_out, B, W, T, H,
+                                HV, scale, s);
+  }
+  KAD_UNSUPPORTED("gdn replay supports bf16 and fp32 q/k/v, got dtype %d", qkv_dtype);
+}

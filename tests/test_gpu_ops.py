@@ -1,0 +1,200 @@
+"""HIP operator parity against the CPU oracle and the reference golden vectors."""
+
+import pytest
+import torch
+
+from _fixtures import bf16_from_bits, conv_inputs, gdn_inputs, load_npz
+from conftest import assert_close_rel
+from kadllm_amd import _lib, ops
+from oracle import ops_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _to(device, *ts):
+    return [t.to(device) for t in ts]
+
+
+# --------------------------------------------------------------------------
+# MFMA operand layouts assumed by every kernel
+
+
+@pytest.mark.parametrize("shape,name", [((16, 32, 16), "kad_selftest_mfma16"),
+                                        ((32, 16, 32), "kad_selftest_mfma32")])
+def test_mfma_lane_layout(device, shape, name):
+    m, kdim, n = shape
+    g = torch.Generator().manual_seed(7)
+    a = torch.randn(m, kdim, generator=g).bfloat16()
+    b = torch.randn(kdim, n, generator=g).bfloat16()
+    ad, bd = a.to(device), b.to(device)
+    c = torch.full((m, n), float("nan"), device=device)
+    _lib.call(name, _lib.ptr(ad), _lib.ptr(bd), _lib.ptr(c), _lib.stream_of(ad))
+    torch.cuda.synchronize()
+    expected = a.double() @ b.double()
+    assert torch.allclose(c.cpu().double(), expected, rtol=1e-5, atol=1e-5)
+
+
+# --------------------------------------------------------------------------
+# Gated DeltaNet suffix replay
+
+GDN_CASES = [
+    # B, W, T, H, HV, K, V
+    (2, 256, 3, 16, 16, 128, 128),   # config-2 head shape, 2 of the 32 requests
+    (3, 5, 2, 2, 4, 64, 64),         # GQA 2:1, ragged beam group
+    (2, 20, 1, 4, 4, 128, 64),
+    (2, 33, 4, 2, 2, 64, 128),
+    (1, 1, 1, 1, 1, 64, 64),
+]
+
+
+@pytest.mark.parametrize("case", GDN_CASES)
+def test_gdn_replay_bf16_matches_oracle(device, case):
+    B, W, T, H, HV, K, V = case
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, seed=sum(case))
+    expected = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W)
+    qd, kd, vd, gd, bd, Sd = _to(device, q, k, v, g, beta, S)
+    S_before = Sd.clone()
+    out = ops.gated_delta(qd, kd, vd, gd, bd, Sd, beam_width=W)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and out.shape == v.shape
+    assert torch.equal(Sd, S_before), "shared prefix state was modified"
+    # bf16 output: one rounding of a value computed from fp32 state
+    assert_close_rel(out.cpu(), expected, rtol=1e-2, atol_frac=2e-3, name=f"gdn {case}")
+
+
+@pytest.mark.parametrize("case", [(2, 7, 3, 2, 4, 64, 64), (1, 16, 4, 4, 4, 128, 128)])
+def test_gdn_replay_fp32_matches_oracle(device, case):
+    B, W, T, H, HV, K, V = case
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, dtype=torch.float32, seed=3)
+    expected = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W, compute=torch.float64)
+    out = ops.gated_delta(*_to(device, q, k, v, g, beta, S), beam_width=W)
+    torch.cuda.synchronize()
+    # hi/lo bf16 split MFMA: ~2^-16 relative products, fp32 accumulation
+    assert_close_rel(out.cpu(), expected.float(), rtol=1e-4, atol_frac=1e-4, name="gdn fp32")
+
+
+def test_gdn_replay_bf16_state_and_gates(device):
+    # bf16 state and bf16 decay (the reference kernel benchmark's dtypes)
+    B, W, T, H, HV, K, V = 2, 9, 3, 2, 2, 128, 128
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, seed=11, state_std=0.1,
+                                     state_dtype=torch.bfloat16)
+    g = g.bfloat16()
+    expected = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W)
+    out = ops.gated_delta(*_to(device, q, k, v, g, beta, S), beam_width=W)
+    torch.cuda.synchronize()
+    assert_close_rel(out.cpu(), expected, rtol=1e-2, atol_frac=2e-3, name="gdn bf16 state")
+
+
+def test_gdn_replay_golden_fixture(device):
+    f = load_npz("ops_bf16.npz")
+    q, k, v = (bf16_from_bits(f[n]) for n in ("gdn_q", "gdn_k", "gdn_v"))
+    g = torch.from_numpy(f["gdn_g"])
+    beta = bf16_from_bits(f["gdn_beta"])
+    S = torch.from_numpy(f["gdn_state"])
+    expected = bf16_from_bits(f["gdn_out"])
+    out = ops.gated_delta(*_to(device, q, k, v, g, beta, S), beam_width=3)
+    torch.cuda.synchronize()
+    assert_close_rel(out.cpu(), expected, rtol=1e-2, atol_frac=2e-3, name="gdn golden")
+
+
+def test_gdn_replay_full_config2_sampled(device):
+    """All 32 requests x 256 beams x 16 heads; requests 0, 17 and 31 checked
+    against the oracle (requests are independent), prefix immutability checked."""
+    B, W, T, H, HV, K, V = 32, 256, 3, 16, 16, 128, 128
+    gen = torch.Generator(device=device).manual_seed(5)
+    BW = B * W
+    q = torch.randn(BW, T, H, K, generator=gen, device=device).bfloat16()
+    k = torch.randn(BW, T, H, K, generator=gen, device=device).bfloat16()
+    v = torch.randn(BW, T, HV, V, generator=gen, device=device).bfloat16()
+    g = -torch.nn.functional.softplus(torch.randn(BW, T, HV, generator=gen, device=device))
+    beta = torch.sigmoid(torch.randn(BW, T, HV, generator=gen, device=device)).bfloat16()
+    S = torch.randn(B, HV, K, V, generator=gen, device=device) * 0.02
+    S_before = S.clone()
+    out = ops.gated_delta(q, k, v, g, beta, S, beam_width=W)
+    torch.cuda.synchronize()
+    assert torch.equal(S, S_before)
+    for r in (0, 17, 31):
+        rows = slice(r * W, (r + 1) * W)
+        args = [t[rows].cpu() for t in (q, k, v, g, beta)] + [S[r:r + 1].cpu()]
+        expected = ops_ref.gated_delta(*args, beam_width=W)
+        assert_close_rel(out[rows].cpu(), expected, rtol=1e-2, atol_frac=2e-3,
+                         name=f"config2 request {r}")
+
+
+def test_gdn_replay_closed_form_beta_zero(device):
+    """beta = 0: o_t = gamma_t S0^T q^_t (no delta update), in float64."""
+    B, W, T, H, HV, K, V = 2, 16, 3, 2, 2, 128, 128
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, dtype=torch.float32, seed=21)
+    beta = torch.zeros_like(beta)
+    out = ops.gated_delta(*_to(device, q, k, v, g, beta, S), beam_width=W)
+    torch.cuda.synchronize()
+    qn = q.double() / (q.double().square().sum(-1, keepdim=True) + 1e-6).sqrt() * K ** -0.5
+    gam = g.double().cumsum(1).exp()                                  # [BW,T,HV]
+    S0 = S.double().repeat_interleave(W, 0)                           # [BW,HV,K,V]
+    expected = torch.einsum("nhkv,nthk->nthv", S0, qn) * gam[..., None]
+    assert_close_rel(out.cpu(), expected.float(), rtol=1e-4, atol_frac=1e-4, name="beta=0")
+
+
+def test_gdn_rejects_long_suffix_on_replay_limits(device):
+    q, k, v, g, beta, S = gdn_inputs(1, 2, 2, 1, 1, 96, 96)
+    with pytest.raises(RuntimeError):
+        ops.gated_delta(*_to(device, q, k, v, g, beta, S), beam_width=2)
+
+
+# --------------------------------------------------------------------------
+# causal conv1d
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("layout", ["reference", "token_major"])
+@pytest.mark.parametrize("case", [(2, 5, 24, 3), (3, 4, 6144, 2), (1, 1, 8, 1)])
+def test_conv_matches_oracle(device, dtype, layout, case):
+    B, W, C, T = case
+    x, st, w = conv_inputs(B, W, C, T, dtype=dtype, seed=C + T)
+    if layout == "token_major":
+        # the adapter's transposed view of a [BW, T, C] projection (strides (T*C, 1, C))
+        x = x.transpose(1, 2).contiguous().transpose(1, 2)
+    expected = ops_ref.causal_conv1d(x, st, w, beam_width=W)
+    xd, sd, wd = x.to(device), st.to(device), w.to(device)
+    if layout == "token_major":
+        xd = xd.transpose(1, 2).contiguous().transpose(1, 2)
+    sd_before = sd.clone()
+    out = ops.causal_conv1d(xd, sd, wd, beam_width=W)
+    torch.cuda.synchronize()
+    assert torch.equal(sd, sd_before)
+    if dtype == torch.bfloat16:
+        a, e = out.cpu().float(), expected.float()
+        ulp = (e.abs() * 2 ** -7).clamp_min(1e-30)
+        assert ((a - e).abs() <= ulp).all(), "bf16 conv differs by more than 1 ulp"
+        exact = (a == e).float().mean().item()
+        assert exact > 0.99, f"only {exact:.4f} bit-exact"
+    else:
+        assert_close_rel(out.cpu(), expected, rtol=1e-5, atol_frac=1e-6, name="conv fp32")
+
+
+def test_conv_golden_fixture(device):
+    f = load_npz("ops_bf16.npz")
+    x, st, w = (bf16_from_bits(f[n]) for n in ("conv_x", "conv_state", "conv_w"))
+    expected = bf16_from_bits(f["conv_out"])
+    out = ops.causal_conv1d(*_to(device, x, st, w), beam_width=3)
+    torch.cuda.synchronize()
+    a, e = out.cpu().float(), expected.float()
+    assert ((a - e).abs() <= e.abs() * 2 ** -7 + 1e-30).all()
+    assert (a == e).float().mean().item() > 0.97
+
+
+def test_conv_width_and_bias_variants(device):
+    B, W, C, T = 2, 3, 16, 3
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(B * W, C, T, generator=g)
+    st = torch.randn(B, C, 5, generator=g)
+    for width in (1, 2, 3, 4):
+        w = torch.randn(C, width, generator=g)
+        bias = torch.randn(C, generator=g)
+        for act in (None, "silu"):
+            expected = ops_ref.causal_conv1d(x, st, w, beam_width=W, bias=bias, activation=act)
+            out = ops.causal_conv1d(*_to(device, x, st, w), beam_width=W, bias=bias.to(device),
+                                    activation=act)
+            torch.cuda.synchronize()
+            assert_close_rel(out.cpu(), expected, rtol=1e-5, atol_frac=1e-6,
+                             name=f"conv width {width} act {act}")
