@@ -84,6 +84,96 @@ int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx
                            kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
+ * bf16 GEMM with fused epilogues: C[M,N] = A[M,K] W[N,K]^T, fp32 accumulate.
+ * Replaces the nn.Linear projections of the decode path
+ * (src/kadllm/adapters/qwen3_5.py:146,161-162,169,175,177,181-188,202,234-235)
+ * and of the transformers prefill they mirror.  Row strides lda, ldw, ldc,
+ * ldr in elements; K % 64 == 0; A, W 16-byte aligned.
+ *   KAD_EPI_STORE     C = bf16(acc)
+ *   KAD_EPI_RESIDUAL  C = bf16(R + bf16(acc)); R may alias C
+ *   KAD_EPI_SWIGLU    W rows interleaved in [gate 32 | up 32] blocks (N % 64
+ *                     == 0); C[:, j] = bf16(bf16(silu(bf16 g_j)) * bf16 u_j),
+ *                     N/2 output columns
+ */
+#define KAD_EPI_STORE 0
+#define KAD_EPI_RESIDUAL 1
+#define KAD_EPI_SWIGLU 2
+int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+                  const void* R, int64_t ldr, int M, int N, int K, int epilogue,
+                  kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Row-wise layer kernels (bf16).  They replace the transformers modules the
+ * reference decode calls between its projections (src/kadllm/adapters/
+ * qwen3_5.py:161-176,184-189,216-226,234-235) and reproduce their bf16
+ * rounding points.
+ *
+ * kad_rmsnorm        Qwen3_5RMSNorm: y = bf16(x rsqrt(mean x^2 + eps) (w_offset + w)),
+ *                    rows of D (D % 8 == 0), row strides ldx/ldy.
+ * kad_rmsnorm_gated  Qwen3_5RMSNormGated over `heads` groups of D per token:
+ *                    y = bf16(bf16(w bf16(x r)) silu(z)).
+ * kad_gdn_gates      g = -exp(A_log) softplus(a + dt_bias) (fp32, [rows, HV]),
+ *                    beta = bf16(sigmoid(b)) ([rows, HV]); a/b strided bf16.
+ * kad_qk_norm_rope   per (token, head): optional RMSNorm(1+w) over D, then
+ *                    rotate-half RoPE on the first `rot` dims with
+ *                    position pos0 + token % pos_period, bf16 cos/sin of
+ *                    fp32 angles pos * inv_freq[i]; writes to
+ *                    dst + (token / period) s_b + (token % period) s_t + head s_h.
+ * kad_scatter_heads  copies [rows, heads, D] head rows into that strided layout.
+ * kad_embedding      out[r] = table[ids[r]] (ids clamped into [0, vocab)).
+ */
+int kad_rmsnorm(const void* x, int64_t ldx, const void* w, float w_offset, void* y, int64_t ldy,
+                int64_t rows, int D, float eps, kad_stream_t stream);
+int kad_rmsnorm_gated(const void* x, int64_t ldx, const void* z, int64_t ldz, const void* w,
+                      void* y, int64_t ldy, int64_t rows, int heads, int D, float eps,
+                      kad_stream_t stream);
+int kad_gdn_gates(const void* a, int64_t lda, const void* b, int64_t ldb, const void* A_log,
+                  const void* dt_bias, float* g, void* beta, int64_t rows, int HV,
+                  kad_stream_t stream);
+int kad_qk_norm_rope(const void* src, int64_t ld_src, int64_t src_head_stride, int heads,
+                     const void* w, void* dst, int64_t period, int64_t s_b, int64_t s_t,
+                     int64_t s_h, int64_t rows, int D, int rot, const float* inv_freq,
+                     int64_t pos0, int64_t pos_period, float eps, int do_norm,
+                     kad_stream_t stream);
+int kad_scatter_heads(const void* src, int64_t ld_src, int heads, int D, void* dst,
+                      int64_t period, int64_t s_b, int64_t s_t, int64_t s_h, int64_t rows,
+                      kad_stream_t stream);
+int kad_embedding(const int64_t* ids, const void* table, void* out, int64_t rows, int D,
+                  int64_t vocab, kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Prefix-shared gated GQA decode attention (bf16 in/out, fp32 softmax).
+ * Replaces src/kadllm/ops.py:229-341 (prefix_attention, merge_attention) and
+ * src/kadllm/kernels/flash_attention.py:11-66, with the sigmoid output gate of
+ * src/kadllm/adapters/qwen3_5.py:199-201 fused (gate may be null).
+ *
+ * Row (n, t, h) of q [B*W, T, H, D] attends to the prefix keys of request
+ * b = n / W (prefix_k/v [B, L, HK, D] strided views, kv head h / (H/HK),
+ * keys with prefix_mask[b, key] == 0 excluded when the mask is given) and to
+ * suffix keys j <= t of its own beam (suffix_k/v [B*W, T, HK, D]).  One
+ * softmax over both (equal to the reference's LSE merge); out = bf16(o),
+ * times bf16(sigmoid(gate)) when gated.  Strides in elements.  T <= 4;
+ * D in {64, 128, 256}; prefix_mask is uint8/bool [B, L].
+ */
+int kad_prefix_attention_decode(
+    const void* q, int64_t sq_n, int64_t sq_t, int64_t sq_h, const void* prefix_k,
+    const void* prefix_v, int64_t sp_b, int64_t sp_l, int64_t sp_h, const void* suffix_k,
+    int64_t ssk_n, int64_t ssk_t, int64_t ssk_h, const void* suffix_v, int64_t ssv_n,
+    int64_t ssv_t, int64_t ssv_h, const void* prefix_mask, const void* gate, int64_t sg_n,
+    int64_t sg_t, int64_t sg_h, void* out, int64_t so_n, int64_t so_t, int64_t so_h, int B,
+    int W, int T, int H, int HK, int L, int D, float scale, kad_stream_t stream);
+
+/* Causal gated GQA attention over full prompts (prefill).  Replaces the
+ * causal SDPA of the transformers forward that the reference prefill runs
+ * (src/kadllm/adapters/qwen3_5.py:111).  q/out/gate [B, L, H, D]-strided,
+ * k/v [B, L, HK, D]-strided (e.g. views of [B, HK, L, D] caches). */
+int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, int64_t sq_h,
+                          const void* k, const void* v, int64_t skv_b, int64_t skv_l,
+                          int64_t skv_h, const void* gate, int64_t sg_b, int64_t sg_l,
+                          int64_t sg_h, void* out, int64_t so_b, int64_t so_l, int64_t so_h,
+                          int B, int L, int H, int HK, int D, float scale, kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
  * MFMA lane-layout self-test (no reference counterpart): C[16x16] = A[16x32]
  * B[32x16] (bf16 in, fp32 out, all row-major) computed by one wave with the
  * operand layout the kernels above assume for v_mfma_f32_16x16x32_bf16, and

@@ -29,6 +29,15 @@ _CTYPES = {"p": _P, "l": _L, "i": _I, "f": _F, "s": _P}
 SIGNATURES = {
     "kad_gdn_suffix_replay": "ppplli" "pipil" "pi" "pl" "iiiiiii" "f" "s",
     "kad_causal_conv_suffix": "plll" "pllli" "pip" "plll" "iiiiii" "s",
+    "kad_gemm_bf16": "plplplpl" "iiii" "s",
+    "kad_rmsnorm": "plpfpllifs",
+    "kad_rmsnorm_gated": "plplpplliifs",
+    "kad_gdn_gates": "plplpppplis",
+    "kad_qk_norm_rope": "plli" "pp" "lllll" "ii" "p" "ll" "f" "i" "s",
+    "kad_scatter_heads": "pliipllllls",
+    "kad_embedding": "ppplils",
+    "kad_prefix_attention_decode": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiii" "f" "s",
+    "kad_attention_prefill": "plll" "pplll" "plll" "plll" "iiiii" "f" "s",
     "kad_selftest_mfma16": "ppps",
     "kad_selftest_mfma32": "ppps",
 }

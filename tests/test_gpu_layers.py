@@ -1,0 +1,228 @@
+"""HIP GEMM, row-wise and attention kernels against fp32 references and the oracle."""
+
+import pytest
+import torch
+from torch.nn import functional as F
+
+from conftest import assert_close_rel
+from kadllm_amd import layers, ops
+from kadllm_amd.attention import attention_prefill
+from oracle import ops_ref, qwen35_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_ulp_close(actual, expected, name, min_exact=0.95):
+    """bf16 results within one ulp of the bf16-rounded fp32 reference.
+
+    An absolute term of 2e-5 * max|e| covers outputs that cancel to near zero,
+    where fp32 accumulation order alone moves the value by many bf16 ulps.
+    """
+    a = actual.float().cpu()
+    e = expected.float().cpu()
+    ulp = e.abs() * 2 ** -7 + 2e-5 * e.abs().max() + 1e-30
+    bad = (a - e).abs() > ulp
+    assert not bad.any(), f"{name}: {int(bad.sum())} elements differ by more than 1 ulp; " \
+        f"max {(a - e).abs().max().item():.3e}"
+    exact = (a == e).float().mean().item()
+    assert exact >= min_exact, f"{name}: only {exact:.4f} bit-exact"
+
+
+# --------------------------------------------------------------------------
+# GEMM
+
+
+@pytest.mark.parametrize("M,N,K", [(37, 200, 64), (130, 384, 128), (32, 4096, 256),
+                                   (1024, 1536, 1024), (300, 8320, 1024)])
+def test_gemm_store(device, M, N, K):
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    out = layers.gemm(a.to(device), w.to(device))
+    torch.cuda.synchronize()
+    ref = (a.float() @ w.float().T).bfloat16()
+    _bf16_ulp_close(out, ref, f"gemm {M}x{N}x{K}")
+
+
+def test_gemm_full_decode_shape_sampled_rows(device):
+    M, N, K = 8192, 8320, 1024
+    gen = torch.Generator(device=device).manual_seed(1)
+    a = torch.randn(M, K, generator=gen, device=device).bfloat16()
+    w = (torch.randn(N, K, generator=gen, device=device) * 0.02).bfloat16()
+    out = layers.gemm(a, w)
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 127, 128, 4095, 8000, 8191])
+    ref = (a[rows].float().cpu() @ w.float().cpu().T).bfloat16()
+    _bf16_ulp_close(out[rows], ref, "gemm 8192x8320x1024")
+
+
+def test_gemm_strided_operands_and_residual(device):
+    M, N, K = 200, 256, 192
+    g = torch.Generator().manual_seed(3)
+    big_a = torch.randn(M, K + 64, generator=g).bfloat16()
+    a = big_a[:, 32:32 + K]                       # row stride K+64, 64-byte offset
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    x = torch.randn(M, N, generator=g).bfloat16()
+    xd = x.to(device)
+    layers.gemm(big_a.to(device)[:, 32:32 + K], w.to(device), out=xd,
+                epilogue=layers.EPI_RESIDUAL, residual=xd)
+    torch.cuda.synchronize()
+    mixed = (a.float() @ w.float().T).bfloat16()
+    ref = (x.float() + mixed.float()).bfloat16()
+    _bf16_ulp_close(xd, ref, "gemm residual")
+
+
+def test_gemm_swiglu(device):
+    M, F_, K = 150, 192, 256
+    g = torch.Generator().manual_seed(4)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    wg = (torch.randn(F_, K, generator=g) * 0.05).bfloat16()
+    wu = (torch.randn(F_, K, generator=g) * 0.05).bfloat16()
+    packed = torch.stack((wg.reshape(F_ // 32, 32, K), wu.reshape(F_ // 32, 32, K)), 1).reshape(2 * F_, K)
+    out = layers.gemm(a.to(device), packed.to(device), epilogue=layers.EPI_SWIGLU)
+    torch.cuda.synchronize()
+    gate = (a.float() @ wg.float().T).bfloat16()
+    up = (a.float() @ wu.float().T).bfloat16()
+    ref = F.silu(gate) * up                        # bf16 ops, as the MLP module
+    _bf16_ulp_close(out, ref, "gemm swiglu", min_exact=0.9)
+
+
+# --------------------------------------------------------------------------
+# row-wise kernels
+
+
+def test_rmsnorm_matches_oracle(device):
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(333, 1024, generator=g).bfloat16()
+    w = (torch.randn(1024, generator=g) * 0.1).bfloat16()
+    out = layers.rmsnorm(x.to(device), w.to(device), 1e-6)
+    torch.cuda.synchronize()
+    _bf16_ulp_close(out, qwen35_ref.rms_norm(x, w, 1e-6), "rmsnorm", min_exact=0.99)
+
+
+def test_rmsnorm_gated_matches_oracle(device):
+    g = torch.Generator().manual_seed(6)
+    rows, heads, D = 97, 16, 128
+    big = torch.randn(rows, 3 * heads * D, generator=g).bfloat16()   # x and z live in a wider row
+    x, z = big[:, :heads * D], big[:, 2 * heads * D:]
+    w = (1 + torch.randn(D, generator=g) * 0.1).bfloat16()
+    bd = big.to(device)
+    out = layers.rmsnorm_gated(bd[:, :heads * D], bd[:, 2 * heads * D:], w.to(device), 1e-6, heads)
+    torch.cuda.synchronize()
+    ref = qwen35_ref.rms_norm_gated(x.reshape(-1, D), z.reshape(-1, D), w, 1e-6).reshape(rows, -1)
+    _bf16_ulp_close(out, ref, "rmsnorm_gated", min_exact=0.99)
+
+
+def test_gdn_gates_match_reference_formula(device):
+    g = torch.Generator().manual_seed(7)
+    rows, HV = 500, 16
+    ab = torch.randn(rows, 40, generator=g).bfloat16()
+    a, b = ab[:, 3:3 + HV], ab[:, 20:20 + HV]
+    A_log = torch.log(torch.rand(HV, generator=g) * 16 + 1e-3).bfloat16()
+    dt_bias = torch.ones(HV).bfloat16()
+    abd = ab.to(device)
+    gd, bd = layers.gdn_gates(abd[:, 3:3 + HV], abd[:, 20:20 + HV], A_log.to(device),
+                              dt_bias.to(device))
+    torch.cuda.synchronize()
+    g_ref = -A_log.float().exp() * F.softplus(a.float() + dt_bias)   # qwen3_5.py:161-163
+    b_ref = b.sigmoid()                                               # qwen3_5.py:169
+    assert_close_rel(gd.cpu(), g_ref, rtol=1e-6, atol_frac=1e-7, name="g")
+    _bf16_ulp_close(bd, b_ref, "beta", min_exact=0.99)
+
+
+def test_qk_norm_rope_matches_oracle(device):
+    from kadllm_amd.config import qwen35_08b_config
+    cfg = qwen35_08b_config()
+    g = torch.Generator().manual_seed(8)
+    rows, T, H, D = 24, 3, 8, 256
+    proj = torch.randn(rows * T, H * 2 * D, generator=g).bfloat16()
+    wq = (torch.randn(D, generator=g) * 0.1).bfloat16()
+    L0 = 1024
+    inv = qwen35_ref.rope_inv_freq(cfg)
+    out = torch.empty(rows * T, H, D, dtype=torch.bfloat16, device=device)
+    layers.qk_norm_rope(proj.to(device), H * 2 * D, 2 * D, H, wq.to(device), out,
+                        (0, H * D, D), rows * T, rows * T, D, 64, inv.to(device), L0, T, 1e-6)
+    torch.cuda.synchronize()
+    q = proj.reshape(rows, T, H, 2 * D)[..., :D]
+    qn = qwen35_ref.rms_norm(q, wq, 1e-6).transpose(1, 2)              # [rows,H,T,D]
+    pos = torch.arange(L0, L0 + T)[None].expand(rows, T)
+    cos, sin = qwen35_ref.rope_cos_sin(cfg, pos, torch.bfloat16)
+    ref = qwen35_ref.apply_rope(qn, cos[:, None], sin[:, None]).transpose(1, 2)
+    _bf16_ulp_close(out.reshape(rows, T, H, D), ref, "qk_norm_rope", min_exact=0.99)
+
+
+def test_embedding(device):
+    g = torch.Generator().manual_seed(9)
+    table = torch.randn(1000, 256, generator=g).bfloat16()
+    ids = torch.randint(0, 1000, (7, 5), generator=g)
+    out = layers.embedding(ids.to(device), table.to(device))
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), table[ids.reshape(-1)])
+
+
+# --------------------------------------------------------------------------
+# attention
+
+
+def _attn_inputs(B, W, T, H, HK, L, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    bf = torch.bfloat16
+    q = torch.randn(B * W, T, H, D, generator=g).to(bf)
+    pk = torch.randn(B, HK, L, D, generator=g).to(bf).transpose(1, 2)    # HF cache view
+    pv = torch.randn(B, HK, L, D, generator=g).to(bf).transpose(1, 2)
+    sk = torch.randn(B * W, T, HK, D, generator=g).to(bf)
+    sv = torch.randn(B * W, T, HK, D, generator=g).to(bf)
+    return q, pk, pv, sk, sv
+
+
+@pytest.mark.parametrize("B,W,T,H,HK,L,D", [
+    (2, 256, 1, 8, 2, 1024, 256), (2, 256, 3, 8, 2, 1024, 256),   # config-3 shape, 2 requests
+    (2, 5, 2, 4, 1, 70, 64), (3, 3, 4, 4, 2, 5, 128), (1, 2, 3, 2, 2, 0, 64),
+])
+def test_prefix_attention_matches_oracle(device, B, W, T, H, HK, L, D):
+    q, pk, pv, sk, sv = _attn_inputs(B, W, T, H, HK, L, D, seed=L + T)
+    exp = ops_ref.prefix_attention(q, pk, pv, sk, sv, beam_width=W, compute=torch.float64)
+    dev = [t.to(device) for t in (q, pk, pv, sk, sv)]
+    pk_before = dev[1].clone()
+    out = ops.prefix_attention(*dev, beam_width=W, backend="flash_attn")
+    torch.cuda.synchronize()
+    assert torch.equal(dev[1], pk_before)
+    assert_close_rel(out.cpu(), exp, rtol=1e-2, atol_frac=4e-3, name="prefix attention")
+
+
+def test_prefix_attention_mask_and_gate(device):
+    B, W, T, H, HK, L, D = 2, 6, 3, 8, 2, 130, 256
+    q, pk, pv, sk, sv = _attn_inputs(B, W, T, H, HK, L, D, seed=31)
+    mask = torch.rand(B, L, generator=torch.Generator().manual_seed(2)) > 0.3
+    mask[1] = False                                                      # fully masked prefix
+    gate = torch.randn(B * W, T, H * D, generator=torch.Generator().manual_seed(3)).bfloat16()
+    exp = ops_ref.prefix_attention(q, pk, pv, sk, sv, beam_width=W, prefix_mask=mask)
+    exp = exp.reshape(B * W, T, -1) * gate.sigmoid()                     # bf16, qwen3_5.py:199-201
+    dev = [t.to(device) for t in (q, pk, pv, sk, sv)]
+    out = ops.prefix_attention(*dev, beam_width=W, prefix_mask=mask.to(device),
+                               gate=gate.to(device))
+    torch.cuda.synchronize()
+    assert_close_rel(out.reshape(B * W, T, -1).cpu(), exp, rtol=1e-2, atol_frac=4e-3,
+                     name="masked gated attention")
+
+
+@pytest.mark.parametrize("B,L,H,HK,D", [(2, 100, 8, 2, 256), (1, 1024, 8, 2, 256), (2, 37, 4, 1, 64)])
+def test_attention_prefill_causal(device, B, L, H, HK, D):
+    g = torch.Generator().manual_seed(L)
+    bf = torch.bfloat16
+    q = torch.randn(B, L, H, D, generator=g).to(bf)
+    kc = torch.randn(B, HK, L, D, generator=g).to(bf)        # cache layout [B,HK,L,D]
+    vc = torch.randn(B, HK, L, D, generator=g).to(bf)
+    gate = torch.randn(B, L, H * D, generator=g).to(bf)
+    rep = H // HK
+    s = q.double().transpose(1, 2) @ kc.double().repeat_interleave(rep, 1).transpose(-1, -2)
+    s = s * D ** -0.5
+    s = s.masked_fill(~torch.ones(L, L, dtype=torch.bool).tril(), -torch.inf)
+    o = (s.softmax(-1) @ vc.double().repeat_interleave(rep, 1)).transpose(1, 2)   # [B,L,H,D]
+    exp = o.to(bf).reshape(B, L, -1) * gate.sigmoid()
+    qd, kd, vd, gd = q.to(device), kc.to(device), vc.to(device), gate.to(device)
+    out = attention_prefill(qd, kd.transpose(1, 2), vd.transpose(1, 2), D ** -0.5, gate=gd,
+                            gate_strides=(gd.stride(0), gd.stride(1), D))
+    torch.cuda.synchronize()
+    assert_close_rel(out.reshape(B, L, -1).cpu(), exp, rtol=1e-2, atol_frac=4e-3,
+                     name="prefill attention")

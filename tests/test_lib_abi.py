@@ -25,14 +25,30 @@ def test_signature_table_covers_header():
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
 
 
-def test_signature_arity_matches_header():
+def _letter(param):
+    p = " ".join(param.split())
+    if p.startswith("kad_stream_t"):
+        return "s"
+    if "*" in p:
+        return "p"
+    if p.startswith("int64_t"):
+        return "l"
+    if p.startswith("int "):
+        return "i"
+    if p.startswith("float"):
+        return "f"
+    raise AssertionError(f"unclassified parameter {param!r}")
+
+
+def test_signature_types_match_header():
     import re
     text = open(_lib.HEADER_PATH).read()
     for name, sig in _lib.SIGNATURES.items():
         m = re.search(r"int\s+" + name + r"\s*\(([^;]*)\);", text, re.S)
         assert m, name
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
-        assert len(params) == len(sig), (name, len(params), len(sig))
+        letters = "".join(_letter(p) for p in params)
+        assert letters == sig, (name, letters, sig)
 
 
 def test_abi_version_and_error_string():
