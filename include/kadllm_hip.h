@@ -174,6 +174,65 @@ int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, int64_t sq_
                           int B, int L, int H, int HK, int D, float scale, kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
+ * Beam selection: full-vocabulary log-softmax, optional bool constraint,
+ * parent-score add and top-W, without fp32 [W, V] temporaries.  Replaces
+ * src/kadllm/grbeam.py:89-104.  Ties are broken by the lower flat index
+ * (parent * V + token); torch.topk leaves that order unspecified.
+ *
+ * kad_beam_row_select    per beam row r (rows = B * Wp, row stride ld of the
+ *                        bf16 logits; mask uint8 [rows, V] (ld_mask) or null):
+ *                        writes the row's K = min(W, V) best candidates,
+ *                        key = ((x - max_r) - log sum exp(x - max_r)) + parent[r]
+ *                        (-inf where masked) and flat index (r % Wp) * V + c,
+ *                        to cand_key / cand_idx [rows, K].
+ * kad_beam_merge_select  per request b: the W best of its ncand = Wp * K
+ *                        candidates, sorted by (key desc, index asc): scores
+ *                        [B, W] fp32, parents = index / V, tokens = index % V
+ *                        (int64), valid = isfinite(score) (uint8).  W <= 1024.
+ * kad_beam_history       out[b, w, :] = [history[b, parents[b, w], :step], tokens[b, w]]
+ *                        (history [B, Wp, step] int64, out [B, W, step + 1]).
+ */
+int kad_beam_row_select(const void* logits, int64_t ld, const void* mask, int64_t ld_mask,
+                        const float* parent_scores, int rows, int Wp, int V, int K,
+                        float* cand_key, int* cand_idx, kad_stream_t stream);
+int kad_beam_merge_select(const float* cand_key, const int* cand_idx, int B, int ncand, int W,
+                          int V, float* scores, int64_t* parents, int64_t* tokens, void* valid,
+                          kad_stream_t stream);
+int kad_beam_history(const int64_t* history, int Wp, int step, const int64_t* parents,
+                     const int64_t* tokens, int64_t* out, int B, int W, kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Chunked gated delta rule over sequences (chunks of 64 tokens).
+ * Replaces the prefill's transformers torch_chunk_gated_delta_rule reached
+ * through src/kadllm/adapters/qwen3_5.py:111, and src/kadllm/ops.py:139-163
+ * (gated_delta) for suffixes longer than kad_gdn_suffix_replay handles and
+ * for final-state requests (ops.py:119-122).
+ *
+ * N sequences of T tokens; q/k/v/out/gates laid out as in
+ * kad_gdn_suffix_replay with n in [0, N).  initial_state (nullable, [N /
+ * beams_per_state, HV, K, V]) is read for sequence n at n / beams_per_state;
+ * final_state (nullable, fp32 [N, HV, K, V]) receives each sequence's final
+ * state.  transformers_l2norm = 1 normalises q and k with the bf16 roundings
+ * of transformers' l2norm (prefill); 0 normalises in fp32 as ops.py:147-148.
+ * bf16 q/k/v; K, V in {64, 128}.
+ */
+int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
+                  int qkv_dtype, const void* log_decay, int gate_dtype, const void* beta,
+                  int beta_dtype, int64_t ld_gate, const void* initial_state, int state_dtype,
+                  int beams_per_state, void* out, int64_t ld_out, float* final_state, int N,
+                  int T, int H, int HV, int K, int V, float scale, int transformers_l2norm,
+                  kad_stream_t stream);
+
+/* Causal width-4 conv + SiLU over whole prompts with zero history, and the
+ * conv state (last 4 pre-conv inputs, [B, C, 4], nullable) that decode reads.
+ * Replaces the prefill's transformers causal_conv1d_fn and conv-state cache
+ * update reached through src/kadllm/adapters/qwen3_5.py:111.  x/out are
+ * [B*L, C] row-strided bf16 (row = b*L + t); weight [C, 4]. */
+int kad_causal_conv_prefill(const void* x, int64_t ldx, const void* weight, void* out,
+                            int64_t ldo, void* state, int B, int L, int C, int activation_silu,
+                            kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
  * MFMA lane-layout self-test (no reference counterpart): C[16x16] = A[16x32]
  * B[32x16] (bf16 in, fp32 out, all row-major) computed by one wave with the
  * operand layout the kernels above assume for v_mfma_f32_16x16x32_bf16, and

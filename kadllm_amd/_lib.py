@@ -38,6 +38,11 @@ SIGNATURES = {
     "kad_embedding": "ppplils",
     "kad_prefix_attention_decode": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiii" "f" "s",
     "kad_attention_prefill": "plll" "pplll" "plll" "plll" "iiiii" "f" "s",
+    "kad_beam_row_select": "plplpiiiipps",
+    "kad_beam_merge_select": "ppiiiipppps",
+    "kad_beam_history": "piipppiis",
+    "kad_gdn_chunk": "ppplli" "pipil" "pii" "plp" "iiiiii" "fi" "s",
+    "kad_causal_conv_prefill": "plpplpiiiis",
     "kad_selftest_mfma16": "ppps",
     "kad_selftest_mfma32": "ppps",
 }
@@ -101,3 +106,8 @@ def dtype_code(dtype):
 
 def ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def ptr_at(address):
+    """A raw device address (e.g. a column offset inside a row-strided buffer)."""
+    return ctypes.c_void_p(address)

@@ -1,0 +1,5 @@
+"""Explicit GRBeam model adapters, separate from kernels and beam selection."""
+
+from .qwen3_5 import Qwen35GRBeamAdapter, Qwen35Prefix, native_model
+
+__all__ = ["Qwen35GRBeamAdapter", "Qwen35Prefix", "native_model"]

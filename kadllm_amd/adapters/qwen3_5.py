@@ -1,0 +1,127 @@
+"""GRBeam inference adapter for the dense Qwen3.5 text model (MI355X HIP path).
+
+Drop-in for src/kadllm/adapters/qwen3_5.py: same constructor, validation,
+exception types and messages, ``Qwen35Prefix`` layout and prefill/decode
+contract.  Pass the transformers ``Qwen3_5TextModel`` and its LM head (for
+``Qwen3_5ForConditionalGeneration``: ``model.model.language_model,
+model.lm_head``), or the package's own ``Qwen35TextModel`` / ``LMHead``.
+
+The wrapped model is not mutated: its weights are packed once, at
+construction, into fused bf16 device buffers, and both prefill and decode run
+the native HIP kernels (kadllm_amd.qwen35.Qwen35Runner).  The backend
+arguments keep their reference names and validation; every accepted value
+runs the single HIP implementation.  The prefix is request-sized and is never
+written by decode.  Models must be bf16 and on one ROCm device.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from ..config import Qwen35Config
+from ..grbeam import PrefillResult
+from ..ops import _gdn_launch
+from ..qwen35 import LMHead, Qwen35Runner, Qwen35TextModel
+
+
+@dataclass(frozen=True)
+class Qwen35Prefix:
+    length: int
+    batch: int
+    owner: object
+    layers: tuple[tuple[torch.Tensor, torch.Tensor], ...]
+
+
+def _is_transformers_text_model(obj):
+    try:
+        from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextModel
+    except ImportError:
+        return False
+    return type(obj) is Qwen3_5TextModel
+
+
+class Qwen35GRBeamAdapter:
+    """Wrap an eval-mode Qwen3.5 text model and its matching LM head.
+
+    gdn_backend / conv_backend accept torch/auto/triton and attention_backend
+    torch/flash_attn, as in the reference; all run the HIP kernels.
+    gdn_triton_config keeps its validation (tile_v, warps, stages[, beam_group])
+    and its requirement of gdn_backend='triton'; the HIP kernel picks its own
+    tiling.
+    """
+
+    def __init__(self, text_model, lm_head, *, gdn_backend="torch", conv_backend="torch",
+                 attention_backend="torch", gdn_triton_config=None):
+        native = isinstance(text_model, Qwen35TextModel)
+        if not native and not _is_transformers_text_model(text_model):
+            raise TypeError("pass the dense Qwen3_5TextModel explicitly")
+        cfg = text_model.config
+        rope = getattr(cfg, "rope_parameters", None) or {}
+        if rope.get("rope_type", "default") != "default":
+            raise ValueError("only default RoPE is supported")
+        if cfg.hidden_act != "silu":
+            raise ValueError("only SiLU convolution is supported")
+        if gdn_backend not in ("torch", "auto", "triton") or conv_backend not in (
+            "torch", "auto", "triton",
+        ):
+            raise ValueError("invalid GDN or convolution backend")
+        if attention_backend not in ("torch", "flash_attn"):
+            raise ValueError("invalid attention backend")
+        if any(kind not in ("linear_attention", "full_attention") for kind in cfg.layer_types):
+            raise ValueError("unsupported layer type")
+        devices = {p.device for module in (text_model, lm_head) for p in module.parameters()}
+        if len(devices) != 1:
+            raise ValueError("only single-device models are supported")
+        device = devices.pop()
+        _gdn_launch(gdn_triton_config)
+        if gdn_triton_config is not None and gdn_backend != "triton":
+            raise ValueError("gdn_triton_config requires gdn_backend='triton'")
+        dtypes = {p.dtype for module in (text_model, lm_head) for p in module.parameters()}
+        if dtypes != {torch.bfloat16}:
+            raise TypeError("the HIP GRBeam path runs bf16 models; convert with .to(torch.bfloat16)")
+        if device.type != "cuda":
+            raise RuntimeError("the HIP GRBeam path needs the model on a ROCm device")
+        self.layer_types = tuple(cfg.layer_types)
+        self.model, self.lm_head = text_model, lm_head
+        self.gdn_backend, self.conv_backend = gdn_backend, conv_backend
+        self.attention_backend = attention_backend
+        self.gdn_triton_config = gdn_triton_config
+        self.config = cfg if native else Qwen35Config.from_hf(cfg)
+        self.device = device
+        self._runner = Qwen35Runner(self.config, text_model.state_dict(),
+                                    lm_head_weight=lm_head.weight, device=device)
+        self._owner = object()
+
+    def _check(self, tokens):
+        if self.model.training or self.lm_head.training:
+            raise RuntimeError("call eval() before replay")
+        if tokens.dtype not in (torch.int32, torch.int64):
+            raise TypeError("token IDs must be integers")
+        if tokens.device != self.device:
+            raise ValueError("tokens and model must share a device")
+
+    @torch.no_grad()
+    def prefill(self, input_ids):
+        self._check(input_ids)
+        if input_ids.ndim != 2 or min(input_ids.shape) < 1:
+            raise ValueError("input_ids must be nonempty unpadded [B,L]")
+        logits, layers = self._runner.prefill(input_ids)
+        state = Qwen35Prefix(input_ids.shape[1], input_ids.shape[0], self._owner, layers)
+        return PrefillResult(logits, state)
+
+    @torch.no_grad()
+    def decode(self, history, state):
+        self._check(history)
+        if not isinstance(state, Qwen35Prefix) or state.owner is not self._owner:
+            raise ValueError("prefix belongs to a different adapter")
+        if history.ndim != 3 or min(history.shape) < 1 or history.shape[0] != state.batch:
+            raise ValueError("history must be nonempty [B,W,T] matching the prefix")
+        if history.shape[2] > 4:
+            raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
+        return self._runner.decode(history, state.layers, state.length)
+
+
+def native_model(cfg, state_dict):
+    """(Qwen35TextModel, LMHead) for a state dict in transformers naming."""
+    head = state_dict.get("lm_head.weight", state_dict["embed_tokens.weight"])
+    return Qwen35TextModel(cfg, state_dict), LMHead(head)

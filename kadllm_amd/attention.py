@@ -13,10 +13,12 @@ def _inner_contiguous(t):
 
 
 def prefix_attention_decode(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_width, prefix_mask,
-                            scale, gate=None, out=None):
+                            scale, gate=None, out=None, gate_strides=None):
     """q [B*W,T,H,D]; prefix K/V [B,L,HK,D] (strided views allowed); suffix K/V
     [B*W,T,HK,D]; optional bool prefix_mask [B,L]; optional gate [B*W,T,H*D]
-    (output multiplied by sigmoid(gate)).  Returns [B*W,T,H,D] bf16."""
+    (output multiplied by sigmoid(gate)), or any tensor whose data pointer is
+    head 0's gate with element strides ``gate_strides`` = (beam, token, head).
+    Returns [B*W,T,H,D] bf16."""
     if q.dtype != torch.bfloat16:
         raise RuntimeError("HIP prefix attention supports bf16 inputs")
     BW, T, H, D = q.shape
@@ -33,7 +35,9 @@ def prefix_attention_decode(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_widt
     mask = None
     if prefix_mask is not None:
         mask = prefix_mask.contiguous().view(torch.uint8)
-    if gate is not None:
+    if gate is not None and gate_strides is not None:
+        g_strides = tuple(gate_strides)
+    elif gate is not None:
         if gate.shape != (BW, T, H * D) or gate.dtype != torch.bfloat16:
             raise ValueError("gate must be bf16 [B*W, T, H*D]")
         if gate.stride(-1) != 1 or any(s % 4 for s in gate.stride()[:-1]):

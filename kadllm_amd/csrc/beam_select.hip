@@ -1,0 +1,359 @@
+// Full-vocabulary log-softmax + beam top-k + history update (gfx950).
+//
+// Replaces the per-request selection loop of src/kadllm/grbeam.py:89-104:
+//   logp = logits[r].float().log_softmax(-1); logp[~mask] = -inf;
+//   logp += scores[r, :, None]; top-W of logp.reshape(-1) (sorted);
+//   parents = idx // V; tokens = idx % V; history = cat(history[parents], tokens)
+// without materialising any [W, V] fp32 temporary.
+//
+// Stage 1, kad_beam_row_select (one workgroup per beam row): a first pass
+// takes the row max and a 4096-bin histogram of the top 12 bits of the bf16
+// order key of every allowed logit; a second pass sums exp(x - max) for the
+// row's log-sum-exp and resolves the low 4 bits inside the bin that holds the
+// row's K-th largest logit, giving its exact value; a third pass emits exactly
+// the row's K best entries (ties taken in column order).  Within a row the score
+// order is the logit order, so the request's top W is among these rows'
+// top min(W, V) entries.  Keys are ((x - max) - log(sum exp)) + parent in fp32.
+//
+// Stage 2, kad_beam_merge_select (one workgroup per request): an 8-bit radix
+// select over the request's Wp*K candidate keys finds the W-th key, a second
+// radix select over flat indices resolves ties (lower flat index first), and
+// the W winners are bitonic-sorted by (key desc, index asc).
+//
+// Stage 3, kad_beam_history: new_history[b, w] = [history[b, parent], token].
+
+#include "kad_common.h"
+
+namespace {
+
+constexpr int kRowThreads = 256;
+constexpr int kBins = 4096;
+
+__device__ __forceinline__ uint32_t order16(uint16_t bits) {
+  return (bits & 0x8000u) ? (uint32_t)(~bits & 0xffffu) : (uint32_t)(bits | 0x8000u);
+}
+__device__ __forceinline__ uint32_t order32(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// block-wide exclusive scan of one int per thread (blockDim = kRowThreads)
+__device__ int block_exclusive_scan(int v, int* scratch, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) scratch[wave] = x;
+  __syncthreads();
+  int base = 0, tot = 0;
+  for (int w = 0; w < kRowThreads / 64; ++w) {
+    if (w < wave) base += scratch[w];
+    tot += scratch[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return base + x - v;
+}
+
+__global__ __launch_bounds__(kRowThreads) void row_select_kernel(
+    const bf16_t* __restrict__ logits, int64_t ld, const uint8_t* __restrict__ mask,
+    int64_t ld_mask, const float* __restrict__ parent, int Wp, int V, int K,
+    float* __restrict__ cand_key, int* __restrict__ cand_idx) {
+  __shared__ int hist[kBins];
+  __shared__ int scan_tmp[kRowThreads / 64];
+  __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64];
+  __shared__ int sh_bin, sh_above, sh_low;
+  __shared__ int sh_emit;
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const bf16_t* x = logits + row * ld;
+  const uint8_t* mk = mask ? mask + row * ld_mask : nullptr;
+
+  for (int i = tid; i < kBins; i += kRowThreads) hist[i] = 0;
+  if (tid == 0) sh_emit = 0;
+  __syncthreads();
+
+  // pass 1: max over all logits (log_softmax normalises before masking);
+  // histogram of the order keys of the allowed logits
+  float m = -INFINITY;
+  for (int c = tid; c < V; c += kRowThreads) {
+    const uint16_t bits = x[c];
+    m = fmaxf(m, bf2f(bits));
+    const bool ok = mk ? mk[c] != 0 : true;
+    atomicAdd(&hist[ok ? (order16(bits) >> 4) : 0], 1);
+  }
+  m = wave_max(m);
+  if ((tid & 63) == 0) red_m[tid >> 6] = m;
+  __syncthreads();
+  float M = -INFINITY;
+  for (int w = 0; w < kRowThreads / 64; ++w) M = fmaxf(M, red_m[w]);
+
+  // find the bin holding the K-th largest allowed key (masked entries count
+  // in bin 0 so that rows with fewer than K allowed logits still yield K)
+  if (tid == 0) {
+    int acc = 0, b = kBins - 1;
+    for (; b > 0; --b) {
+      if (acc + hist[b] >= K) break;
+      acc += hist[b];
+    }
+    sh_bin = b;
+    sh_above = acc;  // entries in bins above b
+  }
+  __syncthreads();
+  const int bin = sh_bin;
+  for (int i = tid; i < 16; i += kRowThreads) hist[i] = 0;
+  __syncthreads();
+
+  // pass 2: exact sum exp(x - M); low-4-bit histogram inside `bin`
+  float se = 0.f;
+  for (int c = tid; c < V; c += kRowThreads) {
+    const uint16_t bits = x[c];
+    se += expf(bf2f(bits) - M);
+    const bool ok = mk ? mk[c] != 0 : true;
+    const uint32_t u = ok ? order16(bits) : 0u;
+    if ((int)(u >> 4) == bin) atomicAdd(&hist[u & 15], 1);
+  }
+  se = wave_sum(se);
+  if ((tid & 63) == 0) red_s[tid >> 6] = se;
+  __syncthreads();
+  if (tid == 0) {
+    int acc = sh_above, lo = 15;
+    for (; lo > 0; --lo) {
+      if (acc + hist[lo] >= K) break;
+      acc += hist[lo];
+    }
+    sh_low = lo;
+    sh_above = acc;  // entries strictly above the threshold key
+  }
+  __syncthreads();
+  float SE = 0.f;
+  for (int w = 0; w < kRowThreads / 64; ++w) SE += red_s[w];
+  const float lse = logf(SE);
+  const uint32_t thr = ((uint32_t)bin << 4) | (uint32_t)sh_low;
+  const int need_ties = K - sh_above;
+  const float p = parent[row];
+  const int r_local = (int)(row % Wp);
+  float* ck = cand_key + row * K;
+  int* ci = cand_idx + row * K;
+
+  // pass 3: emit entries above the threshold, and the first `need_ties`
+  // threshold entries in column order (tiles of kRowThreads consecutive columns)
+  int ties_taken = 0;
+  for (int c0 = 0; c0 < V; c0 += kRowThreads) {
+    const int c = c0 + tid;
+    uint32_t u = 0;
+    float v = -INFINITY;
+    bool ok = false;
+    if (c < V) {
+      const uint16_t bits = x[c];
+      ok = mk ? mk[c] != 0 : true;
+      u = ok ? order16(bits) : 0u;
+      v = bf2f(bits);
+    }
+    const bool above = c < V && u > thr;
+    const bool tie = c < V && u == thr;
+    int tot = 0;
+    const int rank = block_exclusive_scan(tie ? 1 : 0, scan_tmp, &tot);
+    const bool take_tie = tie && (ties_taken + rank < need_ties);
+    if (above || take_tie) {
+      const int slot = atomicAdd(&sh_emit, 1);
+      const float key = ok ? ((v - M) - lse) + p : -INFINITY;
+      if (slot < K) {  // exactly K entries qualify; the bound only guards memory
+        ck[slot] = key;
+        ci[slot] = r_local * V + c;
+      }
+    }
+    ties_taken += tot;
+  }
+}
+
+// ---------------------------------------------------------------------------
+constexpr int kMergeThreads = 1024;
+constexpr int kMaxW = 1024;
+
+__device__ __forceinline__ bool before(float ka, int ia, float kb, int ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+__global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
+    const float* __restrict__ cand_key, const int* __restrict__ cand_idx, int ncand, int W,
+    int V, float* __restrict__ scores, int64_t* __restrict__ parents,
+    int64_t* __restrict__ tokens, uint8_t* __restrict__ valid) {
+  __shared__ int hist[256];
+  __shared__ uint32_t sh_prefix;
+  __shared__ int sh_need, sh_count;
+  __shared__ float sk[kMaxW];
+  __shared__ int si[kMaxW];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const float* keys = cand_key + (int64_t)b * ncand;
+  const int* idxs = cand_idx + (int64_t)b * ncand;
+
+  // radix select of the W-th largest key (order32 space), 4 x 8 bits
+  uint32_t prefix = 0, pmask = 0;
+  int need = W;  // rank (1-based) of the target within the current prefix class
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += kMergeThreads) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < ncand; i += kMergeThreads) {
+      const uint32_t u = order32(keys[i]);
+      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0, d = 255;
+      for (; d > 0; --d) {
+        if (acc + hist[d] >= need) break;
+        acc += hist[d];
+      }
+      sh_prefix = prefix | ((uint32_t)d << shift);
+      sh_need = need - acc;
+    }
+    __syncthreads();
+    prefix = sh_prefix;
+    need = sh_need;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+  const uint32_t kth = prefix;  // order key of the W-th largest
+  // `need` ties at kth are taken, smallest flat index first: radix select on index
+  uint32_t iprefix = 0, imask = 0;
+  int ineed = need;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += kMergeThreads) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < ncand; i += kMergeThreads) {
+      if (order32(keys[i]) != kth) continue;
+      const uint32_t u = (uint32_t)idxs[i];
+      if ((u & imask) == iprefix) atomicAdd(&hist[(u >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0, d = 0;
+      for (; d < 255; ++d) {
+        if (acc + hist[d] >= ineed) break;
+        acc += hist[d];
+      }
+      sh_prefix = iprefix | ((uint32_t)d << shift);
+      sh_need = ineed - acc;
+    }
+    __syncthreads();
+    iprefix = sh_prefix;
+    ineed = sh_need;
+    imask |= 255u << shift;
+    __syncthreads();
+  }
+  const uint32_t idx_cut = iprefix;  // largest tied index taken
+
+  // gather the W winners
+  if (tid == 0) sh_count = 0;
+  __syncthreads();
+  for (int i = tid; i < ncand; i += kMergeThreads) {
+    const uint32_t u = order32(keys[i]);
+    const bool take = u > kth || (u == kth && (uint32_t)idxs[i] <= idx_cut);
+    if (take) {
+      const int slot = atomicAdd(&sh_count, 1);
+      if (slot < kMaxW) {
+        sk[slot] = keys[i];
+        si[slot] = idxs[i];
+      }
+    }
+  }
+  __syncthreads();
+  // pad to a power of two and bitonic-sort by (key desc, idx asc)
+  int P = 1;
+  while (P < W) P <<= 1;
+  for (int i = W + tid; i < P; i += kMergeThreads) {
+    sk[i] = -INFINITY;
+    si[i] = 0x7fffffff;
+  }
+  __syncthreads();
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < P; i += kMergeThreads) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool dir = (i & size) == 0;  // ascending in "before" order
+          const bool sw = dir ? before(sk[j], si[j], sk[i], si[i])
+                              : before(sk[i], si[i], sk[j], si[j]);
+          if (sw) {
+            const float tk = sk[i];
+            sk[i] = sk[j];
+            sk[j] = tk;
+            const int ti = si[i];
+            si[i] = si[j];
+            si[j] = ti;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = tid; i < W; i += kMergeThreads) {
+    const float key = sk[i];
+    const int id = si[i];
+    scores[(int64_t)b * W + i] = key;
+    parents[(int64_t)b * W + i] = id / V;
+    tokens[(int64_t)b * W + i] = id % V;
+    valid[(int64_t)b * W + i] = (key == key) && (key != INFINITY) && (key != -INFINITY);
+  }
+}
+
+__global__ __launch_bounds__(256) void history_kernel(const int64_t* __restrict__ hist, int Wp,
+                                                      int step, const int64_t* __restrict__ parents,
+                                                      const int64_t* __restrict__ tokens,
+                                                      int64_t* __restrict__ out, int B, int W) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)B * W * (step + 1)) return;
+  const int j = (int)(i % (step + 1));
+  const int64_t bw = i / (step + 1);
+  const int b = (int)(bw / W);
+  if (j == step) {
+    out[i] = tokens[bw];
+  } else {
+    int64_t p = parents[bw];
+    p = p < 0 ? 0 : (p >= Wp ? Wp - 1 : p);
+    out[i] = hist[((int64_t)b * Wp + p) * step + j];
+  }
+}
+
+}  // namespace
+
+extern "C" int kad_beam_row_select(const void* logits, int64_t ld, const void* mask,
+                                   int64_t ld_mask, const float* parent_scores, int rows, int Wp,
+                                   int V, int K, float* cand_key, int* cand_idx,
+                                   kad_stream_t stream) {
+  KAD_REQUIRE(logits && parent_scores && cand_key && cand_idx, "null pointer argument");
+  KAD_REQUIRE(rows > 0 && Wp > 0 && rows % Wp == 0 && V > 0 && ld >= V, "bad dimensions");
+  KAD_REQUIRE(K >= 1 && K <= V, "K must be in [1, V]");
+  KAD_REQUIRE((int64_t)Wp * V < 0x7fffffff, "Wp * V must fit in int32 flat indices");
+  hipLaunchKernelGGL(row_select_kernel, dim3(rows), dim3(kRowThreads), 0, (hipStream_t)stream,
+                     (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores, Wp,
+                     V, K, cand_key, cand_idx);
+  return kad_launch_status("row_select_kernel");
+}
+
+extern "C" int kad_beam_merge_select(const float* cand_key, const int* cand_idx, int B, int ncand,
+                                     int W, int V, float* scores, int64_t* parents,
+                                     int64_t* tokens, void* valid, kad_stream_t stream) {
+  KAD_REQUIRE(cand_key && cand_idx && scores && parents && tokens && valid, "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0 && ncand >= W && V > 0, "bad dimensions (need ncand >= W)");
+  if (W > kMaxW) KAD_UNSUPPORTED("beam width %d exceeds %d", W, kMaxW);
+  hipLaunchKernelGGL(merge_select_kernel, dim3(B), dim3(kMergeThreads), 0, (hipStream_t)stream,
+                     cand_key, cand_idx, ncand, W, V, scores, parents, tokens, (uint8_t*)valid);
+  return kad_launch_status("merge_select_kernel");
+}
+
+extern "C" int kad_beam_history(const int64_t* history, int Wp, int step, const int64_t* parents,
+                                const int64_t* tokens, int64_t* out, int B, int W,
+                                kad_stream_t stream) {
+  KAD_REQUIRE(parents && tokens && out && (history || step == 0), "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0 && Wp > 0 && step >= 0, "bad dimensions");
+  const int64_t total = (int64_t)B * W * (step + 1);
+  hipLaunchKernelGGL(history_kernel, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
+                     (hipStream_t)stream, history, Wp, step, parents, tokens, out, B, W);
+  return kad_launch_status("history_kernel");
+}

@@ -113,6 +113,105 @@ __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
   }
 }
 
+
+// Prefill: causal width-4 conv + SiLU over whole prompts with zero history
+// (transformers causal_conv1d_fn, modeling_qwen3_5.py:220-239), and the conv
+// state the decode path reads: the last 4 pre-conv inputs of each sequence
+// (cache_utils.py:1032-1070), zero-padded on the left for prompts shorter
+// than 4.  Rows are tokens (row = b * L + t) with channels contiguous; each
+// thread owns 8 channels of a run of kRun tokens and reads a 3-token halo.
+constexpr int kRun = 16;
+
+__global__ __launch_bounds__(256) void conv_prefill_bf16(
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
+    bf16_t* __restrict__ out, int64_t ldo, bf16_t* __restrict__ state, int B, int L, int C,
+    int silu) {
+  const int C8 = C / 8;
+  const int runs = (L + kRun - 1) / kRun;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)B * runs * C8) return;
+  const int c0 = (int)(idx % C8) * 8;
+  const int64_t br = idx / C8;
+  const int run = (int)(br % runs);
+  const int b = (int)(br / runs);
+  const int t0 = run * kRun;
+  float wt[8][4];
+  {
+    const u32x4* wp = (const u32x4*)(w + (int64_t)c0 * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4 r = wp[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int flat = j * 8 + e * 2;
+        wt[flat / 4][flat % 4] = __uint_as_float(r[e] << 16);
+        wt[(flat + 1) / 4][(flat + 1) % 4] = __uint_as_float(r[e] & 0xffff0000u);
+      }
+    }
+  }
+  float win[8][4];
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch) win[ch][0] = win[ch][1] = win[ch][2] = win[ch][3] = 0.f;
+  // halo: tokens t0-3 .. t0-1 (zero before the sequence start)
+  for (int h = 3; h >= 1; --h) {
+    const int t = t0 - h;
+    float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (t >= 0) {
+      const u32x4 r = *(const u32x4*)(x + ((int64_t)b * L + t) * ldx + c0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xv[2 * e] = __uint_as_float(r[e] << 16);
+        xv[2 * e + 1] = __uint_as_float(r[e] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) {
+      win[ch][0] = win[ch][1];
+      win[ch][1] = win[ch][2];
+      win[ch][2] = win[ch][3];
+      win[ch][3] = xv[ch];
+    }
+  }
+  const int t_end = min(L, t0 + kRun);
+  for (int t = t0; t < t_end; ++t) {
+    const u32x4 r = *(const u32x4*)(x + ((int64_t)b * L + t) * ldx + c0);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xv[2] = {__uint_as_float(r[e] << 16), __uint_as_float(r[e] & 0xffff0000u)};
+      uint32_t packed = 0;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int ch = e * 2 + hh;
+        win[ch][0] = win[ch][1];
+        win[ch][1] = win[ch][2];
+        win[ch][2] = win[ch][3];
+        win[ch][3] = xv[hh];
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc += wt[ch][i] * win[ch][i];
+        float y = round_bf(acc);
+        if (silu) y = silu_f(y);
+        packed |= (uint32_t)f2bf(y) << (16 * hh);
+      }
+      o[e] = packed;
+    }
+    *(u32x4*)(out + ((int64_t)b * L + t) * ldo + c0) = o;
+  }
+  // conv state [B, C, 4]: inputs at positions L-4 .. L-1 (the run holding L-1 writes it)
+  if (state && t_end == L) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = L - 4 + j;
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) {
+        const float v = t >= 0 ? bf2f(x[((int64_t)b * L + t) * ldx + c0 + ch]) : 0.f;
+        state[((int64_t)b * C + c0 + ch) * 4 + j] = f2bf(v);
+      }
+    }
+  }
+}
+
 template <typename T>
 int launch_scalar(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx_t, const void* state,
                   int64_t ss_b, int64_t ss_c, int64_t ss_t, int history, const void* w,
@@ -161,4 +260,20 @@ extern "C" int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c,
                                 width, bias, out, so_n, so_c, so_t, B, W, C, T, activation_silu,
                                 s);
   KAD_UNSUPPORTED("causal conv supports bf16 and fp32, got dtype %d", dtype);
+}
+
+extern "C" int kad_causal_conv_prefill(const void* x, int64_t ldx, const void* weight, void* out,
+                                       int64_t ldo, void* state, int B, int L, int C,
+                                       int activation_silu, kad_stream_t stream) {
+  KAD_REQUIRE(x && weight && out, "null pointer argument");
+  KAD_REQUIRE(B > 0 && L > 0 && C > 0 && C % 8 == 0, "bad dimensions (C %% 8 == 0 required)");
+  KAD_REQUIRE(ldx % 8 == 0 && ldo % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
+                  ((uintptr_t)out % 16) == 0 && ((uintptr_t)weight % 16) == 0,
+              "16-byte aligned rows required");
+  const int runs = (L + kRun - 1) / kRun;
+  const int64_t total = (int64_t)B * runs * (C / 8);
+  hipLaunchKernelGGL(conv_prefill_bf16, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const bf16_t*)x, ldx, (const bf16_t*)weight,
+                     (bf16_t*)out, ldo, (bf16_t*)state, B, L, C, activation_silu);
+  return kad_launch_status("conv_prefill_bf16");
 }

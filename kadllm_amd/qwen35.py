@@ -1,0 +1,313 @@
+"""Native Qwen3.5 hybrid text model on the HIP kernels: prefill and suffix replay.
+
+The layer math is the one the reference path runs: prefill = the transformers
+Qwen3_5TextModel forward (src/kadllm/adapters/qwen3_5.py:106-133),
+decode = Qwen35GRBeamAdapter.decode/_linear/_attention (qwen3_5.py:144-235).
+Each step maps onto a few fused kernels:
+
+  GDN layer   rmsnorm -> GEMM [qkv | z | a | b] -> conv4 (prefill: whole
+              prompt; decode: prefix taps + suffix) -> gates -> chunked GDN
+              (prefill) / factored suffix replay (decode) -> gated rmsnorm ->
+              GEMM out_proj + residual
+  attention   rmsnorm -> GEMM [q+gate | k | v] -> q/k norm + partial RoPE ->
+              causal attention (prefill) / prefix-shared attention (decode),
+              sigmoid gate fused -> GEMM o_proj + residual
+  MLP         rmsnorm -> GEMM [gate | up] with SwiGLU epilogue -> GEMM down + residual
+  head        final rmsnorm on the last token of each row -> GEMM lm_head
+
+Weights are packed once per model into bf16 device buffers; activations are
+bf16 with the reference's rounding points.  Nothing here falls back to a
+non-HIP implementation: every numeric step is a libkadllm_hip entry point.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib, layers
+from .attention import attention_prefill, prefix_attention_decode
+
+_BLOCK = 32  # gate/up interleave granularity of the SwiGLU epilogue
+
+
+def _round_up(x, m):
+    return (x + m - 1) // m * m
+
+
+@dataclass
+class _GdnLayer:
+    input_norm: torch.Tensor
+    post_norm: torch.Tensor
+    w_in: torch.Tensor        # [qkv | z | a | b | pad, H]
+    conv_w: torch.Tensor      # [C, 4]
+    A_log: torch.Tensor
+    dt_bias: torch.Tensor
+    norm_w: torch.Tensor      # [dv]
+    w_out: torch.Tensor       # [H, Vd]
+    w_gu: torch.Tensor        # [2F, H] interleaved
+    w_down: torch.Tensor      # [H, F]
+
+
+@dataclass
+class _AttnLayer:
+    input_norm: torch.Tensor
+    post_norm: torch.Tensor
+    w_qkv: torch.Tensor       # [(2 nh hd) | nkv hd | nkv hd, H]
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    w_o: torch.Tensor         # [H, nh hd]
+    w_gu: torch.Tensor
+    w_down: torch.Tensor
+
+
+def interleave_gate_up(gate, up):
+    """[F, H] gate and up -> [2F, H] in [gate 32 | up 32] row blocks."""
+    F_, H = gate.shape
+    if F_ % _BLOCK:
+        raise ValueError(f"intermediate size must be a multiple of {_BLOCK}")
+    g = gate.reshape(F_ // _BLOCK, _BLOCK, H)
+    u = up.reshape(F_ // _BLOCK, _BLOCK, H)
+    return torch.stack((g, u), dim=1).reshape(2 * F_, H).contiguous()
+
+
+class Qwen35Runner:
+    """Packed bf16 weights of one Qwen3.5 text model plus its forward passes."""
+
+    def __init__(self, cfg, state_dict, lm_head_weight=None, device=None):
+        self.cfg = cfg
+        self.device = torch.device(device) if device is not None else \
+            state_dict["embed_tokens.weight"].device
+        if self.device.type != "cuda":
+            raise RuntimeError("the native Qwen3.5 path runs on a ROCm device")
+        bf = torch.bfloat16
+
+        def get(name):
+            return state_dict[name].detach().to(device=self.device, dtype=bf).contiguous()
+
+        H = cfg.hidden_size
+        for dim, what in ((H, "hidden size"), (cfg.intermediate_size, "intermediate size")):
+            if dim % 64:
+                raise ValueError(f"{what} must be a multiple of 64 for the GEMM kernels")
+        self.embed = get("embed_tokens.weight")
+        head = lm_head_weight if lm_head_weight is not None else state_dict.get("lm_head.weight")
+        self.lm_head = (self.embed if head is None else
+                        head.detach().to(device=self.device, dtype=bf).contiguous())
+        self.norm_w = get("norm.weight")
+        self.kd = cfg.linear_num_key_heads * cfg.linear_key_head_dim
+        self.vd = cfg.linear_num_value_heads * cfg.linear_value_head_dim
+        self.conv_dim = 2 * self.kd + self.vd
+        hv = cfg.linear_num_value_heads
+        self.gdn_cols = _round_up(self.conv_dim + self.vd + 2 * hv, 64)
+        self.attn_cols = (2 * cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+        self.layers = []
+        for i, kind in enumerate(cfg.layer_types):
+            p = f"layers.{i}."
+            w_gu = interleave_gate_up(get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight"))
+            common = dict(input_norm=get(p + "input_layernorm.weight"),
+                          post_norm=get(p + "post_attention_layernorm.weight"),
+                          w_gu=w_gu, w_down=get(p + "mlp.down_proj.weight"))
+            if kind == "linear_attention":
+                a = p + "linear_attn."
+                w_in = torch.zeros(self.gdn_cols, H, dtype=bf, device=self.device)
+                w_in[:self.conv_dim] = get(a + "in_proj_qkv.weight")
+                w_in[self.conv_dim:self.conv_dim + self.vd] = get(a + "in_proj_z.weight")
+                o = self.conv_dim + self.vd
+                w_in[o:o + hv] = get(a + "in_proj_a.weight")
+                w_in[o + hv:o + 2 * hv] = get(a + "in_proj_b.weight")
+                if cfg.linear_conv_kernel_dim != 4:
+                    raise ValueError("the conv kernels are specialised for width 4")
+                self.layers.append(_GdnLayer(
+                    w_in=w_in, conv_w=get(a + "conv1d.weight").reshape(self.conv_dim, 4).contiguous(),
+                    A_log=get(a + "A_log"), dt_bias=get(a + "dt_bias"), norm_w=get(a + "norm.weight"),
+                    w_out=get(a + "out_proj.weight"), **common))
+            else:
+                a = p + "self_attn."
+                w_qkv = torch.cat((get(a + "q_proj.weight"), get(a + "k_proj.weight"),
+                                   get(a + "v_proj.weight")), 0).contiguous()
+                self.layers.append(_AttnLayer(w_qkv=w_qkv, q_norm=get(a + "q_norm.weight"),
+                                              k_norm=get(a + "k_norm.weight"),
+                                              w_o=get(a + "o_proj.weight"), **common))
+        rot = int(cfg.head_dim * cfg.partial_rotary_factor)
+        self.rot = rot
+        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=torch.float) / rot))
+                         ).to(self.device)
+
+    # ------------------------------------------------------------------
+    def _mlp(self, lyr, x, rows):
+        cfg = self.cfg
+        n2 = layers.rmsnorm(x, lyr.post_norm, cfg.rms_norm_eps)
+        h = layers.gemm(n2, lyr.w_gu, epilogue=layers.EPI_SWIGLU)
+        layers.gemm(h, lyr.w_down, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
+
+    def _gdn_gates(self, lyr, proj):
+        hv = self.cfg.linear_num_value_heads
+        o = self.conv_dim + self.vd
+        return layers.gdn_gates(proj[:, o:o + hv], proj[:, o + hv:o + 2 * hv], lyr.A_log,
+                                lyr.dt_bias)
+
+    def _gdn_finish(self, lyr, o, proj, x):
+        cfg = self.cfg
+        z = proj[:, self.conv_dim:self.conv_dim + self.vd]
+        y = layers.rmsnorm_gated(o, z, lyr.norm_w, cfg.rms_norm_eps, cfg.linear_num_value_heads)
+        layers.gemm(y, lyr.w_out, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
+
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def prefill(self, input_ids):
+        """Full prompt forward.  Returns (logits [B, V] bf16, per-layer prefix tuple)."""
+        cfg = self.cfg
+        B, L = input_ids.shape
+        rows = B * L
+        dev = self.device
+        x = layers.embedding(input_ids, self.embed)
+        H_, HV = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+        dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+        nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        snap = []
+        for lyr in self.layers:
+            n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
+            if isinstance(lyr, _GdnLayer):
+                proj = layers.gemm(n, lyr.w_in)
+                conv = torch.empty(rows, self.conv_dim, dtype=torch.bfloat16, device=dev)
+                conv_state = torch.empty(B, self.conv_dim, 4, dtype=torch.bfloat16, device=dev)
+                _lib.call("kad_causal_conv_prefill", _lib.ptr(proj), proj.stride(0),
+                          _lib.ptr(lyr.conv_w), _lib.ptr(conv), conv.stride(0),
+                          _lib.ptr(conv_state), B, L, self.conv_dim, 1, _lib.stream_of(x))
+                g, beta = self._gdn_gates(lyr, proj)
+                o = torch.empty(rows, self.vd, dtype=torch.bfloat16, device=dev)
+                S = torch.empty(B, HV, dk, dv, dtype=torch.float32, device=dev)
+                base = conv.data_ptr()
+                es = conv.element_size()
+                _lib.call("kad_gdn_chunk", _lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
+                          _lib.ptr_at(base + 2 * self.kd * es), self.conv_dim, self.conv_dim, 0,
+                          _lib.ptr(g), 2, _lib.ptr(beta), 0, HV, None, 2, 1, _lib.ptr(o), self.vd,
+                          _lib.ptr(S), B, L, H_, HV, dk, dv, float(dk ** -0.5), 1,
+                          _lib.stream_of(x))
+                self._gdn_finish(lyr, o, proj, x)
+                snap.append((conv_state, S))
+            else:
+                proj = layers.gemm(n, lyr.w_qkv)
+                ld = proj.stride(0)
+                q = torch.empty(B, L, nh, hd, dtype=torch.bfloat16, device=dev)
+                kc = torch.empty(B, nkv, L, hd, dtype=torch.bfloat16, device=dev)
+                vc = torch.empty(B, nkv, L, hd, dtype=torch.bfloat16, device=dev)
+                layers.qk_norm_rope(proj, ld, 2 * hd, nh, lyr.q_norm, q, (0, nh * hd, hd), rows,
+                                    rows, hd, self.rot, self.inv_freq, 0, L, cfg.rms_norm_eps)
+                kv_strides = (nkv * L * hd, hd, L * hd)
+                kp = proj[:, 2 * nh * hd:]
+                layers.qk_norm_rope(kp, ld, hd, nkv, lyr.k_norm, kc, kv_strides, L, rows, hd,
+                                    self.rot, self.inv_freq, 0, L, cfg.rms_norm_eps)
+                layers.scatter_heads(proj[:, (2 * nh + nkv) * hd:], ld, nkv, hd, vc, kv_strides,
+                                     L, rows)
+                att = torch.empty(B, L, nh, hd, dtype=torch.bfloat16, device=dev)
+                gate = proj[:, hd:]
+                attention_prefill(q, kc.transpose(1, 2), vc.transpose(1, 2), hd ** -0.5,
+                                  gate=gate, gate_strides=(L * ld, ld, 2 * hd), out=att)
+                layers.gemm(att.view(rows, nh * hd), lyr.w_o, out=x,
+                            epilogue=layers.EPI_RESIDUAL, residual=x)
+                snap.append((kc.transpose(1, 2), vc.transpose(1, 2)))
+            self._mlp(lyr, x, rows)
+        last = x.view(B, L, -1)[:, -1]
+        hN = layers.rmsnorm(last, self.norm_w, cfg.rms_norm_eps)
+        logits = layers.gemm(hN, self.lm_head)
+        return logits, tuple(snap)
+
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def decode(self, history, prefix_layers, prefix_length):
+        """Replay [B, W, T] suffixes against the prefix; returns logits [B, W, V] bf16."""
+        cfg = self.cfg
+        B, W, T = history.shape
+        BW = B * W
+        R = BW * T
+        dev = self.device
+        x = layers.embedding(history, self.embed)
+        H_, HV = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+        dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+        nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        C = self.conv_dim
+        for lyr, cached in zip(self.layers, prefix_layers):
+            n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
+            if isinstance(lyr, _GdnLayer):
+                proj = layers.gemm(n, lyr.w_in)
+                ld = proj.stride(0)
+                conv = torch.empty(R, C, dtype=torch.bfloat16, device=dev)
+                cs = cached[0]
+                _lib.call("kad_causal_conv_suffix", _lib.ptr(proj), T * ld, 1, ld, _lib.ptr(cs),
+                          *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), 4, None,
+                          _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, _lib.stream_of(x))
+                g, beta = self._gdn_gates(lyr, proj)
+                o = torch.empty(R, self.vd, dtype=torch.bfloat16, device=dev)
+                S = cached[1]
+                base, es = conv.data_ptr(), conv.element_size()
+                _lib.call("kad_gdn_suffix_replay", _lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
+                          _lib.ptr_at(base + 2 * self.kd * es), C, C, 0, _lib.ptr(g), 2,
+                          _lib.ptr(beta), 0, HV, _lib.ptr(S), _lib.dtype_code(S.dtype),
+                          _lib.ptr(o), self.vd, B, W, T, H_, HV, dk, dv, float(dk ** -0.5),
+                          _lib.stream_of(x))
+                self._gdn_finish(lyr, o, proj, x)
+            else:
+                proj = layers.gemm(n, lyr.w_qkv)
+                ld = proj.stride(0)
+                q = torch.empty(BW, T, nh, hd, dtype=torch.bfloat16, device=dev)
+                k = torch.empty(BW, T, nkv, hd, dtype=torch.bfloat16, device=dev)
+                layers.qk_norm_rope(proj, ld, 2 * hd, nh, lyr.q_norm, q, (0, nh * hd, hd), R, R,
+                                    hd, self.rot, self.inv_freq, prefix_length, T,
+                                    cfg.rms_norm_eps)
+                layers.qk_norm_rope(proj[:, 2 * nh * hd:], ld, hd, nkv, lyr.k_norm, k,
+                                    (0, nkv * hd, hd), R, R, hd, self.rot, self.inv_freq,
+                                    prefix_length, T, cfg.rms_norm_eps)
+                v = proj[:, (2 * nh + nkv) * hd:].as_strided((BW, T, nkv, hd), (T * ld, ld, hd, 1))
+                att = prefix_attention_decode(q, cached[0], cached[1], k, v, W, None,
+                                              hd ** -0.5, gate=proj[:, hd:],
+                                              gate_strides=(T * ld, ld, 2 * hd))
+                layers.gemm(att.view(R, nh * hd), lyr.w_o, out=x,
+                            epilogue=layers.EPI_RESIDUAL, residual=x)
+            self._mlp(lyr, x, R)
+        last = x.view(BW, T, -1)[:, -1]
+        hN = layers.rmsnorm(last, self.norm_w, cfg.rms_norm_eps)
+        logits = layers.gemm(hN, self.lm_head)
+        return logits.view(B, W, -1)
+
+
+
+class Qwen35TextModel:
+    """Weights + config of a Qwen3.5 text model without transformers.
+
+    Holds a state dict in the transformers Qwen3_5TextModel naming; accepted
+    by Qwen35GRBeamAdapter wherever a transformers Qwen3_5TextModel is.
+    """
+
+    def __init__(self, config, state_dict):
+        self.config = config
+        self._sd = dict(state_dict)
+        self.training = False
+
+    def state_dict(self):
+        return dict(self._sd)
+
+    def parameters(self):
+        return iter(self._sd.values())
+
+    def eval(self):
+        self.training = False
+        return self
+
+    def train(self, mode=True):
+        self.training = mode
+        return self
+
+
+class LMHead:
+    """A bias-free output projection holding ``weight`` [V, H] (tied or not)."""
+
+    def __init__(self, weight):
+        self.weight = weight
+        self.training = False
+
+    def parameters(self):
+        return iter((self.weight,))
+
+    def eval(self):
+        self.training = False
+        return self

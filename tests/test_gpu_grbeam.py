@@ -1,0 +1,147 @@
+"""HIP beam selection, chunked GDN / conv prefill kernels against the oracle."""
+
+import pytest
+import torch
+from torch.nn import functional as F
+
+from _fixtures import gdn_inputs
+from conftest import assert_close_rel
+from kadllm_amd import _lib, ops
+from kadllm_amd.grbeam import extend_history, select_level
+from oracle import grbeam_ref, ops_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_selection(logits, scores, width, mask=None):
+    dev = logits.device
+    s, p, t, valid = select_level(logits, scores, width, mask)
+    torch.cuda.synchronize()
+    rs, rp, rt = grbeam_ref.level_select(logits.cpu(), scores.cpu(),
+                                         width, None if mask is None else mask.cpu())
+    assert torch.equal(p.cpu(), rp), "parents differ"
+    assert torch.equal(t.cpu(), rt), "tokens differ"
+    finite = torch.isfinite(rs)
+    assert torch.equal(valid.cpu(), finite)
+    assert torch.equal(torch.isfinite(s.cpu()), finite)
+    assert torch.allclose(s.cpu()[finite], rs[finite], rtol=0, atol=2e-5)
+    return s, p, t
+
+
+@pytest.mark.parametrize("B,Wp,V,W", [(3, 5, 1000, 7), (2, 1, 4096, 8), (2, 8, 33, 200),
+                                      (1, 3, 64, 192)])
+def test_select_level_matches_oracle(device, B, Wp, V, W):
+    g = torch.Generator().manual_seed(V + W)
+    logits = torch.randn(B, Wp, V, generator=g).bfloat16()   # bf16 rounding creates ties
+    scores = -torch.rand(B, Wp, generator=g) * 3
+    _check_selection(logits.to(device), scores.to(device), W)
+
+
+def test_select_level_exact_ties_lower_index_first(device):
+    B, Wp, V, W = 2, 4, 50, 9
+    logits = torch.zeros(B, Wp, V, dtype=torch.bfloat16)
+    logits[:, :, 7] = 1.0                     # many exact ties at the top
+    scores = torch.zeros(B, Wp)
+    s, p, t = _check_selection(logits.to(device), scores.to(device), W)
+    assert t[0, :4].tolist() == [7, 7, 7, 7] and p[0, :4].tolist() == [0, 1, 2, 3]
+
+
+def test_select_level_with_mask(device):
+    B, Wp, V, W = 2, 3, 300, 20
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(B, Wp, V, generator=g).bfloat16()
+    scores = -torch.rand(B, Wp, generator=g)
+    mask = torch.rand(B, Wp, V, generator=g) > 0.7
+    mask[1] = False
+    mask[1, 0, :5] = True                      # request 1: only 5 allowed -> 15 invalid slots
+    _check_selection(logits.to(device), scores.to(device), W, mask.to(device))
+
+
+def test_select_level_full_vocab_shape(device):
+    """One decode level at the workload shape: 256 beams x 248320 tokens, 2 requests."""
+    B, Wp, V, W = 2, 256, 248320, 256
+    gen = torch.Generator(device=device).manual_seed(3)
+    logits = (torch.randn(B, Wp, V, generator=gen, device=device) * 2).bfloat16()
+    scores = -torch.rand(B, Wp, generator=gen, device=device) * 4
+    _check_selection(logits, scores, W)
+
+
+def test_history_update(device):
+    B, Wp, step, W = 2, 3, 2, 5
+    hist = torch.arange(B * Wp * step).reshape(B, Wp, step)
+    parents = torch.tensor([[2, 0, 1, 1, 2], [0, 0, 2, 1, 0]])
+    tokens = torch.arange(10).reshape(B, W) + 100
+    out = extend_history(hist.to(device), parents.to(device), tokens.to(device))
+    torch.cuda.synchronize()
+    ref = torch.cat((hist.gather(1, parents[..., None].expand(B, W, step)), tokens[..., None]), -1)
+    assert torch.equal(out.cpu(), ref)
+    out0 = extend_history(torch.empty(B, 1, 0, dtype=torch.int64, device=device),
+                          torch.zeros(B, W, dtype=torch.int64, device=device), tokens.to(device))
+    torch.cuda.synchronize()
+    assert torch.equal(out0.cpu(), tokens[..., None])
+
+
+# --------------------------------------------------------------------------
+# chunked gated delta
+
+
+@pytest.mark.parametrize("B,W,T,H,HV,K,V", [(2, 3, 9, 2, 4, 64, 64), (1, 2, 70, 4, 4, 128, 128),
+                                            (2, 1, 130, 2, 2, 128, 64)])
+def test_gdn_long_suffix_uses_chunk_kernel(device, B, W, T, H, HV, K, V):
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, seed=T, state_std=0.1)
+    expected = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W)
+    out = ops.gated_delta(*(t.to(device) for t in (q, k, v, g, beta, S)), beam_width=W)
+    torch.cuda.synchronize()
+    assert_close_rel(out.cpu(), expected, rtol=1e-2, atol_frac=3e-3, name="chunk ops path")
+
+
+def test_gdn_return_final_state(device):
+    B, W, T, H, HV, K, V = 2, 2, 5, 2, 2, 64, 128
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, seed=2, state_std=0.1)
+    eo, es = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W, return_final_state=True)
+    o, s = ops.gated_delta(*(t.to(device) for t in (q, k, v, g, beta, S)), beam_width=W,
+                           return_final_state=True)
+    torch.cuda.synchronize()
+    assert s.shape == (B * W, HV, K, V) and s.dtype == torch.float32
+    assert_close_rel(o.cpu(), eo, rtol=1e-2, atol_frac=3e-3, name="o")
+    assert_close_rel(s.cpu(), es, rtol=1e-4, atol_frac=1e-5, name="final state")
+
+
+@pytest.mark.parametrize("L", [37, 64, 200, 1024])
+def test_prefill_chunk_matches_transformers_semantics(device, L):
+    """Prefill mode (bf16-rounded l2norm) against the oracle restatement of the
+    transformers chunk routine, including the final fp32 state."""
+    B, H, K = 2, 4, 128
+    q, k, v, g, beta, _ = gdn_inputs(B, 1, L, H, H, K, K, seed=L)
+    q, k, v = (t.reshape(B, L, H, K) for t in (q, k, v))
+    g, beta = g.reshape(B, L, H), beta.reshape(B, L, H)
+    eo, es = ops_ref.chunk_gated_delta(q, k, v, g, beta)
+    dev = [t.to(device).contiguous() for t in (q, k, v, g, beta)]
+    o = torch.empty(B, L, H, K, dtype=torch.bfloat16, device=device)
+    s = torch.empty(B, H, K, K, dtype=torch.float32, device=device)
+    _lib.call("kad_gdn_chunk", _lib.ptr(dev[0]), _lib.ptr(dev[1]), _lib.ptr(dev[2]), H * K, H * K,
+              0, _lib.ptr(dev[3]), 2, _lib.ptr(dev[4]), 0, H, None, 2, 1, _lib.ptr(o), H * K,
+              _lib.ptr(s), B, L, H, H, K, K, float(K ** -0.5), 1, _lib.stream_of(o))
+    torch.cuda.synchronize()
+    assert_close_rel(o.cpu(), eo, rtol=1e-2, atol_frac=3e-3, name="prefill o")
+    assert_close_rel(s.cpu(), es, rtol=1e-3, atol_frac=1e-4, name="prefill state")
+
+
+@pytest.mark.parametrize("L", [1, 3, 50])
+def test_conv_prefill_and_state(device, L):
+    B, C = 2, 64
+    g = torch.Generator().manual_seed(L)
+    x = torch.randn(B, L, C, generator=g).bfloat16()
+    w = (torch.rand(C, 4, generator=g) - 0.5).bfloat16()
+    xd = x.to(device).reshape(B * L, C)
+    out = torch.empty(B * L, C, dtype=torch.bfloat16, device=device)
+    st = torch.empty(B, C, 4, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_causal_conv_prefill", _lib.ptr(xd), C, _lib.ptr(w.to(device)), _lib.ptr(out), C,
+              _lib.ptr(st), B, L, C, 1, _lib.stream_of(xd))
+    torch.cuda.synchronize()
+    pre = x.transpose(1, 2)
+    ref = F.silu(F.conv1d(pre, w[:, None, :], padding=3, groups=C)[..., :L]).transpose(1, 2)
+    a, e = out.cpu().float().reshape(B, L, C), ref.float()
+    assert ((a - e).abs() <= e.abs() * 2 ** -7 + 1e-6).all()
+    ref_state = F.pad(pre, (max(0, 4 - L), 0))[..., -4:]
+    assert torch.equal(st.cpu(), ref_state)
