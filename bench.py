@@ -1,0 +1,188 @@
+"""GRBeam end-to-end benchmark on one MI355X.
+
+Workload (the reference's headline configuration): a Qwen3.5-0.8B-shaped
+hybrid model (24 layers [3x Gated DeltaNet, 1x gated attention] x 6, hidden
+1024, vocabulary 248320, tied embeddings) with random bf16 weights, batch 32,
+prompts of 1024 uniform-random token ids, beam 256, 3 output tokens over the
+full vocabulary.  One step is one ``grbeam_search`` call on the batch with the
+reference's timing protocol (src/kadllm benchmarks/grbeam.py:266-330): output
+token 1 from prefill, two decode calls, selection, synchronisation and the
+copy of the tokens to the host are all inside the timed region; every step's
+output is validated to hold 256 distinct fixed-depth sequences per request.
+
+Printed: one JSON line with requests/s (= batch * steps / elapsed), the
+roofline of the dominant kernel (the bf16 MFMA GEMM: algorithmic flops of all
+GEMM launches in the timed steps divided by their summed durations from HIP
+events recorded on the launch stream) and the CPU baseline (the oracle
+restatement of the reference torch path on this host, one request).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "requests/s at B32/prefix1024/beam256/3 tok; per-kernel HBM GB/s & MFMA util"
+H800_REQ_S = 36.08          # reference README, 1x H800, same workload
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+
+
+def validate_output(tokens, batch, width, depth):
+    """Each request holds `width` distinct fixed-depth sequences (grbeam.py:32-41)."""
+    if len(tokens) != batch or any(
+        len(beams) != width or any(len(s) != depth for s in beams)
+        or len({tuple(s) for s in beams}) != width
+        for beams in tokens
+    ):
+        raise ValueError("search did not return the requested distinct fixed-depth beams")
+
+
+class GemmTimer:
+    """Records a HIP event pair around every GEMM launch (torch's current stream)."""
+
+    def __init__(self):
+        self.events = []
+
+    def __call__(self, launch, flops):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        launch()
+        e1.record()
+        self.events.append((e0, e1, flops))
+
+    def summary(self):
+        torch.cuda.synchronize()
+        ms = sum(e0.elapsed_time(e1) for e0, e1, _ in self.events)
+        flops = sum(f for _, _, f in self.events)
+        return ms, flops, len(self.events)
+
+
+def cpu_baseline(cfg, sd_cpu, prefix, beam, depth, threads):
+    """Oracle search on the host for one request of the workload; returns requests/s."""
+    from oracle import grbeam_ref
+    from oracle.qwen35_ref import Qwen35Oracle
+
+    torch.set_num_threads(threads)
+    oracle = Qwen35Oracle(cfg, sd_cpu)
+
+    class _Adapter:
+        def prefill(self, ids):
+            return oracle.prefill(ids)
+
+        def decode(self, history, state):
+            return oracle.decode(history, state)
+
+    ids = torch.randint(0, cfg.vocab_size, (1, prefix), generator=torch.Generator().manual_seed(1))
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        tokens, _, _, _ = grbeam_ref.grbeam_search(_Adapter(), ids, [beam] * depth)
+    tokens.tolist()
+    dt = time.perf_counter() - t0
+    return 1.0 / dt, dt
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--prefix", type=int, default=1024)
+    ap.add_argument("--beam", type=int, default=256)
+    ap.add_argument("--depth", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {a.gpus}); "
+              "requests shard across GPUs with no exchange, see the design notes", file=sys.stderr)
+        sys.exit(2)
+
+    from kadllm_amd import grbeam_search, layers
+    from kadllm_amd.adapters import Qwen35GRBeamAdapter, native_model
+    from kadllm_amd.config import qwen35_08b_config
+    from kadllm_amd.weights import random_state_dict
+
+    dev = torch.device("cuda:0")
+    cfg = qwen35_08b_config()
+    sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16, device=dev)
+    model, head = native_model(cfg, sd)
+    adapter = Qwen35GRBeamAdapter(model, head)
+    ids = torch.randint(0, cfg.vocab_size, (a.batch, a.prefix),
+                        generator=torch.Generator().manual_seed(0)).to(dev)
+    widths = [a.beam] * a.depth
+
+    def run():
+        return grbeam_search(adapter, ids, widths).tokens.tolist()
+
+    for _ in range(a.warmup):
+        validate_output(run(), a.batch, a.beam, a.depth)
+    torch.cuda.synchronize()
+
+    timer = GemmTimer()
+    layers.set_launch_timer(timer)
+    times, outputs = [], []
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(a.steps):
+        t0 = time.perf_counter()
+        outputs.append(run())
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    layers.set_launch_timer(None)
+    for out in outputs:
+        validate_output(out, a.batch, a.beam, a.depth)
+    gemm_ms, gemm_flops, n_gemm = timer.summary()
+    achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12  # TFLOP/s
+    value = a.batch * a.steps / elapsed
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        sd_cpu = {k: v.cpu() for k, v in sd.items()}
+        threads = min(a.cpu_threads, os.cpu_count() or 1)
+        rps, dt = cpu_baseline(cfg, sd_cpu, a.prefix, a.beam, a.depth, threads)
+        cpu = {"value": round(rps, 6), "unit": "requests/s", "cores": threads, "kind": "port",
+               "sample": f"1 request (prefix {a.prefix}, beam {a.beam}, {a.depth} tokens, full "
+                         f"vocabulary) through the oracle restatement of the reference torch "
+                         f"path, bf16 weights, {dt:.1f} s"}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "requests/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(1000 * elapsed / a.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / H800_REQ_S, 3) if (a.batch, a.prefix, a.beam, a.depth) ==
+        (32, 1024, 256, 3) else None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform-random prompt ids)",
+        "config": {"workload": f"grbeam_e2e qwen3.5-0.8B-shaped B{a.batch} P{a.prefix} "
+                               f"W{a.beam} depth{a.depth} full-vocab",
+                   "batch": a.batch, "prefix": a.prefix, "beam": a.beam, "depth": a.depth,
+                   "vocab": cfg.vocab_size, "layers": cfg.num_hidden_layers},
+        "roofline": {"kernel": "gemm_bf16_kernel (all launches)", "bound": "mfma",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "launches_per_step": n_gemm // a.steps,
+                     "gemm_ms_per_step": round(gemm_ms / a.steps, 3)},
+        "cpu_baseline": cpu,
+        "step_ms": [round(1000 * t, 2) for t in times],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -11,6 +11,15 @@ from . import _lib
 
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
 
+_launch_timer = None
+
+
+def set_launch_timer(timer):
+    """Install (or clear with None) a callable ``timer(launch, flops)`` that wraps
+    every GEMM launch, e.g. to bracket it with HIP events for roofline figures."""
+    global _launch_timer
+    _launch_timer = timer
+
 
 def gemm(a, w, out=None, *, epilogue=EPI_STORE, residual=None):
     """out[M, N'] = epilogue(a[M, K] @ w[N, K]^T) (bf16, fp32 accumulate).
@@ -25,9 +34,16 @@ def gemm(a, w, out=None, *, epilogue=EPI_STORE, residual=None):
     if out is None:
         out = torch.empty(M, n_out, dtype=torch.bfloat16, device=a.device)
     r = residual
-    _lib.call("kad_gemm_bf16", _lib.ptr(a), a.stride(0), _lib.ptr(w), w.stride(0), _lib.ptr(out),
-              out.stride(0), _lib.ptr(r), r.stride(0) if r is not None else 0, M, N, K, epilogue,
-              _lib.stream_of(a))
+
+    def launch():
+        _lib.call("kad_gemm_bf16", _lib.ptr(a), a.stride(0), _lib.ptr(w), w.stride(0),
+                  _lib.ptr(out), out.stride(0), _lib.ptr(r), r.stride(0) if r is not None else 0,
+                  M, N, K, epilogue, _lib.stream_of(a))
+
+    if _launch_timer is None:
+        launch()
+    else:
+        _launch_timer(launch, 2 * M * N * K)
     return out
 
 
