@@ -214,14 +214,17 @@ int kad_beam_history(const int64_t* history, int Wp, int step, const int64_t* pa
  * final_state (nullable, fp32 [N, HV, K, V]) receives each sequence's final
  * state.  transformers_l2norm = 1 normalises q and k with the bf16 roundings
  * of transformers' l2norm (prefill); 0 normalises in fp32 as ops.py:147-148.
- * bf16 q/k/v; K, V in {64, 128}.
+ * workspace: caller-owned device memory of at least the size reported by
+ * kad_gdn_chunk_workspace_bytes (per-chunk intermediates).  bf16 q/k/v;
+ * K, V in {64, 128}; v rows 16-byte aligned.
  */
+int kad_gdn_chunk_workspace_bytes(int N, int T, int HV, int K, int64_t* bytes);
 int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
                   int qkv_dtype, const void* log_decay, int gate_dtype, const void* beta,
                   int beta_dtype, int64_t ld_gate, const void* initial_state, int state_dtype,
-                  int beams_per_state, void* out, int64_t ld_out, float* final_state, int N,
-                  int T, int H, int HV, int K, int V, float scale, int transformers_l2norm,
-                  kad_stream_t stream);
+                  int beams_per_state, void* out, int64_t ld_out, float* final_state,
+                  void* workspace, int64_t workspace_bytes, int N, int T, int H, int HV, int K,
+                  int V, float scale, int transformers_l2norm, kad_stream_t stream);
 
 /* Causal width-4 conv + SiLU over whole prompts with zero history, and the
  * conv state (last 4 pre-conv inputs, [B, C, 4], nullable) that decode reads.

@@ -41,7 +41,8 @@ SIGNATURES = {
     "kad_beam_row_select": "plplpiiiipps",
     "kad_beam_merge_select": "ppiiiipppps",
     "kad_beam_history": "piipppiis",
-    "kad_gdn_chunk": "ppplli" "pipil" "pii" "plp" "iiiiii" "fi" "s",
+    "kad_gdn_chunk_workspace_bytes": "iiiip",
+    "kad_gdn_chunk": "ppplli" "pipil" "pii" "plp" "pl" "iiiiii" "fi" "s",
     "kad_causal_conv_prefill": "plpplpiiiis",
     "kad_selftest_mfma16": "ppps",
     "kad_selftest_mfma32": "ppps",
@@ -95,6 +96,13 @@ def call(name, *args):
     if rc != KAD_OK:
         msg = lib.kad_last_error().decode(errors="replace")
         raise KadLibraryError(f"{name} failed ({ERRORS.get(rc, rc)}): {msg}")
+
+
+def gdn_chunk_workspace(N, T, HV, K, device):
+    """A uint8 device buffer sized for kad_gdn_chunk."""
+    n = ctypes.c_int64(0)
+    call("kad_gdn_chunk_workspace_bytes", N, T, HV, K, ctypes.byref(n))
+    return torch.empty(n.value, dtype=torch.uint8, device=device)
 
 
 def dtype_code(dtype):

@@ -6,244 +6,432 @@
 // operator, src/kadllm/ops.py:139-163 when a suffix is longer than the replay
 // kernel handles or a final state is requested (ops.py:119-122).
 //
-// One workgroup per (sequence n, value head hv) walks the sequence in chunks
-// of 64 tokens; thread v owns column v of the fp32 state S [K, V] in
-// registers.  Per chunk, with G the within-chunk cumulative log decay,
+// Per chunk of 64 tokens, with G the within-chunk cumulative log decay,
 // D_ij = exp(G_i - G_j) and hats the normalised q (incl. scale) and k:
 //   A_ij  = -beta_i (k^_i . k^_j) D_ij (j < i); T' = the routine's forward
-//           substitution of A (rows i = 1..63); T = T' + I
-//   Z_j   = beta_j (v_j - e^{G_j} k^_j S)          (so that v_new = T Z equals
-//           U - W S with U = T beta v, W = T beta k^ e^G of the routine)
-//   o_i   = e^{G_i} q^_i S + sum_{j<=i} (q^_i . k^_j) D_ij v_new_j
+//           substitution of A (rows 1..63); T = T' + I
+//   Z_j   = beta_j (v_j - e^{G_j} k^_j S)           (v_new = T Z equals the
+//           routine's U - W S with U = T beta v, W = T beta k^ e^G)
+//   o_i   = e^{G_i} q^_i S + sum_{j<=i} In_ij v_new_j,  In_ij = (q^_i . k^_j) D_ij
 //   S    <- e^{G_last} S + sum_i e^{G_last - G_i} k^_i v_new_i^T
-// The two 64 x 64 Gram matrices (k k^T, q k^T) run on bf16 MFMA from the bf16
-// q/k rows staged in LDS (raw rows with fp32 norms applied afterwards, or,
-// in the transformers prefill mode, rows normalised with its bf16 roundings,
-// l2norm in modeling_qwen3_5.py:242-246); everything touching S is fp32.
+//
+// Two kernels.  gdn_chunk_prep runs every (sequence, head, chunk) in
+// parallel: normalisation, the two Gram matrices on bf16 MFMA, the decay
+// masks and the triangular solve; it writes the chunk's bf16 q/k rows, T' and
+// In as bf16 hi/lo planes (x = hi + lo to 2^-16) and per-token scalars to a
+// workspace.  gdn_chunk_scan walks the chunks of one (sequence, head) in
+// order with 4 waves, wave w owning value columns [32w, 32w+32) of the fp32
+// state S [K, V].  S lives in MFMA accumulator registers (rows k, columns v)
+// and the same registers, split hi/lo, are the B operand of k S and q S: the
+// accumulator layout gives each lane the k-rows {0-3, 8-11} (+4 in the upper
+// half-wave) of every 16-row block of its column, and the A operands are read
+// from LDS in that same order.  All products run on v_mfma_f32_32x32x16_bf16
+// with fp32 accumulation; fp32 operands take 2-3 hi/lo passes.
 
 #include "kad_common.h"
 
 namespace {
 
 constexpr int kC = 64;
+constexpr int kPrepThreads = 256;
 
+// workspace record of one (sequence, head, chunk), in bytes
 template <int K>
-struct ChunkSmem {
-  static constexpr int ld = K + 8;  // bf16 row stride (16-byte padding)
+struct ChunkRec {
+  static constexpr size_t kn = 0;                              // bf16 [64][K]
+  static constexpr size_t qn = kn + kC * K * 2;                // bf16 [64][K]
+  static constexpr size_t thi = qn + kC * K * 2;               // bf16 [64][64]
+  static constexpr size_t tlo = thi + kC * kC * 2;
+  static constexpr size_t ihi = tlo + kC * kC * 2;
+  static constexpr size_t ilo = ihi + kC * kC * 2;
+  static constexpr size_t scal = ilo + kC * kC * 2;            // fp32 [5][64]
+  static constexpr size_t bytes = scal + 5 * kC * 4;
 };
+enum { S_EG = 0, S_BT = 1, S_KM = 2, S_QM = 3, S_WU = 4 };
 
-template <int K, int V>
-__global__ __launch_bounds__(V) void gdn_chunk_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    int64_t ld_qk, int64_t ld_v, const void* __restrict__ g, int gdt,
-    const void* __restrict__ beta, int bdt, int64_t ld_gate, const void* __restrict__ state0,
-    int sdt, int beams_per_state, bf16_t* __restrict__ out, int64_t ld_out,
-    float* __restrict__ final_state, int T, int H, int HV, float scale, int hf_norm) {
-  constexpr int LD = ChunkSmem<K>::ld;
-  constexpr int NW = V / 64;  // waves
-  __shared__ __attribute__((aligned(16))) bf16_t kb[kC * LD];
-  __shared__ __attribute__((aligned(16))) bf16_t qb[kC * LD];
-  __shared__ float Am[kC][kC + 1];
-  __shared__ float Tm[kC][kC + 1];
-  __shared__ float In[kC][kC + 1];
-  __shared__ float Gs[kC], eG[kC], bt[kC], kmul[kC], qmul[kC], wupd[kC];
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t ld_qk,
+    const void* __restrict__ g, int gdt, const void* __restrict__ beta, int bdt,
+    int64_t ld_gate, uint8_t* __restrict__ ws, int T, int H, int HV, int nchunks, float scale,
+    int hf_norm) {
+  constexpr int LD = K + 8;
+  // the bf16 q/k rows (Gram phase) and the fp32 A / T' matrices (solve phase)
+  // share one LDS region
+  constexpr size_t kRows = 2 * kC * LD * sizeof(bf16_t);
+  constexpr size_t kMats = 2 * kC * (kC + 1) * sizeof(float);
+  __shared__ __attribute__((aligned(16))) unsigned char region[kRows > kMats ? kRows : kMats];
+  bf16_t* kb = (bf16_t*)region;
+  bf16_t* qb = kb + kC * LD;
+  float(*Am)[kC + 1] = (float(*)[kC + 1])region;
+  float(*Tm)[kC + 1] = Am + kC;
+  __shared__ float Gs[kC], bt[kC], kmul[kC], qmul[kC];
 
-  const int col = threadIdx.x;  // value column
-  const int lane = col & 63, wave = col >> 6;
-  const int n = blockIdx.x / HV, hv = blockIdx.x % HV;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x % nchunks;
+  const int nh = blockIdx.x / nchunks;
+  const int n = nh / HV, hv = nh % HV;
   const int h = hv / (HV / H);
+  const int t0 = c * kC;
+  const int nt = min(kC, T - t0);
+  uint8_t* rec = ws + (size_t)blockIdx.x * ChunkRec<K>::bytes;
 
-  float S[K];
-  if (state0) {
-    const int64_t base = ((int64_t)(n / beams_per_state) * HV + hv) * K * V + col;
+  // ---- rows: normalise and stage (one wave per row at a time)
+  for (int i = wave; i < kC; i += kPrepThreads / 64) {
+    float kv[K / 64], qv[K / 64];
+    const bool live = i < nt;
+    const int64_t row = ((int64_t)n * T + t0 + (live ? i : 0)) * ld_qk + (int64_t)h * K;
+    float kss = 0.f, qss = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < K; ++kk) S[kk] = load_as_float(state0, base + (int64_t)kk * V, sdt);
-  } else {
+    for (int e = 0; e < K / 64; ++e) {
+      kv[e] = live ? bf2f(k[row + lane + 64 * e]) : 0.f;
+      qv[e] = live ? bf2f(q[row + lane + 64 * e]) : 0.f;
+      kss += hf_norm ? round_bf(kv[e] * kv[e]) : kv[e] * kv[e];
+      qss += hf_norm ? round_bf(qv[e] * qv[e]) : qv[e] * qv[e];
+    }
+    kss = wave_sum(kss);
+    qss = wave_sum(qss);
+    float km, qm;
+    if (hf_norm) {
+      // transformers l2norm in bf16: x * rsqrt(sum(x*x) + eps), each op rounded
+      const float kr = round_bf(1.0f / sqrtf(round_bf(round_bf(kss) + 1e-6f)));
+      const float qr = round_bf(1.0f / sqrtf(round_bf(round_bf(qss) + 1e-6f)));
 #pragma unroll
-    for (int kk = 0; kk < K; ++kk) S[kk] = 0.f;
+      for (int e = 0; e < K / 64; ++e) {
+        kv[e] = round_bf(kv[e] * kr);
+        qv[e] = round_bf(qv[e] * qr);
+      }
+      km = 1.f;
+      qm = scale;
+    } else {
+      km = 1.0f / sqrtf(kss + 1e-6f);
+      qm = scale / sqrtf(qss + 1e-6f);
+    }
+#pragma unroll
+    for (int e = 0; e < K / 64; ++e) {
+      const bf16_t kbits = f2bf(kv[e]), qbits = f2bf(qv[e]);
+      kb[i * LD + lane + 64 * e] = kbits;
+      qb[i * LD + lane + 64 * e] = qbits;
+      ((bf16_t*)(rec + ChunkRec<K>::kn))[i * K + lane + 64 * e] = kbits;
+      ((bf16_t*)(rec + ChunkRec<K>::qn))[i * K + lane + 64 * e] = qbits;
+    }
+    if (lane == 0) {
+      kmul[i] = km;
+      qmul[i] = qm;
+    }
+  }
+  if (tid < kC) {
+    const bool live = tid < nt;
+    const int64_t gi = ((int64_t)n * T + t0 + (live ? tid : 0)) * ld_gate + hv;
+    Gs[tid] = live ? load_as_float(g, gi, gdt) : 0.f;
+    bt[tid] = live ? load_as_float(beta, gi, bdt) : 0.f;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float acc = 0.f;
+    for (int i = 0; i < kC; ++i) {  // sequential cumulative sum, as torch.cumsum
+      acc += Gs[i];
+      Gs[i] = acc;
+    }
+  }
+  __syncthreads();
+  if (tid < kC) {
+    float* sc = (float*)(rec + ChunkRec<K>::scal);
+    sc[S_EG * kC + tid] = expf(Gs[tid]);
+    sc[S_BT * kC + tid] = bt[tid];
+    sc[S_KM * kC + tid] = kmul[tid];
+    sc[S_QM * kC + tid] = qmul[tid];
+    sc[S_WU * kC + tid] = kmul[tid] * expf(Gs[kC - 1] - Gs[tid]);
   }
 
-  const int nchunks = (T + kC - 1) / kC;
+  // ---- Gram matrices: 8 tiles of 32x32 (4 for k k^T, 4 for q k^T), 2 per wave.
+  // q k^T tiles go straight to the workspace as In hi/lo; k k^T tiles become A
+  // once every wave is done reading the rows.
+  bf16_t* ihi = (bf16_t*)(rec + ChunkRec<K>::ihi);
+  bf16_t* ilo = (bf16_t*)(rec + ChunkRec<K>::ilo);
+  f32x16 gram[2];
+  {
+    const int fr = lane & 31, fk = (lane >> 5) * 8;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tile = wave * 2 + tt;
+      const int which = tile >> 2, ti = (tile >> 1) & 1, tj = tile & 1;
+      const bf16_t* rowsrc = which == 0 ? kb : qb;
+      f32x16 acc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < K / 16; ++s) {
+        const bf16x8 a = as_bf16x8(*(const u32x4*)(rowsrc + (ti * 32 + fr) * LD + s * 16 + fk));
+        const bf16x8 b = as_bf16x8(*(const u32x4*)(kb + (tj * 32 + fr) * LD + s * 16 + fk));
+        acc = mfma32x32x16(a, b, acc);
+      }
+      gram[tt] = acc;
+      if (which == 1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int i = ti * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
+          const int j = tj * 32 + fr;
+          const float iv = j <= i ? (acc[e] * qmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
+          const bf16_t ih = f2bf(iv);
+          ihi[i * kC + j] = ih;
+          ilo[i * kC + j] = f2bf(iv - bf2f(ih));
+        }
+      }
+    }
+  }
+  __syncthreads();  // rows no longer needed: the region becomes A / T'
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tile = wave * 2 + tt;
+    const int which = tile >> 2, ti = (tile >> 1) & 1, tj = tile & 1;
+    if (which == 0) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = ti * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
+        const int j = tj * 32 + (lane & 31);
+        Am[i][j] = j < i ? -bt[i] * (gram[tt][e] * kmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- forward substitution: T'[i][j] = A[i][j] + sum_{j<m<i} A[i][m] T'[m][j]
+  if (tid < kC) Tm[0][tid] = 0.f;
+  for (int i = 1; i < kC; ++i) {
+    __syncthreads();
+    if (tid < i) {
+      float acc = Am[i][tid];
+      for (int m = tid + 1; m < i; ++m) acc += Am[i][m] * Tm[m][tid];
+      Tm[i][tid] = acc;
+    } else if (tid < kC) {
+      Tm[i][tid] = 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- T' as bf16 hi/lo planes
+  bf16_t* thi = (bf16_t*)(rec + ChunkRec<K>::thi);
+  bf16_t* tlo = (bf16_t*)(rec + ChunkRec<K>::tlo);
+  for (int e = tid; e < kC * kC; e += kPrepThreads) {
+    const float tv = Tm[e / kC][e % kC];
+    const bf16_t th = f2bf(tv);
+    thi[e] = th;
+    tlo[e] = f2bf(tv - bf2f(th));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// A fragment whose K slots follow the accumulator order: slot i of lane half
+// `hi` is column base + (i / 4) * 8 + hi * 4 + i % 4 of row `row`.
+__device__ __forceinline__ bf16x8 perm_frag(const bf16_t* rowp, int base, int hi) {
+  const u32x2 a = *(const u32x2*)(rowp + base + hi * 4);
+  const u32x2 b = *(const u32x2*)(rowp + base + 8 + hi * 4);
+  const u32x4 v = {a[0], a[1], b[0], b[1]};
+  return as_bf16x8(v);
+}
+
+// B fragments (hi, lo) of an fp32 accumulator tile for K step s: the 8
+// accumulator entries (s%2)*8 .. +7 of 32-row tile s/2
+__device__ __forceinline__ void acc_frags(const f32x16& t, int half, bf16x8& hi, bf16x8& lo) {
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = t[half * 8 + i];
+  split8(x, hi, lo);
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(V * 2) void gdn_chunk_scan(
+    const bf16_t* __restrict__ v, int64_t ld_v, const uint8_t* __restrict__ ws,
+    const void* __restrict__ state0, int sdt, int beams_per_state, bf16_t* __restrict__ out,
+    int64_t ld_out, float* __restrict__ final_state, int T, int HV, int nchunks) {
+  constexpr int KT = K / 32;      // 32-row k tiles of S
+  constexpr int KS = K / 16;      // k16 steps over K
+  constexpr int LDK = K + 8;      // bf16 [64][K] rows (16-byte padding)
+  constexpr int LD64 = kC + 4;    // bf16 [*][64] rows (8-byte padding)
+  constexpr int NTH = V * 2;      // V/32 waves
+  __shared__ __attribute__((aligned(16))) bf16_t kb[kC * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t qb[kC * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t kbT[K * LD64];
+  __shared__ __attribute__((aligned(16))) bf16_t Th[kC * LD64], Tl[kC * LD64];
+  __shared__ __attribute__((aligned(16))) bf16_t Ih[kC * LD64], Il[kC * LD64];
+  __shared__ __attribute__((aligned(16))) bf16_t vb[kC * (V + 8)];
+  __shared__ float sc[5][kC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hi = lane >> 5, col = lane & 31;
+  const int n = blockIdx.x / HV, hv = blockIdx.x % HV;
+  const int vcol = wave * 32 + col;  // this lane's value column
+
+  // S[k][vcol] in accumulator layout: tile kt, entry e -> k = kt*32 + (e/4)*8 + hi*4 + e%4
+  f32x16 S[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kk = kt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+      S[kt][e] = state0 ? load_as_float(state0,
+                                        ((int64_t)(n / beams_per_state) * HV + hv) * K * V +
+                                            (int64_t)kk * V + vcol,
+                                        sdt)
+                        : 0.f;
+    }
+  }
+
   for (int c = 0; c < nchunks; ++c) {
     const int t0 = c * kC;
     const int nt = min(kC, T - t0);
+    const uint8_t* rec = ws + ((size_t)blockIdx.x * nchunks + c) * ChunkRec<K>::bytes;
     __syncthreads();  // previous chunk done with LDS
-
-    // ---- stage q/k rows (bf16) with their normalisation multipliers
-    for (int i = wave; i < kC; i += NW) {
-      float kv[K / 64], qv[K / 64];
-      const bool live = i < nt;
-      const int64_t row = ((int64_t)n * T + t0 + (live ? i : 0)) * ld_qk + (int64_t)h * K;
-      float kss = 0.f, qss = 0.f;
+    {
+      const bf16_t* kn = (const bf16_t*)(rec + ChunkRec<K>::kn);
+      const bf16_t* qn = (const bf16_t*)(rec + ChunkRec<K>::qn);
+      for (int e = tid; e < kC * K / 8; e += NTH) {
+        const int i = e / (K / 8), k8 = (e % (K / 8)) * 8;
+        const u32x4 kr = *(const u32x4*)(kn + i * K + k8);
+        *(u32x4*)(kb + i * LDK + k8) = kr;
+        *(u32x4*)(qb + i * LDK + k8) = *(const u32x4*)(qn + i * K + k8);
 #pragma unroll
-      for (int e = 0; e < K / 64; ++e) {
-        kv[e] = live ? bf2f(k[row + lane + 64 * e]) : 0.f;
-        qv[e] = live ? bf2f(q[row + lane + 64 * e]) : 0.f;
-        if (hf_norm) {
-          kss += round_bf(kv[e] * kv[e]);
-          qss += round_bf(qv[e] * qv[e]);
-        } else {
-          kss += kv[e] * kv[e];
-          qss += qv[e] * qv[e];
+        for (int w = 0; w < 4; ++w) {
+          kbT[(k8 + 2 * w) * LD64 + i] = (bf16_t)(kr[w] & 0xffffu);
+          kbT[(k8 + 2 * w + 1) * LD64 + i] = (bf16_t)(kr[w] >> 16);
         }
       }
-      kss = wave_sum(kss);
-      qss = wave_sum(qss);
-      float km, qm;
-      if (hf_norm) {
-        // x * rsqrt(sum(x*x) + eps), every op rounded to bf16
-        const float kr = round_bf(1.0f / sqrtf(round_bf(round_bf(kss) + 1e-6f)));
-        const float qr = round_bf(1.0f / sqrtf(round_bf(round_bf(qss) + 1e-6f)));
+      const bf16_t* planes[4] = {(const bf16_t*)(rec + ChunkRec<K>::thi),
+                                 (const bf16_t*)(rec + ChunkRec<K>::tlo),
+                                 (const bf16_t*)(rec + ChunkRec<K>::ihi),
+                                 (const bf16_t*)(rec + ChunkRec<K>::ilo)};
+      bf16_t* dsts[4] = {Th, Tl, Ih, Il};
 #pragma unroll
-        for (int e = 0; e < K / 64; ++e) {
-          kv[e] = round_bf(kv[e] * kr);
-          qv[e] = round_bf(qv[e] * qr);
+      for (int p = 0; p < 4; ++p)
+        for (int e = tid; e < kC * kC / 4; e += NTH) {
+          const int i = e / (kC / 4), j4 = (e % (kC / 4)) * 4;
+          *(u32x2*)(dsts[p] + i * LD64 + j4) = *(const u32x2*)(planes[p] + i * kC + j4);
         }
-        km = 1.f;
-        qm = scale;
-      } else {
-        km = 1.0f / sqrtf(kss + 1e-6f);
-        qm = scale / sqrtf(qss + 1e-6f);
-      }
-#pragma unroll
-      for (int e = 0; e < K / 64; ++e) {
-        kb[i * LD + lane + 64 * e] = f2bf(kv[e]);
-        qb[i * LD + lane + 64 * e] = f2bf(qv[e]);
-      }
-      if (lane == 0) {
-        kmul[i] = km;
-        qmul[i] = qm;
-      }
-    }
-    if (col < kC) {
-      const int i = col;
-      const bool live = i < nt;
-      const int64_t gi = ((int64_t)n * T + t0 + (live ? i : 0)) * ld_gate + hv;
-      Gs[i] = live ? load_as_float(g, gi, gdt) : 0.f;
-      bt[i] = live ? load_as_float(beta, gi, bdt) : 0.f;
-    }
-    __syncthreads();
-    if (col == 0) {
-      float acc = 0.f;
-      for (int i = 0; i < kC; ++i) {  // sequential cumulative sum, as torch.cumsum
-        acc += Gs[i];
-        Gs[i] = acc;
-      }
-    }
-    __syncthreads();
-    if (col < kC) {
-      eG[col] = expf(Gs[col]);
-      wupd[col] = kmul[col] * expf(Gs[kC - 1] - Gs[col]);
-    }
-
-    // ---- Gram matrices on MFMA: wave 0 (or the only wave) k k^T, then q k^T
-    for (int which = wave; which < 2; which += NW) {
-      const bf16_t* rowsrc = which == 0 ? kb : qb;
-      const int fr = lane & 31, fk = (lane >> 5) * 8;
-#pragma unroll
-      for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < 2; ++tj) {
-          f32x16 acc = f32x16{};
-#pragma unroll
-          for (int s = 0; s < K / 16; ++s) {
-            const bf16x8 a = as_bf16x8(*(const u32x4*)(rowsrc + (ti * 32 + fr) * LD + s * 16 + fk));
-            const bf16x8 b = as_bf16x8(*(const u32x4*)(kb + (tj * 32 + fr) * LD + s * 16 + fk));
-            acc = mfma32x32x16(a, b, acc);
-          }
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int i = ti * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
-            const int j = tj * 32 + fr;
-            if (which == 0)
-              Am[i][j] = j < i ? -bt[i] * (acc[e] * kmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
-            else
-              In[i][j] = j <= i ? (acc[e] * qmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
-          }
-        }
-    }
-    __syncthreads();
-
-    // ---- forward substitution: T'[i][j] = A[i][j] + sum_{j<m<i} A[i][m] T'[m][j]
-    if (col < kC) Tm[0][col] = 0.f;
-    for (int i = 1; i < kC; ++i) {
-      __syncthreads();
-      if (col < i) {
-        float acc = Am[i][col];
-        for (int m = col + 1; m < i; ++m) acc += Am[i][m] * Tm[m][col];
-        Tm[i][col] = acc;
-      } else if (col < kC) {
-        Tm[i][col] = 0.f;
+      const float* scg = (const float*)(rec + ChunkRec<K>::scal);
+      for (int e = tid; e < 5 * kC; e += NTH) sc[e / kC][e % kC] = scg[e];
+      for (int e = tid; e < kC * V / 8; e += NTH) {
+        const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (i < nt) val = *(const u32x4*)(v + ((int64_t)n * T + t0 + i) * ld_v + (int64_t)hv * V + v8);
+        *(u32x4*)(vb + i * (V + 8) + v8) = val;
       }
     }
     __syncthreads();
 
-    // ---- Z_j = beta_j (v_j - e^{G_j} k^_j S), then v_new = (T' + I) Z (in place, i descending)
-    float z[kC];
+    // S as B fragments (hi/lo) for every k16 step
+    bf16x8 sh[KS], sl[KS];
 #pragma unroll
-    for (int j = 0; j < kC; ++j) {
-      float dot = 0.f;
-#pragma unroll
-      for (int k8 = 0; k8 < K; k8 += 8) {
-        const u32x4 r = *(const u32x4*)(kb + j * LD + k8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dot += __uint_as_float(r[e] << 16) * S[k8 + 2 * e];
-          dot += __uint_as_float(r[e] & 0xffff0000u) * S[k8 + 2 * e + 1];
-        }
-      }
-      const float vj = j < nt ? bf2f(v[((int64_t)n * T + t0 + j) * ld_v + (int64_t)hv * V + col]) : 0.f;
-      z[j] = bt[j] * (vj - eG[j] * (kmul[j] * dot));
-    }
-#pragma unroll
-    for (int i = kC - 1; i > 0; --i) {
-      float acc = z[i];
-#pragma unroll
-      for (int j = 0; j < i; ++j) acc += Tm[i][j] * z[j];
-      z[i] = acc;
-    }
+    for (int s = 0; s < KS; ++s) acc_frags(S[s / 2], s % 2, sh[s], sl[s]);
 
-    // ---- o_i = e^{G_i} q^_i S + sum_{j<=i} In[i][j] v_new_j
+    // ---- Z_j = beta_j (v_j - e^{G_j} kmul_j (k S)_j), tokens j in two 32-row tiles
+    f32x16 Z[2];
 #pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      float dot = 0.f;
+    for (int jt = 0; jt < 2; ++jt) {
+      f32x16 acc = f32x16{};
+      const bf16_t* rowp = kb + (jt * 32 + col) * LDK;
 #pragma unroll
-      for (int k8 = 0; k8 < K; k8 += 8) {
-        const u32x4 r = *(const u32x4*)(qb + i * LD + k8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dot += __uint_as_float(r[e] << 16) * S[k8 + 2 * e];
-          dot += __uint_as_float(r[e] & 0xffff0000u) * S[k8 + 2 * e + 1];
-        }
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 a = perm_frag(rowp, s * 16, hi);
+        acc = mfma32x32x16(a, sh[s], acc);
+        acc = mfma32x32x16(a, sl[s], acc);
       }
-      float o = eG[i] * (qmul[i] * dot);
 #pragma unroll
-      for (int j = 0; j <= i; ++j) o += In[i][j] * z[j];
-      if (i < nt) out[((int64_t)n * T + t0 + i) * ld_out + (int64_t)hv * V + col] = f2bf(o);
+      for (int e = 0; e < 16; ++e) {
+        const int j = jt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+        const float vj = bf2f(vb[j * (V + 8) + vcol]);
+        Z[jt][e] = sc[S_BT][j] * (vj - sc[S_EG][j] * (sc[S_KM][j] * acc[e]));
+      }
     }
-
-    // ---- S <- e^{G_last} S + sum_i (k^_i e^{G_last - G_i}) v_new_i
-    const float eGl = eG[kC - 1];
+    // ---- v_new = Z + T' Z (K dim = tokens, accumulator order on both sides)
+    bf16x8 zh[4], zl[4];
 #pragma unroll
-    for (int kk = 0; kk < K; ++kk) S[kk] *= eGl;
+    for (int s = 0; s < 4; ++s) acc_frags(Z[s / 2], s % 2, zh[s], zl[s]);
+    f32x16 VN[2];
 #pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      const float w = wupd[i] * z[i];
+    for (int it = 0; it < 2; ++it) {
+      f32x16 acc = Z[it];
+      const bf16_t* th = Th + (it * 32 + col) * LD64;
+      const bf16_t* tl = Tl + (it * 32 + col) * LD64;
 #pragma unroll
-      for (int k8 = 0; k8 < K; k8 += 8) {
-        const u32x4 r = *(const u32x4*)(kb + i * LD + k8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          S[k8 + 2 * e] += __uint_as_float(r[e] << 16) * w;
-          S[k8 + 2 * e + 1] += __uint_as_float(r[e] & 0xffff0000u) * w;
-        }
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 ah = perm_frag(th, s * 16, hi), al = perm_frag(tl, s * 16, hi);
+        acc = mfma32x32x16(ah, zh[s], acc);
+        acc = mfma32x32x16(ah, zl[s], acc);
+        acc = mfma32x32x16(al, zh[s], acc);
       }
+      VN[it] = acc;
+    }
+    // ---- o_i = e^{G_i} qmul_i (q S)_i + In v_new
+    bf16x8 vh[4], vl[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc_frags(VN[s / 2], s % 2, vh[s], vl[s]);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      f32x16 qs = f32x16{};
+      const bf16_t* rowp = qb + (it * 32 + col) * LDK;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 a = perm_frag(rowp, s * 16, hi);
+        qs = mfma32x32x16(a, sh[s], qs);
+        qs = mfma32x32x16(a, sl[s], qs);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = it * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+        qs[e] *= sc[S_EG][i] * sc[S_QM][i];
+      }
+      const bf16_t* ih = Ih + (it * 32 + col) * LD64;
+      const bf16_t* il = Il + (it * 32 + col) * LD64;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 ah = perm_frag(ih, s * 16, hi), al = perm_frag(il, s * 16, hi);
+        qs = mfma32x32x16(ah, vh[s], qs);
+        qs = mfma32x32x16(ah, vl[s], qs);
+        qs = mfma32x32x16(al, vh[s], qs);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = it * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+        if (i < nt) out[((int64_t)n * T + t0 + i) * ld_out + (int64_t)hv * V + vcol] = f2bf(qs[e]);
+      }
+    }
+    // ---- S <- e^{G_last} S + sum_i (kmul_i e^{G_last-G_i}) k_i v_new_i^T
+    bf16x8 wh[4], wl[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float x[8];
+#pragma unroll
+      for (int i8 = 0; i8 < 8; ++i8) {
+        const int e = (s % 2) * 8 + i8;
+        const int i = (s / 2) * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+        x[i8] = VN[s / 2][e] * sc[S_WU][i];
+      }
+      split8(x, wh[s], wl[s]);
+    }
+    const float egl = sc[S_EG][kC - 1];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      f32x16 acc = S[kt];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] *= egl;
+      const bf16_t* rowp = kbT + (kt * 32 + col) * LD64;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 a = perm_frag(rowp, s * 16, hi);
+        acc = mfma32x32x16(a, wh[s], acc);
+        acc = mfma32x32x16(a, wl[s], acc);
+      }
+      S[kt] = acc;
     }
   }
   if (final_state) {
-    const int64_t base = ((int64_t)n * HV + hv) * K * V + col;
 #pragma unroll
-    for (int kk = 0; kk < K; ++kk) final_state[base + (int64_t)kk * V] = S[kk];
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int kk = kt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+        final_state[((int64_t)n * HV + hv) * K * V + (int64_t)kk * V + vcol] = S[kt][e];
+      }
   }
 }
 
@@ -251,41 +439,69 @@ template <int K, int V>
 int launch_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
                  const void* g, int gdt, const void* beta, int bdt, int64_t ld_gate,
                  const void* state0, int sdt, int bps, void* out, int64_t ld_out, float* fin,
-                 int N, int T, int H, int HV, float scale, int hf_norm, hipStream_t s) {
-  hipLaunchKernelGGL((gdn_chunk_kernel<K, V>), dim3((unsigned)((int64_t)N * HV)), dim3(V), 0, s,
-                     (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ld_qk, ld_v, g, gdt,
-                     beta, bdt, ld_gate, state0, sdt, bps, (bf16_t*)out, ld_out, fin, T, H, HV,
-                     scale, hf_norm);
-  return kad_launch_status("gdn_chunk_kernel");
+                 void* ws, int N, int T, int H, int HV, float scale, int hf_norm, hipStream_t s) {
+  const int nchunks = (T + kC - 1) / kC;
+  const int64_t nrec = (int64_t)N * HV * nchunks;
+  hipLaunchKernelGGL((gdn_chunk_prep<K>), dim3((unsigned)nrec), dim3(kPrepThreads), 0, s,
+                     (const bf16_t*)q, (const bf16_t*)k, ld_qk, g, gdt, beta, bdt, ld_gate,
+                     (uint8_t*)ws, T, H, HV, nchunks, scale, hf_norm);
+  int rc = kad_launch_status("gdn_chunk_prep");
+  if (rc) return rc;
+  hipLaunchKernelGGL((gdn_chunk_scan<K, V>), dim3((unsigned)((int64_t)N * HV)), dim3(V * 2), 0, s,
+                     (const bf16_t*)v, ld_v, (const uint8_t*)ws, state0, sdt, bps, (bf16_t*)out,
+                     ld_out, fin, T, HV, nchunks);
+  return kad_launch_status("gdn_chunk_scan");
 }
 
+size_t rec_bytes(int K) { return K == 128 ? ChunkRec<128>::bytes : ChunkRec<64>::bytes; }
+
 }  // namespace
+
+static int64_t chunk_ws_bytes(int N, int T, int HV, int K) {
+  return (int64_t)N * HV * ((T + kC - 1) / kC) * (int64_t)rec_bytes(K);
+}
+
+extern "C" int kad_gdn_chunk_workspace_bytes(int N, int T, int HV, int K, int64_t* bytes) {
+  KAD_REQUIRE(bytes, "null pointer argument");
+  KAD_REQUIRE(N > 0 && T > 0 && HV > 0, "bad dimensions");
+  if (K != 64 && K != 128) KAD_UNSUPPORTED("chunked gated delta supports K in {64, 128}");
+  *bytes = chunk_ws_bytes(N, T, HV, K);
+  return KAD_OK;
+}
 
 extern "C" int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk,
                              int64_t ld_v, int qkv_dtype, const void* log_decay, int gate_dtype,
                              const void* beta, int beta_dtype, int64_t ld_gate,
                              const void* initial_state, int state_dtype, int beams_per_state,
-                             void* out, int64_t ld_out, float* final_state, int N, int T, int H,
-                             int HV, int K, int V, float scale, int transformers_l2norm,
-                             kad_stream_t stream) {
-  KAD_REQUIRE(q && k && v && log_decay && beta && out, "null pointer argument");
+                             void* out, int64_t ld_out, float* final_state, void* workspace,
+                             int64_t workspace_bytes, int N, int T, int H, int HV, int K, int V,
+                             float scale, int transformers_l2norm, kad_stream_t stream) {
+  KAD_REQUIRE(q && k && v && log_decay && beta && out && workspace, "null pointer argument");
   KAD_REQUIRE(N > 0 && T > 0 && H > 0 && HV > 0 && HV % H == 0, "bad dimensions");
   KAD_REQUIRE(!initial_state || (beams_per_state > 0 && N % beams_per_state == 0),
               "N must be a multiple of beams_per_state");
   KAD_REQUIRE(ld_qk >= (int64_t)H * K && ld_v >= (int64_t)HV * V && ld_out >= (int64_t)HV * V &&
                   ld_gate >= HV,
               "row strides smaller than a row");
+  KAD_REQUIRE(ld_v % 8 == 0 && ((uintptr_t)v % 16) == 0, "v rows must be 16-byte aligned");
   if (qkv_dtype != KAD_DTYPE_BF16) KAD_UNSUPPORTED("chunked gated delta takes bf16 q/k/v");
+  if (!((K == 64 || K == 128) && (V == 64 || V == 128)))
+    KAD_UNSUPPORTED("chunked gated delta supports K, V in {64, 128}; got K=%d V=%d", K, V);
+  const int64_t need = chunk_ws_bytes(N, T, HV, K);
+  KAD_REQUIRE(workspace_bytes >= need, "workspace of %lld bytes is smaller than %lld",
+              (long long)workspace_bytes, (long long)need);
+  KAD_REQUIRE(((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-#define KAD_CHUNK(KK, VV)                                                                     \
-  if (K == KK && V == VV)                                                                     \
+#define KAD_CHUNK(KK, VV)                                                                      \
+  if (K == KK && V == VV)                                                                      \
     return launch_chunk<KK, VV>(q, k, v, ld_qk, ld_v, log_decay, gate_dtype, beta, beta_dtype, \
-                                ld_gate, initial_state, state_dtype, beams_per_state, out,    \
-                                ld_out, final_state, N, T, H, HV, scale, transformers_l2norm, s);
+                                ld_gate, initial_state, state_dtype, beams_per_state, out,     \
+                                ld_out, final_state, workspace, N, T, H, HV, scale,            \
+                                transformers_l2norm, s);
   KAD_CHUNK(128, 128)
   KAD_CHUNK(64, 64)
   KAD_CHUNK(128, 64)
   KAD_CHUNK(64, 128)
 #undef KAD_CHUNK
-  KAD_UNSUPPORTED("chunked gated delta supports K, V in {64, 128}; got K=%d V=%d", K, V);
+  KAD_UNSUPPORTED("unreachable");
 }

@@ -24,12 +24,13 @@ def gdn_chunk(q, k, v, log_decay, beta, shared_state, *, beam_width=1, scale=Non
     final = (torch.empty(N, HV, K, V, dtype=torch.float32, device=v.device)
              if want_final else None)
     st = shared_state
+    ws = _lib.gdn_chunk_workspace(N, T, HV, K, v.device)
     _lib.call("kad_gdn_chunk", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), q.stride(1), v.stride(1),
               _lib.dtype_code(q.dtype), _lib.ptr(log_decay), _lib.dtype_code(log_decay.dtype),
               _lib.ptr(beta), _lib.dtype_code(beta.dtype), log_decay.stride(1), _lib.ptr(st),
               _lib.dtype_code(st.dtype) if st is not None else 2, beam_width, _lib.ptr(out),
-              out.stride(1), _lib.ptr(final), N, T, H, HV, K, V, float(scale),
-              int(transformers_l2norm), _lib.stream_of(v))
+              out.stride(1), _lib.ptr(final), _lib.ptr(ws), ws.numel(), N, T, H, HV, K, V,
+              float(scale), int(transformers_l2norm), _lib.stream_of(v))
     return out, final
 
 

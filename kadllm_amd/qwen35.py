@@ -178,11 +178,12 @@ class Qwen35Runner:
                 S = torch.empty(B, HV, dk, dv, dtype=torch.float32, device=dev)
                 base = conv.data_ptr()
                 es = conv.element_size()
+                ws = _lib.gdn_chunk_workspace(B, L, HV, dk, dev)
                 _lib.call("kad_gdn_chunk", _lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
                           _lib.ptr_at(base + 2 * self.kd * es), self.conv_dim, self.conv_dim, 0,
                           _lib.ptr(g), 2, _lib.ptr(beta), 0, HV, None, 2, 1, _lib.ptr(o), self.vd,
-                          _lib.ptr(S), B, L, H_, HV, dk, dv, float(dk ** -0.5), 1,
-                          _lib.stream_of(x))
+                          _lib.ptr(S), _lib.ptr(ws), ws.numel(), B, L, H_, HV, dk, dv,
+                          float(dk ** -0.5), 1, _lib.stream_of(x))
                 self._gdn_finish(lyr, o, proj, x)
                 snap.append((conv_state, S))
             else:

@@ -119,9 +119,11 @@ def test_prefill_chunk_matches_transformers_semantics(device, L):
     dev = [t.to(device).contiguous() for t in (q, k, v, g, beta)]
     o = torch.empty(B, L, H, K, dtype=torch.bfloat16, device=device)
     s = torch.empty(B, H, K, K, dtype=torch.float32, device=device)
+    ws = _lib.gdn_chunk_workspace(B, L, H, K, device)
     _lib.call("kad_gdn_chunk", _lib.ptr(dev[0]), _lib.ptr(dev[1]), _lib.ptr(dev[2]), H * K, H * K,
               0, _lib.ptr(dev[3]), 2, _lib.ptr(dev[4]), 0, H, None, 2, 1, _lib.ptr(o), H * K,
-              _lib.ptr(s), B, L, H, H, K, K, float(K ** -0.5), 1, _lib.stream_of(o))
+              _lib.ptr(s), _lib.ptr(ws), ws.numel(), B, L, H, H, K, K, float(K ** -0.5), 1,
+              _lib.stream_of(o))
     torch.cuda.synchronize()
     assert_close_rel(o.cpu(), eo, rtol=1e-2, atol_frac=3e-3, name="prefill o")
     assert_close_rel(s.cpu(), es, rtol=1e-3, atol_frac=1e-4, name="prefill state")
