@@ -101,6 +101,12 @@ int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx
 int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
                   const void* R, int64_t ldr, int M, int N, int K, int epilogue,
                   kad_stream_t stream);
+/* Same with an explicit tile configuration (0 = automatic choice as
+ * kad_gemm_bf16; 1 = 32x256, 2 = 128x128, 3 = 128x256, 4 = 256x256 with 4
+ * waves; 5 = 256x256 and 6 = 256x128 with 8 waves), for tuning. */
+int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
+                        int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
+                        int epilogue, int tile_config, kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
  * Row-wise layer kernels (bf16).  They replace the transformers modules the

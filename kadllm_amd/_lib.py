@@ -30,6 +30,7 @@ SIGNATURES = {
     "kad_gdn_suffix_replay": "ppplli" "pipil" "pi" "pl" "iiiiiii" "f" "s",
     "kad_causal_conv_suffix": "plll" "pllli" "pip" "plll" "iiiiii" "s",
     "kad_gemm_bf16": "plplplpl" "iiii" "s",
+    "kad_gemm_bf16_tiled": "plplplpl" "iiiii" "s",
     "kad_rmsnorm": "plpfpllifs",
     "kad_rmsnorm_gated": "plplpplliifs",
     "kad_gdn_gates": "plplpppplis",

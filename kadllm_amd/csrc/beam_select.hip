@@ -58,17 +58,15 @@ __device__ int block_exclusive_scan(int v, int* scratch, int* total) {
   return base + x - v;
 }
 
-__global__ __launch_bounds__(kRowThreads) void row_select_kernel(
+__device__ void row_select_exact(int64_t row,
     const bf16_t* __restrict__ logits, int64_t ld, const uint8_t* __restrict__ mask,
     int64_t ld_mask, const float* __restrict__ parent, int Wp, int V, int K,
-    float* __restrict__ cand_key, int* __restrict__ cand_idx) {
-  __shared__ int hist[kBins];
+    float* __restrict__ cand_key, int* __restrict__ cand_idx, int* hist) {
   __shared__ int scan_tmp[kRowThreads / 64];
   __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64];
   __shared__ int sh_bin, sh_above, sh_low;
   __shared__ int sh_emit;
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
   const bf16_t* x = logits + row * ld;
   const uint8_t* mk = mask ? mask + row * ld_mask : nullptr;
 
@@ -167,6 +165,169 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
       }
     }
     ties_taken += tot;
+  }
+}
+
+
+constexpr int kSampleEvery = 64;   // one sampled logit per 64
+constexpr int kSampleRank = 8;     // threshold = 8th largest sampled key
+constexpr int kCandCap = 4096;     // LDS candidate capacity
+
+// Fast path: one vectorised pass for the row max, sum exp (online rescaling)
+// and a strided sample; the sample's kSampleRank-th largest key is a
+// threshold expected to leave ~kSampleRank * kSampleEvery entries above it; a
+// second vectorised pass gathers every entry at or above the threshold into
+// LDS, and a bitonic sort by (key desc, column asc) yields the row's top K.
+// If fewer than K or more than kCandCap entries qualify, the exact
+// histogram path runs instead, so the result never depends on the sample.
+__global__ __launch_bounds__(kRowThreads) void row_select_kernel(
+    const bf16_t* __restrict__ logits, int64_t ld, const uint8_t* __restrict__ mask,
+    int64_t ld_mask, const float* __restrict__ parent, int Wp, int V, int K,
+    float* __restrict__ cand_key, int* __restrict__ cand_idx) {
+  __shared__ __attribute__((aligned(16))) uint64_t cand[kCandCap];
+  __shared__ uint16_t samples[kCandCap];
+  __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64];
+  __shared__ int sh_count, sh_ns;
+  __shared__ uint32_t sh_thr;
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const bf16_t* x = logits + row * ld;
+  const uint8_t* mk = mask ? mask + row * ld_mask : nullptr;
+  const bool vec = (ld % 8) == 0 && (((uintptr_t)logits) % 16) == 0 && !mask;
+  if (tid == 0) {
+    sh_count = 0;
+    sh_ns = 0;
+  }
+  __syncthreads();
+
+  // ---- pass 1: max, online sum exp, strided sample of allowed keys
+  float m = -INFINITY, se = 0.f;
+  auto visit = [&](uint16_t bits, int c) {
+    const float v = bf2f(bits);
+    if (v > m) {
+      se = (m == -INFINITY ? 0.f : se * expf(m - v)) + 1.f;
+      m = v;
+    } else if (v != -INFINITY) {
+      se += expf(v - m);
+    }
+    if ((c % kSampleEvery) == 0) {
+      const bool ok = mk ? mk[c] != 0 : true;
+      const int slot = atomicAdd(&sh_ns, 1);
+      if (slot < kCandCap) samples[slot] = ok ? (uint16_t)order16(bits) : 0;
+    }
+  };
+  const int V8 = vec ? V / 8 : 0;
+  for (int c8 = tid; c8 < V8; c8 += kRowThreads) {
+    const u32x4 r = *(const u32x4*)(x + c8 * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      visit((uint16_t)(r[e] & 0xffffu), c8 * 8 + 2 * e);
+      visit((uint16_t)(r[e] >> 16), c8 * 8 + 2 * e + 1);
+    }
+  }
+  for (int c = V8 * 8 + tid; c < V; c += kRowThreads) visit(x[c], c);
+  {
+    float mm = m, ss = se;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float m2 = __shfl_xor(mm, o, 64), s2 = __shfl_xor(ss, o, 64);
+      const float mx = fmaxf(mm, m2);
+      ss = (mm == -INFINITY ? 0.f : ss * expf(mm - mx)) + (m2 == -INFINITY ? 0.f : s2 * expf(m2 - mx));
+      mm = mx;
+    }
+    if ((tid & 63) == 0) {
+      red_m[tid >> 6] = mm;
+      red_s[tid >> 6] = ss;
+    }
+  }
+  __syncthreads();
+  float M = -INFINITY;
+  for (int w = 0; w < kRowThreads / 64; ++w) M = fmaxf(M, red_m[w]);
+  float SE = 0.f;
+  for (int w = 0; w < kRowThreads / 64; ++w)
+    SE += red_m[w] == -INFINITY ? 0.f : red_s[w] * expf(red_m[w] - M);
+  const float lse = logf(SE);
+
+  // ---- threshold: kSampleRank-th largest sampled key (one wave, in registers)
+  const int ns = min(sh_ns, kCandCap);
+  if (tid < 64) {
+    uint32_t thr = 0xffffffffu;  // keys are 16-bit: start above all of them
+    for (int r = 0; r < kSampleRank; ++r) {
+      uint32_t best = 0;
+      for (int i = tid; i < ns; i += 64) {
+        const uint32_t k = samples[i];
+        if (k < thr && k > best) best = k;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) best = max(best, (uint32_t)__shfl_xor((int)best, o, 64));
+      thr = best;  // strictly decreasing distinct keys; equal keys counted once
+      if (best == 0) break;
+    }
+    if (tid == 0) sh_thr = thr;
+  }
+  __syncthreads();
+  const uint32_t thr = sh_thr;
+
+  // ---- pass 2: gather candidates with key >= thr
+  if (thr > 0) {
+    auto gather = [&](uint16_t bits, int c) {
+      const uint32_t u = order16(bits);
+      if (u >= thr) {
+        const int slot = atomicAdd(&sh_count, 1);
+        if (slot < kCandCap)
+          cand[slot] = ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
+      }
+    };
+    for (int c8 = tid; c8 < V8; c8 += kRowThreads) {
+      const u32x4 r = *(const u32x4*)(x + c8 * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gather((uint16_t)(r[e] & 0xffffu), c8 * 8 + 2 * e);
+        gather((uint16_t)(r[e] >> 16), c8 * 8 + 2 * e + 1);
+      }
+    }
+    for (int c = V8 * 8 + tid; c < V; c += kRowThreads) {
+      const bool ok = mk ? mk[c] != 0 : true;
+      if (ok) gather(x[c], c);
+    }
+  }
+  __syncthreads();
+  const int count = sh_count;
+  if (thr == 0 || count < K || count > kCandCap) {
+    // exact fallback: reuses the candidate buffer as the 4096-bin histogram
+    row_select_exact(row, logits, ld, mask, ld_mask, parent, Wp, V, K, cand_key, cand_idx,
+                     (int*)cand);
+    return;
+  }
+  // ---- bitonic sort of the candidates, descending by (key, -column)
+  int P = 1;
+  while (P < count) P <<= 1;
+  for (int i = count + tid; i < P; i += kRowThreads) cand[i] = 0;
+  __syncthreads();
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < P; i += kRowThreads) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool desc = (i & size) == 0;
+          const uint64_t a = cand[i], b = cand[j];
+          if (desc ? a < b : a > b) {
+            cand[i] = b;
+            cand[j] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const float p = parent[row];
+  const int r_local = (int)(row % Wp);
+  for (int i = tid; i < K; i += kRowThreads) {
+    const uint64_t e = cand[i];
+    const int c = (int)(0xffffffffu - (uint32_t)(e & 0xffffffffu));
+    const float v = bf2f(x[c]);
+    cand_key[row * K + i] = ((v - M) - lse) + p;
+    cand_idx[row * K + i] = r_local * V + c;
   }
 }
 

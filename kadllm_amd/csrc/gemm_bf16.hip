@@ -5,8 +5,7 @@
 // (src/kadllm/adapters/qwen3_5.py:146,161-162,169,175,177,181-188,202,234-235
 // and the transformers layer modules they call).
 //
-// Tiling: a 256-thread workgroup computes a BM x BN tile with 4 waves in a
-// WAVES_M x WAVES_N grid; each wave owns (BM/WAVES_M) x (BN/WAVES_N) outputs
+// Tiling: a workgroup of WAVES_M x WAVES_N waves computes a BM x BN tile; each wave owns (BM/WAVES_M) x (BN/WAVES_N) outputs
 // as 32x32 v_mfma_f32_32x32x16_bf16 tiles.  K advances 64 at a time through
 // double-buffered LDS tiles (rows padded by 16 bytes so that the 16-byte
 // fragment reads of 8 consecutive rows hit distinct bank groups); the next
@@ -31,15 +30,15 @@ constexpr int kPad = 8;
 constexpr int kLdk = kBK + kPad;  // LDS row stride (elements)
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI>
-__global__ __launch_bounds__(256) void gemm_bf16_kernel(
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
     bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major) {
-  static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
+  constexpr int NTH = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int MT = WM / 32, NT = WN / 32;
   constexpr int CPR = kBK / 8;  // 16-byte chunks per tile row
-  constexpr int A_CH = BM * CPR / 256, B_CH = BN * CPR / 256;
-  static_assert(A_CH * 256 == BM * CPR && B_CH * 256 == BN * CPR, "tile/thread mismatch");
+  constexpr int A_CH = BM * CPR / NTH, B_CH = BN * CPR / NTH;
+  static_assert(A_CH * NTH == BM * CPR && B_CH * NTH == BN * CPR, "tile/thread mismatch");
   __shared__ __attribute__((aligned(16))) bf16_t smem[2][(BM + BN) * kLdk];
 
   const int tid = threadIdx.x;
@@ -63,13 +62,13 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
   int a_dst[A_CH], b_dst[B_CH];
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
-    const int c = tid + i * 256, row = c / CPR, kc = c % CPR;
+    const int c = tid + i * NTH, row = c / CPR, kc = c % CPR;
     a_src[i] = A + (int64_t)min(m0 + row, M - 1) * lda + kc * 8;
     a_dst[i] = row * kLdk + kc * 8;
   }
 #pragma unroll
   for (int i = 0; i < B_CH; ++i) {
-    const int c = tid + i * 256, row = c / CPR, kc = c % CPR;
+    const int c = tid + i * NTH, row = c / CPR, kc = c % CPR;
     b_src[i] = Wt + (int64_t)min(n0 + row, N - 1) * ldw + kc * 8;
     b_dst[i] = BM * kLdk + row * kLdk + kc * 8;
   }
@@ -169,27 +168,44 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
   if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
   // reuse the larger operand: weights (N*K) vs activations (M*K)
   const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM_, WN_, EPI>), dim3((unsigned)nblocks), dim3(256),
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM_, WN_, EPI>), dim3((unsigned)nblocks),
+                     dim3(64 * WM_ * WN_),
                      0, s, (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
                      (const bf16_t*)R, ldr, M, N, K, n_major);
   return kad_launch_status("gemm_bf16_kernel");
 }
 
+// tile configurations (tile_config argument of kad_gemm_bf16_tiled)
+enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
+       CFG_256x256_8W = 5, CFG_256x128_8W = 6 };
+
 template <int EPI>
-int pick(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
-  const int64_t big_tiles = kad_cdiv(M, 128) * kad_cdiv(N, 256);
-  if (M <= 64) return launch<32, 256, 1, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-  if (big_tiles >= 1024)
-    return launch<128, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-  return launch<128, 128, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+  if (cfg == CFG_AUTO) {
+    // 256x256 tiles with 8 waves (two per SIMD) when they still fill every CU;
+    // 128x128 otherwise (measured on the decode/prefill projection shapes)
+    const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
+    cfg = M <= 64 ? CFG_32x256 : (tiles256 >= 256 ? CFG_256x256_8W : CFG_128x128);
+  }
+  switch (cfg) {
+    case CFG_32x256: return launch<32, 256, 1, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_128x128: return launch<128, 128, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_128x256: return launch<128, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x256: return launch<256, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x256_8W:
+      return launch<256, 256, 2, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x128_8W:
+      return launch<256, 128, 4, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    default: KAD_UNSUPPORTED("unknown gemm tile configuration %d", cfg);
+  }
 }
 
 }  // namespace
 
-extern "C" int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
-                             int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
-                             int epilogue, kad_stream_t stream) {
+extern "C" int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw,
+                                   void* C, int64_t ldc, const void* R, int64_t ldr, int M, int N,
+                                   int K, int epilogue, int tile_config, kad_stream_t stream) {
   KAD_REQUIRE(A && W && C, "null pointer argument");
   KAD_REQUIRE(M > 0 && N > 0 && K > 0, "dimensions must be positive");
   if (K % kBK) KAD_UNSUPPORTED("gemm requires K %% %d == 0, got K=%d", kBK, K);
@@ -197,18 +213,25 @@ extern "C" int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t 
               "lda/ldw must be >= K and multiples of 8");
   KAD_REQUIRE(((uintptr_t)A | (uintptr_t)W) % 16 == 0, "A and W must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
+  const int cfg = tile_config;
   switch (epilogue) {
     case KAD_EPI_STORE:
       KAD_REQUIRE(ldc >= N, "ldc must be >= N");
-      return pick<KAD_EPI_STORE>(A, lda, W, ldw, C, ldc, nullptr, 0, M, N, K, s);
+      return pick<KAD_EPI_STORE>(cfg, A, lda, W, ldw, C, ldc, nullptr, 0, M, N, K, s);
     case KAD_EPI_RESIDUAL:
       KAD_REQUIRE(R != nullptr && ldr >= N && ldc >= N, "residual epilogue needs R, ldr >= N");
-      return pick<KAD_EPI_RESIDUAL>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return pick<KAD_EPI_RESIDUAL>(cfg, A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case KAD_EPI_SWIGLU:
       KAD_REQUIRE(N % 64 == 0, "swiglu epilogue needs N %% 64 == 0 ([gate 32 | up 32] blocks)");
       KAD_REQUIRE(ldc >= N / 2, "ldc must be >= N/2");
-      return pick<KAD_EPI_SWIGLU>(A, lda, W, ldw, C, ldc, nullptr, 0, M, N, K, s);
+      return pick<KAD_EPI_SWIGLU>(cfg, A, lda, W, ldw, C, ldc, nullptr, 0, M, N, K, s);
     default:
       KAD_REQUIRE(false, "unknown epilogue %d", epilogue);
   }
+}
+
+extern "C" int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
+                             int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
+                             int epilogue, kad_stream_t stream) {
+  return kad_gemm_bf16_tiled(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, epilogue, 0, stream);
 }

@@ -24,7 +24,13 @@ def _check_selection(logits, scores, width, mask=None):
     finite = torch.isfinite(rs)
     assert torch.equal(valid.cpu(), finite)
     assert torch.equal(torch.isfinite(s.cpu()), finite)
-    assert torch.allclose(s.cpu()[finite], rs[finite], rtol=0, atol=2e-5)
+    # Scores against fp64 log-softmax at the selected (parent, token): torch's
+    # fp32 CPU log_softmax itself drifts by ~3e-5 over 248k near-equal terms.
+    logp = logits.cpu().double().log_softmax(-1) + scores.cpu().double()[..., None]
+    flat = rp.clamp(min=0) * logits.shape[-1] + rt.clamp(min=0)
+    s64 = logp.reshape(logp.shape[0], -1).gather(1, flat)
+    assert torch.allclose(s.cpu()[finite].double(), s64[finite], rtol=0, atol=1e-5)
+    assert torch.allclose(s.cpu()[finite], rs[finite], rtol=0, atol=1e-4)
     return s, p, t
 
 
@@ -147,3 +153,24 @@ def test_conv_prefill_and_state(device, L):
     assert ((a - e).abs() <= e.abs() * 2 ** -7 + 1e-6).all()
     ref_state = F.pad(pre, (max(0, 4 - L), 0))[..., -4:]
     assert torch.equal(st.cpu(), ref_state)
+
+
+def test_select_level_masked_fast_path(device):
+    B, Wp, V, W = 2, 4, 4096, 16
+    g = torch.Generator().manual_seed(12)
+    logits = torch.randn(B, Wp, V, generator=g).bfloat16()
+    scores = -torch.rand(B, Wp, generator=g)
+    mask = torch.rand(B, Wp, V, generator=g) > 0.3
+    _check_selection(logits.to(device), scores.to(device), W, mask.to(device))
+
+
+def test_select_level_candidate_overflow_falls_back_exactly(device):
+    """Near-constant rows put far more than the candidate capacity at the sampled
+    threshold; the exact histogram path must take over with the same answer."""
+    B, Wp, V, W = 1, 3, 248320, 64
+    g = torch.Generator().manual_seed(13)
+    logits = torch.randint(0, 10, (B, Wp, V), generator=g).float() / 10   # 10 levels, huge ties
+    logits[0, 1, 12345] = 3.0
+    logits = logits.bfloat16()
+    scores = -torch.rand(B, Wp, generator=g)
+    _check_selection(logits.to(device), scores.to(device), W)
