@@ -169,40 +169,141 @@ __device__ void row_select_exact(int64_t row,
 }
 
 
-constexpr int kSampleEvery = 64;   // one sampled logit per 64
-constexpr int kSampleRank = 8;     // threshold = 8th largest sampled key
-constexpr int kCandCap = 4096;     // LDS candidate capacity
+constexpr int kCandCap = 4096;                 // LDS candidate capacity (32 KB)
+constexpr int kSampleCap = kCandCap * 4;       // bf16 sample keys aliasing the candidates
+constexpr int kLine = 64;                      // logits per 128-byte line
+constexpr int kTargetLines = 128;              // sampled lines per row (~8k samples)
 
-// Fast path: one vectorised pass for the row max, sum exp (online rescaling)
-// and a strided sample; the sample's kSampleRank-th largest key is a
-// threshold expected to leave ~kSampleRank * kSampleEvery entries above it; a
-// second vectorised pass gathers every entry at or above the threshold into
-// LDS, and a bitonic sort by (key desc, column asc) yields the row's top K.
-// If fewer than K or more than kCandCap entries qualify, the exact
-// histogram path runs instead, so the result never depends on the sample.
+// r-th largest of the keys histogrammed in hist[256] (bin 0 excluded), run by
+// one full wave: lane l owns bins 4l..4l+3.  Returns the bin and, through
+// *above, how many keys lie in higher bins; bin -1 if fewer than r keys.
+__device__ int wave_rank_bin(const int* hist, int r, int* above) {
+  const int lane = threadIdx.x & 63;
+  int b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = (lane == 0 && i == 0) ? 0 : hist[lane * 4 + i];
+  const int t = b[0] + b[1] + b[2] + b[3];
+  int suf = t;  // keys in lanes >= lane
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_down(suf, o, 64);
+    if (lane + o < 64) suf += y;
+  }
+  const uint64_t reach = __ballot(suf >= r);
+  const int L = __popcll(reach) - 1;  // suffix sums fall with the lane: reach is a prefix
+  int bin = -1, acc = 0;
+  if (L >= 0 && lane == L) {
+    acc = suf - t;
+    for (int i = 3; i >= 0; --i) {
+      if (acc + b[i] >= r) {
+        bin = lane * 4 + i;
+        break;
+      }
+      acc += b[i];
+    }
+  }
+  if (L < 0) return -1;
+  *above = __shfl(acc, L, 64);
+  return __shfl(bin, L, 64);
+}
+
+// Fast path, one workgroup per beam row:
+//  1. sample every line_stride-th 128-byte line of the row and take the
+//     rank-th largest sampled key (exact, two 8-bit radix rounds); about
+//     rank * line_stride >= 2K + 256 entries are expected at or above it;
+//  2. one vectorised pass over the row computes the max and the sum of exp
+//     (online rescaling) and gathers every allowed entry at or above the
+//     threshold into LDS;
+//  3. a bitonic sort by (key desc, column asc) yields the row's top K.
+// If fewer than K or more than kCandCap entries qualify, the exact histogram
+// path runs instead, so the result never depends on the sample.
 __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
     const bf16_t* __restrict__ logits, int64_t ld, const uint8_t* __restrict__ mask,
     int64_t ld_mask, const float* __restrict__ parent, int Wp, int V, int K,
-    float* __restrict__ cand_key, int* __restrict__ cand_idx) {
+    float* __restrict__ cand_key, int* __restrict__ cand_idx, int line_stride, int rank) {
   __shared__ __attribute__((aligned(16))) uint64_t cand[kCandCap];
-  __shared__ uint16_t samples[kCandCap];
+  __shared__ int hist[256];
   __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64];
-  __shared__ int sh_count, sh_ns;
-  __shared__ uint32_t sh_thr;
+  __shared__ int sh_count, sh_hi, sh_above, sh_thr;
+  uint16_t* samples = (uint16_t*)cand;
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const bf16_t* x = logits + row * ld;
   const uint8_t* mk = mask ? mask + row * ld_mask : nullptr;
-  const bool vec = (ld % 8) == 0 && (((uintptr_t)logits) % 16) == 0 && !mask;
-  if (tid == 0) {
-    sh_count = 0;
-    sh_ns = 0;
+  const bool vec = (ld % 8) == 0 && (((uintptr_t)logits) % 16) == 0 &&
+                   (!mask || ((ld_mask % 8) == 0 && (((uintptr_t)mask) % 8) == 0));
+  auto key_of = [&](uint16_t bits, int c) -> uint32_t {
+    return (mk && mk[c] == 0) ? 0u : order16(bits);
+  };
+
+  // ---- 1. sample and threshold
+  const int nlines = (V + kLine - 1) / kLine;
+  const int ns = min(kSampleCap, ((nlines + line_stride - 1) / line_stride) * kLine);
+  hist[tid] = 0;
+  if (tid == 0) sh_count = 0;
+  __syncthreads();
+  for (int s = tid; s < ns; s += kRowThreads) {
+    const int c = (s / kLine) * line_stride * kLine + (s % kLine);
+    const uint32_t k = c < V ? key_of(x[c], c) : 0u;
+    samples[s] = (uint16_t)k;
+    atomicAdd(&hist[k >> 8], 1);
   }
   __syncthreads();
+  if (tid < 64) {
+    int above = 0;
+    const int hi = wave_rank_bin(hist, rank, &above);
+    if (tid == 0) {
+      sh_hi = hi;
+      sh_above = above;
+    }
+  }
+  __syncthreads();
+  const int hi = sh_hi;
+  if (hi > 0) {
+    hist[tid] = 0;
+    __syncthreads();
+    for (int s = tid; s < ns; s += kRowThreads) {
+      const uint32_t k = samples[s];
+      if ((int)(k >> 8) == hi) atomicAdd(&hist[k & 255], 1);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // bin 0 of this round is a real key (hi > 0): count it
+      const int lane = tid;
+      int b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b[i] = hist[lane * 4 + i];
+      const int t = b[0] + b[1] + b[2] + b[3];
+      int suf = t;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_down(suf, o, 64);
+        if (lane + o < 64) suf += y;
+      }
+      const int need = rank - sh_above;
+      const uint64_t reach = __ballot(suf >= need);
+      const int L = __popcll(reach) - 1;  // need <= keys in bin hi, so L >= 0
+      if (lane == L) {
+        int acc = suf - t, lo = 0;
+        for (int i = 3; i >= 0; --i) {
+          if (acc + b[i] >= need) {
+            lo = lane * 4 + i;
+            break;
+          }
+          acc += b[i];
+        }
+        sh_thr = (hi << 8) | lo;
+      }
+    }
+  } else if (tid == 0) {
+    sh_thr = 0;
+  }
+  __syncthreads();
+  const uint32_t thr = (uint32_t)sh_thr;
 
-  // ---- pass 1: max, online sum exp, strided sample of allowed keys
+  // ---- 2. max, online sum exp, and candidates >= thr in one pass
   float m = -INFINITY, se = 0.f;
-  auto visit = [&](uint16_t bits, int c) {
+  auto visit = [&](uint16_t bits, int c, bool ok) {
     const float v = bf2f(bits);
     if (v > m) {
       se = (m == -INFINITY ? 0.f : se * expf(m - v)) + 1.f;
@@ -210,22 +311,44 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
     } else if (v != -INFINITY) {
       se += expf(v - m);
     }
-    if ((c % kSampleEvery) == 0) {
-      const bool ok = mk ? mk[c] != 0 : true;
-      const int slot = atomicAdd(&sh_ns, 1);
-      if (slot < kCandCap) samples[slot] = ok ? (uint16_t)order16(bits) : 0;
+    const uint32_t u = ok ? order16(bits) : 0u;
+    if (thr > 0 && u >= thr) {
+      const int slot = atomicAdd(&sh_count, 1);
+      if (slot < kCandCap) cand[slot] = ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
     }
   };
   const int V8 = vec ? V / 8 : 0;
-  for (int c8 = tid; c8 < V8; c8 += kRowThreads) {
+  constexpr int kUnroll = 4;
+  int c8 = tid;
+  for (; c8 + (kUnroll - 1) * kRowThreads < V8; c8 += kUnroll * kRowThreads) {
+    u32x4 r[kUnroll];
+    u32x2 mr[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      r[u] = *(const u32x4*)(x + (c8 + u * kRowThreads) * 8);
+      if (mk) mr[u] = *(const u32x2*)(mk + (c8 + u * kRowThreads) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int c = (c8 + u * kRowThreads) * 8;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok0 = mk ? ((mr[u][e / 2] >> (16 * (e % 2))) & 0xffu) != 0 : true;
+        const bool ok1 = mk ? ((mr[u][e / 2] >> (16 * (e % 2) + 8)) & 0xffu) != 0 : true;
+        visit((uint16_t)(r[u][e] & 0xffffu), c + 2 * e, ok0);
+        visit((uint16_t)(r[u][e] >> 16), c + 2 * e + 1, ok1);
+      }
+    }
+  }
+  for (; c8 < V8; c8 += kRowThreads) {
     const u32x4 r = *(const u32x4*)(x + c8 * 8);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      visit((uint16_t)(r[e] & 0xffffu), c8 * 8 + 2 * e);
-      visit((uint16_t)(r[e] >> 16), c8 * 8 + 2 * e + 1);
+      visit((uint16_t)(r[e] & 0xffffu), c8 * 8 + 2 * e, mk ? mk[c8 * 8 + 2 * e] != 0 : true);
+      visit((uint16_t)(r[e] >> 16), c8 * 8 + 2 * e + 1, mk ? mk[c8 * 8 + 2 * e + 1] != 0 : true);
     }
   }
-  for (int c = V8 * 8 + tid; c < V; c += kRowThreads) visit(x[c], c);
+  for (int c = V8 * 8 + tid; c < V; c += kRowThreads) visit(x[c], c, mk ? mk[c] != 0 : true);
   {
     float mm = m, ss = se;
 #pragma unroll
@@ -247,59 +370,15 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   for (int w = 0; w < kRowThreads / 64; ++w)
     SE += red_m[w] == -INFINITY ? 0.f : red_s[w] * expf(red_m[w] - M);
   const float lse = logf(SE);
-
-  // ---- threshold: kSampleRank-th largest sampled key (one wave, in registers)
-  const int ns = min(sh_ns, kCandCap);
-  if (tid < 64) {
-    uint32_t thr = 0xffffffffu;  // keys are 16-bit: start above all of them
-    for (int r = 0; r < kSampleRank; ++r) {
-      uint32_t best = 0;
-      for (int i = tid; i < ns; i += 64) {
-        const uint32_t k = samples[i];
-        if (k < thr && k > best) best = k;
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) best = max(best, (uint32_t)__shfl_xor((int)best, o, 64));
-      thr = best;  // strictly decreasing distinct keys; equal keys counted once
-      if (best == 0) break;
-    }
-    if (tid == 0) sh_thr = thr;
-  }
-  __syncthreads();
-  const uint32_t thr = sh_thr;
-
-  // ---- pass 2: gather candidates with key >= thr
-  if (thr > 0) {
-    auto gather = [&](uint16_t bits, int c) {
-      const uint32_t u = order16(bits);
-      if (u >= thr) {
-        const int slot = atomicAdd(&sh_count, 1);
-        if (slot < kCandCap)
-          cand[slot] = ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
-      }
-    };
-    for (int c8 = tid; c8 < V8; c8 += kRowThreads) {
-      const u32x4 r = *(const u32x4*)(x + c8 * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        gather((uint16_t)(r[e] & 0xffffu), c8 * 8 + 2 * e);
-        gather((uint16_t)(r[e] >> 16), c8 * 8 + 2 * e + 1);
-      }
-    }
-    for (int c = V8 * 8 + tid; c < V; c += kRowThreads) {
-      const bool ok = mk ? mk[c] != 0 : true;
-      if (ok) gather(x[c], c);
-    }
-  }
-  __syncthreads();
   const int count = sh_count;
   if (thr == 0 || count < K || count > kCandCap) {
     // exact fallback: reuses the candidate buffer as the 4096-bin histogram
+    __syncthreads();
     row_select_exact(row, logits, ld, mask, ld_mask, parent, Wp, V, K, cand_key, cand_idx,
                      (int*)cand);
     return;
   }
-  // ---- bitonic sort of the candidates, descending by (key, -column)
+  // ---- 3. bitonic sort of the candidates, descending by (key, -column)
   int P = 1;
   while (P < count) P <<= 1;
   for (int i = count + tid; i < P; i += kRowThreads) cand[i] = 0;
@@ -491,9 +570,13 @@ extern "C" int kad_beam_row_select(const void* logits, int64_t ld, const void* m
   KAD_REQUIRE(rows > 0 && Wp > 0 && rows % Wp == 0 && V > 0 && ld >= V, "bad dimensions");
   KAD_REQUIRE(K >= 1 && K <= V, "K must be in [1, V]");
   KAD_REQUIRE((int64_t)Wp * V < 0x7fffffff, "Wp * V must fit in int32 flat indices");
+  // sample ~kTargetLines lines; rank chosen so that rank * line_stride >= 2K + 256
+  const int nlines = (V + kLine - 1) / kLine;
+  const int line_stride = nlines > kTargetLines ? nlines / kTargetLines : 1;
+  const int rank = (int)kad_cdiv(2 * (int64_t)K + 256, line_stride);
   hipLaunchKernelGGL(row_select_kernel, dim3(rows), dim3(kRowThreads), 0, (hipStream_t)stream,
                      (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores, Wp,
-                     V, K, cand_key, cand_idx);
+                     V, K, cand_key, cand_idx, line_stride, rank);
   return kad_launch_status("row_select_kernel");
 }
 

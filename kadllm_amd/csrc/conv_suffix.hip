@@ -51,18 +51,24 @@ __global__ __launch_bounds__(256) void conv_suffix_scalar(
   }
 }
 
-// 8 contiguous bf16 channels per thread; width 4 (3 taps), any T.
+// 8 contiguous bf16 channels per thread, kConvBeams beams of one request per
+// thread (the request's weights and prefix taps are loaded once); width 4
+// (3 taps), any T.  Grid: x = request x beam group, y = channel groups of 256
+// threads.  The next (beam, token) row is loaded before the current one is
+// computed so that every thread keeps one 16-byte load in flight.
+constexpr int kConvBeams = 8;
+
 __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
     const bf16_t* __restrict__ x, int64_t sx_n, int64_t sx_t, const bf16_t* __restrict__ state,
     int64_t ss_b, int64_t ss_c, int64_t ss_t, int history, const bf16_t* __restrict__ w,
-    bf16_t* __restrict__ out, int64_t so_n, int64_t so_t, int W, int C, int T_, int64_t total,
+    bf16_t* __restrict__ out, int64_t so_n, int64_t so_t, int W, int C, int T_, int nbg,
     int silu) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int C8 = C / 8;
-  const int c0 = (int)(idx % C8) * 8;
-  const int64_t n = idx / C8;
-  const int64_t b = n / W;
+  const int c8 = blockIdx.y * 256 + threadIdx.x;
+  if (c8 >= C / 8) return;
+  const int c0 = c8 * 8;
+  const int b = blockIdx.x / nbg;
+  const int j0 = (blockIdx.x % nbg) * kConvBeams;
+  const int nj = min(W - j0, kConvBeams);
   float wt[8][4];
   {
     const u32x4* wp = (const u32x4*)(w + (int64_t)c0 * 4);
@@ -77,17 +83,48 @@ __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
       }
     }
   }
-  float win[8][4];
+  // prefix taps: the last 3 of the request's state, per channel
+  float tap[8][3];
+  const bf16_t* sb = state + (int64_t)b * ss_b;
+  if (ss_t == 1 && ss_c == 4 && history == 4 && (((uintptr_t)sb) % 16) == 0) {
+    const u32x4* sp = (const u32x4*)(sb + (int64_t)c0 * 4);
 #pragma unroll
-  for (int ch = 0; ch < 8; ++ch) {
-    win[ch][0] = 0.f;
+    for (int j = 0; j < 4; ++j) {
+      u32x4 r = sp[j];
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-      win[ch][1 + i] = bf2f(state[b * ss_b + (int64_t)(c0 + ch) * ss_c +
-                                  (int64_t)(history - 3 + i) * ss_t]);
+      for (int e = 0; e < 4; ++e) {
+        const int flat = j * 8 + e * 2;  // channel flat/4, slot flat%4 (slots 1..3 are taps)
+        if (flat % 4 != 0) tap[flat / 4][flat % 4 - 1] = __uint_as_float(r[e] << 16);
+        tap[(flat + 1) / 4][(flat + 1) % 4 - 1] = __uint_as_float(r[e] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        tap[ch][i] = bf2f(sb[(int64_t)(c0 + ch) * ss_c + (int64_t)(history - 3 + i) * ss_t]);
   }
-  for (int t = 0; t < T_; ++t) {
-    u32x4 r = *(const u32x4*)(x + n * sx_n + (int64_t)t * sx_t + c0);
+
+  const int64_t n0 = (int64_t)b * W + j0;
+  const int steps = nj * T_;
+  auto row = [&](int k) {
+    const int j = k / T_, t = k - (k / T_) * T_;
+    return x + (n0 + j) * sx_n + (int64_t)t * sx_t + c0;
+  };
+  u32x4 next = *(const u32x4*)row(0);
+  float win[8][4];
+  for (int k = 0, t = 0; k < steps; ++k) {
+    const u32x4 r = next;
+    if (k + 1 < steps) next = *(const u32x4*)row(k + 1);
+    if (t == 0) {
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) {
+        win[ch][1] = tap[ch][0];
+        win[ch][2] = tap[ch][1];
+        win[ch][3] = tap[ch][2];
+      }
+    }
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -109,7 +146,9 @@ __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
       }
       o[e] = packed;
     }
-    *(u32x4*)(out + n * so_n + (int64_t)t * so_t + c0) = o;
+    const int j = k / T_;
+    *(u32x4*)(out + (n0 + j) * so_n + (int64_t)t * so_t + c0) = o;
+    if (++t == T_) t = 0;
   }
 }
 
@@ -244,11 +283,12 @@ extern "C" int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c,
                    so_t % 8 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 16) == 0 &&
                    ((uintptr_t)weight % 16) == 0;
   if (vec) {
-    const int64_t total = (int64_t)B * W * (C / 8);
-    hipLaunchKernelGGL(conv_suffix_vec_bf16, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0, s,
-                       (const bf16_t*)x, sx_n, sx_t, (const bf16_t*)state, ss_b, ss_c, ss_t,
-                       history, (const bf16_t*)weight, (bf16_t*)out, so_n, so_t, W, C, T, total,
-                       activation_silu);
+    const int nbg = (int)kad_cdiv(W, kConvBeams);
+    KAD_REQUIRE((int64_t)B * nbg < 2147483647, "too many beams for the grid");
+    hipLaunchKernelGGL(conv_suffix_vec_bf16, dim3((unsigned)(B * nbg), (unsigned)kad_cdiv(C / 8, 256)),
+                       dim3(256), 0, s, (const bf16_t*)x, sx_n, sx_t, (const bf16_t*)state, ss_b,
+                       ss_c, ss_t, history, (const bf16_t*)weight, (bf16_t*)out, so_n, so_t, W, C,
+                       T, nbg, activation_silu);
     return kad_launch_status("conv_suffix_vec_bf16");
   }
   if (dtype == KAD_DTYPE_BF16)

@@ -172,6 +172,23 @@ def test_conv_matches_oracle(device, dtype, layout, case):
         assert_close_rel(out.cpu(), expected, rtol=1e-5, atol_frac=1e-6, name="conv fp32")
 
 
+@pytest.mark.parametrize("T", [1, 2, 5])
+@pytest.mark.parametrize("history", [3, 4, 6])
+def test_conv_beam_groups_and_state_history(device, T, history):
+    """Beam counts that straddle the kernel's beam groups, and prefix states holding
+    3, 4 (the model's conv cache) or more taps."""
+    B, W, C = 3, 13, 64
+    x, st, w = conv_inputs(B, W, C, T, seed=history * 10 + T, history=history)
+    x = x.transpose(1, 2).contiguous().transpose(1, 2)
+    expected = ops_ref.causal_conv1d(x, st, w, beam_width=W)
+    xd = x.to(device).transpose(1, 2).contiguous().transpose(1, 2)
+    out = ops.causal_conv1d(xd, st.to(device), w.to(device), beam_width=W)
+    torch.cuda.synchronize()
+    a, e = out.cpu().float(), expected.float()
+    assert ((a - e).abs() <= (e.abs() * 2 ** -7).clamp_min(1e-30)).all()
+    assert (a == e).float().mean().item() > 0.99
+
+
 def test_conv_golden_fixture(device):
     f = load_npz("ops_bf16.npz")
     x, st, w = (bf16_from_bits(f[n]) for n in ("conv_x", "conv_state", "conv_w"))
