@@ -21,6 +21,8 @@
 //   SWIGLU    weight rows interleaved per 32 as [gate 32 | up 32] blocks;
 //             C[:, j] = bf16(bf16(silu(bf16(g))) * bf16(u)), N/2 columns
 
+#include <cstdlib>
+
 #include "kad_common.h"
 
 namespace {
@@ -160,6 +162,243 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
   }
 }
 
+// 256x256 tile, 4 waves (2 x 2), each wave a 128x128 sub-tile: 16 MFMA
+// 32x32x16 per 16-deep K step against 8 fragment loads, the highest
+// MFMA-to-LDS ratio the 512-register file allows (a second wave per SIMD
+// would halve it).
+//
+// Operand tiles move HBM -> LDS with global_load_lds_dwordx4 (no register
+// staging): one wave instruction writes 64 x 16 bytes contiguously, i.e. 8
+// tile rows of 128 bytes.  Within a row the 16-byte chunk c of K is stored at
+// chunk c ^ ((row >> 1) & 7), so that the fragment reads (16 lanes = 16
+// consecutive rows at one chunk) hit 16 distinct 16-byte bank groups; each
+// lane of a load therefore fetches the global chunk that belongs at its LDS
+// slot.  Two stages of 64-deep K: tile kt+1 is in flight while tile kt feeds
+// the MFMAs.  Each 16-deep step is its own scheduling region with its MFMAs
+// interleaved with the next step's fragment reads (and, in step 0, with the
+// next tile's loads).
+//
+// Operands are swapped (weight rows are the MFMA's A operand), so each lane's
+// accumulators hold 4 consecutive output columns: the epilogue packs them 8
+// bytes at a time into LDS, and the wave then writes its sub-tile with
+// 16-byte stores (fusing the residual add or SwiGLU on the way).
+constexpr int kT = 256;
+constexpr int kEpiLd = 128 + 8;                  // epilogue LDS row stride (elements)
+constexpr int kStage = 2 * kT * kBK;             // elements per stage: A rows then W rows
+constexpr int kSmem = 2 * kStage > 4 * 128 * kEpiLd ? 2 * kStage : 4 * 128 * kEpiLd;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+__device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)g, (lds_void_t*)lds_block, 16, 0, 0);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm256_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group) {
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[kSmem];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int mtiles = (M + kT - 1) / kT, ntiles = (N + kT - 1) / kT;
+  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  // grouped order: `group` consecutive tiles along the outer dimension share
+  // each inner-dimension tile, so an XCD's resident tiles form a 2-D block
+  // and both operands are reused from its L2
+  const int nx = n_major ? ntiles : mtiles, ny = n_major ? mtiles : ntiles;
+  const int gx0 = (lid / (group * ny)) * group, gs = min(nx - gx0, group);
+  const int within = lid % (group * ny);
+  const int tx = gx0 + within % gs, ty = within / gs;
+  const int mi = n_major ? ty : tx, ni = n_major ? tx : ty;
+  const int m0 = mi * kT, n0 = ni * kT;
+
+  // DMA: this wave loads row groups g = wave + 4 i (i < 8) of both tiles;
+  // lane L -> row g*8 + L/8, LDS chunk L%8, global chunk (L%8) ^ ((row>>1)&7)
+  const int d_row = lane >> 3;
+  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
+  const bf16_t* a_src[8];
+  const bf16_t* b_src[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = (wave + 4 * i) * 8 + d_row;
+    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
+    b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
+  }
+  auto issue = [&](int stage, int k0) {
+    bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      dma16(a_src[i] + k0, base + i * 32 * kBK);
+      dma16(b_src[i] + k0, base + kT * kBK + i * 32 * kBK);
+    }
+  };
+
+  // fragments: lane reads row lane%32 of a 32-row block at K chunk
+  // kk*2 + lane/32, stored at chunk ^ ((row >> 1) & 7)
+  const int f_row = lane & 31, f_sw = (lane >> 1) & 7, f_hi = lane >> 5;
+  const int fa_row = (wm * 128 + f_row) * kBK;
+  const int fw_row = kT * kBK + (wn * 128 + f_row) * kBK;
+  bf16x8 fa[2][4], fw[2][4];
+  auto load_frags = [&](int stage, int kk, int slot) {
+    const bf16_t* base = smem + stage * kStage + (((kk * 2 + f_hi) ^ f_sw) * 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[slot][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kBK));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      fw[slot][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kBK));
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  auto mfma_step = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(fw[slot][j], fa[slot][i], acc[i][j]);
+  };
+  // issue order inside one 16-deep step: 8 x (1 MFMA, 1 fragment read
+  // [, 2 DMA loads]), then the remaining 8 MFMAs
+  auto interleave = [&](bool with_dma) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (with_dma) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);  // steps are separate scheduling regions
+  };
+
+  const int KT = K / kBK;
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  load_frags(0, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int stage = kt & 1;
+    // step 0: DMA of the next tile into the idle stage (the last iteration
+    // re-fetches the final tile, keeping the loop body one basic block)
+    issue(stage ^ 1, min(kt + 1, KT - 1) * kBK);
+    load_frags(stage, 1, 1);
+    mfma_step(0);
+    interleave(true);
+    load_frags(stage, 2, 0);
+    mfma_step(1);
+    interleave(false);
+    load_frags(stage, 3, 1);
+    mfma_step(0);
+    interleave(false);
+    // step 3: every read of this stage and the DMA of the next have completed
+    // once all waves pass the barrier; prefetch the next stage's step 0
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    load_frags(stage ^ 1, 0, 0);
+    mfma_step(1);
+    interleave(false);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // epilogue.  acc[i][j][e]: row m = i*32 + lane%32, column
+  // n = j*32 + (e/4)*8 + (lane/32)*4 + e%4 of the wave's 128x128 sub-tile.
+  bf16_t* ep = smem + wave * 128 * kEpiLd;
+  const int e_row = lane & 31, e_col = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (EPI == KAD_EPI_SWIGLU) {
+#pragma unroll
+      for (int j = 0; j < 4; j += 2) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2 packed;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            uint32_t two = 0;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const int e = g * 4 + h * 2 + q;
+              const float gv = round_bf(acc[i][j][e]);
+              const float uv = round_bf(acc[i][j + 1][e]);
+              two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+            }
+            packed[h] = two;
+          }
+          *(u32x2*)(ep + (i * 32 + e_row) * kEpiLd + (j / 2) * 32 + g * 8 + e_col) = packed;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2 packed;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            packed[h] = (uint32_t)f2bf(acc[i][j][g * 4 + h * 2]) |
+                        ((uint32_t)f2bf(acc[i][j][g * 4 + h * 2 + 1]) << 16);
+          *(u32x2*)(ep + (i * 32 + e_row) * kEpiLd + j * 32 + g * 8 + e_col) = packed;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? 64 : 128;  // wave sub-tile output columns
+  constexpr int kChunks = kCols / 8, kRowsPer = 64 / kChunks;
+  const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
+  const int out_n0 = EPI == KAD_EPI_SWIGLU ? n0 / 2 + wn * 64 : n0 + wn * 128;
+  const int n_out = EPI == KAD_EPI_SWIGLU ? N / 2 : N;
+#pragma unroll 4
+  for (int r = c_row; r < 128; r += kRowsPer) {
+    const int row = m0 + wm * 128 + r, col = out_n0 + c_col;
+    if (row >= M || col >= n_out) continue;
+    u32x4 v = *(const u32x4*)(ep + r * kEpiLd + c_col);
+    if constexpr (EPI == KAD_EPI_RESIDUAL) {
+      const u32x4 rr = *(const u32x4*)(R + (int64_t)row * ldr + col);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float lo = __uint_as_float(rr[h] << 16) + __uint_as_float(v[h] << 16);
+        const float hi = __uint_as_float(rr[h] & 0xffff0000u) + __uint_as_float(v[h] & 0xffff0000u);
+        v[h] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+      }
+    }
+    *(u32x4*)(C + (int64_t)row * ldc + col) = v;
+  }
+}
+
+template <int EPI>
+int launch256(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+              const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, kT);
+  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  static const int group = [] {
+    const char* e = getenv("KAD_GEMM_GROUP");
+    return e ? atoi(e) : 8;
+  }();
+  hipLaunchKernelGGL((gemm256_kernel<EPI>), dim3((unsigned)nblocks), dim3(256), 0, s,
+                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group);
+  return kad_launch_status("gemm256_kernel");
+}
+
+// 16-byte epilogue stores need aligned, 8-column-granular outputs
+bool vector_epilogue_ok(const void* C, int64_t ldc, const void* R, int64_t ldr, int N, int epi) {
+  const int n_out = epi == KAD_EPI_SWIGLU ? N / 2 : N;
+  bool ok = ((uintptr_t)C % 16) == 0 && ldc % 8 == 0 && n_out % 8 == 0;
+  if (epi == KAD_EPI_RESIDUAL) ok = ok && ((uintptr_t)R % 16) == 0 && ldr % 8 == 0;
+  return ok;
+}
+
 template <int BM, int BN, int WM_, int WN_, int EPI>
 int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
            const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
@@ -177,16 +416,22 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled)
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
-       CFG_256x256_8W = 5, CFG_256x128_8W = 6 };
+       CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
-    // 256x256 tiles with 8 waves (two per SIMD) when they still fill every CU;
-    // 128x128 otherwise (measured on the decode/prefill projection shapes)
+    // the pipelined 256x256 kernel when its tiles still fill every CU (and
+    // the output suits 16-byte stores); 128x128 otherwise (measured on the
+    // decode/prefill projection shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
-    cfg = M <= 64 ? CFG_32x256 : (tiles256 >= 256 ? CFG_256x256_8W : CFG_128x128);
+    if (M <= 64)
+      cfg = CFG_32x256;
+    else if (tiles256 >= 256)
+      cfg = vector_epilogue_ok(C, ldc, R, ldr, N, EPI) ? CFG_256x256_PIPE : CFG_256x256_8W;
+    else
+      cfg = CFG_128x128;
   }
   switch (cfg) {
     case CFG_32x256: return launch<32, 256, 1, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
@@ -195,6 +440,10 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_256x256: return launch<256, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_8W:
       return launch<256, 256, 2, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x256_PIPE:
+      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
+        KAD_UNSUPPORTED("tile configuration 7 needs 16-byte aligned outputs in 8-column units");
+      return launch256<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x128_8W:
       return launch<256, 128, 4, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     default: KAD_UNSUPPORTED("unknown gemm tile configuration %d", cfg);

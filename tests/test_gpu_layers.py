@@ -87,6 +87,60 @@ def test_gemm_swiglu(device):
     _bf16_ulp_close(out, ref, "gemm swiglu", min_exact=0.9)
 
 
+@pytest.mark.parametrize("epi", [layers.EPI_STORE, layers.EPI_RESIDUAL, layers.EPI_SWIGLU])
+def test_gemm_tile_configurations_agree(device, epi):
+    """Every tile configuration (including the pipelined 256x256 one) on ragged
+    M and N, a strided output and an in-place residual: bit-identical results
+    (same K order) within 1 ulp of the fp32 reference."""
+    from kadllm_amd import _lib
+    M, N, K = 600, 832, 384
+    g = torch.Generator().manual_seed(40 + epi)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    n_out = N // 2 if epi == layers.EPI_SWIGLU else N
+    x = torch.randn(M, n_out, generator=g).bfloat16()
+    ad, wd = a.to(device), w.to(device)
+    outs = {}
+    for cfg in range(1, 8):
+        c = torch.zeros(M, n_out + 16, dtype=torch.bfloat16, device=device)  # ldc > width
+        cv = c[:, :n_out]
+        if epi == layers.EPI_RESIDUAL:
+            cv.copy_(x.to(device))
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(ad), K, _lib.ptr(wd), K, _lib.ptr(cv), c.stride(0),
+                  _lib.ptr(cv) if epi == layers.EPI_RESIDUAL else None,
+                  c.stride(0) if epi == layers.EPI_RESIDUAL else 0, M, N, K, epi, cfg,
+                  _lib.stream_of(ad))
+        torch.cuda.synchronize()
+        assert (c[:, n_out:] == 0).all(), f"config {cfg} wrote past the output width"
+        outs[cfg] = cv.cpu()
+    for cfg in range(2, 8):
+        assert torch.equal(outs[cfg], outs[1]), f"config {cfg} differs from config 1"
+    prod = (a.float() @ w.float().T).bfloat16()
+    if epi == layers.EPI_STORE:
+        _bf16_ulp_close(outs[7], prod, "gemm tiles store")
+    elif epi == layers.EPI_RESIDUAL:
+        # bf16(x + bf16(acc)): the inner rounding may differ by one ulp of the
+        # product (fp32 summation order), which survives the add
+        ref = (x.float() + prod.float()).bfloat16().float()
+        tol = (ref.abs() + prod.float().abs()) * 2 ** -7 + 1e-30
+        assert ((outs[7].float() - ref).abs() <= tol).all(), "gemm tiles residual"
+        assert (outs[7].float() == ref).float().mean().item() > 0.9
+    else:
+        gu = prod.reshape(M, N // 64, 2, 32)
+        ref = (F.silu(gu[:, :, 0]) * gu[:, :, 1]).reshape(M, n_out)
+        _bf16_ulp_close(outs[7], ref, "gemm tiles swiglu", min_exact=0.9)
+
+
+def test_gemm_pipelined_tile_rejects_unaligned_output(device):
+    from kadllm_amd import _lib
+    a = torch.zeros(256, 64, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(256, 64, dtype=torch.bfloat16, device=device)
+    c = torch.zeros(256, 263, dtype=torch.bfloat16, device=device)  # ldc not a multiple of 8
+    with pytest.raises(_lib.KadLibraryError):
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), 64, _lib.ptr(w), 64, _lib.ptr(c), 263, None,
+                  0, 256, 256, 64, layers.EPI_STORE, 7, _lib.stream_of(a))
+
+
 # --------------------------------------------------------------------------
 # row-wise kernels
 
