@@ -57,15 +57,17 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
     int64_t ld_gate, uint8_t* __restrict__ ws, int T, int H, int HV, int nchunks, float scale,
     int hf_norm) {
   constexpr int LD = K + 8;
-  // the bf16 q/k rows (Gram phase) and the fp32 A / T' matrices (solve phase)
-  // share one LDS region
+  constexpr int CPR = K / 8;       // 16-byte chunks per q/k row
+  constexpr int RPI = 64 / CPR;    // rows per wave instruction
+  // the bf16 q/k rows (Gram phase) and, later, A in residue-major order plus
+  // the T' staging tile share one LDS region
   constexpr size_t kRows = 2 * kC * LD * sizeof(bf16_t);
-  constexpr size_t kMats = 2 * kC * (kC + 1) * sizeof(float);
+  constexpr size_t kMats = (kC * kC + kC * (kC + 1)) * sizeof(float);
   __shared__ __attribute__((aligned(16))) unsigned char region[kRows > kMats ? kRows : kMats];
   bf16_t* kb = (bf16_t*)region;
   bf16_t* qb = kb + kC * LD;
-  float(*Am)[kC + 1] = (float(*)[kC + 1])region;
-  float(*Tm)[kC + 1] = Am + kC;
+  float* Ar = (float*)region;                         // Ar[i*64 + (j%4)*16 + j/4] = A[i][j]
+  float(*Tm)[kC + 1] = (float(*)[kC + 1])(Ar + kC * kC);
   __shared__ float Gs[kC], bt[kC], kmul[kC], qmul[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -77,48 +79,65 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   const int nt = min(kC, T - t0);
   uint8_t* rec = ws + (size_t)blockIdx.x * ChunkRec<K>::bytes;
 
-  // ---- rows: normalise and stage (one wave per row at a time)
-  for (int i = wave; i < kC; i += kPrepThreads / 64) {
-    float kv[K / 64], qv[K / 64];
-    const bool live = i < nt;
-    const int64_t row = ((int64_t)n * T + t0 + (live ? i : 0)) * ld_qk + (int64_t)h * K;
-    float kss = 0.f, qss = 0.f;
+  // ---- rows: wave w normalises rows 16w..16w+15, RPI rows per instruction
+  // (lane -> row lane / CPR, 16-byte chunk lane % CPR)
+  {
+    const int rsub = lane / CPR, ch = lane % CPR;
 #pragma unroll
-    for (int e = 0; e < K / 64; ++e) {
-      kv[e] = live ? bf2f(k[row + lane + 64 * e]) : 0.f;
-      qv[e] = live ? bf2f(q[row + lane + 64 * e]) : 0.f;
-      kss += hf_norm ? round_bf(kv[e] * kv[e]) : kv[e] * kv[e];
-      qss += hf_norm ? round_bf(qv[e] * qv[e]) : qv[e] * qv[e];
-    }
-    kss = wave_sum(kss);
-    qss = wave_sum(qss);
-    float km, qm;
-    if (hf_norm) {
-      // transformers l2norm in bf16: x * rsqrt(sum(x*x) + eps), each op rounded
-      const float kr = round_bf(1.0f / sqrtf(round_bf(round_bf(kss) + 1e-6f)));
-      const float qr = round_bf(1.0f / sqrtf(round_bf(round_bf(qss) + 1e-6f)));
+    for (int it = 0; it < 16 / RPI; ++it) {
+      const int i = wave * 16 + it * RPI + rsub;
+      const bool live = i < nt;
+      const int64_t off = ((int64_t)n * T + t0 + (live ? i : 0)) * ld_qk + (int64_t)h * K + ch * 8;
+      u32x4 kr = live ? *(const u32x4*)(k + off) : u32x4{0, 0, 0, 0};
+      u32x4 qr = live ? *(const u32x4*)(q + off) : u32x4{0, 0, 0, 0};
+      float kv[8], qv[8];
 #pragma unroll
-      for (int e = 0; e < K / 64; ++e) {
-        kv[e] = round_bf(kv[e] * kr);
-        qv[e] = round_bf(qv[e] * qr);
+      for (int e = 0; e < 4; ++e) {
+        kv[2 * e] = __uint_as_float(kr[e] << 16);
+        kv[2 * e + 1] = __uint_as_float(kr[e] & 0xffff0000u);
+        qv[2 * e] = __uint_as_float(qr[e] << 16);
+        qv[2 * e + 1] = __uint_as_float(qr[e] & 0xffff0000u);
       }
-      km = 1.f;
-      qm = scale;
-    } else {
-      km = 1.0f / sqrtf(kss + 1e-6f);
-      qm = scale / sqrtf(qss + 1e-6f);
-    }
+      float kss = 0.f, qss = 0.f;
 #pragma unroll
-    for (int e = 0; e < K / 64; ++e) {
-      const bf16_t kbits = f2bf(kv[e]), qbits = f2bf(qv[e]);
-      kb[i * LD + lane + 64 * e] = kbits;
-      qb[i * LD + lane + 64 * e] = qbits;
-      ((bf16_t*)(rec + ChunkRec<K>::kn))[i * K + lane + 64 * e] = kbits;
-      ((bf16_t*)(rec + ChunkRec<K>::qn))[i * K + lane + 64 * e] = qbits;
-    }
-    if (lane == 0) {
-      kmul[i] = km;
-      qmul[i] = qm;
+      for (int e = 0; e < 8; ++e) {
+        kss += hf_norm ? round_bf(kv[e] * kv[e]) : kv[e] * kv[e];
+        qss += hf_norm ? round_bf(qv[e] * qv[e]) : qv[e] * qv[e];
+      }
+#pragma unroll
+      for (int o = CPR / 2; o > 0; o >>= 1) {
+        kss += __shfl_xor(kss, o, 64);
+        qss += __shfl_xor(qss, o, 64);
+      }
+      float km, qm;
+      if (hf_norm) {
+        // transformers l2norm in bf16: x * rsqrt(sum(x*x) + eps), each op rounded
+        const float krs = round_bf(1.0f / sqrtf(round_bf(round_bf(kss) + 1e-6f)));
+        const float qrs = round_bf(1.0f / sqrtf(round_bf(round_bf(qss) + 1e-6f)));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          kv[e] = round_bf(kv[e] * krs);
+          qv[e] = round_bf(qv[e] * qrs);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kr[e] = (uint32_t)f2bf(kv[2 * e]) | ((uint32_t)f2bf(kv[2 * e + 1]) << 16);
+          qr[e] = (uint32_t)f2bf(qv[2 * e]) | ((uint32_t)f2bf(qv[2 * e + 1]) << 16);
+        }
+        km = 1.f;
+        qm = scale;
+      } else {
+        km = 1.0f / sqrtf(kss + 1e-6f);
+        qm = scale / sqrtf(qss + 1e-6f);
+      }
+      *(u32x4*)(kb + i * LD + ch * 8) = kr;
+      *(u32x4*)(qb + i * LD + ch * 8) = qr;
+      *(u32x4*)((bf16_t*)(rec + ChunkRec<K>::kn) + i * K + ch * 8) = kr;
+      *(u32x4*)((bf16_t*)(rec + ChunkRec<K>::qn) + i * K + ch * 8) = qr;
+      if (ch == 0) {
+        kmul[i] = km;
+        qmul[i] = qm;
+      }
     }
   }
   if (tid < kC) {
@@ -189,34 +208,72 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
       for (int e = 0; e < 16; ++e) {
         const int i = ti * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
         const int j = tj * 32 + (lane & 31);
-        Am[i][j] = j < i ? -bt[i] * (gram[tt][e] * kmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
+        Ar[i * kC + (j & 3) * 16 + (j >> 2)] =
+            j < i ? -bt[i] * (gram[tt][e] * kmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
       }
     }
   }
   __syncthreads();
 
-  // ---- forward substitution: T'[i][j] = A[i][j] + sum_{j<m<i} A[i][m] T'[m][j]
-  if (tid < kC) Tm[0][tid] = 0.f;
-  for (int i = 1; i < kC; ++i) {
-    __syncthreads();
-    if (tid < i) {
-      float acc = Am[i][tid];
-      for (int m = tid + 1; m < i; ++m) acc += Am[i][m] * Tm[m][tid];
-      Tm[i][tid] = acc;
-    } else if (tid < kC) {
-      Tm[i][tid] = 0.f;
+  // ---- forward substitution T'[i][j] = A[i][j] + sum_{m<i} A[i][m] T'[m][j]
+  // (A strictly lower).  Columns are independent: wave w owns columns
+  // 16w..16w+15 with 4 lanes per column; lane r of column j keeps rows
+  // m = 4q + r (q < 16) of the column in registers.  Rows not yet computed are
+  // zero, so each row needs no masking; no barriers are involved.
+  {
+    const int col = wave * 16 + (lane >> 2), r = lane & 3;
+    float treg[16];
+#pragma unroll
+    for (int qq = 0; qq < 16; ++qq) treg[qq] = 0.f;
+#pragma unroll
+    for (int i = 1; i < kC; ++i) {
+      constexpr int kMaxQ = 16;
+      const int nq = (i + 3) / 4;  // q < nq covers every m < i of residue r
+      const float* arow = Ar + i * kC + r * 16;
+      float part = 0.f;
+#pragma unroll
+      for (int q4 = 0; q4 < kMaxQ / 4; ++q4) {
+        if (q4 * 4 >= nq) break;
+        const float4 av = *(const float4*)(arow + q4 * 4);
+        part += av.x * treg[q4 * 4];
+        if (q4 * 4 + 1 < nq) part += av.y * treg[q4 * 4 + 1];
+        if (q4 * 4 + 2 < nq) part += av.z * treg[q4 * 4 + 2];
+        if (q4 * 4 + 3 < nq) part += av.w * treg[q4 * 4 + 3];
+      }
+      part += __shfl_xor(part, 1, 64);
+      part += __shfl_xor(part, 2, 64);
+      const float val = Ar[i * kC + (col & 3) * 16 + (col >> 2)] + part;
+      if (r == (i & 3)) treg[i >> 2] = val;
     }
+#pragma unroll
+    for (int qq = 0; qq < 16; ++qq) Tm[qq * 4 + r][col] = treg[qq];
   }
   __syncthreads();
 
-  // ---- T' as bf16 hi/lo planes
-  bf16_t* thi = (bf16_t*)(rec + ChunkRec<K>::thi);
-  bf16_t* tlo = (bf16_t*)(rec + ChunkRec<K>::tlo);
-  for (int e = tid; e < kC * kC; e += kPrepThreads) {
-    const float tv = Tm[e / kC][e % kC];
-    const bf16_t th = f2bf(tv);
-    thi[e] = th;
-    tlo[e] = f2bf(tv - bf2f(th));
+  // ---- T' as bf16 hi/lo planes, 16 elements (32 bytes per plane) per thread
+  {
+    bf16_t* thi = (bf16_t*)(rec + ChunkRec<K>::thi);
+    bf16_t* tlo = (bf16_t*)(rec + ChunkRec<K>::tlo);
+    const int i = tid >> 2, j0 = (tid & 3) * 16;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      u32x4 hv4, lv4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t hw = 0, lw = 0;
+#pragma unroll
+        for (int b2 = 0; b2 < 2; ++b2) {
+          const float tv = Tm[i][j0 + half * 8 + e * 2 + b2];
+          const bf16_t th = f2bf(tv);
+          hw |= (uint32_t)th << (16 * b2);
+          lw |= (uint32_t)f2bf(tv - bf2f(th)) << (16 * b2);
+        }
+        hv4[e] = hw;
+        lv4[e] = lw;
+      }
+      *(u32x4*)(thi + i * kC + j0 + half * 8) = hv4;
+      *(u32x4*)(tlo + i * kC + j0 + half * 8) = lv4;
+    }
   }
 }
 
@@ -484,6 +541,8 @@ extern "C" int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_
                   ld_gate >= HV,
               "row strides smaller than a row");
   KAD_REQUIRE(ld_v % 8 == 0 && ((uintptr_t)v % 16) == 0, "v rows must be 16-byte aligned");
+  KAD_REQUIRE(ld_qk % 8 == 0 && ((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0,
+              "q and k rows must be 16-byte aligned");
   if (qkv_dtype != KAD_DTYPE_BF16) KAD_UNSUPPORTED("chunked gated delta takes bf16 q/k/v");
   if (!((K == 64 || K == 128) && (V == 64 || V == 128)))
     KAD_UNSUPPORTED("chunked gated delta supports K, V in {64, 128}; got K=%d V=%d", K, V);
