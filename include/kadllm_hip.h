@@ -105,8 +105,8 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
  * kad_gemm_bf16; 1 = 32x256, 2 = 128x128, 3 = 128x256, 4 = 256x256 with 4
  * waves; 5 = 256x256 and 6 = 256x128 with 8 waves; 7 = 256x256 with 4 waves,
  * fragment double-buffering and a 16-byte store epilogue, which needs 16-byte
- * aligned C (and R) with ldc, ldr and the output width multiples of 8), for
- * tuning. */
+ * aligned C (and R) with ldc, ldr and the output width multiples of 8; 8 = the
+ * same with register-staged instead of direct-to-LDS loads), for tuning. */
 int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
                         int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                         int epilogue, int tile_config, kad_stream_t stream);

@@ -194,7 +194,10 @@ __device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
   __builtin_amdgcn_global_load_lds((global_void_t*)g, (lds_void_t*)lds_block, 16, 0, 0);
 }
 
-template <int EPI>
+// DMA = false: the same tile flow with the loads staged through registers
+// (global_load_dwordx4 in step 0, ds_write_b128 in step 2 to the same
+// swizzled positions).
+template <int EPI, bool DMA>
 __global__ __launch_bounds__(256, 1) void gemm256_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
     bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
@@ -234,6 +237,22 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
     for (int i = 0; i < 8; ++i) {
       dma16(a_src[i] + k0, base + i * 32 * kBK);
       dma16(b_src[i] + k0, base + kT * kBK + i * 32 * kBK);
+    }
+  };
+  u32x4 ra[DMA ? 1 : 8], rb[DMA ? 1 : 8];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
+      ra[i] = *(const u32x4*)(a_src[i] + k0);
+      rb[i] = *(const u32x4*)(b_src[i] + k0);
+    }
+  };
+  auto stash = [&](int stage) {
+    bf16_t* base = smem + stage * kStage + wave * 8 * kBK + lane * 8;
+#pragma unroll
+    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
+      *(u32x4*)(base + i * 32 * kBK) = ra[i];
+      *(u32x4*)(base + kT * kBK + i * 32 * kBK) = rb[i];
     }
   };
 
@@ -278,17 +297,38 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
     __builtin_amdgcn_sched_barrier(0);  // steps are separate scheduling regions
   };
 
+  // issue order inside one 16-deep step with LDS writes: 8 x (1 MFMA, 1
+  // fragment read, 2 LDS writes), then the remaining 8 MFMAs
+  auto interleave_stash = [&]() {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
   const int KT = K / kBK;
-  issue(0, 0);
+  if constexpr (DMA) {
+    issue(0, 0);
+  } else {
+    fetch(0);
+    stash(0);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   load_frags(0, 0, 0);
   for (int kt = 0; kt < KT; ++kt) {
     __builtin_amdgcn_sched_barrier(0);
     const int stage = kt & 1;
-    // step 0: DMA of the next tile into the idle stage (the last iteration
-    // re-fetches the final tile, keeping the loop body one basic block)
-    issue(stage ^ 1, min(kt + 1, KT - 1) * kBK);
+    // step 0: loads of the next tile (the last iteration re-fetches the final
+    // tile, keeping the loop body one basic block)
+    if constexpr (DMA)
+      issue(stage ^ 1, min(kt + 1, KT - 1) * kBK);
+    else
+      fetch(min(kt + 1, KT - 1) * kBK);
     load_frags(stage, 1, 1);
     mfma_step(0);
     interleave(true);
@@ -296,10 +336,15 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
     mfma_step(1);
     interleave(false);
     load_frags(stage, 3, 1);
+    if constexpr (!DMA) stash(stage ^ 1);  // nobody reads the idle stage
     mfma_step(0);
-    interleave(false);
-    // step 3: every read of this stage and the DMA of the next have completed
-    // once all waves pass the barrier; prefetch the next stage's step 0
+    if constexpr (DMA)
+      interleave(false);
+    else
+      interleave_stash();
+    // step 3: every read of this stage and the next tile's writes have
+    // completed once all waves pass the barrier; prefetch the next stage's
+    // step 0
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     load_frags(stage ^ 1, 0, 0);
@@ -377,7 +422,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
 
 template <int EPI>
 int launch256(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-              const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+              const void* R, int64_t ldr, int M, int N, int K, bool dma, hipStream_t s) {
   const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, kT);
   if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
   const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
@@ -385,7 +430,13 @@ int launch256(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, i
     const char* e = getenv("KAD_GEMM_GROUP");
     return e ? atoi(e) : 8;
   }();
-  hipLaunchKernelGGL((gemm256_kernel<EPI>), dim3((unsigned)nblocks), dim3(256), 0, s,
+  if (!dma) {
+    hipLaunchKernelGGL((gemm256_kernel<EPI, false>), dim3((unsigned)nblocks), dim3(256), 0, s,
+                       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                       (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group);
+    return kad_launch_status("gemm256_kernel");
+  }
+  hipLaunchKernelGGL((gemm256_kernel<EPI, true>), dim3((unsigned)nblocks), dim3(256), 0, s,
                      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
                      (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group);
   return kad_launch_status("gemm256_kernel");
@@ -416,7 +467,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled)
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
-       CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7 };
+       CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
@@ -443,7 +494,11 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_256x256_PIPE:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration 7 needs 16-byte aligned outputs in 8-column units");
-      return launch256<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return launch256<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, true, s);
+    case CFG_256x256_PIPE_REG:
+      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
+        KAD_UNSUPPORTED("tile configuration 8 needs 16-byte aligned outputs in 8-column units");
+      return launch256<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, false, s);
     case CFG_256x128_8W:
       return launch<256, 128, 4, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     default: KAD_UNSUPPORTED("unknown gemm tile configuration %d", cfg);

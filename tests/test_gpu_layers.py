@@ -101,7 +101,7 @@ def test_gemm_tile_configurations_agree(device, epi):
     x = torch.randn(M, n_out, generator=g).bfloat16()
     ad, wd = a.to(device), w.to(device)
     outs = {}
-    for cfg in range(1, 8):
+    for cfg in range(1, 9):
         c = torch.zeros(M, n_out + 16, dtype=torch.bfloat16, device=device)  # ldc > width
         cv = c[:, :n_out]
         if epi == layers.EPI_RESIDUAL:
@@ -113,7 +113,7 @@ def test_gemm_tile_configurations_agree(device, epi):
         torch.cuda.synchronize()
         assert (c[:, n_out:] == 0).all(), f"config {cfg} wrote past the output width"
         outs[cfg] = cv.cpu()
-    for cfg in range(2, 8):
+    for cfg in range(2, 9):
         assert torch.equal(outs[cfg], outs[1]), f"config {cfg} differs from config 1"
     prod = (a.float() @ w.float().T).bfloat16()
     if epi == layers.EPI_STORE:
