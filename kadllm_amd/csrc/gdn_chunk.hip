@@ -340,37 +340,76 @@ __global__ __launch_bounds__(V * 2) void gdn_chunk_scan(
     const uint8_t* rec = ws + ((size_t)blockIdx.x * nchunks + c) * ChunkRec<K>::bytes;
     __syncthreads();  // previous chunk done with LDS
     {
+      // every global load of the chunk is issued before any LDS store, so the
+      // load latency is paid once per chunk
+      constexpr int kRowV = kC * K / 8 / NTH;       // q/k 16-byte chunks per thread
+      constexpr int kPlaneV = kC * kC / 8 / NTH;    // T'/In plane chunks per thread
+      constexpr int kVV = kC * V / 8 / NTH;         // v chunks per thread
+      static_assert(kRowV * NTH * 8 == kC * K && kPlaneV * NTH * 8 == kC * kC &&
+                        kVV * NTH * 8 == kC * V, "chunk tiles must split evenly");
       const bf16_t* kn = (const bf16_t*)(rec + ChunkRec<K>::kn);
       const bf16_t* qn = (const bf16_t*)(rec + ChunkRec<K>::qn);
-      for (int e = tid; e < kC * K / 8; e += NTH) {
-        const int i = e / (K / 8), k8 = (e % (K / 8)) * 8;
-        const u32x4 kr = *(const u32x4*)(kn + i * K + k8);
-        *(u32x4*)(kb + i * LDK + k8) = kr;
-        *(u32x4*)(qb + i * LDK + k8) = *(const u32x4*)(qn + i * K + k8);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          kbT[(k8 + 2 * w) * LD64 + i] = (bf16_t)(kr[w] & 0xffffu);
-          kbT[(k8 + 2 * w + 1) * LD64 + i] = (bf16_t)(kr[w] >> 16);
-        }
-      }
       const bf16_t* planes[4] = {(const bf16_t*)(rec + ChunkRec<K>::thi),
                                  (const bf16_t*)(rec + ChunkRec<K>::tlo),
                                  (const bf16_t*)(rec + ChunkRec<K>::ihi),
                                  (const bf16_t*)(rec + ChunkRec<K>::ilo)};
+      u32x4 rk[kRowV], rq[kRowV], rp[4][kPlaneV], rv[kVV];
+#pragma unroll
+      for (int u = 0; u < kRowV; ++u) {
+        const int e = tid + u * NTH;
+        rk[u] = *(const u32x4*)(kn + e * 8);
+        rq[u] = *(const u32x4*)(qn + e * 8);
+      }
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int u = 0; u < kPlaneV; ++u) rp[p][u] = *(const u32x4*)(planes[p] + (tid + u * NTH) * 8);
+#pragma unroll
+      for (int u = 0; u < kVV; ++u) {
+        const int e = tid + u * NTH;
+        const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
+        rv[u] = i < nt ? *(const u32x4*)(v + ((int64_t)n * T + t0 + i) * ld_v + (int64_t)hv * V + v8)
+                       : u32x4{0u, 0u, 0u, 0u};
+      }
+      const float* scg = (const float*)(rec + ChunkRec<K>::scal);
+      float rs[(5 * kC + NTH - 1) / NTH];
+#pragma unroll
+      for (int u = 0; u < (5 * kC + NTH - 1) / NTH; ++u) {
+        const int e = tid + u * NTH;
+        rs[u] = e < 5 * kC ? scg[e] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kRowV; ++u) {
+        const int e = tid + u * NTH;
+        const int i = e / (K / 8), k8 = (e % (K / 8)) * 8;
+        *(u32x4*)(kb + i * LDK + k8) = rk[u];
+        *(u32x4*)(qb + i * LDK + k8) = rq[u];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          kbT[(k8 + 2 * w) * LD64 + i] = (bf16_t)(rk[u][w] & 0xffffu);
+          kbT[(k8 + 2 * w + 1) * LD64 + i] = (bf16_t)(rk[u][w] >> 16);
+        }
+      }
       bf16_t* dsts[4] = {Th, Tl, Ih, Il};
 #pragma unroll
       for (int p = 0; p < 4; ++p)
-        for (int e = tid; e < kC * kC / 4; e += NTH) {
-          const int i = e / (kC / 4), j4 = (e % (kC / 4)) * 4;
-          *(u32x2*)(dsts[p] + i * LD64 + j4) = *(const u32x2*)(planes[p] + i * kC + j4);
+#pragma unroll
+        for (int u = 0; u < kPlaneV; ++u) {
+          const int e = tid + u * NTH;
+          const int i = e / (kC / 8), j8 = (e % (kC / 8)) * 8;
+          *(u32x2*)(dsts[p] + i * LD64 + j8) = u32x2{rp[p][u][0], rp[p][u][1]};
+          *(u32x2*)(dsts[p] + i * LD64 + j8 + 4) = u32x2{rp[p][u][2], rp[p][u][3]};
         }
-      const float* scg = (const float*)(rec + ChunkRec<K>::scal);
-      for (int e = tid; e < 5 * kC; e += NTH) sc[e / kC][e % kC] = scg[e];
-      for (int e = tid; e < kC * V / 8; e += NTH) {
+#pragma unroll
+      for (int u = 0; u < kVV; ++u) {
+        const int e = tid + u * NTH;
         const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (i < nt) val = *(const u32x4*)(v + ((int64_t)n * T + t0 + i) * ld_v + (int64_t)hv * V + v8);
-        *(u32x4*)(vb + i * (V + 8) + v8) = val;
+        *(u32x4*)(vb + i * (V + 8) + v8) = rv[u];
+      }
+#pragma unroll
+      for (int u = 0; u < (5 * kC + NTH - 1) / NTH; ++u) {
+        const int e = tid + u * NTH;
+        if (e < 5 * kC) sc[e / kC][e % kC] = rs[u];
       }
     }
     __syncthreads();
