@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
     float* __restrict__ cand_key, int* __restrict__ cand_idx, int line_stride, int rank) {
   __shared__ __attribute__((aligned(16))) uint64_t cand[kCandCap];
   __shared__ int hist[256];
-  __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64];
+  __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64], red_smax[kRowThreads / 64];
   __shared__ int sh_count, sh_hi, sh_above, sh_thr;
   uint16_t* samples = (uint16_t*)cand;
   const int tid = threadIdx.x;
@@ -242,12 +242,20 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   hist[tid] = 0;
   if (tid == 0) sh_count = 0;
   __syncthreads();
+  float smax = -INFINITY;  // max sampled logit (masked or not): the sum's start
   for (int s = tid; s < ns; s += kRowThreads) {
     const int c = (s / kLine) * line_stride * kLine + (s % kLine);
-    const uint32_t k = c < V ? key_of(x[c], c) : 0u;
+    uint32_t k = 0u;
+    if (c < V) {
+      const uint16_t bits = x[c];
+      k = key_of(bits, c);
+      smax = fmaxf(smax, bf2f(bits));
+    }
     samples[s] = (uint16_t)k;
     atomicAdd(&hist[k >> 8], 1);
   }
+  smax = wave_max(smax);
+  if ((tid & 63) == 0) red_smax[tid >> 6] = smax;
   __syncthreads();
   if (tid < 64) {
     int above = 0;
@@ -301,20 +309,28 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   __syncthreads();
   const uint32_t thr = (uint32_t)sh_thr;
 
-  // ---- 2. max, online sum exp, and candidates >= thr in one pass
+  // ---- 2. max, online sum exp, and candidates >= thr in one pass.  The sum
+  // starts from the sample max, so the rescaling branch is rare; terms use the
+  // hardware exp2 (exp(x) = 2^(x log2 e)); candidates are screened with a float
+  // compare against the threshold's value and confirmed on the order key.
   float m = -INFINITY, se = 0.f;
+  for (int w = 0; w < kRowThreads / 64; ++w) m = fmaxf(m, red_smax[w]);
+  const uint32_t tb = thr & 0x8000u ? (thr & 0x7fffu) : (~thr & 0xffffu);
+  const float tf = thr > 0 ? bf2f((uint16_t)tb) : INFINITY;
   auto visit = [&](uint16_t bits, int c, bool ok) {
     const float v = bf2f(bits);
     if (v > m) {
-      se = (m == -INFINITY ? 0.f : se * expf(m - v)) + 1.f;
+      se = (m == -INFINITY ? 0.f : se * __expf(m - v)) + 1.f;
       m = v;
     } else if (v != -INFINITY) {
-      se += expf(v - m);
+      se += __expf(v - m);
     }
-    const uint32_t u = ok ? order16(bits) : 0u;
-    if (thr > 0 && u >= thr) {
-      const int slot = atomicAdd(&sh_count, 1);
-      if (slot < kCandCap) cand[slot] = ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
+    if (v >= tf && ok) {
+      const uint32_t u = order16(bits);
+      if (u >= thr) {
+        const int slot = atomicAdd(&sh_count, 1);
+        if (slot < kCandCap) cand[slot] = ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
+      }
     }
   };
   const int V8 = vec ? V / 8 : 0;

@@ -27,7 +27,7 @@
 
 namespace {
 
-constexpr int kTMax = 4;
+constexpr int kTLimit = 4;  // longest suffix the replay handles
 
 template <typename TIN>
 struct QKFrag;
@@ -92,7 +92,7 @@ __device__ __forceinline__ void store4<float>(float* p, const float* f) {
   *(f32x4*)p = r;
 }
 
-template <int KD, int VD, typename TIN>
+template <int KD, int VD, typename TIN, int kTMax>
 __global__ __launch_bounds__(256) void gdn_replay_kernel(
     const TIN* __restrict__ q, const TIN* __restrict__ k, const TIN* __restrict__ v,
     int64_t ld_qk, int64_t ld_v, const void* __restrict__ gdecay, int gate_dtype,
@@ -288,11 +288,23 @@ int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, in
     kad_set_error("gdn replay grid too large");
     return KAD_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((gdn_replay_kernel<KD, VD, TIN>), dim3((unsigned)nblocks), dim3(256), 0,
-                     stream, (const TIN*)q, (const TIN*)k, (const TIN*)v, ld_qk, ld_v, g, gdt,
-                     beta, bdt, ld_gate, state, sdt, (TIN*)out, ld_out, W, T, H, HV, scale,
-                     bpb, nbb);
-  return kad_launch_status("gdn_replay_kernel");
+  // one instantiation per suffix length: the per-token arrays then hold only
+  // T entries, which keeps the register count (and so the occupancy) down
+#define KAD_REPLAY_T(TT)                                                                      \
+  if (T == TT) {                                                                              \
+    hipLaunchKernelGGL((gdn_replay_kernel<KD, VD, TIN, TT>), dim3((unsigned)nblocks),          \
+                       dim3(256), 0, stream, (const TIN*)q, (const TIN*)k, (const TIN*)v,     \
+                       ld_qk, ld_v, g, gdt, beta, bdt, ld_gate, state, sdt, (TIN*)out, ld_out, \
+                       W, T, H, HV, scale, bpb, nbb);                                         \
+    return kad_launch_status("gdn_replay_kernel");                                            \
+  }
+  KAD_REPLAY_T(1)
+  KAD_REPLAY_T(2)
+  KAD_REPLAY_T(3)
+  KAD_REPLAY_T(4)
+#undef KAD_REPLAY_T
+  kad_set_error("gdn replay supports suffixes of 1..%d tokens, got %d", kTLimit, T);
+  return KAD_ERR_UNSUPPORTED;
 }
 
 template <typename TIN>
@@ -332,7 +344,7 @@ extern "C" int kad_gdn_suffix_replay(const void* q, const void* k, const void* v
               "q/k row stride must be a multiple of 8 and v/out of 4 elements");
   KAD_REQUIRE(((uintptr_t)q | (uintptr_t)k) % 16 == 0 && ((uintptr_t)v | (uintptr_t)out) % 8 == 0,
               "q/k must be 16-byte and v/out 8-byte aligned");
-  if (T > kTMax) KAD_UNSUPPORTED("gdn replay supports T <= %d suffix tokens, got %d", kTMax, T);
+  if (T > kTLimit) KAD_UNSUPPORTED("gdn replay supports T <= %d suffix tokens, got %d", kTLimit, T);
   for (int dt : {gate_dtype, beta_dtype, state_dtype})
     KAD_REQUIRE(dt == KAD_DTYPE_BF16 || dt == KAD_DTYPE_F16 || dt == KAD_DTYPE_F32,
                 "unknown dtype code %d", dt);
