@@ -171,6 +171,20 @@ int kad_prefix_attention_decode(
     int64_t ssv_t, int64_t ssv_h, const void* prefix_mask, const void* gate, int64_t sg_n,
     int64_t sg_t, int64_t sg_h, void* out, int64_t so_n, int64_t so_t, int64_t so_h, int B,
     int W, int T, int H, int HK, int L, int D, float scale, kad_stream_t stream);
+/* The same for queries that are only the last Tq of a beam's Tk suffix tokens
+ * (q/gate/out [B*W, Tq, H, D], suffix_k/v [B*W, Tk, HK, D]): query t sees
+ * suffix keys j <= t + Tk - Tq.  Each query row's arithmetic is exactly that
+ * of kad_prefix_attention_decode with T = Tk, which lets a level that extends
+ * cached suffixes by one token (src/kadllm/grbeam.py:76-77, where the
+ * reference replays the whole suffix, src/kadllm/adapters/qwen3_5.py:216) skip
+ * the queries of the cached tokens.  Tq <= Tk <= 4. */
+int kad_prefix_attention_decode_ex(
+    const void* q, int64_t sq_n, int64_t sq_t, int64_t sq_h, const void* prefix_k,
+    const void* prefix_v, int64_t sp_b, int64_t sp_l, int64_t sp_h, const void* suffix_k,
+    int64_t ssk_n, int64_t ssk_t, int64_t ssk_h, const void* suffix_v, int64_t ssv_n,
+    int64_t ssv_t, int64_t ssv_h, const void* prefix_mask, const void* gate, int64_t sg_n,
+    int64_t sg_t, int64_t sg_h, void* out, int64_t so_n, int64_t so_t, int64_t so_h, int B,
+    int W, int Tq, int Tk, int H, int HK, int L, int D, float scale, kad_stream_t stream);
 
 /* Causal gated GQA attention over full prompts (prefill).  Replaces the
  * causal SDPA of the transformers forward that the reference prefill runs
@@ -209,6 +223,16 @@ int kad_beam_merge_select(const float* cand_key, const int* cand_idx, int B, int
                           kad_stream_t stream);
 int kad_beam_history(const int64_t* history, int Wp, int step, const int64_t* parents,
                      const int64_t* tokens, int64_t* out, int B, int W, kad_stream_t stream);
+/* Per-token rows cached for a level's beams follow the beams' parents into the
+ * next level: for beam n = b * W + w and t < rows_copy, dst row
+ * n * dst_rows_per_beam + t = src row (b * Wp + parents[n]) * src_rows_per_beam
+ * + t (row_bytes each, byte strides ld_*; 16-byte aligned; parents clamped to
+ * [0, Wp)).  Serves the suffix dedup across levels: the reference recomputes
+ * these rows (src/kadllm/adapters/qwen3_5.py:216, README.md:252). */
+int kad_gather_beam_rows(const void* src, int64_t ld_src_bytes, int src_rows_per_beam, void* dst,
+                         int64_t ld_dst_bytes, int dst_rows_per_beam, int rows_copy,
+                         int64_t row_bytes, const int64_t* parents, int B, int W, int Wp,
+                         kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
  * Chunked gated delta rule over sequences (chunks of 64 tokens).

@@ -38,10 +38,13 @@ SIGNATURES = {
     "kad_scatter_heads": "pliipllllls",
     "kad_embedding": "ppplils",
     "kad_prefix_attention_decode": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiii" "f" "s",
+    "kad_prefix_attention_decode_ex": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiiii" "f"
+                                      "s",
     "kad_attention_prefill": "plll" "pplll" "plll" "plll" "iiiii" "f" "s",
     "kad_beam_row_select": "plplpiiiipps",
     "kad_beam_merge_select": "ppiiiipppps",
     "kad_beam_history": "piipppiis",
+    "kad_gather_beam_rows": "pli" "pli" "i" "l" "p" "iii" "s",
     "kad_gdn_chunk_workspace_bytes": "iiiip",
     "kad_gdn_chunk": "ppplli" "pipil" "pii" "plp" "pl" "iiiiii" "fi" "s",
     "kad_causal_conv_prefill": "plpplpiiiis",

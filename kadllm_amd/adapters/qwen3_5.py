@@ -120,6 +120,29 @@ class Qwen35GRBeamAdapter:
             raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
         return self._runner.decode(history, state.layers, state.length)
 
+    @torch.no_grad()
+    def decode_incremental(self, history, parents, state, cache=None):
+        """decode(history, state) for a level whose beams extend the previous
+        level's beams by one token: history[b, w] = history_prev[b, parents[b, w]]
+        followed by one new token.  ``cache`` is what the previous call returned
+        (None for the first decode level).  Returns (logits, cache); the logits
+        equal decode(history, state) while only the new token goes through the
+        projections.  grbeam_search uses it when the adapter offers it."""
+        self._check(history)
+        if not isinstance(state, Qwen35Prefix) or state.owner is not self._owner:
+            raise ValueError("prefix belongs to a different adapter")
+        if history.ndim != 3 or min(history.shape) < 1 or history.shape[0] != state.batch:
+            raise ValueError("history must be nonempty [B,W,T] matching the prefix")
+        T = history.shape[2]
+        if (cache is None and T != 1) or (cache is not None and T != cache.T + 1):
+            raise ValueError("history must extend the cached suffixes by exactly one token")
+        if history.shape[2] > 4:
+            raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
+        if cache is not None and (parents.shape != history.shape[:2] or parents.device != history.device):
+            raise ValueError("parents must be [B, W] on the history's device")
+        tokens = history[:, :, -1].contiguous()
+        return self._runner.decode_step(tokens, parents, state.layers, state.length, cache)
+
 
 def native_model(cfg, state_dict):
     """(Qwen35TextModel, LMHead) for a state dict in transformers naming."""

@@ -15,13 +15,15 @@ def _inner_contiguous(t):
 def prefix_attention_decode(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_width, prefix_mask,
                             scale, gate=None, out=None, gate_strides=None):
     """q [B*W,T,H,D]; prefix K/V [B,L,HK,D] (strided views allowed); suffix K/V
-    [B*W,T,HK,D]; optional bool prefix_mask [B,L]; optional gate [B*W,T,H*D]
-    (output multiplied by sigmoid(gate)), or any tensor whose data pointer is
-    head 0's gate with element strides ``gate_strides`` = (beam, token, head).
-    Returns [B*W,T,H,D] bf16."""
+    [B*W,Tk,HK,D] with Tk >= T (the queries are the last T of the Tk suffix
+    tokens; Tk = T is the reference operator); optional bool prefix_mask [B,L];
+    optional gate [B*W,T,H*D] (output multiplied by sigmoid(gate)), or any
+    tensor whose data pointer is head 0's gate with element strides
+    ``gate_strides`` = (beam, token, head).  Returns [B*W,T,H,D] bf16."""
     if q.dtype != torch.bfloat16:
         raise RuntimeError("HIP prefix attention supports bf16 inputs")
     BW, T, H, D = q.shape
+    Tk = suffix_k.shape[1]
     B, L, HK, _ = prefix_k.shape
     q = _inner_contiguous(q)
     suffix_k = _inner_contiguous(suffix_k)
@@ -48,11 +50,11 @@ def prefix_attention_decode(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_widt
     if out is None:
         out = torch.empty(BW, T, H, D, dtype=q.dtype, device=q.device)
     pk_strides = (prefix_k.stride(0), prefix_k.stride(1), prefix_k.stride(2)) if L else (0, 0, 0)
-    _lib.call("kad_prefix_attention_decode", _lib.ptr(q), *q.stride()[:3],
+    _lib.call("kad_prefix_attention_decode_ex", _lib.ptr(q), *q.stride()[:3],
               _lib.ptr(prefix_k if L else None), _lib.ptr(prefix_v if L else None), *pk_strides,
               _lib.ptr(suffix_k), *suffix_k.stride()[:3], _lib.ptr(suffix_v),
               *suffix_v.stride()[:3], _lib.ptr(mask), _lib.ptr(gate), *g_strides,
-              _lib.ptr(out), *out.stride()[:3], B, beam_width, T, H, HK, L, D, float(scale),
+              _lib.ptr(out), *out.stride()[:3], B, beam_width, T, Tk, H, HK, L, D, float(scale),
               _lib.stream_of(q))
     return out
 

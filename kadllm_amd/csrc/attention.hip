@@ -53,9 +53,10 @@ struct AttnArgs {
   const uint8_t* mask;                                             // [B, L] or null
   const bf16_t* gate; int64_t sg_n, sg_t, sg_h;                     // or null
   bf16_t* out; int64_t so_n, so_t, so_h;
-  int W, T, H, HK, L;
+  int W, T, H, HK, L;     // T: query tokens per beam
   float scale;
   int nqblk;
+  int Tk, qoff;           // suffix keys per beam; query t is suffix position t + qoff
 };
 
 template <int D, bool CAUSAL>
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       sc[j] = -INFINITY;
-      if (j < a.T) {
+      if (j < a.Tk) {
         const bf16_t* krow = a.sk + n * a.ssk_n + (int64_t)j * a.ssk_t + (int64_t)kh * a.ssk_h;
         float part = 0.f;
 #pragma unroll
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
           for (int i = 0; i < 8; ++i) part += (float)qf[s][i] * (float)kb[i];
         }
         part += __shfl_xor(part, 32, 64);
-        if (j <= t) sc[j] = part * sl2;
+        if (j <= t + a.qoff) sc[j] = part * sl2;
       }
     }
 #pragma unroll
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (j < a.T && pj[j] != 0.f) {
+      if (j < a.Tk && pj[j] != 0.f) {
         const bf16_t* vrow = a.sv + n * a.ssv_n + (int64_t)j * a.ssv_t + (int64_t)kh * a.ssv_h;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
@@ -338,18 +339,19 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
-extern "C" int kad_prefix_attention_decode(
+extern "C" int kad_prefix_attention_decode_ex(
     const void* q, int64_t sq_n, int64_t sq_t, int64_t sq_h, const void* prefix_k,
     const void* prefix_v, int64_t sp_b, int64_t sp_l, int64_t sp_h, const void* suffix_k,
     int64_t ssk_n, int64_t ssk_t, int64_t ssk_h, const void* suffix_v, int64_t ssv_n,
     int64_t ssv_t, int64_t ssv_h, const void* prefix_mask, const void* gate, int64_t sg_n,
     int64_t sg_t, int64_t sg_h, void* out, int64_t so_n, int64_t so_t, int64_t so_h, int B,
-    int W, int T, int H, int HK, int L, int D, float scale, kad_stream_t stream) {
+    int W, int Tq, int Tk, int H, int HK, int L, int D, float scale, kad_stream_t stream) {
   KAD_REQUIRE(q && suffix_k && suffix_v && out, "null pointer argument");
   KAD_REQUIRE(L == 0 || (prefix_k && prefix_v), "null prefix pointer with L > 0");
-  KAD_REQUIRE(B > 0 && W > 0 && T > 0 && H > 0 && HK > 0 && L >= 0 && D > 0, "bad dimensions");
+  KAD_REQUIRE(B > 0 && W > 0 && Tq > 0 && Tq <= Tk && H > 0 && HK > 0 && L >= 0 && D > 0,
+              "bad dimensions");
   KAD_REQUIRE(H % HK == 0, "H must be divisible by HK");
-  if (T > 4) KAD_UNSUPPORTED("prefix attention supports suffixes of <= 4 tokens, got %d", T);
+  if (Tk > 4) KAD_UNSUPPORTED("prefix attention supports suffixes of <= 4 tokens, got %d", Tk);
   KAD_REQUIRE(al16(q) && al16(suffix_k) && (L == 0 || (al16(prefix_k) && al16(prefix_v))),
               "q, suffix_k and prefix K/V must be 16-byte aligned");
   KAD_REQUIRE(((uintptr_t)suffix_v | (uintptr_t)out | (uintptr_t)gate) % 8 == 0,
@@ -362,12 +364,25 @@ extern "C" int kad_prefix_attention_decode(
              (const bf16_t*)prefix_v, sp_b, sp_l, sp_h, (const bf16_t*)suffix_k,
              (const bf16_t*)suffix_v, ssk_n, ssk_t, ssk_h, ssv_n, ssv_t, ssv_h,
              (const uint8_t*)prefix_mask, (const bf16_t*)gate, sg_n, sg_t, sg_h, (bf16_t*)out,
-             so_n, so_t, so_h, W, T, H, HK, L, scale, 0};
-  const int64_t rows = (int64_t)W * (H / HK) * T;
+             so_n, so_t, so_h, W, Tq, H, HK, L, scale, 0, Tk, Tk - Tq};
+  const int64_t rows = (int64_t)W * (H / HK) * Tq;
   a.nqblk = (int)kad_cdiv(rows, kRows);
   const int64_t nblocks = (int64_t)B * HK * a.nqblk;
   KAD_REQUIRE(nblocks < 0x7fffffff, "grid too large");
   return dispatch<false>(D, a, nblocks, (hipStream_t)stream);
+}
+
+extern "C" int kad_prefix_attention_decode(
+    const void* q, int64_t sq_n, int64_t sq_t, int64_t sq_h, const void* prefix_k,
+    const void* prefix_v, int64_t sp_b, int64_t sp_l, int64_t sp_h, const void* suffix_k,
+    int64_t ssk_n, int64_t ssk_t, int64_t ssk_h, const void* suffix_v, int64_t ssv_n,
+    int64_t ssv_t, int64_t ssv_h, const void* prefix_mask, const void* gate, int64_t sg_n,
+    int64_t sg_t, int64_t sg_h, void* out, int64_t so_n, int64_t so_t, int64_t so_h, int B,
+    int W, int T, int H, int HK, int L, int D, float scale, kad_stream_t stream) {
+  return kad_prefix_attention_decode_ex(q, sq_n, sq_t, sq_h, prefix_k, prefix_v, sp_b, sp_l, sp_h,
+                                        suffix_k, ssk_n, ssk_t, ssk_h, suffix_v, ssv_n, ssv_t,
+                                        ssv_h, prefix_mask, gate, sg_n, sg_t, sg_h, out, so_n,
+                                        so_t, so_h, B, W, T, T, H, HK, L, D, scale, stream);
 }
 
 extern "C" int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, int64_t sq_h,
@@ -386,7 +401,7 @@ extern "C" int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, 
     KAD_REQUIRE(st % 4 == 0, "out/gate strides must be multiples of 4 elements");
   AttnArgs a{(const bf16_t*)q, sq_b, sq_l, sq_h, (const bf16_t*)k, (const bf16_t*)v, skv_b, skv_l,
              skv_h, nullptr, nullptr, 0, 0, 0, 0, 0, 0, nullptr, (const bf16_t*)gate, sg_b, sg_l,
-             sg_h, (bf16_t*)out, so_b, so_l, so_h, 1, 1, H, HK, L, scale, 0};
+             sg_h, (bf16_t*)out, so_b, so_l, so_h, 1, 1, H, HK, L, scale, 0, 0, 0};
   const int64_t rows = (int64_t)L * (H / HK);
   a.nqblk = (int)kad_cdiv(rows, kRows);
   const int64_t nblocks = (int64_t)B * HK * a.nqblk;

@@ -576,6 +576,26 @@ __global__ __launch_bounds__(256) void history_kernel(const int64_t* __restrict_
   }
 }
 
+// dst rows (n, t), t < rows_copy, of beam n = b * W + w  <-  src rows
+// (b * Wp + parents[n], t): a beam's cached per-token rows follow its parent.
+// 16 bytes per thread; rows are row_bytes long (a multiple of 16).
+__global__ __launch_bounds__(256) void gather_beam_rows_kernel(
+    const uint8_t* __restrict__ src, int64_t ld_src, int src_rows_per_beam,
+    uint8_t* __restrict__ dst, int64_t ld_dst, int dst_rows_per_beam, int rows_copy,
+    const int64_t* __restrict__ parents, int W, int Wp, int64_t nbeams, int chunks_per_row) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_beam = (int64_t)rows_copy * chunks_per_row;
+  if (idx >= nbeams * per_beam) return;
+  const int64_t n = idx / per_beam;
+  const int rest = (int)(idx - n * per_beam);
+  const int t = rest / chunks_per_row, c = rest - t * chunks_per_row;
+  const int64_t b = n / W;
+  const int64_t pn = parents[n];
+  const int64_t sn = b * Wp + (pn < 0 ? 0 : (pn >= Wp ? Wp - 1 : pn));  // stay in bounds
+  const u32x4 v = *(const u32x4*)(src + (sn * src_rows_per_beam + t) * ld_src + c * 16);
+  *(u32x4*)(dst + (n * dst_rows_per_beam + t) * ld_dst + c * 16) = v;
+}
+
 }  // namespace
 
 extern "C" int kad_beam_row_select(const void* logits, int64_t ld, const void* mask,
@@ -616,4 +636,27 @@ extern "C" int kad_beam_history(const int64_t* history, int Wp, int step, const 
   hipLaunchKernelGGL(history_kernel, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
                      (hipStream_t)stream, history, Wp, step, parents, tokens, out, B, W);
   return kad_launch_status("history_kernel");
+}
+
+extern "C" int kad_gather_beam_rows(const void* src, int64_t ld_src_bytes, int src_rows_per_beam,
+                                    void* dst, int64_t ld_dst_bytes, int dst_rows_per_beam,
+                                    int rows_copy, int64_t row_bytes, const int64_t* parents,
+                                    int B, int W, int Wp, kad_stream_t stream) {
+  KAD_REQUIRE(src && dst && parents, "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0 && Wp > 0 && rows_copy >= 0 && rows_copy <= src_rows_per_beam &&
+                  rows_copy <= dst_rows_per_beam && row_bytes > 0,
+              "bad dimensions");
+  KAD_REQUIRE(row_bytes % 16 == 0 && ld_src_bytes % 16 == 0 && ld_dst_bytes % 16 == 0 &&
+                  ((uintptr_t)src % 16) == 0 && ((uintptr_t)dst % 16) == 0,
+              "rows must be 16-byte aligned multiples of 16 bytes");
+  KAD_REQUIRE(ld_src_bytes >= row_bytes && ld_dst_bytes >= row_bytes, "row strides too small");
+  if (rows_copy == 0) return KAD_OK;
+  const int64_t nbeams = (int64_t)B * W;
+  const int cpr = (int)(row_bytes / 16);
+  const int64_t total = nbeams * rows_copy * cpr;
+  hipLaunchKernelGGL(gather_beam_rows_kernel, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)src, ld_src_bytes, src_rows_per_beam,
+                     (uint8_t*)dst, ld_dst_bytes, dst_rows_per_beam, rows_copy, parents, W, Wp,
+                     nbeams, cpr);
+  return kad_launch_status("gather_beam_rows_kernel");
 }

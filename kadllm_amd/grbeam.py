@@ -126,9 +126,16 @@ def grbeam_search(
     scores = torch.zeros(B, 1, device=dev)
     valid = None
     logits = prefill.logits[:, None, :]
+    # An adapter that can extend the previous level's suffixes (keeping their
+    # per-token state) gets the parents; its logits equal decode(history).
+    incremental = getattr(adapter, "decode_incremental", None)
+    cache = parents = None
     for step, width in enumerate(widths):
         if step:
-            logits = adapter.decode(history, prefill.state)
+            if incremental is not None:
+                logits, cache = incremental(history, parents, prefill.state, cache)
+            else:
+                logits = adapter.decode(history, prefill.state)
         if logits.shape != (*history.shape[:2], V):
             raise ValueError("decode logits must be [B, current_width, vocabulary]")
         mask = None

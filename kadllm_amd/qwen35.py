@@ -270,6 +270,119 @@ class Qwen35Runner:
         logits = layers.gemm(hN, self.lm_head)
         return logits.view(B, W, -1)
 
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def decode_step(self, tokens, parents, prefix_layers, prefix_length, cache=None):
+        """One search level that extends each parent beam's suffix by one token.
+
+        tokens [B, W] int64 are the new tokens, parents [B, W] int64 the
+        indices of the previous level's beams they extend (ignored for the
+        first level, ``cache=None``, whose parent is the prefix itself), and
+        ``cache`` the DecodeCache the previous level returned.  Returns
+        (logits [B, W, V] bf16, DecodeCache).
+
+        The logits equal ``decode(history)`` for history = the parents'
+        suffixes followed by ``tokens``: every per-token quantity of the cached
+        tokens (GDN projection rows, attention K/V after norm and RoPE) is what
+        the parent level computed for the same token at the same position, and
+        every kernel's per-row arithmetic is independent of the batch, so only
+        the new token's rows go through the projections, norms and MLP; the
+        conv and the GDN replay run over the whole suffix and attention takes
+        the new token's queries only.  The reference replays the whole suffix
+        at every level (src/kadllm/adapters/qwen3_5.py:216; README.md:252).
+        """
+        cfg = self.cfg
+        B, W = tokens.shape
+        BW = B * W
+        T = 1 if cache is None else cache.T + 1
+        Wp = 1 if cache is None else cache.W
+        if T > 4:
+            raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
+        dev = self.device
+        parents = parents.to(torch.int64).contiguous() if cache is not None else None
+        x = layers.embedding(tokens, self.embed)
+        H_, HV = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+        dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+        nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        C = self.conv_dim
+        pos = prefix_length + T - 1
+        stream = _lib.stream_of(x)
+
+        def follow(src, dst, rows_per_beam_src, row_bytes, ld_src, ld_dst):
+            _lib.call("kad_gather_beam_rows", _lib.ptr(src), ld_src, rows_per_beam_src,
+                      _lib.ptr(dst), ld_dst, T, T - 1, row_bytes, _lib.ptr(parents), B, W, Wp,
+                      stream)
+
+        new_layers = []
+        for li, (lyr, cached) in enumerate(zip(self.layers, prefix_layers)):
+            n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
+            if isinstance(lyr, _GdnLayer):
+                cols = self.gdn_cols
+                proj = torch.empty(BW * T, cols, dtype=torch.bfloat16, device=dev)
+                pv = proj.view(BW, T, cols)
+                if T > 1:
+                    follow(cache.layers[li], proj, T - 1, cols * 2, cols * 2, cols * 2)
+                layers.gemm(n, lyr.w_in, out=pv[:, T - 1])
+                conv = torch.empty(BW * T, C, dtype=torch.bfloat16, device=dev)
+                cs = cached[0]
+                _lib.call("kad_causal_conv_suffix", _lib.ptr(proj), T * cols, 1, cols, _lib.ptr(cs),
+                          *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), 4, None,
+                          _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, stream)
+                g, beta = self._gdn_gates(lyr, proj)
+                o = torch.empty(BW * T, self.vd, dtype=torch.bfloat16, device=dev)
+                base, es = conv.data_ptr(), conv.element_size()
+                _lib.call("kad_gdn_suffix_replay", _lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
+                          _lib.ptr_at(base + 2 * self.kd * es), C, C, 0, _lib.ptr(g), 2,
+                          _lib.ptr(beta), 0, HV, _lib.ptr(cached[1]),
+                          _lib.dtype_code(cached[1].dtype), _lib.ptr(o), self.vd, B, W, T, H_,
+                          HV, dk, dv, float(dk ** -0.5), stream)
+                o_new = o.view(BW, T, self.vd)[:, T - 1]
+                z_new = pv[:, T - 1, C:C + self.vd]
+                y = layers.rmsnorm_gated(o_new, z_new, lyr.norm_w, cfg.rms_norm_eps, HV)
+                layers.gemm(y, lyr.w_out, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
+                new_layers.append(proj)
+            else:
+                proj = layers.gemm(n, lyr.w_qkv)
+                ld = proj.stride(0)
+                q = torch.empty(BW, 1, nh, hd, dtype=torch.bfloat16, device=dev)
+                k_all = torch.empty(BW, T, nkv, hd, dtype=torch.bfloat16, device=dev)
+                v_all = torch.empty(BW, T, nkv, hd, dtype=torch.bfloat16, device=dev)
+                if T > 1:
+                    kp, vp = cache.layers[li]
+                    rb = nkv * hd * 2
+                    follow(kp, k_all, T - 1, rb, rb, rb)
+                    follow(vp, v_all, T - 1, rb, rb, rb)
+                layers.qk_norm_rope(proj, ld, 2 * hd, nh, lyr.q_norm, q, (0, nh * hd, hd), BW, BW,
+                                    hd, self.rot, self.inv_freq, pos, 1, cfg.rms_norm_eps)
+                tok = (0, T * nkv * hd, hd)
+                layers.qk_norm_rope(proj[:, 2 * nh * hd:], ld, hd, nkv, lyr.k_norm, k_all[:, T - 1],
+                                    tok, BW, BW, hd, self.rot, self.inv_freq, pos, 1,
+                                    cfg.rms_norm_eps)
+                layers.scatter_heads(proj[:, (2 * nh + nkv) * hd:], ld, nkv, hd, v_all[:, T - 1],
+                                     tok, BW, BW)
+                att = prefix_attention_decode(q, cached[0], cached[1], k_all, v_all, W, None,
+                                              hd ** -0.5, gate=proj[:, hd:],
+                                              gate_strides=(ld, ld, 2 * hd))
+                layers.gemm(att.view(BW, nh * hd), lyr.w_o, out=x, epilogue=layers.EPI_RESIDUAL,
+                            residual=x)
+                new_layers.append((k_all, v_all))
+            self._mlp(lyr, x, BW)
+        hN = layers.rmsnorm(x, self.norm_w, cfg.rms_norm_eps)
+        logits = layers.gemm(hN, self.lm_head)
+        return logits.view(B, W, -1), DecodeCache(T, W, tuple(new_layers))
+
+
+@dataclass
+class DecodeCache:
+    """Per-layer rows of the suffixes of one search level's beams.
+
+    GDN layers: the fused input projection rows [B*W*T, cols] (token-major
+    within each beam); attention layers: (K, V) [B*W, T, HK, D] after norm and
+    RoPE.  Read by the next level through each beam's parent."""
+
+    T: int
+    W: int
+    layers: tuple
 
 
 class Qwen35TextModel:

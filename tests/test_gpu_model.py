@@ -167,3 +167,59 @@ def test_08b_shape_prefill_and_decode(device):
     assert_bf16_parity(res.logits, ref_logits, truth_logits, "0.8B prefill logits")
     assert_bf16_parity(logits, oracle.decode(hist, ref_state), truth.decode(hist, truth_state),
                        "0.8B decode logits")
+
+
+def _incremental_matches_stateless(adapter, state, B, widths, V, device, seed):
+    """Chain decode_incremental over levels with random parents and tokens and
+    compare every level's logits with the stateless decode of the same history."""
+    g = torch.Generator().manual_seed(seed)
+    history = torch.randint(0, V, (B, widths[0], 1), generator=g).to(device)
+    logits, cache = adapter.decode_incremental(history, None, state, None)
+    assert torch.equal(logits, adapter.decode(history, state)), "level 1"
+    for level, W in enumerate(widths[1:], start=2):
+        Wp = history.shape[1]
+        parents = torch.randint(0, Wp, (B, W), generator=g).to(device)
+        tokens = torch.randint(0, V, (B, W, 1), generator=g).to(device)
+        history = torch.cat((history.gather(1, parents[..., None].expand(B, W, level - 1)),
+                             tokens), -1)
+        logits, cache = adapter.decode_incremental(history, parents, state, cache)
+        stateless = adapter.decode(history, state)
+        torch.cuda.synchronize()
+        assert torch.equal(logits, stateless), f"level {level}: incremental logits differ"
+
+
+def test_incremental_decode_equals_stateless_tiny(device, tiny):
+    """Suffix dedup across levels: exactly the stateless replay's logits, T = 1..4."""
+    cfg, _, adapter = tiny
+    ids = torch.randint(0, cfg.vocab_size, (3, 50), generator=torch.Generator().manual_seed(21))
+    res = adapter.prefill(ids.to(device))
+    _incremental_matches_stateless(adapter, res.state, 3, [5, 7, 6, 9], cfg.vocab_size, device, 22)
+
+
+def test_incremental_decode_equals_stateless_08b(device):
+    """The 0.8B shape at 4 x 256 beams, where the stateless and incremental
+    projections run with different GEMM tile configurations."""
+    cfg = qwen35_08b_config()
+    sd = random_state_dict(cfg, seed=3, dtype=torch.bfloat16, device=device)
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, sd))
+    ids = torch.randint(0, cfg.vocab_size, (4, 64), generator=torch.Generator().manual_seed(5))
+    res = adapter.prefill(ids.to(device))
+    _incremental_matches_stateless(adapter, res.state, 4, [256, 256], cfg.vocab_size, device, 6)
+
+
+def test_search_with_and_without_incremental_decode(device, tiny):
+    cfg, _, adapter = tiny
+
+    class Stateless:
+        def prefill(self, ids):
+            return adapter.prefill(ids)
+
+        def decode(self, history, state):
+            return adapter.decode(history, state)
+
+    ids = torch.randint(0, cfg.vocab_size, (2, 33), generator=torch.Generator().manual_seed(8))
+    a = grbeam_search(adapter, ids.to(device), [6, 9, 7, 5])
+    b = grbeam_search(Stateless(), ids.to(device), [6, 9, 7, 5])
+    torch.cuda.synchronize()
+    assert torch.equal(a.tokens, b.tokens) and torch.equal(a.scores, b.scores)
+    assert torch.equal(a.valid, b.valid)
