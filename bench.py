@@ -44,24 +44,33 @@ def validate_output(tokens, batch, width, depth):
 
 
 class GemmTimer:
-    """Records a HIP event pair around every GEMM launch (torch's current stream)."""
+    """Records a HIP event pair around every GEMM launch (torch's current stream,
+    the stream the GEMM is launched on)."""
 
     def __init__(self):
         self.events = []
 
-    def __call__(self, launch, flops):
+    def __call__(self, launch, flops, nbytes):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         launch()
         e1.record()
-        self.events.append((e0, e1, flops))
+        self.events.append((e0, e1, flops, nbytes))
 
     def summary(self):
         torch.cuda.synchronize()
-        ms = sum(e0.elapsed_time(e1) for e0, e1, _ in self.events)
-        flops = sum(f for _, _, f in self.events)
-        return ms, flops, len(self.events)
+        ms = sum(e0.elapsed_time(e1) for e0, e1, _, _ in self.events)
+        flops = sum(f for _, _, f, _ in self.events)
+        nbytes = sum(b for _, _, _, b in self.events)
+        return ms, flops, nbytes, len(self.events)
+
+
+# HBM bytes per GEMM launch of this workload: rocprofv3 FETCH_SIZE and
+# WRITE_SIZE over the GEMM dispatches of one search, each scaled by its reading
+# for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the launch
+# count.  Re-measured with the command in profiles/gemm_hbm_traffic_b32_p1024_w256.md.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 469.7e6
 
 
 def cpu_baseline(cfg, sd_cpu, prefix, beam, depth, threads):
@@ -141,7 +150,7 @@ def main():
     layers.set_launch_timer(None)
     for out in outputs:
         validate_output(out, a.batch, a.beam, a.depth)
-    gemm_ms, gemm_flops, n_gemm = timer.summary()
+    gemm_ms, gemm_flops, gemm_bytes, n_gemm = timer.summary()
     achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12  # TFLOP/s
     value = a.batch * a.steps / elapsed
 
@@ -155,6 +164,7 @@ def main():
                          f"vocabulary) through the oracle restatement of the reference torch "
                          f"path, bf16 weights, {dt:.1f} s"}
 
+    workload_default = (a.batch, a.prefix, a.beam, a.depth) == (32, 1024, 256, 3)
     line = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -165,17 +175,18 @@ def main():
         "ms_per_step": round(1000 * elapsed / a.steps, 3),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(value / H800_REQ_S, 3) if (a.batch, a.prefix, a.beam, a.depth) ==
-        (32, 1024, 256, 3) else None,
+        "vs_baseline": round(value / H800_REQ_S, 3) if workload_default else None,
         "dtype": "bf16",
         "data": "synthetic (random-init weights, uniform-random prompt ids)",
         "config": {"workload": f"grbeam_e2e qwen3.5-0.8B-shaped B{a.batch} P{a.prefix} "
                                f"W{a.beam} depth{a.depth} full-vocab",
                    "batch": a.batch, "prefix": a.prefix, "beam": a.beam, "depth": a.depth,
                    "vocab": cfg.vocab_size, "layers": cfg.num_hidden_layers},
-        "roofline": {"kernel": "gemm_bf16_kernel (all launches)", "bound": "mfma",
+        "roofline": {"kernel": "bf16 MFMA GEMM (all launches)", "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH if workload_default else None,
+                     "algorithmic_bytes_per_launch": round(gemm_bytes / n_gemm),
                      "launches_per_step": n_gemm // a.steps,
                      "gemm_ms_per_step": round(gemm_ms / a.steps, 3)},
         "cpu_baseline": cpu,

@@ -15,8 +15,10 @@ _launch_timer = None
 
 
 def set_launch_timer(timer):
-    """Install (or clear with None) a callable ``timer(launch, flops)`` that wraps
-    every GEMM launch, e.g. to bracket it with HIP events for roofline figures."""
+    """Install (or clear with None) a callable ``timer(launch, flops, nbytes)``
+    that wraps every GEMM launch, e.g. to bracket it with HIP events for
+    roofline figures; nbytes = the launch's algorithmic HBM bytes (A, W, the
+    output and the residual each once)."""
     global _launch_timer
     _launch_timer = timer
 
@@ -43,7 +45,8 @@ def gemm(a, w, out=None, *, epilogue=EPI_STORE, residual=None):
     if _launch_timer is None:
         launch()
     else:
-        _launch_timer(launch, 2 * M * N * K)
+        nbytes = 2 * (M * K + N * K + M * n_out + (M * n_out if r is not None else 0))
+        _launch_timer(launch, 2 * M * N * K, nbytes)
     return out
 
 
