@@ -108,7 +108,14 @@ def main():
     ap.add_argument("--depth", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--workload", choices=("grbeam", "conditional_sid"), default="grbeam",
+                    help="grbeam: the headline full-vocabulary search (default); "
+                         "conditional_sid: B8, prefix 4096, coarse widths [32, 32] over the full "
+                         "vocabulary, then 16 children per coarse beam for 2 tokens with "
+                         "candidates restricted to a seeded 8192-id subset")
     a = ap.parse_args()
+    if a.workload == "conditional_sid":
+        return conditional_sid(a)
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {a.gpus}); "
               "requests shard across GPUs with no exchange, see the design notes", file=sys.stderr)
@@ -193,6 +200,59 @@ def main():
         "step_ms": [round(1000 * t, 2) for t in times],
     }
     print(json.dumps(line), flush=True)
+
+
+def conditional_sid(a):
+    """Two-level conditional semantic-ID search (no reference runner exists for it;
+    vs_baseline is null).  One step is one conditional_search call on the batch,
+    tokens copied to the host, inside the timed region."""
+    if a.gpus != 1:
+        print("bench.py runs on one GPU", file=sys.stderr)
+        sys.exit(2)
+    from kadllm_amd import conditional_search
+    from kadllm_amd.adapters import Qwen35GRBeamAdapter, native_model
+    from kadllm_amd.config import qwen35_08b_config
+    from kadllm_amd.weights import random_state_dict
+
+    B, P, coarse, fine, n_sub = 8, 4096, [32, 32], [16, 16], 8192
+    dev = torch.device("cuda:0")
+    cfg = qwen35_08b_config()
+    sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16, device=dev)
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, sd))
+    ids = torch.randint(0, cfg.vocab_size, (B, P), generator=torch.Generator().manual_seed(0)).to(dev)
+    sub = torch.zeros(cfg.vocab_size, dtype=torch.bool)
+    sub[torch.randperm(cfg.vocab_size, generator=torch.Generator().manual_seed(0))[:n_sub]] = True
+    sub = sub.to(dev)
+    everything = torch.ones(cfg.vocab_size, dtype=torch.bool, device=dev)
+
+    def allowed(history, logits):
+        return sub if history.shape[2] >= len(coarse) else everything
+
+    def run():
+        res = conditional_search(adapter, ids, coarse, fine, allowed=allowed)
+        return res.tokens.tolist()
+
+    width = coarse[-1] * fine[-1]
+    for _ in range(a.warmup):
+        validate_output(run(), B, width, len(coarse) + len(fine))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    outs = [run() for _ in range(a.steps)]
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    for out in outs:
+        validate_output(out, B, width, len(coarse) + len(fine))
+    value = B * a.steps / elapsed
+    print(json.dumps({
+        "metric": "requests/s, two-level conditional SID search",
+        "value": round(value, 3), "unit": "requests/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(1000 * elapsed / a.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform-random prompt ids, seeded 8192-id subset)",
+        "config": {"workload": f"conditional_sid qwen3.5-0.8B-shaped B{B} P{P} coarse{coarse} "
+                               f"fine{fine}x{coarse[-1]} subset{n_sub}",
+                   "batch": B, "prefix": P, "coarse_widths": coarse, "fine_widths": fine},
+        "roofline": None, "cpu_baseline": None}), flush=True)
 
 
 if __name__ == "__main__":

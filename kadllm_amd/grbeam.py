@@ -52,8 +52,10 @@ def select_level(logits, scores, width, mask=None):
     """One selection level on the GPU (src/kadllm/grbeam.py:89-104).
 
     logits [B, Wp, V] bf16 (last dim contiguous), scores [B, Wp] fp32, mask
-    [B, Wp, V] bool or None.  Returns (scores [B, width] fp32, parents,
-    tokens [B, width] int64, valid [B, width] bool).
+    [B, Wp, V] bool or None; a mask that is one [V] row broadcast to every beam
+    row (an ``expand``-ed view, row stride 0) is read in place.  Returns
+    (scores [B, width] fp32, parents, tokens [B, width] int64, valid [B, width]
+    bool).
     """
     B, Wp, V = logits.shape
     if logits.dtype != torch.bfloat16:
@@ -68,12 +70,18 @@ def select_level(logits, scores, width, mask=None):
     parent = scores.to(device=dev, dtype=torch.float32).contiguous()
     cand_key = torch.empty(rows, K, dtype=torch.float32, device=dev)
     cand_idx = torch.empty(rows, K, dtype=torch.int32, device=dev)
-    m = None
+    m, ld_mask = None, V
     if mask is not None:
-        m = mask.contiguous().view(torch.uint8)
+        if mask.shape != logits.shape or mask.dtype != torch.bool:
+            raise ValueError("mask must be a bool tensor shaped like the logits")
+        if mask.stride(2) == 1 and mask.stride(0) == Wp * mask.stride(1) and mask.is_cuda:
+            m, ld_mask = mask.view(torch.uint8), mask.stride(1)
+        else:
+            m = mask.contiguous().view(torch.uint8)
     stream = _lib.stream_of(logits)
     _lib.call("kad_beam_row_select", _lib.ptr(logits), logits.stride(1), _lib.ptr(m),
-              V, _lib.ptr(parent), rows, Wp, V, K, _lib.ptr(cand_key), _lib.ptr(cand_idx), stream)
+              ld_mask, _lib.ptr(parent), rows, Wp, V, K, _lib.ptr(cand_key), _lib.ptr(cand_idx),
+              stream)
     new_scores = torch.empty(B, width, dtype=torch.float32, device=dev)
     parents = torch.empty(B, width, dtype=torch.int64, device=dev)
     tokens = torch.empty(B, width, dtype=torch.int64, device=dev)
@@ -81,6 +89,35 @@ def select_level(logits, scores, width, mask=None):
     _lib.call("kad_beam_merge_select", _lib.ptr(cand_key), _lib.ptr(cand_idx), B, Wp * K, width,
               V, _lib.ptr(new_scores), _lib.ptr(parents), _lib.ptr(tokens), _lib.ptr(valid), stream)
     return new_scores, parents, tokens, valid
+
+
+def select_level_grouped(logits, scores, groups, width, mask=None):
+    """Per-group selection: the Wp beam rows of each request form ``groups``
+    contiguous groups of Wp / groups rows, and every group keeps its own
+    ``width`` best candidates (ties to the lower (row, token) inside the group).
+    Returns (scores, parents, tokens, valid), each [B, groups * width], beams
+    ordered by group; parents index the request's Wp rows."""
+    B, Wp, V = logits.shape
+    if Wp % groups:
+        raise ValueError("beam rows must split evenly into the groups")
+    rpg = Wp // groups
+    if logits.stride(2) != 1 or logits.stride(0) != Wp * logits.stride(1):
+        logits = logits.contiguous()
+    lg = logits.view(B * groups, rpg, V)
+    sc = scores.reshape(B * groups, rpg)
+    mk = None
+    if mask is not None:
+        if mask.shape != logits.shape or mask.dtype != torch.bool:
+            raise ValueError("mask must be a bool tensor shaped like the logits")
+        if mask.stride(2) == 1 and mask.stride(0) == Wp * mask.stride(1):
+            mk = mask.as_strided((B * groups, rpg, V), (rpg * mask.stride(1), mask.stride(1), 1))
+        else:
+            mk = mask.contiguous().view(B * groups, rpg, V)
+    s, p, t, v = select_level(lg, sc, width, mk)
+    offset = torch.arange(groups, device=p.device, dtype=torch.int64)[:, None] * rpg
+    parents = (p.view(B, groups, width) + offset).view(B, groups * width)
+    return (s.view(B, groups * width), parents, t.view(B, groups * width),
+            v.view(B, groups * width))
 
 
 def extend_history(history, parents, tokens):
@@ -146,6 +183,73 @@ def grbeam_search(
         if width > history.shape[1] * V:
             raise ValueError("beam width exceeds the number of candidate slots")
         scores, parents, tokens, valid = select_level(logits, scores, width, mask)
+        del logits, mask
+        history = extend_history(history, parents, tokens)
+    return GRBeamResult(history, scores, valid)
+
+
+@torch.no_grad()
+def conditional_search(
+    adapter: GRBeamAdapter,
+    input_ids: torch.Tensor,
+    coarse_widths: Sequence[int],
+    fine_widths: Sequence[int],
+    *,
+    allowed: Constraint | None = None,
+) -> GRBeamResult:
+    """Two-level conditional search (semantic-ID generation with coarse and fine
+    code levels): ``coarse_widths`` levels of ordinary GRBeam selection over the
+    full vocabulary, then ``fine_widths`` levels in which every coarse beam
+    keeps its own ``fine_widths[i]`` best descendants, so the level holds
+    coarse_width * fine_widths[i] beams ordered by coarse beam.  Scores are
+    cumulative full-vocabulary log-probabilities throughout; ``allowed`` masks
+    candidates without renormalisation (src/kadllm/grbeam.py:41-42,80-84) and
+    may return a [V] row broadcast to the logits' shape.  Each coarse beam's
+    suffix is the shared prefix for its children: decoding reuses the request
+    prefix state for every beam and extends cached suffixes by one token.
+    Returns GRBeamResult(tokens [B, Wc * fine_widths[-1], depth], scores, valid).
+    """
+    for ws in (coarse_widths, fine_widths):
+        if not ws or any(not isinstance(w, int) or isinstance(w, bool) or w < 1 for w in ws):
+            raise ValueError("widths must contain positive integers")
+    if input_ids.ndim != 2 or min(input_ids.shape) < 1:
+        raise ValueError("input_ids must be nonempty [B, prompt_length]")
+    prefill = adapter.prefill(input_ids)
+    B = input_ids.shape[0]
+    V = prefill.logits.shape[-1]
+    dev = prefill.logits.device
+    history = torch.empty(B, 1, 0, dtype=torch.int64, device=dev)
+    scores = torch.zeros(B, 1, device=dev)
+    logits = prefill.logits[:, None, :]
+    incremental = getattr(adapter, "decode_incremental", None)
+    cache = parents = valid = None
+    levels = [(w, None) for w in coarse_widths] + [(w, "fine") for w in fine_widths]
+    groups = None
+    for step, (width, kind) in enumerate(levels):
+        if step:
+            if incremental is not None:
+                logits, cache = incremental(history, parents, prefill.state, cache)
+            else:
+                logits = adapter.decode(history, prefill.state)
+        if logits.shape != (*history.shape[:2], V):
+            raise ValueError("decode logits must be [B, current_width, vocabulary]")
+        mask = None
+        if allowed is not None:
+            mask = allowed(history, logits)
+            if mask.dtype != torch.bool:
+                raise ValueError("constraint must return a bool mask")
+            mask = mask.expand(logits.shape)
+        if kind is None:
+            if width > history.shape[1] * V:
+                raise ValueError("beam width exceeds the number of candidate slots")
+            scores, parents, tokens, valid = select_level(logits, scores, width, mask)
+        else:
+            if groups is None:
+                groups = history.shape[1]  # the coarse beams
+            if width > (history.shape[1] // groups) * V:
+                raise ValueError("fine width exceeds a coarse beam's candidate slots")
+            scores, parents, tokens, valid = select_level_grouped(logits, scores, groups, width,
+                                                                  mask)
         del logits, mask
         history = extend_history(history, parents, tokens)
     return GRBeamResult(history, scores, valid)

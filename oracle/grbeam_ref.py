@@ -102,3 +102,80 @@ def brute_force_beam(logprob_fn, B, V, widths):
 
 def all_sequences(V, depth):
     return list(itertools.product(range(V), repeat=depth))
+
+
+def level_select_grouped(logits, scores, groups, width, mask=None):
+    """Per-group selection: each request's Wp rows form ``groups`` contiguous
+    groups; every group keeps its ``width`` best candidates by cumulative
+    full-vocabulary log-prob (ties to the lower (row, token) in the group).
+    Returns (scores, parents, tokens) [B, groups * width], parents indexing the
+    request's rows."""
+    B, Wp, V = logits.shape
+    rpg = Wp // groups
+    s, p, t = level_select(logits.reshape(B * groups, rpg, V), scores.reshape(B * groups, rpg),
+                           width, None if mask is None else mask.reshape(B * groups, rpg, V))
+    p = p.view(B, groups, width) + torch.arange(groups)[:, None] * rpg
+    return s.reshape(B, -1), p.reshape(B, -1), t.reshape(B, -1)
+
+
+def conditional_search(adapter, input_ids, coarse_widths, fine_widths, *, allowed=None):
+    """Two-level conditional search: ordinary levels over the full vocabulary
+    (src/kadllm/grbeam.py:89-104), then levels in which every coarse beam keeps
+    its own best ``fine_widths[i]`` descendants.  Returns (tokens, scores,
+    valid, per-level logits)."""
+    logits0, state = adapter.prefill(input_ids)
+    B = input_ids.shape[0]
+    V = logits0.shape[-1]
+    history = input_ids.new_empty(B, 1, 0)
+    scores = torch.zeros(B, 1)
+    logits = logits0[:, None, :]
+    seen = []
+    groups = None
+    levels = [(w, False) for w in coarse_widths] + [(w, True) for w in fine_widths]
+    for step, (width, fine) in enumerate(levels):
+        if step:
+            logits = adapter.decode(history, state)
+        seen.append(logits)
+        mask = None if allowed is None else allowed(history, logits).expand(logits.shape)
+        if fine:
+            groups = history.shape[1] if groups is None else groups
+            scores, parents, tokens = level_select_grouped(logits, scores, groups, width, mask)
+        else:
+            scores, parents, tokens = level_select(logits, scores, width, mask)
+        old = history.gather(1, parents[..., None].expand(B, parents.shape[1], step))
+        history = torch.cat((old, tokens[..., None]), dim=-1)
+    return history, scores, torch.isfinite(scores), seen
+
+
+def brute_force_conditional(logprob_fn, B, V, coarse_widths, fine_widths, allowed_fn=None):
+    """Exhaustive conditional search for tiny vocabularies: the coarse levels
+    are beam search by definition (best ``width`` cumulative log-probs over all
+    expansions), then each coarse beam's subtree is searched on its own with
+    the fine widths.  ``allowed_fn(request, prefix_tuple) -> bool [V]``;
+    disallowed candidates score -inf and rank after every allowed one, ties to
+    the lower (parent rank, token).  Returns per request a list of
+    (sequence, score)."""
+    def expand(r, beams, width):
+        cand = []
+        for rank, (seq, sc) in enumerate(beams):
+            lp = logprob_fn(r, seq)
+            ok = allowed_fn(r, seq) if allowed_fn is not None else None
+            for tok in range(V):
+                val = sc + float(lp[tok]) if ok is None or bool(ok[tok]) else float("-inf")
+                cand.append((val, rank * V + tok, seq + (tok,)))
+        cand.sort(key=lambda c: (-c[0], c[1]))
+        return [(c[2], c[0]) for c in cand[:width]]
+
+    results = []
+    for r in range(B):
+        beams = [((), 0.0)]
+        for width in coarse_widths:
+            beams = expand(r, beams, width)
+        final = []
+        for beam in beams:
+            sub = [beam]
+            for width in fine_widths:
+                sub = expand(r, sub, width)
+            final.extend(sub)
+        results.append(final)
+    return results

@@ -174,3 +174,75 @@ def test_select_level_candidate_overflow_falls_back_exactly(device):
     logits = logits.bfloat16()
     scores = -torch.rand(B, Wp, generator=g)
     _check_selection(logits.to(device), scores.to(device), W)
+
+
+def test_select_level_grouped_with_shared_mask(device):
+    """Per-group quotas with one allowed-token row broadcast to every beam row
+    (read in place, row stride 0): exactly the oracle's grouped selection."""
+    from kadllm_amd.grbeam import select_level_grouped
+    B, G, rpg, V, W = 2, 4, 3, 5000, 6
+    g = torch.Generator().manual_seed(31)
+    logits = torch.randn(B, G * rpg, V, generator=g).bfloat16()
+    scores = -torch.rand(B, G * rpg, generator=g) * 2
+    sub = torch.zeros(V, dtype=torch.bool)
+    sub[torch.randperm(V, generator=g)[:700]] = True
+    mask = sub.to(device).expand(B, G * rpg, V)
+    s, p, t, valid = select_level_grouped(logits.to(device), scores.to(device), G, W, mask)
+    torch.cuda.synchronize()
+    rs, rp, rt = grbeam_ref.level_select_grouped(logits, scores, G, W, sub.expand(B, G * rpg, V))
+    assert torch.equal(p.cpu(), rp) and torch.equal(t.cpu(), rt)
+    assert torch.allclose(s.cpu(), rs, rtol=0, atol=1e-4) and bool(valid.all())
+    assert bool(sub[t.cpu()].all()), "a disallowed token was selected"
+    # the same mask materialised gives the same answer
+    s2, p2, t2, _ = select_level_grouped(logits.to(device), scores.to(device), G, W,
+                                         mask.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(p2, p) and torch.equal(t2, t) and torch.equal(s2, s)
+
+
+def test_conditional_search_teacher_forced(device):
+    """Two-level conditional search on the tiny model: coarse [4, 4], fine [3, 2]
+    with an allowed-token subset on the fine levels; each level's selection is
+    the oracle's (grouped) selection applied to the GPU's own logits."""
+    from kadllm_amd import conditional_search
+    from kadllm_amd.adapters import Qwen35GRBeamAdapter, native_model
+    from kadllm_amd.config import tiny_hybrid_config
+    from kadllm_amd.weights import random_state_dict
+    cfg = tiny_hybrid_config()
+    sd = random_state_dict(cfg, seed=2, dtype=torch.bfloat16, device=device)
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, sd))
+    V = cfg.vocab_size
+    sub = torch.zeros(V, dtype=torch.bool)
+    sub[torch.randperm(V, generator=torch.Generator().manual_seed(4))[:300]] = True
+    subd = sub.to(device)
+    coarse, fine = [4, 4], [3, 2]
+
+    def allowed(history, logits):
+        if history.shape[2] < len(coarse):
+            return torch.ones(V, dtype=torch.bool, device=logits.device)
+        return subd
+
+    ids = torch.randint(0, V, (2, 40), generator=torch.Generator().manual_seed(5)).to(device)
+    res = conditional_search(adapter, ids, coarse, fine, allowed=allowed)
+    torch.cuda.synchronize()
+    B = 2
+    assert res.tokens.shape == (B, coarse[-1] * fine[-1], 4) and bool(res.valid.all())
+    assert bool(sub[res.tokens[:, :, 2:].cpu()].all())
+    # teacher forcing through the oracle selection rules
+    pre = adapter.prefill(ids)
+    history = torch.empty(B, 1, 0, dtype=torch.int64)
+    scores = torch.zeros(B, 1)
+    logits = pre.logits.cpu()[:, None]
+    for step, (w, is_fine) in enumerate([(w, False) for w in coarse] + [(w, True) for w in fine]):
+        if step:
+            logits = adapter.decode(history.to(device), pre.state).cpu()
+        m = allowed(history, logits).cpu().expand(logits.shape)
+        if is_fine:
+            scores, parents, tokens = grbeam_ref.level_select_grouped(logits, scores, coarse[-1],
+                                                                      w, m)
+        else:
+            scores, parents, tokens = grbeam_ref.level_select(logits, scores, w, m)
+        history = torch.cat((history.gather(1, parents[..., None].expand(B, parents.shape[1], step)),
+                             tokens[..., None]), -1)
+    assert torch.equal(history, res.tokens.cpu())
+    assert torch.allclose(scores, res.scores.cpu(), atol=1e-4)

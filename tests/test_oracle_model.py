@@ -186,3 +186,35 @@ def test_select_topk_ties_to_lower_index():
     big[4999] = big[17] = 2.0
     s, i = grbeam_ref.select_topk(big, 3)
     assert i.tolist() == [17, 4999, 0]
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_conditional_search_equals_exhaustive(masked):
+    """Coarse levels, then per-coarse-beam quotas, against enumeration; with a
+    fixed allowed-token subset on the fine levels (a broadcast [V] row)."""
+    B, V, coarse, fine = 2, 12, [3, 4], [2, 3]
+    lm = _TableModel(B, V, len(coarse) + len(fine), seed=11 + masked)
+    sub = torch.zeros(V, dtype=torch.bool)
+    sub[torch.randperm(V, generator=torch.Generator().manual_seed(3))[:5]] = True
+
+    def allowed(history, logits):
+        if not masked or history.shape[2] < len(coarse):
+            return torch.ones(V, dtype=torch.bool)
+        return sub
+
+    def allowed_fn(r, seq):
+        return sub if masked and len(seq) >= len(coarse) else None
+
+    tokens, scores, valid, _ = grbeam_ref.conditional_search(
+        lm, torch.zeros(B, 3, dtype=torch.int64), coarse, fine, allowed=allowed)
+    assert tokens.shape == (B, coarse[-1] * fine[-1], len(coarse) + len(fine))
+    brute = grbeam_ref.brute_force_conditional(lm.logprob, B, V, coarse, fine, allowed_fn)
+    for r in range(B):
+        assert [tuple(s) for s in tokens[r].tolist()] == [s for s, _ in brute[r]]
+        assert np.allclose(scores[r].double().numpy(), [sc for _, sc in brute[r]], atol=1e-5)
+        # every coarse beam keeps exactly fine[-1] descendants, grouped in order
+        prefixes = [tuple(s[:len(coarse)]) for s in tokens[r].tolist()]
+        groups = [prefixes[i:i + fine[-1]] for i in range(0, len(prefixes), fine[-1])]
+        assert all(len(set(g)) == 1 for g in groups) and len({g[0] for g in groups}) == coarse[-1]
+    if masked:
+        assert bool(torch.isin(tokens[:, :, len(coarse):], torch.nonzero(sub)[:, 0]).all())
