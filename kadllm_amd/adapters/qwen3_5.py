@@ -120,6 +120,39 @@ class Qwen35GRBeamAdapter:
             raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
         return self._runner.decode(history, state.layers, state.length)
 
+    @classmethod
+    def from_pretrained(cls, path, device="cuda", **kwargs):
+        """Adapter over a transformers Qwen3.5 checkpoint directory (safetensors +
+        config.json, e.g. the reference's benchmark model), loaded natively."""
+        from ..formats import load_checkpoint
+
+        cfg, sd = load_checkpoint(path, device=device)
+        return cls(*native_model(cfg, sd), **kwargs)
+
+    def prefix_from_cache(self, cache, length):
+        """A prefix owned by this adapter from a transformers cache of `length`
+        prompt tokens (the layout src/kadllm/adapters/qwen3_5.py:113-142 reads)."""
+        from ..formats import prefix_layers_from_cache
+
+        layers = []
+        for kind, (a, b) in zip(self.layer_types,
+                                prefix_layers_from_cache(cache, self.layer_types)):
+            if kind == "linear_attention":
+                layers.append((a.to(self.device, torch.bfloat16), b.to(self.device, torch.float32)))
+            else:
+                layers.append((a.to(self.device, torch.bfloat16), b.to(self.device, torch.bfloat16)))
+        batch = layers[0][0].shape[0]
+        return Qwen35Prefix(int(length), batch, self._owner, tuple(layers))
+
+    def prefix_to_cache(self, state, hf_config=None):
+        """A transformers DynamicCache holding this adapter's prefix."""
+        from ..formats import cache_from_prefix_layers
+
+        if not isinstance(state, Qwen35Prefix) or state.owner is not self._owner:
+            raise ValueError("prefix belongs to a different adapter")
+        return cache_from_prefix_layers(state.layers, self.layer_types,
+                                        hf_config if hf_config is not None else self.config.to_hf())
+
     @torch.no_grad()
     def decode_incremental(self, history, parents, state, cache=None):
         """decode(history, state) for a level whose beams extend the previous

@@ -51,6 +51,34 @@ class Qwen35Config:
                 "partial_rotary_factor": self.partial_rotary_factor}
 
     @staticmethod
+    def from_dict(d):
+        """Read a Qwen3.5 text config dict (``config.json``'s ``text_config``, or a
+        text-model config), with rope settings in ``rope_parameters`` or at the
+        top level."""
+        rope = dict(d.get("rope_parameters") or {})
+        return Qwen35Config(
+            vocab_size=d["vocab_size"],
+            hidden_size=d["hidden_size"],
+            num_hidden_layers=d["num_hidden_layers"],
+            intermediate_size=d["intermediate_size"],
+            linear_num_key_heads=d["linear_num_key_heads"],
+            linear_num_value_heads=d["linear_num_value_heads"],
+            linear_key_head_dim=d["linear_key_head_dim"],
+            linear_value_head_dim=d["linear_value_head_dim"],
+            num_attention_heads=d["num_attention_heads"],
+            num_key_value_heads=d["num_key_value_heads"],
+            head_dim=d["head_dim"],
+            layer_types=tuple(d["layer_types"]) if d.get("layer_types") else None,
+            linear_conv_kernel_dim=d.get("linear_conv_kernel_dim", 4),
+            rope_theta=float(rope.get("rope_theta", d.get("rope_theta", 10000.0))),
+            partial_rotary_factor=float(rope.get("partial_rotary_factor",
+                                                 d.get("partial_rotary_factor", 0.25))),
+            rms_norm_eps=d.get("rms_norm_eps", 1e-6),
+            tie_word_embeddings=bool(d.get("tie_word_embeddings", False)),
+            hidden_act=d.get("hidden_act", "silu"),
+        )
+
+    @staticmethod
     def from_hf(hf_config):
         """Read the fields of a transformers Qwen3_5TextConfig."""
         rope = dict(getattr(hf_config, "rope_parameters", None) or {})

@@ -223,3 +223,42 @@ def test_search_with_and_without_incremental_decode(device, tiny):
     torch.cuda.synchronize()
     assert torch.equal(a.tokens, b.tokens) and torch.equal(a.scores, b.scores)
     assert torch.equal(a.valid, b.valid)
+
+
+def test_checkpoint_and_cache_interop(device, tmp_path):
+    """from_pretrained on a save_pretrained checkpoint equals the in-memory model;
+    a transformers prefill cache, taken as the prefix, decodes like the native
+    prefix; and the native prefix continues in the transformers forward."""
+    from transformers import Qwen3_5ForCausalLM
+    cfg = tiny_hybrid_config()
+    sd = random_state_dict(cfg, seed=7, dtype=torch.bfloat16)
+    model, head = build_hf_text_model(cfg, sd)
+    lm = Qwen3_5ForCausalLM(model.config).eval().to(torch.bfloat16)
+    lm.model.load_state_dict(model.state_dict())
+    lm.lm_head.weight.data.copy_(head.weight.data)
+    lm.save_pretrained(tmp_path)
+    a1 = Qwen35GRBeamAdapter.from_pretrained(str(tmp_path), device=device)
+    a2 = Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}))
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, cfg.vocab_size, (2, 48), generator=g).to(device)
+    hist = torch.randint(0, cfg.vocab_size, (2, 4, 2), generator=g).to(device)
+    r1, r2 = a1.prefill(ids), a2.prefill(ids)
+    torch.cuda.synchronize()
+    assert torch.equal(r1.logits, r2.logits)
+    lm = lm.to(device)
+    with torch.no_grad():
+        out = lm.model(input_ids=ids, use_cache=True, return_dict=True)
+    hf_prefix = a1.prefix_from_cache(out.past_key_values, ids.shape[1])
+    native = a1.decode(hist, r1.state)
+    via_hf = a1.decode(hist, hf_prefix)
+    truth = Qwen35Oracle(cfg, {k: v.float() for k, v in sd.items()})
+    _, tstate = truth.prefill(ids.cpu())
+    exact = truth.decode(hist.cpu(), tstate)
+    assert_bf16_parity(via_hf, native, exact, "decode from a transformers prefix")
+    cache = a1.prefix_to_cache(r1.state, lm.config)
+    nxt = hist[:, 0, :1]
+    with torch.no_grad():
+        hf_next = lm(input_ids=nxt, past_key_values=cache, use_cache=True).logits[:, -1]
+    ours = a1.decode(nxt[:, None, :], r1.state)[:, 0]
+    assert_bf16_parity(hf_next, ours, truth.decode(nxt[:, None, :].cpu(), tstate)[:, 0],
+                       "transformers continuing the native prefix")
