@@ -51,7 +51,7 @@ class Qwen35GRBeamAdapter:
     """
 
     def __init__(self, text_model, lm_head, *, gdn_backend="torch", conv_backend="torch",
-                 attention_backend="torch", gdn_triton_config=None):
+                 attention_backend="torch", gdn_triton_config=None, head_tokens=None):
         native = isinstance(text_model, Qwen35TextModel)
         if not native and not _is_transformers_text_model(text_model):
             raise TypeError("pass the dense Qwen3_5TextModel explicitly")
@@ -89,7 +89,10 @@ class Qwen35GRBeamAdapter:
         self.config = cfg if native else Qwen35Config.from_hf(cfg)
         self.device = device
         self._runner = Qwen35Runner(self.config, text_model.state_dict(),
-                                    lm_head_weight=lm_head.weight, device=device)
+                                    lm_head_weight=lm_head.weight, device=device,
+                                    head_tokens=head_tokens)
+        # logits column -> token id for a SID-only head (None: the full vocabulary)
+        self.vocab_ids = self._runner.head_ids
         self._owner = object()
 
     def _check(self, tokens):

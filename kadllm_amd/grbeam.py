@@ -131,6 +131,16 @@ def extend_history(history, parents, tokens):
     return out
 
 
+def _column_tokens(adapter, tokens):
+    """Token ids of selected logits columns.  An adapter whose head projects to
+    a sub-vocabulary (a SID-only head) names the token of each column in
+    ``vocab_ids``; history and results then hold real token ids."""
+    ids = getattr(adapter, "vocab_ids", None)
+    if ids is None:
+        return tokens
+    return ids.index_select(0, tokens.reshape(-1)).view(tokens.shape)
+
+
 @torch.no_grad()
 def grbeam_search(
     adapter: GRBeamAdapter,
@@ -143,7 +153,9 @@ def grbeam_search(
 
     Call model.eval() first. EOS handling and length penalties are outside
     this fixed-depth API.  No CPU conversion of candidates is performed.
-    Invalid constrained slots remain marked rather than invented.
+    Invalid constrained slots remain marked rather than invented.  With a
+    SID-only head (``adapter.vocab_ids``), logits cover that sub-vocabulary and
+    the softmax runs over it; selected columns become token ids.
     """
     if input_ids.ndim != 2 or min(input_ids.shape) < 1:
         raise ValueError("input_ids must be nonempty [B, prompt_length]")
@@ -184,7 +196,7 @@ def grbeam_search(
             raise ValueError("beam width exceeds the number of candidate slots")
         scores, parents, tokens, valid = select_level(logits, scores, width, mask)
         del logits, mask
-        history = extend_history(history, parents, tokens)
+        history = extend_history(history, parents, _column_tokens(adapter, tokens))
     return GRBeamResult(history, scores, valid)
 
 
@@ -251,5 +263,5 @@ def conditional_search(
             scores, parents, tokens, valid = select_level_grouped(logits, scores, groups, width,
                                                                   mask)
         del logits, mask
-        history = extend_history(history, parents, tokens)
+        history = extend_history(history, parents, _column_tokens(adapter, tokens))
     return GRBeamResult(history, scores, valid)

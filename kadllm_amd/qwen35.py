@@ -70,10 +70,31 @@ def interleave_gate_up(gate, up):
     return torch.stack((g, u), dim=1).reshape(2 * F_, H).contiguous()
 
 
-class Qwen35Runner:
-    """Packed bf16 weights of one Qwen3.5 text model plus its forward passes."""
+def pack_mlp(gate, up, down):
+    """(w_gu, w_down) for the SwiGLU GEMM pair.  Any FFN width works (e.g. the
+    wider MLPs that WideTuning's to_dense merges, src/kadllm/widetuning.py:96-127):
+    the width is zero-padded to a multiple of 64, which adds exact zeros --
+    silu(0) * 0 = 0 through padded gate/up rows, and zero down-projection
+    columns."""
+    F_, H = gate.shape
+    pad = (-F_) % 64
+    if pad:
+        gate = torch.cat((gate, gate.new_zeros(pad, H)), 0)
+        up = torch.cat((up, up.new_zeros(pad, H)), 0)
+        down = torch.cat((down, down.new_zeros(down.shape[0], pad)), 1)
+    return interleave_gate_up(gate, up), down.contiguous()
 
-    def __init__(self, cfg, state_dict, lm_head_weight=None, device=None):
+
+class Qwen35Runner:
+    """Packed bf16 weights of one Qwen3.5 text model plus its forward passes.
+
+    ``head_tokens`` (optional int64 token ids) gives a SID-only head: the LM
+    head projects only to those tokens (README.md:164, the production head that
+    projects to the semantic-ID tokens), logits column c is token
+    head_tokens[c], and the softmax of a search runs over that sub-vocabulary.
+    """
+
+    def __init__(self, cfg, state_dict, lm_head_weight=None, device=None, head_tokens=None):
         self.cfg = cfg
         self.device = torch.device(device) if device is not None else \
             state_dict["embed_tokens.weight"].device
@@ -85,13 +106,20 @@ class Qwen35Runner:
             return state_dict[name].detach().to(device=self.device, dtype=bf).contiguous()
 
         H = cfg.hidden_size
-        for dim, what in ((H, "hidden size"), (cfg.intermediate_size, "intermediate size")):
-            if dim % 64:
-                raise ValueError(f"{what} must be a multiple of 64 for the GEMM kernels")
+        if H % 64:
+            raise ValueError("hidden size must be a multiple of 64 for the GEMM kernels")
         self.embed = get("embed_tokens.weight")
         head = lm_head_weight if lm_head_weight is not None else state_dict.get("lm_head.weight")
         self.lm_head = (self.embed if head is None else
                         head.detach().to(device=self.device, dtype=bf).contiguous())
+        self.head_ids = None
+        if head_tokens is not None:
+            ids = torch.as_tensor(head_tokens, dtype=torch.int64, device=self.device)
+            if ids.ndim != 1 or ids.numel() < 1 or int(ids.min()) < 0 or \
+                    int(ids.max()) >= self.lm_head.shape[0]:
+                raise ValueError("head_tokens must be a nonempty 1-D list of vocabulary ids")
+            self.head_ids = ids.contiguous()
+            self.lm_head = self.lm_head.index_select(0, self.head_ids).contiguous()
         self.norm_w = get("norm.weight")
         self.kd = cfg.linear_num_key_heads * cfg.linear_key_head_dim
         self.vd = cfg.linear_num_value_heads * cfg.linear_value_head_dim
@@ -102,10 +130,11 @@ class Qwen35Runner:
         self.layers = []
         for i, kind in enumerate(cfg.layer_types):
             p = f"layers.{i}."
-            w_gu = interleave_gate_up(get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight"))
+            w_gu, w_down = pack_mlp(get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight"),
+                                    get(p + "mlp.down_proj.weight"))
             common = dict(input_norm=get(p + "input_layernorm.weight"),
                           post_norm=get(p + "post_attention_layernorm.weight"),
-                          w_gu=w_gu, w_down=get(p + "mlp.down_proj.weight"))
+                          w_gu=w_gu, w_down=w_down)
             if kind == "linear_attention":
                 a = p + "linear_attn."
                 w_in = torch.zeros(self.gdn_cols, H, dtype=bf, device=self.device)

@@ -262,3 +262,88 @@ def test_checkpoint_and_cache_interop(device, tmp_path):
     ours = a1.decode(nxt[:, None, :], r1.state)[:, 0]
     assert_bf16_parity(hf_next, ours, truth.decode(nxt[:, None, :].cpu(), tstate)[:, 0],
                        "transformers continuing the native prefix")
+
+
+def _widened_state_dict(cfg, seed, extra):
+    """A bf16 state dict whose layer i MLP is ``extra[i]`` units wider, as
+    WideTuning's to_dense leaves it (src/kadllm/widetuning.py:96-127)."""
+    sd = random_state_dict(cfg, seed=seed, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(seed + 100)
+    for i, n in enumerate(extra):
+        p = f"layers.{i}.mlp."
+        for name in ("gate_proj", "up_proj"):
+            w = sd[p + name + ".weight"]
+            add = (torch.randn(n, w.shape[1], generator=g) * 0.02).to(w.dtype)
+            sd[p + name + ".weight"] = torch.cat((w, add), 0)
+        w = sd[p + "down_proj.weight"]
+        add = (torch.randn(w.shape[0], n, generator=g) * 0.02).to(w.dtype)
+        sd[p + "down_proj.weight"] = torch.cat((w, add), 1)
+    return sd
+
+
+def test_widened_ffn_layers_match_oracle(device):
+    """Per-layer FFN widths that are not multiples of the GEMM tiles (768 + 40,
+    + 1, + 0, + 232): prefill and a 2-token decode."""
+    cfg = tiny_hybrid_config()
+    sd = _widened_state_dict(cfg, 12, [40, 1, 0, 232])
+    assert sd["layers.0.mlp.gate_proj.weight"].shape[0] == 808
+    oracle = Qwen35Oracle(cfg, sd)
+    truth = Qwen35Oracle(cfg, {k: v.float() for k, v in sd.items()})
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}))
+    g = torch.Generator().manual_seed(13)
+    ids = torch.randint(0, cfg.vocab_size, (2, 70), generator=g)
+    hist = torch.randint(0, cfg.vocab_size, (2, 6, 2), generator=g)
+    res = adapter.prefill(ids.to(device))
+    logits = adapter.decode(hist.to(device), res.state)
+    torch.cuda.synchronize()
+    ref_logits, ref_state = oracle.prefill(ids)
+    t_logits, t_state = truth.prefill(ids)
+    assert_bf16_parity(res.logits, ref_logits, t_logits, "widened prefill")
+    assert_bf16_parity(logits, oracle.decode(hist, ref_state), truth.decode(hist, t_state),
+                       "widened decode")
+
+
+def test_sid_only_head_search(device, tiny):
+    """A head that projects only to a subset of token ids (in arbitrary order):
+    logits are the oracle's columns for those ids, the softmax runs over the
+    subset, and the search returns real token ids, each level equal to the
+    oracle's selection on the GPU's own logits."""
+    cfg, oracle, full = tiny
+    g = torch.Generator().manual_seed(31)
+    sid = torch.randperm(cfg.vocab_size, generator=g)[:357]
+    sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16)
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}),
+                                  head_tokens=sid)
+    assert torch.equal(adapter.vocab_ids.cpu(), sid)
+    ids = torch.randint(0, cfg.vocab_size, (2, 45), generator=g)
+    widths = [16, 12, 9]
+    result = grbeam_search(adapter, ids.to(device), widths)
+    torch.cuda.synchronize()
+    toks = result.tokens.cpu()
+    assert toks.shape == (2, 9, 3) and result.valid.all()
+    assert torch.isin(toks, sid).all(), "search returned a token outside the head"
+    pre_logits, state = oracle.prefill(ids)
+    t_logits, t_state = full.truth.prefill(ids)
+    gpu_pre = adapter.prefill(ids.to(device))
+    assert_bf16_parity(gpu_pre.logits, pre_logits[:, sid], t_logits[:, sid], "SID prefill logits")
+    # the same model with the full head: its columns for the subset
+    assert_logits_close(gpu_pre.logits, full.prefill(ids.to(device)).logits[:, sid.to(device)],
+                        "SID vs full-head columns", rel=2e-3, max_frac=1e-2)
+    scores = torch.zeros(2, 1)
+    history = torch.empty(2, 1, 0, dtype=torch.int64)
+    logits = gpu_pre.logits.cpu()[:, None]
+    for step, w in enumerate(widths):
+        if step:
+            logits = adapter.decode(history.to(device), gpu_pre.state).cpu()
+            assert logits.shape == (2, history.shape[1], sid.numel())
+            assert_bf16_parity(logits, oracle.decode(history, state)[..., sid],
+                               full.truth.decode(history, t_state)[..., sid],
+                               f"SID level-{step} logits")
+        scores, parents, cols = grbeam_ref.level_select(logits, scores, w)
+        history = torch.cat((history.gather(1, parents[..., None].expand(2, w, step)),
+                             sid[cols][..., None]), -1)
+    assert torch.equal(history, toks), "GPU search differs from its own teacher-forced replay"
+    assert torch.allclose(result.scores.cpu(), scores, atol=1e-4)
+    with pytest.raises(ValueError):
+        Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}),
+                            head_tokens=[cfg.vocab_size])
