@@ -108,6 +108,9 @@ def main():
     ap.add_argument("--depth", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--prompts", choices=("uniform", "pattern"), default="uniform",
+                    help="uniform: uniform-random prompt ids (default); pattern: the reference "
+                         "runner's prompts, token i of request r = 10 + (i + 17 r) % 100")
     ap.add_argument("--workload", choices=("grbeam", "conditional_sid"), default="grbeam",
                     help="grbeam: the headline full-vocabulary search (default); "
                          "conditional_sid: B8, prefix 4096, coarse widths [32, 32] over the full "
@@ -131,8 +134,12 @@ def main():
     sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16, device=dev)
     model, head = native_model(cfg, sd)
     adapter = Qwen35GRBeamAdapter(model, head)
-    ids = torch.randint(0, cfg.vocab_size, (a.batch, a.prefix),
-                        generator=torch.Generator().manual_seed(0)).to(dev)
+    if a.prompts == "pattern":   # benchmarks/grbeam.py:254-257
+        r = torch.arange(a.batch)[:, None]
+        ids = (10 + (torch.arange(a.prefix)[None, :] + 17 * r) % 100).to(dev)
+    else:
+        ids = torch.randint(0, cfg.vocab_size, (a.batch, a.prefix),
+                            generator=torch.Generator().manual_seed(0)).to(dev)
     widths = [a.beam] * a.depth
 
     def run():
@@ -184,7 +191,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": round(value / H800_REQ_S, 3) if workload_default else None,
         "dtype": "bf16",
-        "data": "synthetic (random-init weights, uniform-random prompt ids)",
+        "data": "synthetic (random-init weights, " + (
+            "uniform-random prompt ids)" if a.prompts == "uniform"
+            else "prompt ids 10 + (i + 17 r) % 100 as in the reference runner)"),
         "config": {"workload": f"grbeam_e2e qwen3.5-0.8B-shaped B{a.batch} P{a.prefix} "
                                f"W{a.beam} depth{a.depth} full-vocab",
                    "batch": a.batch, "prefix": a.prefix, "beam": a.beam, "depth": a.depth,

@@ -162,10 +162,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
   }
 }
 
-// 256x256 tile, 4 waves (2 x 2), each wave a 128x128 sub-tile: 16 MFMA
-// 32x32x16 per 16-deep K step against 8 fragment loads, the highest
-// MFMA-to-LDS ratio the 512-register file allows (a second wave per SIMD
-// would halve it).
+// 256 x BN tiles (BN = 256 or 128), 4 waves (2 x 2), each wave a 128 x BN/2
+// sub-tile: 4 * BN/64 MFMA 32x32x16 per 16-deep K step against 4 + BN/64
+// fragment loads.  256x256 gives the highest MFMA-to-LDS ratio the
+// 512-register file allows (a second wave per SIMD would halve it); 256x128
+// fills the chip on narrow outputs (N = 1024 at M = 8192 is 256 tiles).
 //
 // Operand tiles move HBM -> LDS with global_load_lds_dwordx4 (no register
 // staging): one wave instruction writes 64 x 16 bytes contiguously, i.e. 8
@@ -175,194 +176,70 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
 // lane of a load therefore fetches the global chunk that belongs at its LDS
 // slot.  Two stages of 64-deep K: tile kt+1 is in flight while tile kt feeds
 // the MFMAs.  Each 16-deep step is its own scheduling region with its MFMAs
-// interleaved with the next step's fragment reads (and, in step 0, with the
-// next tile's loads).
+// interleaved with the next step's fragment reads and the next tile's loads
+// (MODE 0: all in step 0; MODE 2: split over steps 0 and 1, which measured
+// 2-5% faster).  MODE 1 stages the same loads through registers
+// (global_load_dwordx4 in step 0, ds_write_b128 in step 2 to the same
+// swizzled positions).
 //
 // Operands are swapped (weight rows are the MFMA's A operand), so each lane's
 // accumulators hold 4 consecutive output columns: the epilogue packs them 8
 // bytes at a time into LDS, and the wave then writes its sub-tile with
-// 16-byte stores (fusing the residual add or SwiGLU on the way).
+// 16-byte stores (fusing the residual add or SwiGLU on the way).  Every
+// configuration accumulates K in the same order, so results are bit-identical
+// across tile shapes.
 constexpr int kT = 256;
-constexpr int kEpiLd = 128 + 8;                  // epilogue LDS row stride (elements)
-constexpr int kStage = 2 * kT * kBK;             // elements per stage: A rows then W rows
-constexpr int kSmem = 2 * kStage > 4 * 128 * kEpiLd ? 2 * kStage : 4 * 128 * kEpiLd;
+
+template <int BN>
+struct Tile256 {
+  static constexpr int NJ = BN / 64;                 // 32-column blocks per wave
+  static constexpr int Stage = (kT + BN) * kBK;      // elements per stage: A rows then W rows
+  static constexpr int EpiLd = BN / 2 + 8;           // epilogue LDS row stride (elements)
+  static constexpr int Smem = 2 * Stage > 4 * 128 * EpiLd ? 2 * Stage : 4 * 128 * EpiLd;
+};
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
 
-__device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)g, (lds_void_t*)lds_block, 16, 0, 0);
-}
-
-// DMA = false: the same tile flow with the loads staged through registers
-// (global_load_dwordx4 in step 0, ds_write_b128 in step 2 to the same
-// swizzled positions).
-template <int EPI, bool DMA>
-__global__ __launch_bounds__(256, 1) void gemm256_kernel(
-    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
-    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
-    int group) {
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[kSmem];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int mtiles = (M + kT - 1) / kT, ntiles = (N + kT - 1) / kT;
+// Origin of this workgroup's 256 x BN tile.  Grouped order: `group`
+// consecutive tiles along the outer dimension share each inner-dimension
+// tile, so an XCD's resident tiles form a 2-D block and both operands are
+// reused from its L2.
+__device__ __forceinline__ void tile_origin(int M, int N, int BN, int n_major, int group, int& m0,
+                                           int& n0) {
+  const int mtiles = (M + kT - 1) / kT, ntiles = (N + BN - 1) / BN;
   const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
-  // grouped order: `group` consecutive tiles along the outer dimension share
-  // each inner-dimension tile, so an XCD's resident tiles form a 2-D block
-  // and both operands are reused from its L2
   const int nx = n_major ? ntiles : mtiles, ny = n_major ? mtiles : ntiles;
   const int gx0 = (lid / (group * ny)) * group, gs = min(nx - gx0, group);
   const int within = lid % (group * ny);
   const int tx = gx0 + within % gs, ty = within / gs;
   const int mi = n_major ? ty : tx, ni = n_major ? tx : ty;
-  const int m0 = mi * kT, n0 = ni * kT;
+  m0 = mi * kT;
+  n0 = ni * BN;
+}
 
-  // DMA: this wave loads row groups g = wave + 4 i (i < 8) of both tiles;
-  // lane L -> row g*8 + L/8, LDS chunk L%8, global chunk (L%8) ^ ((row>>1)&7)
-  const int d_row = lane >> 3;
-  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
-  const bf16_t* a_src[8];
-  const bf16_t* b_src[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = (wave + 4 * i) * 8 + d_row;
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
-    b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
-  }
-  auto issue = [&](int stage, int k0) {
-    bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      dma16(a_src[i] + k0, base + i * 32 * kBK);
-      dma16(b_src[i] + k0, base + kT * kBK + i * 32 * kBK);
-    }
-  };
-  u32x4 ra[DMA ? 1 : 8], rb[DMA ? 1 : 8];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
-      ra[i] = *(const u32x4*)(a_src[i] + k0);
-      rb[i] = *(const u32x4*)(b_src[i] + k0);
-    }
-  };
-  auto stash = [&](int stage) {
-    bf16_t* base = smem + stage * kStage + wave * 8 * kBK + lane * 8;
-#pragma unroll
-    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
-      *(u32x4*)(base + i * 32 * kBK) = ra[i];
-      *(u32x4*)(base + kT * kBK + i * 32 * kBK) = rb[i];
-    }
-  };
+__device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)g, (lds_void_t*)lds_block, 16, 0, 0);
+}
 
-  // fragments: lane reads row lane%32 of a 32-row block at K chunk
-  // kk*2 + lane/32, stored at chunk ^ ((row >> 1) & 7)
-  const int f_row = lane & 31, f_sw = (lane >> 1) & 7, f_hi = lane >> 5;
-  const int fa_row = (wm * 128 + f_row) * kBK;
-  const int fw_row = kT * kBK + (wn * 128 + f_row) * kBK;
-  bf16x8 fa[2][4], fw[2][4];
-  auto load_frags = [&](int stage, int kk, int slot) {
-    const bf16_t* base = smem + stage * kStage + (((kk * 2 + f_hi) ^ f_sw) * 8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      fa[slot][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kBK));
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      fw[slot][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kBK));
-  };
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-  auto mfma_step = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(fw[slot][j], fa[slot][i], acc[i][j]);
-  };
-  // issue order inside one 16-deep step: 8 x (1 MFMA, 1 fragment read
-  // [, 2 DMA loads]), then the remaining 8 MFMAs
-  auto interleave = [&](bool with_dma) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (with_dma) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);  // steps are separate scheduling regions
-  };
-
-  // issue order inside one 16-deep step with LDS writes: 8 x (1 MFMA, 1
-  // fragment read, 2 LDS writes), then the remaining 8 MFMAs
-  auto interleave_stash = [&]() {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  const int KT = K / kBK;
-  if constexpr (DMA) {
-    issue(0, 0);
-  } else {
-    fetch(0);
-    stash(0);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  load_frags(0, 0, 0);
-  for (int kt = 0; kt < KT; ++kt) {
-    __builtin_amdgcn_sched_barrier(0);
-    const int stage = kt & 1;
-    // step 0: loads of the next tile (the last iteration re-fetches the final
-    // tile, keeping the loop body one basic block)
-    if constexpr (DMA)
-      issue(stage ^ 1, min(kt + 1, KT - 1) * kBK);
-    else
-      fetch(min(kt + 1, KT - 1) * kBK);
-    load_frags(stage, 1, 1);
-    mfma_step(0);
-    interleave(true);
-    load_frags(stage, 2, 0);
-    mfma_step(1);
-    interleave(false);
-    load_frags(stage, 3, 1);
-    if constexpr (!DMA) stash(stage ^ 1);  // nobody reads the idle stage
-    mfma_step(0);
-    if constexpr (DMA)
-      interleave(false);
-    else
-      interleave_stash();
-    // step 3: every read of this stage and the next tile's writes have
-    // completed once all waves pass the barrier; prefetch the next stage's
-    // step 0
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    load_frags(stage ^ 1, 0, 0);
-    mfma_step(1);
-    interleave(false);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  // epilogue.  acc[i][j][e]: row m = i*32 + lane%32, column
-  // n = j*32 + (e/4)*8 + (lane/32)*4 + e%4 of the wave's 128x128 sub-tile.
+// Epilogue.  acc[i][j][e]: row m = i*32 + lane%32, column
+// n = j*32 + (e/4)*8 + (lane/32)*4 + e%4 of the wave's 128 x BN/2 sub-tile
+// (waves 2 x 2).  The accumulators go through LDS (smem free on entry) and
+// leave as 16-byte row stores, fusing the residual add or SwiGLU.
+template <int EPI, int BN>
+__device__ __forceinline__ void epilogue_tile(f32x16 (&acc)[4][Tile256<BN>::NJ], bf16_t* smem,
+                                              int lane, int wave, int m0, int n0, bf16_t* C,
+                                              int64_t ldc, const bf16_t* R, int64_t ldr, int M,
+                                              int N) {
+  constexpr int NJ = Tile256<BN>::NJ, kEpiLd = Tile256<BN>::EpiLd;
+  const int wm = wave >> 1, wn = wave & 1;
   bf16_t* ep = smem + wave * 128 * kEpiLd;
   const int e_row = lane & 31, e_col = (lane >> 5) * 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if constexpr (EPI == KAD_EPI_SWIGLU) {
 #pragma unroll
-      for (int j = 0; j < 4; j += 2) {
+      for (int j = 0; j < NJ; j += 2) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           u32x2 packed;
@@ -383,7 +260,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           u32x2 packed;
@@ -397,10 +274,10 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
     }
   }
   __syncthreads();
-  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? 64 : 128;  // wave sub-tile output columns
+  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? BN / 4 : BN / 2;  // wave sub-tile output columns
   constexpr int kChunks = kCols / 8, kRowsPer = 64 / kChunks;
   const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
-  const int out_n0 = EPI == KAD_EPI_SWIGLU ? n0 / 2 + wn * 64 : n0 + wn * 128;
+  const int out_n0 = EPI == KAD_EPI_SWIGLU ? n0 / 2 + wn * kCols : n0 + wn * kCols;
   const int n_out = EPI == KAD_EPI_SWIGLU ? N / 2 : N;
 #pragma unroll 4
   for (int r = c_row; r < 128; r += kRowsPer) {
@@ -420,23 +297,174 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
   }
 }
 
-template <int EPI>
-int launch256(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-              const void* R, int64_t ldr, int M, int N, int K, bool dma, hipStream_t s) {
-  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, kT);
+// issue order inside one 16-deep step: NM MFMAs, each followed by up to one
+// fragment read (NR in all), and the step's NV global loads and NW LDS writes
+// spread one per MFMA (two when there are at least NM of them)
+template <int NM, int NR, int NV, int NW>
+__device__ __forceinline__ void interleave_step() {
+  constexpr int PV = NV >= NM ? 2 : 1, PW = NW >= NM ? 2 : 1;
+#pragma unroll
+  for (int t = 0; t < NM; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (t < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (t * PV < NV) __builtin_amdgcn_sched_group_barrier(0x020, PV, 0);
+    if (t * PW < NW) __builtin_amdgcn_sched_group_barrier(0x200, PW, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // steps are separate scheduling regions
+}
+
+template <int EPI, int BN, int MODE>
+__global__ __launch_bounds__(256, 1) void gemm256_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group) {
+  using TL = Tile256<BN>;
+  constexpr int NJ = TL::NJ, kStage = TL::Stage;
+  constexpr int WG = BN / 32;          // W row groups of 8 rows per wave
+  constexpr bool DMA = MODE != 1;
+  constexpr int NM = 4 * NJ, NR = 4 + NJ;  // MFMAs and fragment reads per step
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[TL::Smem];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int m0, n0;
+  tile_origin(M, N, BN, n_major, group, m0, n0);
+
+  // this wave loads row groups g = wave + 4 i (8 rows each) of both tiles;
+  // lane L -> row g*8 + L/8, LDS chunk L%8, global chunk (L%8) ^ ((row>>1)&7)
+  const int d_row = lane >> 3;
+  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
+  const bf16_t* a_src[8];
+  const bf16_t* b_src[WG];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = (wave + 4 * i) * 8 + d_row;
+    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
+    if (i < WG) b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
+  }
+  // row groups [i0, i1) of the A tile and [i0 * WG / 8, i1 * WG / 8) of the W tile
+  auto issue = [&](int stage, int k0, int i0, int i1) {
+    bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
+#pragma unroll
+    for (int i = i0; i < i1; ++i) dma16(a_src[i] + k0, base + i * 32 * kBK);
+#pragma unroll
+    for (int i = i0 * WG / 8; i < i1 * WG / 8; ++i)
+      dma16(b_src[i] + k0, base + kT * kBK + i * 32 * kBK);
+  };
+  u32x4 ra[DMA ? 1 : 8], rb[DMA ? 1 : WG];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
+      ra[i] = *(const u32x4*)(a_src[i] + k0);
+      if (i < WG) rb[i] = *(const u32x4*)(b_src[i] + k0);
+    }
+  };
+  auto stash = [&](int stage) {
+    bf16_t* base = smem + stage * kStage + wave * 8 * kBK + lane * 8;
+#pragma unroll
+    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
+      *(u32x4*)(base + i * 32 * kBK) = ra[i];
+      if (i < WG) *(u32x4*)(base + kT * kBK + i * 32 * kBK) = rb[i];
+    }
+  };
+
+  // fragments: lane reads row lane%32 of a 32-row block at K chunk
+  // kk*2 + lane/32, stored at chunk ^ ((row >> 1) & 7)
+  const int f_row = lane & 31, f_sw = (lane >> 1) & 7, f_hi = lane >> 5;
+  const int fa_row = (wm * 128 + f_row) * kBK;
+  const int fw_row = kT * kBK + (wn * (BN / 2) + f_row) * kBK;
+  bf16x8 fa[2][4], fw[2][NJ];
+  auto load_frags = [&](int stage, int kk, int slot) {
+    const bf16_t* base = smem + stage * kStage + (((kk * 2 + f_hi) ^ f_sw) * 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[slot][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kBK));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      fw[slot][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kBK));
+  };
+
+  f32x16 acc[4][NJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
+  auto mfma_step = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x16(fw[slot][j], fa[slot][i], acc[i][j]);
+  };
+
+  constexpr int kLoads = 8 + WG;  // global loads per wave per K tile
+  const int KT = K / kBK;
+  if constexpr (DMA) {
+    issue(0, 0, 0, 8);
+  } else {
+    fetch(0);
+    stash(0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  load_frags(0, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int stage = kt & 1;
+    // loads of the next tile (the last iteration re-fetches the final tile,
+    // keeping the loop body one basic block)
+    const int kn = min(kt + 1, KT - 1) * kBK;
+    if constexpr (MODE == 2) {
+      issue(stage ^ 1, kn, 0, 4);
+      load_frags(stage, 1, 1);
+      mfma_step(0);
+      interleave_step<NM, NR, kLoads / 2, 0>();
+      issue(stage ^ 1, kn, 4, 8);
+      load_frags(stage, 2, 0);
+      mfma_step(1);
+      interleave_step<NM, NR, kLoads / 2, 0>();
+    } else {
+      if constexpr (DMA)
+        issue(stage ^ 1, kn, 0, 8);
+      else
+        fetch(kn);
+      load_frags(stage, 1, 1);
+      mfma_step(0);
+      interleave_step<NM, NR, kLoads, 0>();
+      load_frags(stage, 2, 0);
+      mfma_step(1);
+      interleave_step<NM, NR, 0, 0>();
+    }
+    load_frags(stage, 3, 1);
+    if constexpr (!DMA) stash(stage ^ 1);  // nobody reads the idle stage
+    mfma_step(0);
+    interleave_step<NM, NR, 0, DMA ? 0 : kLoads>();
+    // step 3: every read of this stage and the next tile's writes have
+    // completed once all waves pass the barrier; prefetch the next stage's
+    // step 0
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    load_frags(stage ^ 1, 0, 0);
+    mfma_step(1);
+    interleave_step<NM, NR, 0, 0>();
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  epilogue_tile<EPI, BN>(acc, smem, lane, wave, m0, n0, C, ldc, R, ldr, M, N);
+}
+
+template <int EPI, int BN, int MODE>
+int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
   if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
   const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
   static const int group = [] {
     const char* e = getenv("KAD_GEMM_GROUP");
     return e ? atoi(e) : 8;
   }();
-  if (!dma) {
-    hipLaunchKernelGGL((gemm256_kernel<EPI, false>), dim3((unsigned)nblocks), dim3(256), 0, s,
-                       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
-                       (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group);
-    return kad_launch_status("gemm256_kernel");
-  }
-  hipLaunchKernelGGL((gemm256_kernel<EPI, true>), dim3((unsigned)nblocks), dim3(256), 0, s,
+  hipLaunchKernelGGL((gemm256_kernel<EPI, BN, MODE>), dim3((unsigned)nblocks), dim3(256), 0, s,
                      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
                      (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group);
   return kad_launch_status("gemm256_kernel");
@@ -467,20 +495,25 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled)
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
-       CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8 };
+       CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8,
+       CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
     // the pipelined 256x256 kernel when its tiles still fill every CU (and
-    // the output suits 16-byte stores); 128x128 otherwise (measured on the
-    // decode/prefill projection shapes)
+    // the output suits 16-byte stores), then the pipelined 256x128 one;
+    // 128x128 otherwise (measured on the decode/prefill projection shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
+    const int64_t tiles128 = kad_cdiv(M, 256) * kad_cdiv(N, 128);
+    const bool vec = vector_epilogue_ok(C, ldc, R, ldr, N, EPI);
     if (M <= 64)
       cfg = CFG_32x256;
     else if (tiles256 >= 256)
-      cfg = vector_epilogue_ok(C, ldc, R, ldr, N, EPI) ? CFG_256x256_PIPE : CFG_256x256_8W;
+      cfg = vec ? CFG_256x256_SPREAD : CFG_256x256_8W;
+    else if (vec && tiles128 >= 256)
+      cfg = CFG_256x128_PIPE;
     else
       cfg = CFG_128x128;
   }
@@ -492,13 +525,19 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_256x256_8W:
       return launch<256, 256, 2, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_PIPE:
-      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
-        KAD_UNSUPPORTED("tile configuration 7 needs 16-byte aligned outputs in 8-column units");
-      return launch256<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, true, s);
     case CFG_256x256_PIPE_REG:
+    case CFG_256x256_SPREAD:
+    case CFG_256x128_PIPE:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
-        KAD_UNSUPPORTED("tile configuration 8 needs 16-byte aligned outputs in 8-column units");
-      return launch256<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, false, s);
+        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
+                        cfg);
+      if (cfg == CFG_256x256_PIPE)
+        return launch_tile<EPI, 256, 0>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_256x256_PIPE_REG)
+        return launch_tile<EPI, 256, 1>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_256x256_SPREAD)
+        return launch_tile<EPI, 256, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return launch_tile<EPI, 128, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x128_8W:
       return launch<256, 128, 4, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     default: KAD_UNSUPPORTED("unknown gemm tile configuration %d", cfg);

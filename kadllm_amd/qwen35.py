@@ -38,7 +38,8 @@ def _round_up(x, m):
 class _GdnLayer:
     input_norm: torch.Tensor
     post_norm: torch.Tensor
-    w_in: torch.Tensor        # [qkv | z | a | b | pad, H]
+    w_in: torch.Tensor        # [qkv | z, H]
+    w_ab: torch.Tensor        # [a | b, H]
     conv_w: torch.Tensor      # [C, 4]
     A_log: torch.Tensor
     dt_bias: torch.Tensor
@@ -137,16 +138,18 @@ class Qwen35Runner:
                           w_gu=w_gu, w_down=w_down)
             if kind == "linear_attention":
                 a = p + "linear_attn."
-                w_in = torch.zeros(self.gdn_cols, H, dtype=bf, device=self.device)
-                w_in[:self.conv_dim] = get(a + "in_proj_qkv.weight")
-                w_in[self.conv_dim:self.conv_dim + self.vd] = get(a + "in_proj_z.weight")
-                o = self.conv_dim + self.vd
-                w_in[o:o + hv] = get(a + "in_proj_a.weight")
-                w_in[o + hv:o + 2 * hv] = get(a + "in_proj_b.weight")
+                # two GEMMs fill one projection row [qkv | z | a | b | pad]: the
+                # wide [qkv | z] one keeps its N a multiple of the 256-column
+                # tile (the 32 gate columns would add a nearly empty column
+                # of tiles to it)
+                w_in = torch.cat((get(a + "in_proj_qkv.weight"), get(a + "in_proj_z.weight")),
+                                 0).contiguous()
+                w_ab = torch.cat((get(a + "in_proj_a.weight"), get(a + "in_proj_b.weight")),
+                                 0).contiguous()
                 if cfg.linear_conv_kernel_dim != 4:
                     raise ValueError("the conv kernels are specialised for width 4")
                 self.layers.append(_GdnLayer(
-                    w_in=w_in, conv_w=get(a + "conv1d.weight").reshape(self.conv_dim, 4).contiguous(),
+                    w_in=w_in, w_ab=w_ab, conv_w=get(a + "conv1d.weight").reshape(self.conv_dim, 4).contiguous(),
                     A_log=get(a + "A_log"), dt_bias=get(a + "dt_bias"), norm_w=get(a + "norm.weight"),
                     w_out=get(a + "out_proj.weight"), **common))
             else:
@@ -167,6 +170,15 @@ class Qwen35Runner:
         n2 = layers.rmsnorm(x, lyr.post_norm, cfg.rms_norm_eps)
         h = layers.gemm(n2, lyr.w_gu, epilogue=layers.EPI_SWIGLU)
         layers.gemm(h, lyr.w_down, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
+
+    def _gdn_proj(self, lyr, n, out=None):
+        """[rows, gdn_cols] projection row [qkv | z | a | b | pad] of n (or into out)."""
+        if out is None:
+            out = torch.empty(n.shape[0], self.gdn_cols, dtype=torch.bfloat16, device=n.device)
+        c = self.conv_dim + self.vd
+        layers.gemm(n, lyr.w_in, out=out[:, :c])
+        layers.gemm(n, lyr.w_ab, out=out[:, c:c + lyr.w_ab.shape[0]])
+        return out
 
     def _gdn_gates(self, lyr, proj):
         hv = self.cfg.linear_num_value_heads
@@ -196,7 +208,7 @@ class Qwen35Runner:
         for lyr in self.layers:
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
-                proj = layers.gemm(n, lyr.w_in)
+                proj = self._gdn_proj(lyr, n)
                 conv = torch.empty(rows, self.conv_dim, dtype=torch.bfloat16, device=dev)
                 conv_state = torch.empty(B, self.conv_dim, 4, dtype=torch.bfloat16, device=dev)
                 _lib.call("kad_causal_conv_prefill", _lib.ptr(proj), proj.stride(0),
@@ -259,7 +271,7 @@ class Qwen35Runner:
         for lyr, cached in zip(self.layers, prefix_layers):
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
-                proj = layers.gemm(n, lyr.w_in)
+                proj = self._gdn_proj(lyr, n)
                 ld = proj.stride(0)
                 conv = torch.empty(R, C, dtype=torch.bfloat16, device=dev)
                 cs = cached[0]
@@ -351,7 +363,7 @@ class Qwen35Runner:
                 pv = proj.view(BW, T, cols)
                 if T > 1:
                     follow(cache.layers[li], proj, T - 1, cols * 2, cols * 2, cols * 2)
-                layers.gemm(n, lyr.w_in, out=pv[:, T - 1])
+                self._gdn_proj(lyr, n, out=pv[:, T - 1])
                 conv = torch.empty(BW * T, C, dtype=torch.bfloat16, device=dev)
                 cs = cached[0]
                 _lib.call("kad_causal_conv_suffix", _lib.ptr(proj), T * cols, 1, cols, _lib.ptr(cs),
