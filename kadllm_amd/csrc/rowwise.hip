@@ -178,6 +178,87 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   for (int i = 0; i < per; ++i) o[lane + 64 * i] = f2bf(outv[i]);
 }
 
+// The same operation with 16-byte accesses: one wave per token, LPH = D/8
+// lanes per head (8 consecutive elements each), 64/LPH heads per pass.  The
+// rotary cos/sin are computed once per token (lane l evaluates frequency
+// l % (rot/2)) and reused by every head; the rotate-half partner (dim d +- rot/2, P = rot/16 lanes
+// away) comes from a lane exchange.  Needs rot/16 a power of two (or rot 0).
+__global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
+    const bf16_t* __restrict__ src, int64_t ld_src, int64_t src_head_stride, int heads,
+    const bf16_t* __restrict__ w, bf16_t* __restrict__ dst, int64_t period, int64_t s_b,
+    int64_t s_t, int64_t s_h, int64_t rows, int D, int rot, const float* __restrict__ inv_freq,
+    int64_t pos0, int64_t pos_period, float eps, int do_norm) {
+  const int64_t tok = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+  const int lane = threadIdx.x & 63;
+  if (tok >= rows) return;
+  const int lph = D / 8, hpp = 64 / lph;
+  const int m = lane % lph, d0 = m * 8;
+  const int half = rot / 2, P = rot / 16;
+  const bool in_rot = d0 < rot;
+  float wv[8];
+  if (do_norm) {
+    unpack8(*(const u32x4*)(w + d0), wv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wv[i] += 1.0f;
+  }
+  float cs[8], sn[8];
+  const float pos = (float)(pos0 + tok % pos_period);
+  if (half <= 64) {
+    // lane l evaluates frequency l % half once; lanes fetch their 8
+    float c1 = 0.f, s1 = 0.f;
+    if (half) {
+      const float ang = pos * inv_freq[lane % half];
+      c1 = round_bf(cosf(ang));
+      s1 = round_bf(sinf(ang));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int src_lane = half ? (d0 + i) % half : 0;
+      cs[i] = __shfl(c1, src_lane, 64);
+      sn[i] = __shfl(s1, src_lane, 64);
+    }
+  } else if (in_rot) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float ang = pos * inv_freq[(d0 + i) % half];
+      cs[i] = round_bf(cosf(ang));
+      sn[i] = round_bf(sinf(ang));
+    }
+  }
+  const bf16_t* srow = src + tok * ld_src;
+  bf16_t* drow = dst + (tok / period) * s_b + (tok % period) * s_t;
+  for (int h0 = 0; h0 < heads; h0 += hpp) {
+    const int hh = h0 + lane / lph;
+    const bool live = hh < heads;
+    float v[8];
+    unpack8(*(const u32x4*)(srow + (int64_t)(live ? hh : h0) * src_head_stride + d0), v);
+    if (do_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+      ss = group_sum(ss, lph);
+      const float r = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = round_bf((v[i] * r) * wv[i]);
+    }
+    if (rot) {
+      // every lane takes part in the exchange; lanes outside [0, rot) keep v
+      float pr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pr[i] = __shfl_xor(v[i], P, 64);
+      if (in_rot) {
+        const bool lo = d0 < half;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float rh = lo ? -pr[i] : pr[i];
+          v[i] = round_bf(round_bf(v[i] * cs[i]) + round_bf(rh * sn[i]));
+        }
+      }
+    }
+    if (live) *(u32x4*)(drow + (int64_t)hh * s_h + d0) = pack8(v);
+  }
+}
+
 // copy [rows, heads, D] head rows into a strided destination (prefill V cache)
 __global__ __launch_bounds__(256) void scatter_heads_kernel(const bf16_t* __restrict__ src,
                                                             int64_t ld_src, int heads, int D,
@@ -271,6 +352,19 @@ extern "C" int kad_qk_norm_rope(const void* src, int64_t ld_src, int64_t src_hea
   KAD_REQUIRE(rows > 0 && heads > 0 && D % 64 == 0 && D <= 512, "D must be a multiple of 64, <= 512");
   KAD_REQUIRE(rot >= 0 && rot <= D && rot % 2 == 0, "bad rotary dimension");
   KAD_REQUIRE(period > 0 && pos_period > 0, "bad periods");
+  const int P = rot / 16;
+  const bool vec = D % 8 == 0 && D / 8 <= 64 && (64 % (D / 8)) == 0 &&
+                   (rot == 0 || (rot % 16 == 0 && (P & (P - 1)) == 0)) &&
+                   aligned16(src) && aligned16(dst) && (!do_norm || aligned16(w)) &&
+                   ld_src % 8 == 0 && src_head_stride % 8 == 0 && s_b % 8 == 0 && s_t % 8 == 0 &&
+                   s_h % 8 == 0;
+  if (vec) {
+    hipLaunchKernelGGL(qk_norm_rope_vec_kernel, dim3((unsigned)kad_cdiv(rows, 4)), dim3(256), 0,
+                       (hipStream_t)stream, (const bf16_t*)src, ld_src, src_head_stride, heads,
+                       (const bf16_t*)w, (bf16_t*)dst, period, s_b, s_t, s_h, rows, D, rot,
+                       inv_freq, pos0, pos_period, eps, do_norm);
+    return kad_launch_status("qk_norm_rope_vec_kernel");
+  }
   const int64_t waves = rows * heads;
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)kad_cdiv(waves, 4)), dim3(256), 0,
                      (hipStream_t)stream, (const bf16_t*)src, ld_src, src_head_stride, heads,
