@@ -310,6 +310,470 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Attention with 64 query rows per wave (two 32-row MFMA column blocks), so
+// every K and V fragment read from LDS feeds two MFMAs.  Work unit: one
+// (request, KV head) and 256 query rows; 32-key tiles of K and V move
+// HBM -> LDS by global_load_lds_dwordx4 (three stages in flight) in their
+// row-major layout, XOR-swizzled per 16-byte chunk so that every fragment
+// read is bank-conflict free.  Vᵀ fragments come straight from the row-major
+// V tile with ds_read_b64_tr_b16 (within each 16-lane group, lane i receives
+// element i % 4 of the 8-byte pieces addressed by lanes 4e + i / 4, e < 4):
+// lanes address 4 keys x 4 pieces of d and each receives 4 keys of one d.
+// The running max is raised lazily (only when a tile's max exceeds it by
+// more than 2^8), which skips the rescale of O in almost every tile; a row's
+// result does not depend on the other rows of its wave.
+constexpr int kKeys2 = 32;                 // keys per tile
+constexpr int kStages2 = 3;
+
+template <int D>
+struct Attn2 {
+  // head dim 256: two waves share 64 query rows and split the head dim (the
+  // full 256 x 64 fp32 O^T plus 64 query rows of Q would not fit one wave's
+  // registers): each forms the partial scores over its half of d, the two
+  // exchange them through LDS, and each accumulates its half of O.  Smaller
+  // heads: one wave per 64 rows.
+  static constexpr int DS = D > 128 ? 2 : 1;
+  static constexpr int ROWS = 64 * 4 / DS;          // query rows per workgroup
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per K/V row
+  static constexpr int tile = kKeys2 * D;           // elements per K (or V) tile
+  static constexpr int stage = 2 * tile;
+  // bytes: the K/V stages, then (head dim 256) the partial-score exchange of
+  // the two waves of a query group, 32 floats per lane
+  static constexpr int xoff = kStages2 * stage;     // elements
+  static constexpr int lds = kStages2 * stage * 2 + (DS == 2 ? 4 * 64 * 32 * 4 : 0);
+  static constexpr int LOADS = CPR / 8;             // DMA instructions per wave per K (or V) tile
+  // physical chunk of logical chunk c in row r
+  __device__ static __forceinline__ int swk(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
+  __device__ static __forceinline__ int swv(int r) { return D == 64 ? ((r >> 1) & 1) * 4 : (r & 3) * 4; }
+};
+
+// barrier without the full memory fence of __syncthreads (which also waits
+// for the prefetch loads still in flight); LDS traffic is ordered by the
+// caller's waits
+__device__ __forceinline__ void tile_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void attn_lds_t;
+typedef __attribute__((address_space(1))) void attn_global_t;
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
+  using AT = Attn2<D>;
+  constexpr int KS = D / 16;   // k16 steps over the head dim
+  constexpr int DS = AT::DS;   // waves sharing one group of 64 query rows
+  constexpr int DT = D / 32 / DS;  // 32-row d tiles of O^T per wave
+  constexpr int KSW = KS / DS;     // k16 steps of the partial scores per wave
+  constexpr int ROWS = AT::ROWS;
+  constexpr int CPR = AT::CPR;
+  extern __shared__ __attribute__((aligned(1024))) bf16_t smem[];
+  __shared__ int redo;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hi = lane >> 5, col = lane & 31;
+  const int qgrp = wave / DS;            // query group of 64 rows
+  const int dbase = (wave % DS) * DT;    // this wave's first d tile
+  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int qb_blk = lid % a.nqblk;
+  const int bk = lid / a.nqblk;
+  const int kh = bk % a.HK, b = bk / a.HK;
+  const int G = a.H / a.HK;
+  const int64_t rows_total = CAUSAL ? (int64_t)a.L * G : (int64_t)a.W * G * a.T;
+
+  // this lane's query row of block qb: token n (batch row), suffix position
+  // or prompt position t, head h (recomputed where needed to save registers)
+  auto row_of_q = [&](int qb, int64_t& n, int& t, int& h) {
+    int64_t r = (int64_t)qb_blk * ROWS + qgrp * 64 + qb * 32 + col;
+    if (r >= rows_total) r = 0;
+    int g;
+    if (CAUSAL) {
+      t = (int)(r / G);
+      g = (int)(r % G);
+      n = b;
+    } else {
+      t = (int)(r % a.T);
+      const int64_t wg = r / a.T;
+      g = (int)(wg % G);
+      n = (int64_t)b * a.W + wg / G;
+    }
+    h = kh * G + g;
+  };
+  bf16x8 qf[2][KSW];  // this wave's half of d (head dim 256) or all of it
+  int pos[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int64_t n;
+    int t, h;
+    row_of_q(qb, n, t, h);
+    pos[qb] = t;
+    const bf16_t* qrow = a.q + n * a.sq_n + (int64_t)t * a.sq_t + (int64_t)h * a.sq_h;
+#pragma unroll
+    for (int s = 0; s < KSW; ++s)
+      qf[qb][s] = as_bf16x8(*(const u32x4*)(qrow + (dbase * 2 + s) * 16 + hi * 8));
+  }
+  // partial scores of the two waves of a query group: written as 32 floats
+  // per lane (8 x 16 bytes, lane-contiguous), read back and added by both
+  float* xbuf = (float*)(smem + AT::xoff);
+  auto exchange = [&](float* v, int n) {  // n <= 32, a multiple of 4
+    if constexpr (DS == 2) {
+      float* mine = xbuf + wave * 64 * 32;
+      const float* other = xbuf + (wave ^ 1) * 64 * 32;
+#pragma unroll
+      for (int c = 0; c < n / 4; ++c)
+        *(f32x4*)(mine + (c * 64 + lane) * 4) = f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < n / 4; ++c) {
+        const f32x4 o = *(const f32x4*)(other + (c * 64 + lane) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * c + e] += o[e];
+      }
+    }
+  };
+  const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
+
+  // this wave's part of the raw suffix dot product j of block qb (decode)
+  auto suffix_part = [&](int qb, int j) -> float {
+    if (CAUSAL || j >= a.Tk) return 0.f;
+    int64_t n;
+    int t, h;
+    row_of_q(qb, n, t, h);
+    const bf16_t* krow = a.sk + n * a.ssk_n + (int64_t)j * a.ssk_t + (int64_t)kh * a.ssk_h;
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < KSW; ++s) {
+      const bf16x8 kb = as_bf16x8(*(const u32x4*)(krow + (dbase * 2 + s) * 16 + hi * 8));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part += (float)qf[qb][s][i] * (float)kb[i];
+    }
+    return part + __shfl_xor(part, 32, 64);
+  };
+
+  // ---- prefix key range and the DMA plan
+  int kend = a.L;
+  if (CAUSAL) {
+    const int64_t rlast = min((int64_t)(qb_blk + 1) * ROWS, rows_total) - 1;
+    kend = (int)(rlast / G) + 1;
+  }
+  const int ntiles = (kend + kKeys2 - 1) / kKeys2;
+  const bf16_t* pkb = a.pk + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
+  const bf16_t* pvb = a.pv + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
+  // DMA: instruction ii = wave + 4 k of a tile covers tile chunks ii*64 + lane
+  // (row = chunk / CPR, physical chunk = chunk % CPR; the lane fetches the
+  // logical chunk that belongs there).  Rows of instruction k are
+  // (wave + 4k) * (64 / CPR) + lane / CPR.
+  const int d_row = lane / CPR, d_pc = lane % CPR;
+  auto issue = [&](int tile, int stage) {
+    const int k0 = tile * kKeys2;
+    bf16_t* kd = smem + stage * AT::stage;
+    bf16_t* vd = kd + AT::tile;
+#pragma unroll
+    for (int k = 0; k < AT::LOADS; ++k) {
+      const int r = (wave + 4 * k) * (64 / CPR) + d_row;
+      const int64_t key = min(k0 + r, a.L - 1);
+      const int ioff = (wave + 4 * k) * 64 * 8;
+      __builtin_amdgcn_global_load_lds(
+          (attn_global_t*)(pkb + key * a.sp_l + (d_pc ^ AT::swk(r)) * 8),
+          (attn_lds_t*)(kd + ioff), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (attn_global_t*)(pvb + key * a.sp_l + (d_pc ^ AT::swv(r)) * 8),
+          (attn_lds_t*)(vd + ioff), 16, 0, 0);
+    }
+  };
+
+  // K fragment (A operand, 32 keys x 16 d): row col, logical chunk 2s + hi.
+  // The swizzle only touches the low 4 bits of the chunk, so the offsets of
+  // steps s and s + 8 differ by 16 chunks: 8 per-lane offsets cover all steps.
+  int k_off[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int c = 2 * s + hi;
+    k_off[s] = col * D + (c < CPR ? (c ^ AT::swk(col)) * 8 : 0);
+  }
+  // V^T fragment pieces: lane i of group g (h = g / 2, dg = g % 2) addresses
+  // key 16 ks + 8 rd + 4 h + i / 4 at d = dt*32 + dg*16 + (i % 4)*4.  The
+  // swizzle depends on key % 4 = (i / 4) % 4 only, and touches the low two
+  // bits of the 32-d tile index: 4 per-lane offsets cover every (ks, rd, dt).
+  int v_off[4];
+  {
+    const int grp = lane >> 4, gi = lane & 15;
+    const int v_row = 4 * (grp >> 1) + (gi >> 2);
+    const int v_dq = (grp & 1) * 16 + (gi & 3) * 4;
+    const int v_sw = AT::swv(v_row);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int d = dt * 32 + v_dq;
+      v_off[dt] = v_row * D + ((d >> 3) < CPR ? (((d >> 3) ^ v_sw) * 8) + (d & 7) : 0);
+    }
+  }
+
+  // Softmax with a fixed reference: p = 2^(s - m_ref), where m_ref is the
+  // first max a row sees (its suffix, or its first key tile).  O is never
+  // rescaled; a row whose later scores exceed m_ref by more than 2^64 is
+  // flagged, and then the workgroup runs the whole key loop again with
+  // m_ref = the row's true max (which no score exceeds).  The suffix keys'
+  // scores are formed first (they set m_ref in decode) and their V rows are
+  // added in the epilogue, so that O is only ever touched by MFMAs in the loop.
+  float m_ref[2] = {-INFINITY, -INFINITY};
+  float sc[2][4];
+  if (!CAUSAL) {
+    float part[8];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) part[qb * 4 + j] = suffix_part(qb, j);
+    exchange(part, 8);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      int64_t n;
+      int t, h;
+      row_of_q(qb, n, t, h);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sc[qb][j] = j < a.Tk && j <= t + a.qoff ? part[qb * 4 + j] * sl2 : -INFINITY;
+        m_ref[qb] = fmaxf(m_ref[qb], sc[qb][j]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sc[qb][j] = -INFINITY;
+  }
+  float m_true[2] = {m_ref[0], m_ref[1]};
+  float l[2];
+  f32x16 O[2][DT];
+  for (int pass = 0; pass < 2; ++pass) {
+    bool overflow = false;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      l[qb] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (sc[qb][j] != -INFINITY) l[qb] += exp2f(sc[qb][j] - m_ref[qb]);
+#pragma unroll
+      for (int i = 0; i < DT; ++i) O[qb][i] = f32x16{};
+    }
+
+    // ---- prefix keys [0, kend)
+    if (ntiles > 0) issue(0, 0);
+    if (ntiles > 1) issue(1, 1);
+    for (int tile = 0; tile < ntiles; ++tile) {
+      const int stage = tile % kStages2;
+      // this tile's loads have landed (the newer tile's stay in flight)
+      if (tile + 1 < ntiles)
+        __builtin_amdgcn_s_waitcnt(0x0070 | ((2 * AT::LOADS) & 0xF) | (((2 * AT::LOADS) >> 4) << 14));
+      else
+        __builtin_amdgcn_s_waitcnt(0x0070);
+      tile_barrier();
+      const bf16_t* ks = smem + stage * AT::stage;
+      const bf16_t* vs = ks + AT::tile;
+
+      // S^T[key, query] for 32 keys, both query blocks; each K fragment read
+      // is issued one step ahead of its two MFMAs
+      f32x16 st[2] = {f32x16{}, f32x16{}};
+      auto kfrag = [&](int s) {
+        const int sg = dbase * 2 + s;  // d step
+        return as_bf16x8(*(const u32x4*)(ks + k_off[sg & 7] + (sg >> 3) * 128));
+      };
+      __builtin_amdgcn_sched_barrier(0);
+      bf16x8 kf[2];
+      kf[0] = kfrag(0);
+#pragma unroll
+      for (int s = 0; s < KSW; ++s) {
+        // step s: the read of step s + 1, then the two MFMAs of step s
+        if (s + 1 < KSW) kf[(s + 1) & 1] = kfrag(s + 1);
+        st[0] = mfma32x32x16(kf[s & 1], qf[0][s], st[0]);
+        st[1] = mfma32x32x16(kf[s & 1], qf[1][s], st[1]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (DS == 2) {
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          v[j] = st[0][j];
+          v[16 + j] = st[1][j];
+        }
+        exchange(v, 32);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          st[0][j] = v[j];
+          st[1][j] = v[16 + j];
+        }
+      }
+
+      const int k0 = tile * kKeys2;
+      // keys of this tile a lane sees: k0 + hi*4 + kj, kj = (j/4)*8 + j%4 <= 27;
+      // tiles wholly visible to every row of the wave skip the masking
+      int lim[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+        lim[qb] = (CAUSAL ? min(kend - 1, pos[qb]) : kend - 1) - k0 - hi * 4;
+      const bool masked = __ballot(min(lim[0], lim[1]) < 27) != 0 || (!CAUSAL && a.mask);
+      if (masked) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int kj = (j / 4) * 8 + (j % 4);
+            bool ok = kj <= lim[qb];
+            if (!CAUSAL && a.mask)
+              ok = ok && a.mask[(int64_t)b * a.L + min(k0 + hi * 4 + kj, a.L - 1)] != 0;
+            if (!ok) st[qb][j] = -INFINITY;
+          }
+      }
+      bf16x8 pf[2][2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        // raw scores: the max is taken before scaling (scale > 0)
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) tmax = fmaxf(tmax, st[qb][j]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * sl2;
+        if (m_ref[qb] == -INFINITY) m_ref[qb] = tmax;  // nothing accumulated yet
+        m_true[qb] = fmaxf(m_true[qb], tmax);
+        overflow |= tmax > m_ref[qb] + 64.0f;
+        // p = 2^(s*scale - m_ref): the hardware exp2 gives 0 for -inf
+        const float nm = m_ref[qb] == -INFINITY ? 0.f : -m_ref[qb];
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float p = __builtin_amdgcn_exp2f(fminf(fmaf(st[qb][j], sl2, nm), 64.0f));
+          psum += p;
+          pf[qb][j / 8][j % 8] = (__bf16)p;
+        }
+        psum += __shfl_xor(psum, 32, 64);
+        l[qb] += psum;
+      }
+      // O^T[d, query] += V^T[d, keys] P^T[keys, query]; k-step ks covers keys
+      // 16ks + {0-3, 8-11} (+4 for the upper half-wave), the order S^T leaves.
+      // Each fragment's two transpose reads are issued one step ahead.
+      __builtin_amdgcn_sched_barrier(0);
+      // fragment f = ks2 * DT + dt: two transpose reads
+      auto vfrag = [&](int f) {
+        const int ks2 = f / DT, dg = dbase + f % DT;
+        v4s_t part[2];
+#pragma unroll
+        for (int rd = 0; rd < 2; ++rd) {
+          const bf16_t* p = vs + v_off[dg & 3] + (dg >> 2) * 128 + (16 * ks2 + 8 * rd) * D;
+          part[rd] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)p);
+        }
+        const u32x2 lo = __builtin_bit_cast(u32x2, part[0]);
+        const u32x2 up = __builtin_bit_cast(u32x2, part[1]);
+        return as_bf16x8(u32x4{lo[0], lo[1], up[0], up[1]});
+      };
+      bf16x8 vf[2];
+      vf[0] = vfrag(0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int f = 0; f < 2 * DT; ++f) {
+        if (f + 1 < 2 * DT) vf[(f + 1) & 1] = vfrag(f + 1);
+        const int ks2 = f / DT, dt = f % DT;
+        O[0][dt] = mfma32x32x16(vf[f & 1], pf[0][ks2], O[0][dt]);
+        O[1][dt] = mfma32x32x16(vf[f & 1], pf[1][ks2], O[1][dt]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // tile + 2 goes into the stage of tile - 1, which every wave finished
+      // before the barrier above.  Issued after this tile's LDS reads: the
+      // compiler makes the transpose reads wait for all outstanding LDS DMA,
+      // and this way only tile + 1's (issued an iteration ago) is pending.
+      if (tile + 2 < ntiles) issue(tile + 2, (tile + 2) % kStages2);
+    }
+    // every wave has finished with the LDS stages; decide together
+    __builtin_amdgcn_s_waitcnt(0);
+    if (tid == 0) redo = 0;
+    __syncthreads();
+    if (__ballot(overflow) != 0 && lane == 0) atomicOr(&redo, 1);
+    __syncthreads();
+    if (pass == 1 || redo == 0) break;
+    m_ref[0] = m_true[0];
+    m_ref[1] = m_true[1];
+    __syncthreads();
+  }
+
+  // suffix keys' V rows (decode), then normalise, gate and store
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int64_t n;
+    int t, h;
+    row_of_q(qb, n, t, h);
+    if (!CAUSAL) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float sj = sc[qb][j];
+        if (sj == -INFINITY) continue;
+        const float pj = exp2f(sj - m_ref[qb]);
+        const bf16_t* vrow = a.sv + n * a.ssv_n + (int64_t)j * a.ssv_t + (int64_t)kh * a.ssv_h;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int d0 = (dbase + dt) * 32 + gq * 8 + hi * 4;
+            const u32x2 v2 = *(const u32x2*)(vrow + d0);
+            O[qb][dt][gq * 4 + 0] += pj * __uint_as_float(v2[0] << 16);
+            O[qb][dt][gq * 4 + 1] += pj * __uint_as_float(v2[0] & 0xffff0000u);
+            O[qb][dt][gq * 4 + 2] += pj * __uint_as_float(v2[1] << 16);
+            O[qb][dt][gq * 4 + 3] += pj * __uint_as_float(v2[1] & 0xffff0000u);
+          }
+      }
+    }
+    const int64_t r = (int64_t)qb_blk * ROWS + qgrp * 64 + qb * 32 + col;
+    if (r >= rows_total) continue;
+    const float inv = l[qb] > 0.f ? 1.0f / l[qb] : 0.f;
+    bf16_t* orow = a.out + n * a.so_n + (int64_t)t * a.so_t + (int64_t)h * a.so_h;
+    const bf16_t* grow =
+        a.gate ? a.gate + n * a.sg_n + (int64_t)t * a.sg_t + (int64_t)h * a.sg_h : nullptr;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d0 = (dbase + dt) * 32 + gq * 8 + hi * 4;
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = round_bf(O[qb][dt][gq * 4 + i] * inv);
+        if (grow) {
+          const u32x2 g2 = *(const u32x2*)(grow + d0);
+          const float gv[4] = {__uint_as_float(g2[0] << 16), __uint_as_float(g2[0] & 0xffff0000u),
+                               __uint_as_float(g2[1] << 16), __uint_as_float(g2[1] & 0xffff0000u)};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = o[i] * round_bf(sigmoid_f(gv[i]));
+        }
+        u32x2 packed;
+        packed[0] = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
+        packed[1] = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
+        *(u32x2*)(orow + d0) = packed;
+      }
+  }
+}
+
+template <int D, bool CAUSAL>
+int launch_attn2(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
+  a.nqblk = (int)kad_cdiv(rows, Attn2<D>::ROWS);
+  const int64_t nblocks = bh * a.nqblk;
+  KAD_REQUIRE(nblocks < 0x7fffffff, "grid too large");
+  const size_t lds = Attn2<D>::lds;
+  static bool configured = false;
+  if (!configured) {
+    if (hipFuncSetAttribute((const void*)attn2_kernel<D, CAUSAL>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+      kad_set_error("attention: cannot reserve %zu bytes of LDS", lds);
+      return KAD_ERR_HIP;
+    }
+    configured = true;
+  }
+  hipLaunchKernelGGL((attn2_kernel<D, CAUSAL>), dim3((unsigned)nblocks), dim3(kThreads), lds, s,
+                     a);
+  return kad_launch_status("attn2_kernel");
+}
+
 template <int D, bool CAUSAL>
 int launch_attn(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   const size_t lds = 2 * AttnSmem<D>::stage * sizeof(bf16_t);
@@ -327,11 +791,12 @@ int launch_attn(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   return kad_launch_status("attention_kernel");
 }
 
+// rows: query rows per (request, KV head); bh: number of (request, KV head)
 template <bool CAUSAL>
-int dispatch(int D, const AttnArgs& a, int64_t nblocks, hipStream_t s) {
-  if (D == 256) return launch_attn<256, CAUSAL>(a, nblocks, s);
-  if (D == 128) return launch_attn<128, CAUSAL>(a, nblocks, s);
-  if (D == 64) return launch_attn<64, CAUSAL>(a, nblocks, s);
+int dispatch(int D, const AttnArgs& a, int64_t rows, int64_t bh, hipStream_t s) {
+  if (D == 256) return launch_attn2<256, CAUSAL>(a, rows, bh, s);
+  if (D == 128) return launch_attn2<128, CAUSAL>(a, rows, bh, s);
+  if (D == 64) return launch_attn2<64, CAUSAL>(a, rows, bh, s);
   KAD_UNSUPPORTED("attention supports head dim 64, 128, 256; got %d", D);
 }
 
@@ -352,6 +817,7 @@ extern "C" int kad_prefix_attention_decode_ex(
               "bad dimensions");
   KAD_REQUIRE(H % HK == 0, "H must be divisible by HK");
   if (Tk > 4) KAD_UNSUPPORTED("prefix attention supports suffixes of <= 4 tokens, got %d", Tk);
+  KAD_REQUIRE(scale > 0.f && scale < INFINITY, "scale must be positive and finite");
   KAD_REQUIRE(al16(q) && al16(suffix_k) && (L == 0 || (al16(prefix_k) && al16(prefix_v))),
               "q, suffix_k and prefix K/V must be 16-byte aligned");
   KAD_REQUIRE(((uintptr_t)suffix_v | (uintptr_t)out | (uintptr_t)gate) % 8 == 0,
@@ -366,10 +832,7 @@ extern "C" int kad_prefix_attention_decode_ex(
              (const uint8_t*)prefix_mask, (const bf16_t*)gate, sg_n, sg_t, sg_h, (bf16_t*)out,
              so_n, so_t, so_h, W, Tq, H, HK, L, scale, 0, Tk, Tk - Tq};
   const int64_t rows = (int64_t)W * (H / HK) * Tq;
-  a.nqblk = (int)kad_cdiv(rows, kRows);
-  const int64_t nblocks = (int64_t)B * HK * a.nqblk;
-  KAD_REQUIRE(nblocks < 0x7fffffff, "grid too large");
-  return dispatch<false>(D, a, nblocks, (hipStream_t)stream);
+  return dispatch<false>(D, a, rows, (int64_t)B * HK, (hipStream_t)stream);
 }
 
 extern "C" int kad_prefix_attention_decode(
@@ -393,6 +856,7 @@ extern "C" int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, 
                                      float scale, kad_stream_t stream) {
   KAD_REQUIRE(q && k && v && out, "null pointer argument");
   KAD_REQUIRE(B > 0 && L > 0 && H > 0 && HK > 0 && D > 0 && H % HK == 0, "bad dimensions");
+  KAD_REQUIRE(scale > 0.f && scale < INFINITY, "scale must be positive and finite");
   KAD_REQUIRE(al16(q) && al16(k) && al16(v), "q, k, v must be 16-byte aligned");
   KAD_REQUIRE(((uintptr_t)out | (uintptr_t)gate) % 8 == 0, "out and gate must be 8-byte aligned");
   for (int64_t st : {sq_b, sq_l, sq_h, skv_b, skv_l, skv_h})
@@ -403,8 +867,5 @@ extern "C" int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, 
              skv_h, nullptr, nullptr, 0, 0, 0, 0, 0, 0, nullptr, (const bf16_t*)gate, sg_b, sg_l,
              sg_h, (bf16_t*)out, so_b, so_l, so_h, 1, 1, H, HK, L, scale, 0, 0, 0};
   const int64_t rows = (int64_t)L * (H / HK);
-  a.nqblk = (int)kad_cdiv(rows, kRows);
-  const int64_t nblocks = (int64_t)B * HK * a.nqblk;
-  KAD_REQUIRE(nblocks < 0x7fffffff, "grid too large");
-  return dispatch<true>(D, a, nblocks, (hipStream_t)stream);
+  return dispatch<true>(D, a, rows, (int64_t)B * HK, (hipStream_t)stream);
 }

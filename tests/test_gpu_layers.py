@@ -260,6 +260,28 @@ def test_prefix_attention_mask_and_gate(device):
                      name="masked gated attention")
 
 
+@pytest.mark.parametrize("D", [64, 256])
+def test_prefix_attention_wide_score_range(device, D):
+    """Scores that grow by far more than 2^64 (log2 units) after the first
+    ones a row sees: the kernel's fixed softmax reference must be raised (its
+    second pass), for the suffix-first decode order and across key tiles."""
+    B, W, T, H, HK, L = 1, 4, 2, 4, 1, 200
+    q, pk, pv, sk, sv = _attn_inputs(B, W, T, H, HK, L, D, seed=77)
+    u = torch.randn(D, generator=torch.Generator().manual_seed(5))
+    u = u / u.norm()
+    q = (u * 12.0).expand_as(q).bfloat16().contiguous()     # every query along u
+    sk = (-u * 12.0).expand_as(sk).bfloat16().contiguous()  # suffix scores -144, prefix ~N(0, 144)
+    pk = pk.clone()
+    pk[:, 150:] = (u * 14.0).bfloat16()                     # late prefix keys score far higher
+    dev = [t.to(device) for t in (q, pk, pv, sk, sv)]
+    out = ops.prefix_attention(*dev, beam_width=W, scale=1.0, backend="flash_attn")
+    exp = ops_ref.prefix_attention(q, pk, pv, sk, sv, beam_width=W, scale=1.0,
+                                   compute=torch.float64)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert_close_rel(out.cpu(), exp, rtol=1e-2, atol_frac=4e-3, name="wide-range attention")
+
+
 @pytest.mark.parametrize("B,L,H,HK,D", [(2, 100, 8, 2, 256), (1, 1024, 8, 2, 256), (2, 37, 4, 1, 64)])
 def test_attention_prefill_causal(device, B, L, H, HK, D):
     g = torch.Generator().manual_seed(L)
