@@ -58,6 +58,17 @@ struct QKFrag<float> {
   }
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// acc + sum_i a_i b_i over 8 bf16 pairs, as four v_dot2_f32_bf16
+__device__ __forceinline__ float dot8_bf16(bf16x8 a, bf16x8 b, float acc) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2_t{a[2 * p], a[2 * p + 1]},
+                                          bf16x2_t{b[2 * p], b[2 * p + 1]}, acc, false);
+  return acc;
+}
+
 template <typename TIN>
 __device__ __forceinline__ void load4(const TIN* p, float* f);
 template <>
@@ -178,17 +189,28 @@ __global__ __launch_bounds__(256) void gdn_replay_kernel(
 #pragma unroll
       for (int t = 0; t < kTMax; ++t) {
         if (t < T) {
+          if constexpr (!kSplitB) {
+            // bf16 rows: packed dot2 (products exact, fp32 sums) on the raw fragments
+            qq[t] = dot8_bf16(fq[t].hi, fq[t].hi, qq[t]);
+            kk[t] = dot8_bf16(fk[t].hi, fk[t].hi, kk[t]);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            qq[t] += xq[t][i] * xq[t][i];
-            kk[t] += xk[t][i] * xk[t][i];
-          }
-#pragma unroll
-          for (int j = 0; j <= t; ++j) {
+            for (int j = 0; j <= t; ++j) {
+              kqx[j][t] = dot8_bf16(fk[j].hi, fq[t].hi, kqx[j][t]);
+              if (j < t) kkx[j][t] = dot8_bf16(fk[j].hi, fk[t].hi, kkx[j][t]);
+            }
+          } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-              kqx[j][t] += xk[j][i] * xq[t][i];
-              if (j < t) kkx[j][t] += xk[j][i] * xk[t][i];
+              qq[t] += xq[t][i] * xq[t][i];
+              kk[t] += xk[t][i] * xk[t][i];
+            }
+#pragma unroll
+            for (int j = 0; j <= t; ++j) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                kqx[j][t] += xk[j][i] * xq[t][i];
+                if (j < t) kkx[j][t] += xk[j][i] * xk[t][i];
+              }
             }
           }
 #pragma unroll
