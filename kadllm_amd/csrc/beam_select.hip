@@ -214,7 +214,8 @@ __device__ int wave_rank_bin(const int* hist, int r, int* above) {
 //  2. one vectorised pass over the row computes the max and the sum of exp
 //     (online rescaling) and gathers every allowed entry at or above the
 //     threshold into LDS;
-//  3. a bitonic sort by (key desc, column asc) yields the row's top K.
+//  3. a radix select over the candidates' keys (ties at the K-th key ranked by
+//     column) emits the row's top K, unordered: the merge stage orders them.
 // If fewer than K or more than kCandCap entries qualify, the exact histogram
 // path runs instead, so the result never depends on the sample.
 __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
@@ -309,22 +310,24 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   __syncthreads();
   const uint32_t thr = (uint32_t)sh_thr;
 
-  // ---- 2. max, online sum exp, and candidates >= thr in one pass.  The sum
-  // starts from the sample max, so the rescaling branch is rare; terms use the
-  // hardware exp2 (exp(x) = 2^(x log2 e)); candidates are screened with a float
-  // compare against the threshold's value and confirmed on the order key.
+  // ---- 2. max, sum exp, and candidates >= thr in one pass.  The sum is taken
+  // against a fixed reference, the sample max (each term one fma and the
+  // hardware exp2: exp(v - m) = 2^(v log2 e - m log2 e)); a row whose true max
+  // exceeds it by more than 60 sums again against the true max.  Candidates
+  // are screened with a float compare against the threshold's value and
+  // confirmed on the order key.
+  constexpr float kLog2e = 1.4426950408889634f;
+  float mref = -INFINITY;
+  for (int w = 0; w < kRowThreads / 64; ++w) mref = fmaxf(mref, red_smax[w]);
+  if (mref == -INFINITY) mref = 0.f;
   float m = -INFINITY, se = 0.f;
-  for (int w = 0; w < kRowThreads / 64; ++w) m = fmaxf(m, red_smax[w]);
+  float nb = -mref * kLog2e;
   const uint32_t tb = thr & 0x8000u ? (thr & 0x7fffu) : (~thr & 0xffffu);
   const float tf = thr > 0 ? bf2f((uint16_t)tb) : INFINITY;
   auto visit = [&](uint16_t bits, int c, bool ok) {
     const float v = bf2f(bits);
-    if (v > m) {
-      se = (m == -INFINITY ? 0.f : se * __expf(m - v)) + 1.f;
-      m = v;
-    } else if (v != -INFINITY) {
-      se += __expf(v - m);
-    }
+    m = fmaxf(m, v);
+    se += __builtin_amdgcn_exp2f(fmaf(v, kLog2e, nb));
     if (v >= tf && ok) {
       const uint32_t u = order16(bits);
       if (u >= thr) {
@@ -366,14 +369,7 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   }
   for (int c = V8 * 8 + tid; c < V; c += kRowThreads) visit(x[c], c, mk ? mk[c] != 0 : true);
   {
-    float mm = m, ss = se;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float m2 = __shfl_xor(mm, o, 64), s2 = __shfl_xor(ss, o, 64);
-      const float mx = fmaxf(mm, m2);
-      ss = (mm == -INFINITY ? 0.f : ss * expf(mm - mx)) + (m2 == -INFINITY ? 0.f : s2 * expf(m2 - mx));
-      mm = mx;
-    }
+    const float mm = wave_max(m), ss = wave_sum(se);
     if ((tid & 63) == 0) {
       red_m[tid >> 6] = mm;
       red_s[tid >> 6] = ss;
@@ -383,9 +379,22 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   float M = -INFINITY;
   for (int w = 0; w < kRowThreads / 64; ++w) M = fmaxf(M, red_m[w]);
   float SE = 0.f;
-  for (int w = 0; w < kRowThreads / 64; ++w)
-    SE += red_m[w] == -INFINITY ? 0.f : red_s[w] * expf(red_m[w] - M);
-  const float lse = logf(SE);
+  for (int w = 0; w < kRowThreads / 64; ++w) SE += red_s[w];
+  if (M > mref + 60.f) {
+    // the sample missed the top by far: sum again against the true max
+    __syncthreads();
+    mref = M;
+    nb = -mref * kLog2e;
+    float s2 = 0.f;
+    for (int c = tid; c < V; c += kRowThreads) s2 += __builtin_amdgcn_exp2f(fmaf(bf2f(x[c]), kLog2e, nb));
+    s2 = wave_sum(s2);
+    if ((tid & 63) == 0) red_s[tid >> 6] = s2;
+    __syncthreads();
+    SE = 0.f;
+    for (int w = 0; w < kRowThreads / 64; ++w) SE += red_s[w];
+  }
+  // log sum exp(v - M) = log(sum exp(v - mref)) + (mref - M)
+  const float lse = logf(SE) + (mref - M);
   const int count = sh_count;
   if (thr == 0 || count < K || count > kCandCap) {
     // exact fallback: reuses the candidate buffer as the 4096-bin histogram
@@ -394,35 +403,123 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
                      (int*)cand);
     return;
   }
-  // ---- 3. bitonic sort of the candidates, descending by (key, -column)
-  int P = 1;
-  while (P < count) P <<= 1;
-  for (int i = count + tid; i < P; i += kRowThreads) cand[i] = 0;
-  __syncthreads();
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < P; i += kRowThreads) {
-        const int j = i ^ stride;
-        if (j > i) {
-          const bool desc = (i & size) == 0;
-          const uint64_t a = cand[i], b = cand[j];
-          if (desc ? a < b : a > b) {
-            cand[i] = b;
-            cand[j] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
+  // ---- 3. exact top K of the candidates (the merge stage orders them; the
+  // row's output order is free).  Candidate = (order key u << 32) | ~column,
+  // unique per column: a radix select over u (two 8-bit rounds) finds the
+  // K-th largest key u*; the ties at u* are ranked by column.
   const float p = parent[row];
   const int r_local = (int)(row % Wp);
-  for (int i = tid; i < K; i += kRowThreads) {
-    const uint64_t e = cand[i];
-    const int c = (int)(0xffffffffu - (uint32_t)(e & 0xffffffffu));
+  int* bins = hist;  // 256 ints
+  auto select_bin = [&](int need_in, int* above_out) -> int {
+    // one wave: the bin holding the need_in-th largest entry of bins[]
+    if (tid < 64) {
+      int above = 0;
+      int b = -1;
+      {
+        const int lane = tid;
+        int v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = bins[lane * 4 + i];
+        const int t = v[0] + v[1] + v[2] + v[3];
+        int suf = t;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_down(suf, o, 64);
+          if (lane + o < 64) suf += y;
+        }
+        const uint64_t reach = __ballot(suf >= need_in);
+        const int L = __popcll(reach) - 1;
+        int acc = 0;
+        if (lane == L) {
+          acc = suf - t;
+          for (int i = 3; i >= 0; --i) {
+            if (acc + v[i] >= need_in) {
+              b = lane * 4 + i;
+              break;
+            }
+            acc += v[i];
+          }
+        }
+        above = __shfl(acc, L, 64);
+        b = __shfl(b, L, 64);
+      }
+      if (tid == 0) {
+        sh_hi = b;
+        sh_above = above;
+      }
+    }
+    __syncthreads();
+    *above_out = sh_above;
+    return sh_hi;
+  };
+  // round 1: high byte of u
+  bins[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < count; i += kRowThreads) atomicAdd(&bins[(uint32_t)(cand[i] >> 40) & 255], 1);
+  __syncthreads();
+  int above1;
+  const int b1 = select_bin(K, &above1);
+  __syncthreads();
+  // round 2: low byte of u inside bin b1
+  bins[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < count; i += kRowThreads) {
+    const uint32_t u = (uint32_t)(cand[i] >> 32);
+    if ((int)(u >> 8) == b1) atomicAdd(&bins[u & 255], 1);
+  }
+  __syncthreads();
+  int above2;
+  const int b2 = select_bin(K - above1, &above2);
+  const uint32_t ustar = ((uint32_t)b1 << 8) | (uint32_t)b2;
+  const int need = K - above1 - above2;  // ties at u* to take, lowest columns first
+  auto emit = [&](uint64_t e) {
+    const int slot = atomicAdd(&sh_count, 1);
+    const int c = (int)(0xffffffffu - (uint32_t)e);
     const float v = bf2f(x[c]);
-    cand_key[row * K + i] = ((v - M) - lse) + p;
-    cand_idx[row * K + i] = r_local * V + c;
+    if (slot < K) {  // exactly K qualify; the bound only guards memory
+      cand_key[row * K + slot] = ((v - M) - lse) + p;
+      cand_idx[row * K + slot] = r_local * V + c;
+    }
+  };
+  // keys above u* are taken; the ties at u* (their ~column words) are gathered
+  uint32_t* ties = (uint32_t*)bins;
+  if (tid == 0) {
+    sh_count = 0;
+    sh_thr = 0;  // number of ties
+  }
+  __syncthreads();
+  for (int i = tid; i < count; i += kRowThreads) {
+    const uint64_t e = cand[i];
+    const uint32_t u = (uint32_t)(e >> 32);
+    if (u > ustar) {
+      emit(e);
+    } else if (u == ustar) {
+      const int t = atomicAdd(&sh_thr, 1);
+      if (t < 256) ties[t] = (uint32_t)e;
+    }
+  }
+  __syncthreads();
+  const int nties = sh_thr;
+  if (nties <= 256) {
+    // rank of each tie = ties with a lower column (a larger ~column word)
+    for (int t = tid; t < nties; t += kRowThreads) {
+      const uint32_t me = ties[t];
+      int rank_t = 0;
+      for (int j = 0; j < nties; ++j) rank_t += ties[j] > me ? 1 : 0;
+      if (rank_t < need) emit(((uint64_t)ustar << 32) | me);
+    }
+  } else {
+    // many equal keys: rank every tie against the whole candidate list
+    for (int i = tid; i < count; i += kRowThreads) {
+      const uint64_t e = cand[i];
+      if ((uint32_t)(e >> 32) != ustar) continue;
+      int rank_t = 0;
+      for (int j = 0; j < count; ++j) {
+        const uint64_t f = cand[j];
+        rank_t += ((uint32_t)(f >> 32) == ustar && (uint32_t)f > (uint32_t)e) ? 1 : 0;
+      }
+      if (rank_t < need) emit(e);
+    }
   }
 }
 

@@ -72,6 +72,18 @@ def test_select_level_full_vocab_shape(device):
     _check_selection(logits, scores, W)
 
 
+def test_select_level_unsampled_outlier(device):
+    """A logit far above everything the row sample sees (line 1 of the row is
+    not sampled): the log-sum-exp is taken again against the true max."""
+    B, Wp, V, W = 1, 4, 248320, 64
+    gen = torch.Generator(device=device).manual_seed(8)
+    logits = torch.randn(B, Wp, V, generator=gen, device=device).bfloat16()
+    logits[0, 0, 65] = 90.0
+    logits[0, 2, 70] = 75.0
+    scores = -torch.rand(B, Wp, generator=gen, device=device)
+    _check_selection(logits, scores, W)
+
+
 def test_history_update(device):
     B, Wp, step, W = 2, 3, 2, 5
     hist = torch.arange(B * Wp * step).reshape(B, Wp, step)
