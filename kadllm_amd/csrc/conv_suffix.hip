@@ -212,8 +212,16 @@ __global__ __launch_bounds__(256) void conv_prefill_bf16(
     }
   }
   const int t_end = min(L, t0 + kRun);
-  for (int t = t0; t < t_end; ++t) {
-    const u32x4 r = *(const u32x4*)(x + ((int64_t)b * L + t) * ldx + c0);
+  // the run's rows are all loaded before any is used (kRun loads in flight)
+  u32x4 rows_in[kRun];
+#pragma unroll
+  for (int i = 0; i < kRun; ++i)
+    rows_in[i] = *(const u32x4*)(x + ((int64_t)b * L + min(t0 + i, L - 1)) * ldx + c0);
+#pragma unroll
+  for (int i = 0; i < kRun; ++i) {
+    const int t = t0 + i;
+    if (t >= t_end) break;
+    const u32x4 r = rows_in[i];
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
