@@ -106,7 +106,9 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
  * waves; 5 = 256x256 and 6 = 256x128 with 8 waves; 7 = 256x256 with 4 waves,
  * fragment double-buffering and a 16-byte store epilogue, which needs 16-byte
  * aligned C (and R) with ldc, ldr and the output width multiples of 8; 8 = the
- * same with register-staged instead of direct-to-LDS loads), for tuning. */
+ * same with register-staged instead of direct-to-LDS loads; 9 = 7 with the
+ * next tile's loads split over two K steps; 10 = 9 with 256x128 tiles;
+ * 11 = 128x32 with 4 waves, no SwiGLU epilogue), for tuning. */
 int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
                         int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                         int epilogue, int tile_config, kad_stream_t stream);

@@ -496,7 +496,8 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled)
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
        CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8,
-       CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10 };
+       CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10,
+       CFG_128x32 = 11 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
@@ -504,12 +505,15 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
   if (cfg == CFG_AUTO) {
     // the pipelined 256x256 kernel when its tiles still fill every CU (and
     // the output suits 16-byte stores), then the pipelined 256x128 one;
+    // 128x32 for outputs of at most 32 columns (the GDN gate projection);
     // 128x128 otherwise (measured on the decode/prefill projection shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
     const int64_t tiles128 = kad_cdiv(M, 256) * kad_cdiv(N, 128);
     const bool vec = vector_epilogue_ok(C, ldc, R, ldr, N, EPI);
     if (M <= 64)
       cfg = CFG_32x256;
+    else if (N <= 32)
+      cfg = CFG_128x32;
     else if (tiles256 >= 256)
       cfg = vec ? CFG_256x256_SPREAD : CFG_256x256_8W;
     else if (vec && tiles128 >= 256)
@@ -520,6 +524,10 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
   switch (cfg) {
     case CFG_32x256: return launch<32, 256, 1, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_128x128: return launch<128, 128, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_128x32:
+      if (EPI == KAD_EPI_SWIGLU) KAD_UNSUPPORTED("tile configuration 11 has no SwiGLU epilogue");
+      return launch<128, 32, 4, 1, EPI == KAD_EPI_SWIGLU ? KAD_EPI_STORE : EPI>(
+          A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_128x256: return launch<128, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256: return launch<256, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_8W:

@@ -101,7 +101,8 @@ def test_gemm_tile_configurations_agree(device, epi):
     x = torch.randn(M, n_out, generator=g).bfloat16()
     ad, wd = a.to(device), w.to(device)
     outs = {}
-    for cfg in range(1, 11):
+    cfgs = [c for c in range(1, 12) if not (c == 11 and epi == layers.EPI_SWIGLU)]
+    for cfg in cfgs:
         c = torch.zeros(M, n_out + 16, dtype=torch.bfloat16, device=device)  # ldc > width
         cv = c[:, :n_out]
         if epi == layers.EPI_RESIDUAL:
@@ -113,7 +114,7 @@ def test_gemm_tile_configurations_agree(device, epi):
         torch.cuda.synchronize()
         assert (c[:, n_out:] == 0).all(), f"config {cfg} wrote past the output width"
         outs[cfg] = cv.cpu()
-    for cfg in range(2, 11):
+    for cfg in cfgs[1:]:
         assert torch.equal(outs[cfg], outs[1]), f"config {cfg} differs from config 1"
     prod = (a.float() @ w.float().T).bfloat16()
     if epi == layers.EPI_STORE:
