@@ -192,6 +192,35 @@ class Qwen35Runner:
         y = layers.rmsnorm_gated(o, z, lyr.norm_w, cfg.rms_norm_eps, cfg.linear_num_value_heads)
         layers.gemm(y, lyr.w_out, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
 
+    def _attn_terminal(self, lyr, n, x_last, B, L):
+        """Last-layer attention of the prefill: K/V for every position (the
+        prefix), the query, attention, gate and o_proj for the last position
+        only (added into x_last).  Returns the layer's (K, V) prefix views."""
+        cfg = self.cfg
+        nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        rows = n.shape[0]
+        dev = n.device
+        qcols = 2 * nh * hd
+        kv = layers.gemm(n, lyr.w_qkv[qcols:])                  # [rows, k | v]
+        ld = kv.stride(0)
+        kc = torch.empty(B, nkv, L, hd, dtype=torch.bfloat16, device=dev)
+        vc = torch.empty(B, nkv, L, hd, dtype=torch.bfloat16, device=dev)
+        kv_strides = (nkv * L * hd, hd, L * hd)
+        layers.qk_norm_rope(kv, ld, hd, nkv, lyr.k_norm, kc, kv_strides, L, rows, hd, self.rot,
+                            self.inv_freq, 0, L, cfg.rms_norm_eps)
+        layers.scatter_heads(kv[:, nkv * hd:], ld, nkv, hd, vc, kv_strides, L, rows)
+        qg = layers.gemm(n.view(B, L, -1)[:, -1], lyr.w_qkv[:qcols])   # [B, q | gate per head]
+        q = torch.empty(B, 1, nh, hd, dtype=torch.bfloat16, device=dev)
+        layers.qk_norm_rope(qg, qg.stride(0), 2 * hd, nh, lyr.q_norm, q, (nh * hd, nh * hd, hd),
+                            1, B, hd, self.rot, self.inv_freq, L - 1, 1, cfg.rms_norm_eps)
+        k_all, v_all = kc.transpose(1, 2), vc.transpose(1, 2)  # [B, L, nkv, hd]
+        att = prefix_attention_decode(q, k_all[:, :L - 1], v_all[:, :L - 1], k_all[:, L - 1:],
+                                      v_all[:, L - 1:], 1, None, hd ** -0.5, gate=qg[:, hd:],
+                                      gate_strides=(qg.stride(0), qg.stride(0), 2 * hd))
+        layers.gemm(att.view(B, nh * hd), lyr.w_o, out=x_last, epilogue=layers.EPI_RESIDUAL,
+                    residual=x_last)
+        return k_all, v_all
+
     # ------------------------------------------------------------------
     @torch.no_grad()
     def prefill(self, input_ids):
@@ -205,7 +234,12 @@ class Qwen35Runner:
         dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
         nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         snap = []
-        for lyr in self.layers:
+        # Terminal pruning: past the last layer's token mixer only the last
+        # position of each prompt is used (its logits); the prefix needs that
+        # layer's state or K/V for every position, but not its outputs.
+        x_last = x.view(B, L, -1)[:, -1]
+        for li, lyr in enumerate(self.layers):
+            terminal = li == len(self.layers) - 1
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
                 proj = self._gdn_proj(lyr, n)
@@ -225,8 +259,14 @@ class Qwen35Runner:
                           _lib.ptr(g), 2, _lib.ptr(beta), 0, HV, None, 2, 1, _lib.ptr(o), self.vd,
                           _lib.ptr(S), _lib.ptr(ws), ws.numel(), B, L, H_, HV, dk, dv,
                           float(dk ** -0.5), 1, _lib.stream_of(x))
-                self._gdn_finish(lyr, o, proj, x)
+                if terminal:
+                    self._gdn_finish(lyr, o.view(B, L, -1)[:, -1], proj.view(B, L, -1)[:, -1],
+                                     x_last)
+                else:
+                    self._gdn_finish(lyr, o, proj, x)
                 snap.append((conv_state, S))
+            elif terminal:
+                snap.append(self._attn_terminal(lyr, n, x_last, B, L))
             else:
                 proj = layers.gemm(n, lyr.w_qkv)
                 ld = proj.stride(0)
@@ -248,9 +288,11 @@ class Qwen35Runner:
                 layers.gemm(att.view(rows, nh * hd), lyr.w_o, out=x,
                             epilogue=layers.EPI_RESIDUAL, residual=x)
                 snap.append((kc.transpose(1, 2), vc.transpose(1, 2)))
-            self._mlp(lyr, x, rows)
-        last = x.view(B, L, -1)[:, -1]
-        hN = layers.rmsnorm(last, self.norm_w, cfg.rms_norm_eps)
+            if terminal:
+                self._mlp(lyr, x_last, B)
+            else:
+                self._mlp(lyr, x, rows)
+        hN = layers.rmsnorm(x_last, self.norm_w, cfg.rms_norm_eps)
         logits = layers.gemm(hN, self.lm_head)
         return logits, tuple(snap)
 
