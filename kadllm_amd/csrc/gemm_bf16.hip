@@ -205,10 +205,9 @@ typedef __attribute__((address_space(1))) void global_void_t;
 // consecutive tiles along the outer dimension share each inner-dimension
 // tile, so an XCD's resident tiles form a 2-D block and both operands are
 // reused from its L2.
-__device__ __forceinline__ void tile_origin(int M, int N, int BN, int n_major, int group, int& m0,
-                                           int& n0) {
+__device__ __forceinline__ void tile_origin_of(int lid, int M, int N, int BN, int n_major,
+                                              int group, int& m0, int& n0) {
   const int mtiles = (M + kT - 1) / kT, ntiles = (N + BN - 1) / BN;
-  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
   const int nx = n_major ? ntiles : mtiles, ny = n_major ? mtiles : ntiles;
   const int gx0 = (lid / (group * ny)) * group, gs = min(nx - gx0, group);
   const int within = lid % (group * ny);
@@ -216,6 +215,11 @@ __device__ __forceinline__ void tile_origin(int M, int N, int BN, int n_major, i
   const int mi = n_major ? ty : tx, ni = n_major ? tx : ty;
   m0 = mi * kT;
   n0 = ni * BN;
+}
+
+__device__ __forceinline__ void tile_origin(int M, int N, int BN, int n_major, int group, int& m0,
+                                           int& n0) {
+  tile_origin_of(xcd_logical_id(blockIdx.x, gridDim.x), M, N, BN, n_major, group, m0, n0);
 }
 
 __device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
@@ -311,6 +315,28 @@ __device__ __forceinline__ void interleave_step() {
     if (t * PW < NW) __builtin_amdgcn_sched_group_barrier(0x200, PW, 0);
   }
   __builtin_amdgcn_sched_barrier(0);  // steps are separate scheduling regions
+}
+
+// issue order inside one 16-deep step when the step's fragment reads come
+// before its global loads in program order (the loads write LDS, so they
+// cannot be hoisted above reads that might alias): NR MFMAs each followed by
+// one fragment read, then the NV global loads spread evenly over the
+// remaining NM - NR MFMAs
+template <int NM, int NR, int NV>
+__device__ __forceinline__ void interleave_reads_then_loads() {
+#pragma unroll
+  for (int t = 0; t < NM; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (t < NR) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    } else {
+      constexpr int kSlots = NM - NR;
+      const int c = ((t - NR + 1) * NV) / kSlots - ((t - NR) * NV) / kSlots;
+#pragma unroll
+      for (int q = 0; q < c; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int EPI, int BN, int MODE>
@@ -414,7 +440,16 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
     // loads of the next tile (the last iteration re-fetches the final tile,
     // keeping the loop body one basic block)
     const int kn = min(kt + 1, KT - 1) * kBK;
-    if constexpr (MODE == 2) {
+    if constexpr (MODE == 4) {
+      load_frags(stage, 1, 1);
+      issue(stage ^ 1, kn, 0, 4);
+      mfma_step(0);
+      interleave_reads_then_loads<NM, NR, kLoads / 2>();
+      load_frags(stage, 2, 0);
+      issue(stage ^ 1, kn, 4, 8);
+      mfma_step(1);
+      interleave_reads_then_loads<NM, NR, kLoads / 2>();
+    } else if constexpr (MODE == 2) {
       issue(stage ^ 1, kn, 0, 4);
       load_frags(stage, 1, 1);
       mfma_step(0);
@@ -470,6 +505,156 @@ int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
   return kad_launch_status("gemm256_kernel");
 }
 
+// 256 x BN tile fed through a ring of 4 LDS slots of 32-deep K slices.  The
+// loads of slice t + 3 are issued while slice t is consumed, half in each of
+// its two 16-deep steps and spread between MFMAs, so they have two slices of
+// time to land and never arrive in a burst.  One barrier per slice, in its
+// middle: past it, slice t + 1 has landed (each wave waits for its own loads
+// with a partial vmcnt, the barrier makes every wave's part visible) and
+// every wave has finished reading slice t - 1, whose slot the next loads
+// reuse.
+constexpr int kRK = 32;    // K depth of a slot
+constexpr int kRing = 4;   // slots
+
+template <int BN>
+struct Ring256 {
+  static constexpr int NJ = BN / 64;              // 32-column blocks per wave
+  static constexpr int WG = BN / 64;              // W 16-row groups per wave
+  static constexpr int Loads = 4 + WG;            // DMA instructions per wave per slot
+  static constexpr int Slot = (kT + BN) * kRK;    // elements per slot: A rows then W rows
+  static constexpr int Smem = kRing * Slot > 4 * 128 * Tile256<BN>::EpiLd
+                                  ? kRing * Slot
+                                  : 4 * 128 * Tile256<BN>::EpiLd;
+};
+
+// workgroup barrier without __syncthreads' wait for every outstanding load;
+// the empty asm statements keep LDS accesses on their side of it
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt not waited (vmcnt is bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int wait_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
+
+template <int EPI, int BN>
+__global__ __launch_bounds__(256, 1) void gemm_ring_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group) {
+  using RL = Ring256<BN>;
+  constexpr int NJ = RL::NJ, WG = RL::WG, kLoads = RL::Loads, kSlot = RL::Slot;
+  constexpr int NM = 4 * NJ, NR = 4 + NJ;   // MFMAs and fragment reads per step
+  constexpr int kHalf = kLoads / 2;
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[RL::Smem];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int m0, n0;
+  tile_origin(M, N, BN, n_major, group, m0, n0);
+
+  // one DMA instruction fills 16 rows of 64 bytes; this wave loads the
+  // 16-row groups g = wave + 4 i of the A slice (i < 4) and of the W slice
+  // (i < WG).  Lane L -> row g*16 + L/4, LDS chunk L%4 holding global chunk
+  // (L%4) ^ (L/16): a row's 16-byte chunk c sits at c ^ ((row >> 2) & 3)
+  const int d_row = lane >> 2;
+  const int d_kc = ((lane & 3) ^ (lane >> 4)) * 8;
+  const bf16_t* a_src[4];
+  const bf16_t* b_src[WG];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (wave + 4 * i) * 16 + d_row;
+    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
+    if (i < WG) b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
+  }
+  // loads [j0, j1) of one slot: j < 4 are A groups, the rest W groups
+  auto issue = [&](int slot, int k0, int j0, int j1) {
+    bf16_t* base = smem + slot * kSlot + wave * 16 * kRK;
+#pragma unroll
+    for (int j = j0; j < j1; ++j) {
+      if (j < 4)
+        dma16(a_src[j] + k0, base + j * 64 * kRK);
+      else
+        dma16(b_src[j - 4] + k0, base + kT * kRK + (j - 4) * 64 * kRK);
+    }
+  };
+
+  // fragments: lane reads row lane%32 of a 32-row block at K chunk
+  // step*2 + lane/32, stored at chunk ^ ((row >> 2) & 3)
+  const int f_row = lane & 31, f_sw = (lane >> 2) & 3, f_hi = lane >> 5;
+  const int fa_row = (wm * 128 + f_row) * kRK;
+  const int fw_row = kT * kRK + (wn * (BN / 2) + f_row) * kRK;
+  bf16x8 fa[2][4], fw[2][NJ];
+  auto load_frags = [&](int slot, int step, int buf) {
+    const bf16_t* base = smem + slot * kSlot + (((step * 2 + f_hi) ^ f_sw) * 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[buf][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kRK));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      fw[buf][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kRK));
+  };
+
+  f32x16 acc[4][NJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
+  auto mfma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x16(fw[buf][j], fa[buf][i], acc[i][j]);
+  };
+
+  // past the last slice the loads re-fetch it, which keeps every
+  // iteration's wait counts the same
+  const int KT = K / kRK;
+  issue(0, 0, 0, kLoads);
+  issue(1, min(1, KT - 1) * kRK, 0, kLoads);
+  issue(2, min(2, KT - 1) * kRK, 0, kLoads);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * kLoads));   // slice 0 landed
+  ring_barrier();
+  load_frags(0, 0, 0);
+  for (int t = 0; t < KT; ++t) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int slot = t & (kRing - 1), slot3 = (t + 3) & (kRing - 1);
+    const int k3 = min(t + 3, KT - 1) * kRK;
+    load_frags(slot, 1, 1);
+    issue(slot3, k3, 0, kHalf);
+    mfma_step(0);
+    interleave_reads_then_loads<NM, NR, kHalf>();
+    // slice t + 1 landed: only slice t + 2's loads and the first half of
+    // slice t + 3's may still be in flight
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoads + kHalf));
+    ring_barrier();
+    load_frags((t + 1) & (kRing - 1), 0, 0);
+    issue(slot3, k3, kHalf, kLoads);
+    mfma_step(1);
+    interleave_reads_then_loads<NM, NR, kLoads - kHalf>();
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  epilogue_tile<EPI, BN>(acc, smem, lane, wave, m0, n0, C, ldc, R, ldr, M, N);
+}
+
+template <int EPI, int BN>
+int launch_ring(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  if (K % kRK) KAD_UNSUPPORTED("ring gemm needs K %% 32 == 0, got %d", K);
+  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
+  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  hipLaunchKernelGGL((gemm_ring_kernel<EPI, BN>), dim3((unsigned)nblocks), dim3(256), 0, s,
+                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N, K, n_major, 8);
+  return kad_launch_status("gemm_ring_kernel");
+}
+
 // 16-byte epilogue stores need aligned, 8-column-granular outputs
 bool vector_epilogue_ok(const void* C, int64_t ldc, const void* R, int64_t ldr, int N, int epi) {
   const int n_out = epi == KAD_EPI_SWIGLU ? N / 2 : N;
@@ -497,16 +682,18 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
        CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8,
        CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10,
-       CFG_128x32 = 11 };
+       CFG_128x32 = 11, CFG_256x256_RDFIRST = 12, CFG_256x256_RING = 13 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
     // the pipelined 256x256 kernel when its tiles still fill every CU (and
-    // the output suits 16-byte stores), then the pipelined 256x128 one;
+    // the output suits 16-byte stores): the 4-slot ring for K >= 3072, the
+    // reads-first schedule for very wide outputs (the vocabulary head), the
+    // split-load schedule otherwise; then the pipelined 256x128 one;
     // 128x32 for outputs of at most 32 columns (the GDN gate projection);
-    // 128x128 otherwise (measured on the decode/prefill projection shapes)
+    // 128x128 otherwise (all measured on the decode/prefill shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
     const int64_t tiles128 = kad_cdiv(M, 256) * kad_cdiv(N, 128);
     const bool vec = vector_epilogue_ok(C, ldc, R, ldr, N, EPI);
@@ -514,8 +701,10 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       cfg = CFG_32x256;
     else if (N <= 32)
       cfg = CFG_128x32;
+    else if (tiles256 >= 256 && !vec)
+      cfg = CFG_256x256_8W;
     else if (tiles256 >= 256)
-      cfg = vec ? CFG_256x256_SPREAD : CFG_256x256_8W;
+      cfg = K >= 3072 ? CFG_256x256_RING : N >= 65536 ? CFG_256x256_RDFIRST : CFG_256x256_SPREAD;
     else if (vec && tiles128 >= 256)
       cfg = CFG_256x128_PIPE;
     else
@@ -546,6 +735,14 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       if (cfg == CFG_256x256_SPREAD)
         return launch_tile<EPI, 256, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       return launch_tile<EPI, 128, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x256_RDFIRST:
+    case CFG_256x256_RING:
+      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
+        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
+                        cfg);
+      if (cfg == CFG_256x256_RDFIRST)
+        return launch_tile<EPI, 256, 4>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return launch_ring<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x128_8W:
       return launch<256, 128, 4, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     default: KAD_UNSUPPORTED("unknown gemm tile configuration %d", cfg);
