@@ -253,7 +253,7 @@ int kad_gather_beam_rows(const void* src, int64_t ld_src_bytes, int src_rows_per
  * of transformers' l2norm (prefill); 0 normalises in fp32 as ops.py:147-148.
  * workspace: caller-owned device memory of at least the size reported by
  * kad_gdn_chunk_workspace_bytes (per-chunk intermediates).  bf16 q/k/v;
- * K, V in {64, 128}; v rows 16-byte aligned.
+ * K, V in {64, 128}; q/k/v and out rows 16-byte aligned.
  */
 int kad_gdn_chunk_workspace_bytes(int N, int T, int HV, int K, int64_t* bytes);
 int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,

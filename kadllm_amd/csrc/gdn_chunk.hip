@@ -2,9 +2,9 @@
 //
 // Replaces, for the prefill, transformers' torch_chunk_gated_delta_rule
 // (modeling_qwen3_5.py:249-327) that the reference prefill runs through the
-// native model forward (src/kadllm/adapters/qwen3_5.py:111), and, for the
-// operator, src/kadllm/ops.py:139-163 when a suffix is longer than the replay
-// kernel handles or a final state is requested (ops.py:119-122).
+// native model forward (src/kadllm/adapters/qwen3_5.py:111), and, for the operator,
+// src/kadllm/ops.py:139-163 when a suffix is longer than the replay kernel
+// handles or a final state is requested (ops.py:119-122).
 //
 // Per chunk of 64 tokens, with G the within-chunk cumulative log decay,
 // D_ij = exp(G_i - G_j) and hats the normalised q (incl. scale) and k:
@@ -16,17 +16,21 @@
 //   S    <- e^{G_last} S + sum_i e^{G_last - G_i} k^_i v_new_i^T
 //
 // Two kernels.  gdn_chunk_prep runs every (sequence, head, chunk) in
-// parallel: normalisation, the two Gram matrices on bf16 MFMA, the decay
-// masks and the triangular solve; it writes the chunk's bf16 q/k rows, T' and
-// In as bf16 hi/lo planes (x = hi + lo to 2^-16) and per-token scalars to a
-// workspace.  gdn_chunk_scan walks the chunks of one (sequence, head) in
-// order with 4 waves, wave w owning value columns [32w, 32w+32) of the fp32
-// state S [K, V].  S lives in MFMA accumulator registers (rows k, columns v)
-// and the same registers, split hi/lo, are the B operand of k S and q S: the
-// accumulator layout gives each lane the k-rows {0-3, 8-11} (+4 in the upper
-// half-wave) of every 16-row block of its column, and the A operands are read
-// from LDS in that same order.  All products run on v_mfma_f32_32x32x16_bf16
-// with fp32 accumulation; fp32 operands take 2-3 hi/lo passes.
+// parallel and does the part that needs no state: the q and k row scales,
+// the k Gram matrix on bf16 MFMA, the decay masks and the triangular solve.  It writes T' as bf16 hi/lo planes (x = hi + lo to 2^-16),
+// already in the scan's MFMA fragment order, and per-token scalars: 17 KB per
+// chunk.  gdn_chunk_scan walks the chunks of one (sequence, head) in order
+// with 4 waves, wave w owning value columns [32w, 32w+32) of the fp32 state
+// S [K, V]; two workgroups share a CU so one's loads overlap the other's
+// MFMAs.  It reads q, k and v itself and scales q and k with the prep's row
+// scales (k to the prep's bits), so In never goes through memory: the In^T
+// tiles come out of the
+// MFMA with tokens j in the accumulator order, which is the K order of the
+// In v_new product.  S lives in accumulator registers (rows k, columns v) and
+// the same registers, split hi/lo, are the B operand of k S and q S; the S
+// update reads k^T straight from the row-major k tile with transposing LDS
+// reads.  All products run on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation; fp32 operands take 2-3 hi/lo passes.
 
 #include "kad_common.h"
 
@@ -35,40 +39,74 @@ namespace {
 constexpr int kC = 64;
 constexpr int kPrepThreads = 256;
 
-// workspace record of one (sequence, head, chunk), in bytes
-template <int K>
+// per-token scalars of a chunk record
+// (EG e^G, BT beta, KM k multiplier, WU state-update weight, G2 G log2(e),
+// KRS / QRS the bf16 l2norm row scales of k / q (1 in fp32 mode), QM the q
+// multiplier incl. scale)
+enum { S_EG = 0, S_BT, S_KM, S_WU, S_G2, S_KRS, S_QRS, S_QM, kScal };
+constexpr float kLog2e = 1.4426950408889634f;
+
+// workspace record of one (sequence, head, chunk), in bytes: T' hi/lo as the
+// scan's A fragments ([it 2][s 4][plane 2][lane 64][8] bf16: lane L of
+// fragment (it, s) holds T'[it*32 + L%32][s*16 + (t/4)*8 + (L/32)*4 + t%4],
+// t < 8), then fp32 [kScal][64]
 struct ChunkRec {
-  static constexpr size_t kn = 0;                              // bf16 [64][K]
-  static constexpr size_t qn = kn + kC * K * 2;                // bf16 [64][K]
-  static constexpr size_t thi = qn + kC * K * 2;               // bf16 [64][64]
-  static constexpr size_t tlo = thi + kC * kC * 2;
-  static constexpr size_t ihi = tlo + kC * kC * 2;
-  static constexpr size_t ilo = ihi + kC * kC * 2;
-  static constexpr size_t scal = ilo + kC * kC * 2;            // fp32 [5][64]
-  static constexpr size_t bytes = scal + 5 * kC * 4;
+  static constexpr int tf_elems = 2 * 4 * 2 * 64 * 8;
+  static constexpr size_t tf = 0;
+  static constexpr size_t scal = tf + tf_elems * 2;
+  static constexpr size_t bytes = scal + kScal * kC * 4;
 };
-enum { S_EG = 0, S_BT = 1, S_KM = 2, S_QM = 3, S_WU = 4 };
+
+// sum of squares of a row whose CPR 16-byte slices sit in CPR consecutive
+// lanes (aligned groups); hf: the squares rounded to bf16 as transformers'
+// bf16 l2norm computes them.  Identical in the prep and the scan, so both
+// normalise k to the same bits.
+template <int CPR>
+__device__ __forceinline__ float row_sumsq(const u32x4& r, bool hf) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = __uint_as_float(r[e] << 16), hi = __uint_as_float(r[e] & 0xffff0000u);
+    ss += hf ? round_bf(lo * lo) : lo * lo;
+    ss += hf ? round_bf(hi * hi) : hi * hi;
+  }
+#pragma unroll
+  for (int o = CPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  return ss;
+}
+
+// transformers l2norm in bf16: x * rsqrt(sum(x*x) + eps), each op rounded;
+// hf_l2_rs gives the row scale, hf_l2_apply the scaled slice
+__device__ __forceinline__ float hf_l2_rs(float ss) {
+  return round_bf(1.0f / sqrtf(round_bf(round_bf(ss) + 1e-6f)));
+}
+__device__ __forceinline__ void hf_l2_apply(u32x4& r, float rs) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = round_bf(__uint_as_float(r[e] << 16) * rs);
+    const float hi = round_bf(__uint_as_float(r[e] & 0xffff0000u) * rs);
+    r[e] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  }
+}
 
 // ---------------------------------------------------------------------------
 template <int K>
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t ld_qk,
-    const void* __restrict__ g, int gdt, const void* __restrict__ beta, int bdt,
-    int64_t ld_gate, uint8_t* __restrict__ ws, int T, int H, int HV, int nchunks, float scale,
-    int hf_norm) {
+    const void* __restrict__ g, int gdt, const void* __restrict__ beta, int bdt, int64_t ld_gate,
+    uint8_t* __restrict__ ws, int T, int H, int HV, int nchunks, float scale, int hf_norm) {
   constexpr int LD = K + 8;
-  constexpr int CPR = K / 8;       // 16-byte chunks per q/k row
+  constexpr int CPR = K / 8;       // 16-byte slices per k row
   constexpr int RPI = 64 / CPR;    // rows per wave instruction
-  // the bf16 q/k rows (Gram phase) and, later, A in residue-major order plus
-  // the T' staging tile share one LDS region
-  constexpr size_t kRows = 2 * kC * LD * sizeof(bf16_t);
+  // the bf16 k rows (Gram phase) and, later, A in residue-major order plus
+  // the T' tile share one LDS region
+  constexpr size_t kRows = kC * LD * sizeof(bf16_t);
   constexpr size_t kMats = (kC * kC + kC * (kC + 1)) * sizeof(float);
   __shared__ __attribute__((aligned(16))) unsigned char region[kRows > kMats ? kRows : kMats];
   bf16_t* kb = (bf16_t*)region;
-  bf16_t* qb = kb + kC * LD;
   float* Ar = (float*)region;                         // Ar[i*64 + (j%4)*16 + j/4] = A[i][j]
   float(*Tm)[kC + 1] = (float(*)[kC + 1])(Ar + kC * kC);
-  __shared__ float Gs[kC], bt[kC], kmul[kC], qmul[kC];
+  __shared__ float Gs[kC], bt[kC], kmul[kC], krs[kC], qrs[kC], qmul[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x % nchunks;
@@ -77,10 +115,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   const int h = hv / (HV / H);
   const int t0 = c * kC;
   const int nt = min(kC, T - t0);
-  uint8_t* rec = ws + (size_t)blockIdx.x * ChunkRec<K>::bytes;
+  uint8_t* rec = ws + (size_t)blockIdx.x * ChunkRec::bytes;
 
-  // ---- rows: wave w normalises rows 16w..16w+15, RPI rows per instruction
-  // (lane -> row lane / CPR, 16-byte chunk lane % CPR)
+  // ---- k rows (normalised into LDS) and the q row scales: wave w handles
+  // rows 16w..16w+15, RPI rows per instruction (lane -> row lane / CPR,
+  // 16-byte slice lane % CPR)
   {
     const int rsub = lane / CPR, ch = lane % CPR;
 #pragma unroll
@@ -89,53 +128,23 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
       const bool live = i < nt;
       const int64_t off = ((int64_t)n * T + t0 + (live ? i : 0)) * ld_qk + (int64_t)h * K + ch * 8;
       u32x4 kr = live ? *(const u32x4*)(k + off) : u32x4{0, 0, 0, 0};
-      u32x4 qr = live ? *(const u32x4*)(q + off) : u32x4{0, 0, 0, 0};
-      float kv[8], qv[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kv[2 * e] = __uint_as_float(kr[e] << 16);
-        kv[2 * e + 1] = __uint_as_float(kr[e] & 0xffff0000u);
-        qv[2 * e] = __uint_as_float(qr[e] << 16);
-        qv[2 * e + 1] = __uint_as_float(qr[e] & 0xffff0000u);
-      }
-      float kss = 0.f, qss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        kss += hf_norm ? round_bf(kv[e] * kv[e]) : kv[e] * kv[e];
-        qss += hf_norm ? round_bf(qv[e] * qv[e]) : qv[e] * qv[e];
-      }
-#pragma unroll
-      for (int o = CPR / 2; o > 0; o >>= 1) {
-        kss += __shfl_xor(kss, o, 64);
-        qss += __shfl_xor(qss, o, 64);
-      }
-      float km, qm;
+      const u32x4 qr = live ? *(const u32x4*)(q + off) : u32x4{0, 0, 0, 0};
+      const float kss = row_sumsq<CPR>(kr, hf_norm);
+      const float qss = row_sumsq<CPR>(qr, hf_norm);
+      float km = 1.f, kr_s = 1.f, qr_s = 1.f, qm = scale;
       if (hf_norm) {
-        // transformers l2norm in bf16: x * rsqrt(sum(x*x) + eps), each op rounded
-        const float krs = round_bf(1.0f / sqrtf(round_bf(round_bf(kss) + 1e-6f)));
-        const float qrs = round_bf(1.0f / sqrtf(round_bf(round_bf(qss) + 1e-6f)));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          kv[e] = round_bf(kv[e] * krs);
-          qv[e] = round_bf(qv[e] * qrs);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kr[e] = (uint32_t)f2bf(kv[2 * e]) | ((uint32_t)f2bf(kv[2 * e + 1]) << 16);
-          qr[e] = (uint32_t)f2bf(qv[2 * e]) | ((uint32_t)f2bf(qv[2 * e + 1]) << 16);
-        }
-        km = 1.f;
-        qm = scale;
+        kr_s = hf_l2_rs(kss);
+        qr_s = hf_l2_rs(qss);
+        hf_l2_apply(kr, kr_s);
       } else {
         km = 1.0f / sqrtf(kss + 1e-6f);
         qm = scale / sqrtf(qss + 1e-6f);
       }
       *(u32x4*)(kb + i * LD + ch * 8) = kr;
-      *(u32x4*)(qb + i * LD + ch * 8) = qr;
-      *(u32x4*)((bf16_t*)(rec + ChunkRec<K>::kn) + i * K + ch * 8) = kr;
-      *(u32x4*)((bf16_t*)(rec + ChunkRec<K>::qn) + i * K + ch * 8) = qr;
       if (ch == 0) {
         kmul[i] = km;
+        krs[i] = kr_s;
+        qrs[i] = qr_s;
         qmul[i] = qm;
       }
     }
@@ -156,62 +165,39 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   }
   __syncthreads();
   if (tid < kC) {
-    float* sc = (float*)(rec + ChunkRec<K>::scal);
+    float* sc = (float*)(rec + ChunkRec::scal);
     sc[S_EG * kC + tid] = expf(Gs[tid]);
     sc[S_BT * kC + tid] = bt[tid];
     sc[S_KM * kC + tid] = kmul[tid];
-    sc[S_QM * kC + tid] = qmul[tid];
     sc[S_WU * kC + tid] = kmul[tid] * expf(Gs[kC - 1] - Gs[tid]);
+    sc[S_G2 * kC + tid] = Gs[tid] * kLog2e;
+    sc[S_KRS * kC + tid] = krs[tid];
+    sc[S_QRS * kC + tid] = qrs[tid];
+    sc[S_QM * kC + tid] = qmul[tid];
   }
 
-  // ---- Gram matrices: 8 tiles of 32x32 (4 for k k^T, 4 for q k^T), 2 per wave.
-  // q k^T tiles go straight to the workspace as In hi/lo; k k^T tiles become A
-  // once every wave is done reading the rows.
-  bf16_t* ihi = (bf16_t*)(rec + ChunkRec<K>::ihi);
-  bf16_t* ilo = (bf16_t*)(rec + ChunkRec<K>::ilo);
-  f32x16 gram[2];
-  {
+  // ---- k k^T: the three 32x32 tiles on or below the diagonal, waves 0..2
+  // (tile (0,1) lies above it: A is zero there)
+  const int ti = wave == 0 ? 0 : 1, tj = wave == 2 ? 1 : 0;
+  f32x16 gram = f32x16{};
+  if (wave < 3) {
     const int fr = lane & 31, fk = (lane >> 5) * 8;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tile = wave * 2 + tt;
-      const int which = tile >> 2, ti = (tile >> 1) & 1, tj = tile & 1;
-      const bf16_t* rowsrc = which == 0 ? kb : qb;
-      f32x16 acc = f32x16{};
-#pragma unroll
-      for (int s = 0; s < K / 16; ++s) {
-        const bf16x8 a = as_bf16x8(*(const u32x4*)(rowsrc + (ti * 32 + fr) * LD + s * 16 + fk));
-        const bf16x8 b = as_bf16x8(*(const u32x4*)(kb + (tj * 32 + fr) * LD + s * 16 + fk));
-        acc = mfma32x32x16(a, b, acc);
-      }
-      gram[tt] = acc;
-      if (which == 1) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int i = ti * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
-          const int j = tj * 32 + fr;
-          const float iv = j <= i ? (acc[e] * qmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
-          const bf16_t ih = f2bf(iv);
-          ihi[i * kC + j] = ih;
-          ilo[i * kC + j] = f2bf(iv - bf2f(ih));
-        }
-      }
+    for (int s = 0; s < K / 16; ++s) {
+      const bf16x8 a = as_bf16x8(*(const u32x4*)(kb + (ti * 32 + fr) * LD + s * 16 + fk));
+      const bf16x8 b = as_bf16x8(*(const u32x4*)(kb + (tj * 32 + fr) * LD + s * 16 + fk));
+      gram = mfma32x32x16(a, b, gram);
     }
   }
   __syncthreads();  // rows no longer needed: the region becomes A / T'
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int tile = wave * 2 + tt;
-    const int which = tile >> 2, ti = (tile >> 1) & 1, tj = tile & 1;
-    if (which == 0) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int i = ti * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
-        const int j = tj * 32 + (lane & 31);
-        Ar[i * kC + (j & 3) * 16 + (j >> 2)] =
-            j < i ? -bt[i] * (gram[tt][e] * kmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
-      }
-    }
+  for (int e = 0; e < 16; ++e) {
+    // wave 3 clears tile (0,1)
+    const int ri = wave == 3 ? 0 : ti, rj = wave == 3 ? 1 : tj;
+    const int i = ri * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
+    const int j = rj * 32 + (lane & 31);
+    Ar[i * kC + (j & 3) * 16 + (j >> 2)] =
+        wave < 3 && j < i ? -bt[i] * (gram[e] * kmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
   }
   __syncthreads();
 
@@ -250,29 +236,21 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   }
   __syncthreads();
 
-  // ---- T' as bf16 hi/lo planes, 16 elements (32 bytes per plane) per thread
+  // ---- T' hi/lo in fragment order: 512 (it, s, lane) fragments, 2 per thread
   {
-    bf16_t* thi = (bf16_t*)(rec + ChunkRec<K>::thi);
-    bf16_t* tlo = (bf16_t*)(rec + ChunkRec<K>::tlo);
-    const int i = tid >> 2, j0 = (tid & 3) * 16;
+    bf16_t* tf = (bf16_t*)(rec + ChunkRec::tf);
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      u32x4 hv4, lv4;
+    for (int u = 0; u < 2; ++u) {
+      const int f = tid + u * kPrepThreads;
+      const int it = f >> 8, s = (f >> 6) & 3, L = f & 63;
+      const int i = it * 32 + (L & 31), jb = s * 16 + (L >> 5) * 4;
+      float x[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint32_t hw = 0, lw = 0;
-#pragma unroll
-        for (int b2 = 0; b2 < 2; ++b2) {
-          const float tv = Tm[i][j0 + half * 8 + e * 2 + b2];
-          const bf16_t th = f2bf(tv);
-          hw |= (uint32_t)th << (16 * b2);
-          lw |= (uint32_t)f2bf(tv - bf2f(th)) << (16 * b2);
-        }
-        hv4[e] = hw;
-        lv4[e] = lw;
-      }
-      *(u32x4*)(thi + i * kC + j0 + half * 8) = hv4;
-      *(u32x4*)(tlo + i * kC + j0 + half * 8) = lv4;
+      for (int t = 0; t < 8; ++t) x[t] = Tm[i][jb + (t / 4) * 8 + t % 4];
+      bf16x8 fh, fl;
+      split8(x, fh, fl);
+      *(bf16x8*)(tf + (((it * 4 + s) * 2 + 0) * 64 + L) * 8) = fh;
+      *(bf16x8*)(tf + (((it * 4 + s) * 2 + 1) * 64 + L) * 8) = fl;
     }
   }
 }
@@ -296,149 +274,186 @@ __device__ __forceinline__ void acc_frags(const f32x16& t, int half, bf16x8& hi,
   split8(x, hi, lo);
 }
 
+typedef short tr_v4s_t __attribute__((ext_vector_type(4)));
+
+// A fragment of k^T for the state update: lane L gets feature kt*32 + L%32 of
+// the tokens s*16 + (t/4)*8 + (L/32)*4 + t%4 (t < 8), read transposed from the
+// row-major [token][feature] tile.  ds_read_b64_tr_b16: within each 16-lane
+// group lane i receives element i%4 of the 8-byte pieces addressed by lanes
+// 4e + i/4 (e < 4), so lane 16g + 4e + m addresses token
+// s*16 + r*8 + (g/2)*4 + e, features kt*32 + (g%2)*16 + 4m .. +3.
+template <int LDK>
+__device__ __forceinline__ bf16x8 kt_frag(const bf16_t* kb, int kt, int s, int lane) {
+  const int g = lane >> 4, e = (lane >> 2) & 3, m = lane & 3;
+  tr_v4s_t part[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const bf16_t* p = kb + (s * 16 + r * 8 + (g >> 1) * 4 + e) * LDK + kt * 32 + (g & 1) * 16 + 4 * m;
+    part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tr_v4s_t*)p);
+  }
+  const u32x2 lo = __builtin_bit_cast(u32x2, part[0]);
+  const u32x2 up = __builtin_bit_cast(u32x2, part[1]);
+  return as_bf16x8(u32x4{lo[0], lo[1], up[0], up[1]});
+}
+
 template <int K, int V>
-__global__ __launch_bounds__(V * 2) void gdn_chunk_scan(
+__global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t ld_qk,
     const bf16_t* __restrict__ v, int64_t ld_v, const uint8_t* __restrict__ ws,
     const void* __restrict__ state0, int sdt, int beams_per_state, bf16_t* __restrict__ out,
-    int64_t ld_out, float* __restrict__ final_state, int T, int HV, int nchunks) {
+    int64_t ld_out, float* __restrict__ final_state, int T, int H, int HV, int nchunks,
+    int hf_norm) {
   constexpr int KT = K / 32;      // 32-row k tiles of S
   constexpr int KS = K / 16;      // k16 steps over K
   constexpr int LDK = K + 8;      // bf16 [64][K] rows (16-byte padding)
-  constexpr int LD64 = kC + 4;    // bf16 [*][64] rows (8-byte padding)
-  constexpr int NTH = V * 2;      // V/32 waves
+  constexpr int LDV = V + 8;
+  constexpr int NTH = V * 2;
+  constexpr int CPR = K / 8;      // 16-byte slices per q/k row
   __shared__ __attribute__((aligned(16))) bf16_t kb[kC * LDK];
   __shared__ __attribute__((aligned(16))) bf16_t qb[kC * LDK];
-  __shared__ __attribute__((aligned(16))) bf16_t kbT[K * LD64];
-  __shared__ __attribute__((aligned(16))) bf16_t Th[kC * LD64], Tl[kC * LD64];
-  __shared__ __attribute__((aligned(16))) bf16_t Ih[kC * LD64], Il[kC * LD64];
-  __shared__ __attribute__((aligned(16))) bf16_t vb[kC * (V + 8)];
-  __shared__ float sc[5][kC];
+  __shared__ __attribute__((aligned(16))) bf16_t vb[kC * LDV];
+  __shared__ __attribute__((aligned(16))) bf16_t tf[ChunkRec::tf_elems];
+  __shared__ float sc[kScal][kC];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hi = lane >> 5, col = lane & 31;
+  const int tid0 = threadIdx.x, wave = tid0 >> 6;
   const int n = blockIdx.x / HV, hv = blockIdx.x % HV;
-  const int vcol = wave * 32 + col;  // this lane's value column
+  const int h = hv / (HV / H);
 
   // S[k][vcol] in accumulator layout: tile kt, entry e -> k = kt*32 + (e/4)*8 + hi*4 + e%4
   f32x16 S[KT];
+  {
+    const int lane = tid0 & 63, hi = lane >> 5, vcol = wave * 32 + (lane & 31);
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int kk = kt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
-      S[kt][e] = state0 ? load_as_float(state0,
-                                        ((int64_t)(n / beams_per_state) * HV + hv) * K * V +
-                                            (int64_t)kk * V + vcol,
-                                        sdt)
-                        : 0.f;
+      for (int e = 0; e < 16; ++e) {
+        const int kk = kt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+        S[kt][e] = state0 ? load_as_float(state0,
+                                          ((int64_t)(n / beams_per_state) * HV + hv) * K * V +
+                                              (int64_t)kk * V + vcol,
+                                          sdt)
+                          : 0.f;
+      }
     }
   }
 
   for (int c = 0; c < nchunks; ++c) {
+    // lane-derived indices are recomputed from an opaque copy of the thread
+    // id every chunk, so the compiler does not keep dozens of precomputed
+    // addresses live across the loop
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, hi = lane >> 5, col = lane & 31;
+    const int vcol = wave * 32 + col;  // this lane's value column
     const int t0 = c * kC;
     const int nt = min(kC, T - t0);
-    const uint8_t* rec = ws + ((size_t)blockIdx.x * nchunks + c) * ChunkRec<K>::bytes;
+    const uint8_t* rec = ws + ((size_t)blockIdx.x * nchunks + c) * ChunkRec::bytes;
+    const int64_t row0 = (int64_t)n * T + t0;
     __syncthreads();  // previous chunk done with LDS
     {
       // every global load of the chunk is issued before any LDS store, so the
       // load latency is paid once per chunk
-      constexpr int kRowV = kC * K / 8 / NTH;       // q/k 16-byte chunks per thread
-      constexpr int kPlaneV = kC * kC / 8 / NTH;    // T'/In plane chunks per thread
-      constexpr int kVV = kC * V / 8 / NTH;         // v chunks per thread
-      static_assert(kRowV * NTH * 8 == kC * K && kPlaneV * NTH * 8 == kC * kC &&
-                        kVV * NTH * 8 == kC * V, "chunk tiles must split evenly");
-      const bf16_t* kn = (const bf16_t*)(rec + ChunkRec<K>::kn);
-      const bf16_t* qn = (const bf16_t*)(rec + ChunkRec<K>::qn);
-      const bf16_t* planes[4] = {(const bf16_t*)(rec + ChunkRec<K>::thi),
-                                 (const bf16_t*)(rec + ChunkRec<K>::tlo),
-                                 (const bf16_t*)(rec + ChunkRec<K>::ihi),
-                                 (const bf16_t*)(rec + ChunkRec<K>::ilo)};
-      u32x4 rk[kRowV], rq[kRowV], rp[4][kPlaneV], rv[kVV];
+      constexpr int kRowU = kC * CPR / NTH;               // q/k slices per thread
+      constexpr int kVU = kC * V / 8 / NTH;               // v slices per thread
+      constexpr int kTU = ChunkRec::tf_elems / 8 / NTH;   // T' slices per thread
+      constexpr int kSU = (kScal * kC + NTH - 1) / NTH;
+      static_assert(kRowU * NTH == kC * CPR && kVU * NTH * 8 == kC * V &&
+                        kTU * NTH * 8 == ChunkRec::tf_elems && NTH % CPR == 0,
+                    "chunk tiles must split evenly");
+      const float* scg = (const float*)(rec + ChunkRec::scal);
+      u32x4 rk[kRowU], rq[kRowU], rv[kVU], rt[kTU];
+      float rs[kSU], krs_u[kRowU], qrs_u[kRowU];
 #pragma unroll
-      for (int u = 0; u < kRowV; ++u) {
+      for (int u = 0; u < kRowU; ++u) {
         const int e = tid + u * NTH;
-        rk[u] = *(const u32x4*)(kn + e * 8);
-        rq[u] = *(const u32x4*)(qn + e * 8);
+        const int i = e / CPR, ch = e % CPR;
+        const bool live = i < nt;
+        const int64_t off = (row0 + (live ? i : 0)) * ld_qk + (int64_t)h * K + ch * 8;
+        rk[u] = live ? *(const u32x4*)(k + off) : u32x4{0u, 0u, 0u, 0u};
+        rq[u] = live ? *(const u32x4*)(q + off) : u32x4{0u, 0u, 0u, 0u};
+        krs_u[u] = scg[S_KRS * kC + i];
+        qrs_u[u] = scg[S_QRS * kC + i];
       }
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int u = 0; u < kPlaneV; ++u) rp[p][u] = *(const u32x4*)(planes[p] + (tid + u * NTH) * 8);
-#pragma unroll
-      for (int u = 0; u < kVV; ++u) {
+      for (int u = 0; u < kVU; ++u) {
         const int e = tid + u * NTH;
         const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
-        rv[u] = i < nt ? *(const u32x4*)(v + ((int64_t)n * T + t0 + i) * ld_v + (int64_t)hv * V + v8)
+        rv[u] = i < nt ? *(const u32x4*)(v + (row0 + i) * ld_v + (int64_t)hv * V + v8)
                        : u32x4{0u, 0u, 0u, 0u};
       }
-      const float* scg = (const float*)(rec + ChunkRec<K>::scal);
-      float rs[(5 * kC + NTH - 1) / NTH];
+      const bf16_t* tfg = (const bf16_t*)(rec + ChunkRec::tf);
 #pragma unroll
-      for (int u = 0; u < (5 * kC + NTH - 1) / NTH; ++u) {
+      for (int u = 0; u < kTU; ++u) rt[u] = *(const u32x4*)(tfg + (tid + u * NTH) * 8);
+#pragma unroll
+      for (int u = 0; u < kSU; ++u) {
         const int e = tid + u * NTH;
-        rs[u] = e < 5 * kC ? scg[e] : 0.f;
+        rs[u] = e < kScal * kC ? scg[e] : 0.f;
+      }
+      // q and k rows, normalised with the prep's row scales (bit-identical
+      // to the prep's own k rows)
+#pragma unroll
+      for (int u = 0; u < kRowU; ++u) {
+        const int e = tid + u * NTH;
+        const int i = e / CPR, ch = e % CPR;
+        if (hf_norm) {
+          hf_l2_apply(rk[u], krs_u[u]);
+          hf_l2_apply(rq[u], qrs_u[u]);
+        }
+        *(u32x4*)(kb + i * LDK + ch * 8) = rk[u];
+        *(u32x4*)(qb + i * LDK + ch * 8) = rq[u];
       }
 #pragma unroll
-      for (int u = 0; u < kRowV; ++u) {
-        const int e = tid + u * NTH;
-        const int i = e / (K / 8), k8 = (e % (K / 8)) * 8;
-        *(u32x4*)(kb + i * LDK + k8) = rk[u];
-        *(u32x4*)(qb + i * LDK + k8) = rq[u];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          kbT[(k8 + 2 * w) * LD64 + i] = (bf16_t)(rk[u][w] & 0xffffu);
-          kbT[(k8 + 2 * w + 1) * LD64 + i] = (bf16_t)(rk[u][w] >> 16);
-        }
-      }
-      bf16_t* dsts[4] = {Th, Tl, Ih, Il};
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int u = 0; u < kPlaneV; ++u) {
-          const int e = tid + u * NTH;
-          const int i = e / (kC / 8), j8 = (e % (kC / 8)) * 8;
-          *(u32x2*)(dsts[p] + i * LD64 + j8) = u32x2{rp[p][u][0], rp[p][u][1]};
-          *(u32x2*)(dsts[p] + i * LD64 + j8 + 4) = u32x2{rp[p][u][2], rp[p][u][3]};
-        }
-#pragma unroll
-      for (int u = 0; u < kVV; ++u) {
+      for (int u = 0; u < kVU; ++u) {
         const int e = tid + u * NTH;
         const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
-        *(u32x4*)(vb + i * (V + 8) + v8) = rv[u];
+        *(u32x4*)(vb + i * LDV + v8) = rv[u];
       }
 #pragma unroll
-      for (int u = 0; u < (5 * kC + NTH - 1) / NTH; ++u) {
+      for (int u = 0; u < kTU; ++u) *(u32x4*)(tf + (tid + u * NTH) * 8) = rt[u];
+#pragma unroll
+      for (int u = 0; u < kSU; ++u) {
         const int e = tid + u * NTH;
-        if (e < 5 * kC) sc[e / kC][e % kC] = rs[u];
+        if (e < kScal * kC) sc[e / kC][e % kC] = rs[u];
       }
     }
     __syncthreads();
 
-    // S as B fragments (hi/lo) for every k16 step
-    bf16x8 sh[KS], sl[KS];
+    // ---- k S and q S for both 32-token tiles, S split hi/lo per k16 step
+    f32x16 KSa[2], QSa[2];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) acc_frags(S[s / 2], s % 2, sh[s], sl[s]);
-
-    // ---- Z_j = beta_j (v_j - e^{G_j} kmul_j (k S)_j), tokens j in two 32-row tiles
+    for (int tt = 0; tt < 2; ++tt) {
+      KSa[tt] = f32x16{};
+      QSa[tt] = f32x16{};
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8 shf, slf;
+      acc_frags(S[s / 2], s % 2, shf, slf);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const bf16x8 ak = perm_frag(kb + (tt * 32 + col) * LDK, s * 16, hi);
+        const bf16x8 aq = perm_frag(qb + (tt * 32 + col) * LDK, s * 16, hi);
+        KSa[tt] = mfma32x32x16(ak, shf, KSa[tt]);
+        KSa[tt] = mfma32x32x16(ak, slf, KSa[tt]);
+        QSa[tt] = mfma32x32x16(aq, shf, QSa[tt]);
+        QSa[tt] = mfma32x32x16(aq, slf, QSa[tt]);
+      }
+      // one step of fragments in flight at a time keeps the register count
+      // within the two-workgroups-per-CU budget
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // ---- Z_j = beta_j (v_j - e^{G_j} kmul_j (k S)_j)
     f32x16 Z[2];
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
-      f32x16 acc = f32x16{};
-      const bf16_t* rowp = kb + (jt * 32 + col) * LDK;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 a = perm_frag(rowp, s * 16, hi);
-        acc = mfma32x32x16(a, sh[s], acc);
-        acc = mfma32x32x16(a, sl[s], acc);
-      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int j = jt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
-        const float vj = bf2f(vb[j * (V + 8) + vcol]);
-        Z[jt][e] = sc[S_BT][j] * (vj - sc[S_EG][j] * (sc[S_KM][j] * acc[e]));
+        const float vj = bf2f(vb[j * LDV + vcol]);
+        Z[jt][e] = sc[S_BT][j] * (vj - sc[S_EG][j] * (sc[S_KM][j] * KSa[jt][e]));
       }
     }
-    // ---- v_new = Z + T' Z (K dim = tokens, accumulator order on both sides)
+    // ---- v_new = Z + T' Z (T' strictly lower: rows 0..31 see tokens 0..31)
     bf16x8 zh[4], zl[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc_frags(Z[s / 2], s % 2, zh[s], zl[s]);
@@ -446,51 +461,78 @@ __global__ __launch_bounds__(V * 2) void gdn_chunk_scan(
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       f32x16 acc = Z[it];
-      const bf16_t* th = Th + (it * 32 + col) * LD64;
-      const bf16_t* tl = Tl + (it * 32 + col) * LD64;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 ah = perm_frag(th, s * 16, hi), al = perm_frag(tl, s * 16, hi);
+      for (int s = 0; s < 2 * (it + 1); ++s) {
+        const bf16x8 ah = *(const bf16x8*)(tf + (((it * 4 + s) * 2 + 0) * 64 + lane) * 8);
+        const bf16x8 al = *(const bf16x8*)(tf + (((it * 4 + s) * 2 + 1) * 64 + lane) * 8);
         acc = mfma32x32x16(ah, zh[s], acc);
         acc = mfma32x32x16(ah, zl[s], acc);
         acc = mfma32x32x16(al, zh[s], acc);
       }
       VN[it] = acc;
     }
-    // ---- o_i = e^{G_i} qmul_i (q S)_i + In v_new
+    // v_new as B fragments (hi + lo carries it to 2^-16 relative; the state
+    // update takes its weights from them, which keeps the register count
+    // within budget)
     bf16x8 vh[4], vl[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc_frags(VN[s / 2], s % 2, vh[s], vl[s]);
+    // ---- o_i = e^{G_i} qmul_i (q S)_i + sum_{j<=i} In_ij v_new_j.  In^T tiles
+    // (tokens j as rows) come from k rows x q rows; their accumulator order
+    // is the K order of the In v_new product.
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-      f32x16 qs = f32x16{};
-      const bf16_t* rowp = qb + (it * 32 + col) * LDK;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 a = perm_frag(rowp, s * 16, hi);
-        qs = mfma32x32x16(a, sh[s], qs);
-        qs = mfma32x32x16(a, sl[s], qs);
-      }
+      f32x16& o = QSa[it];
+      const int irow = it * 32 + col;  // this lane's query token in the In^T tiles
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int i = it * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
-        qs[e] *= sc[S_EG][i] * sc[S_QM][i];
-      }
-      const bf16_t* ih = Ih + (it * 32 + col) * LD64;
-      const bf16_t* il = Il + (it * 32 + col) * LD64;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 ah = perm_frag(ih, s * 16, hi), al = perm_frag(il, s * 16, hi);
-        qs = mfma32x32x16(ah, vh[s], qs);
-        qs = mfma32x32x16(ah, vl[s], qs);
-        qs = mfma32x32x16(al, vh[s], qs);
+        o[e] *= sc[S_EG][i] * sc[S_QM][i];
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int i = it * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
-        if (i < nt) out[((int64_t)n * T + t0 + i) * ld_out + (int64_t)hv * V + vcol] = f2bf(qs[e]);
+      for (int jt = 0; jt <= it; ++jt) {
+        f32x16 inT = f32x16{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 a = as_bf16x8(*(const u32x4*)(kb + (jt * 32 + col) * LDK + s * 16 + hi * 8));
+          const bf16x8 b = as_bf16x8(*(const u32x4*)(qb + irow * LDK + s * 16 + hi * 8));
+          inT = mfma32x32x16(a, b, inT);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const float qmi = sc[S_QM][irow], gi = sc[S_G2][irow];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int j = jt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+          inT[e] = j <= irow ? (inT[e] * qmi * sc[S_KM][j]) *
+                                   __builtin_amdgcn_exp2f(gi - sc[S_G2][j])
+                             : 0.f;
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          bf16x8 ih, il;
+          acc_frags(inT, half, ih, il);
+          const int s = jt * 2 + half;
+          o = mfma32x32x16(ih, vh[s], o);
+          o = mfma32x32x16(ih, vl[s], o);
+          o = mfma32x32x16(il, vh[s], o);
+        }
       }
     }
+    // ---- output: o goes through LDS (the v tile, which every wave has
+    // finished reading after the barrier) and leaves as 16-byte row slices;
+    // the state update runs between the two barriers
+    constexpr int CPV = V / 8;                // 16-byte slices per output row
+    constexpr int kOU = kC * CPV / NTH;       // slices per thread
+    static_assert(kOU * NTH == kC * CPV && NTH % CPV == 0, "output tile must split evenly");
+    const int och = tid % CPV;
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = it * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
+        vb[i * LDV + vcol] = f2bf(QSa[it][e]);
+      }
     // ---- S <- e^{G_last} S + sum_i (kmul_i e^{G_last-G_i}) k_i v_new_i^T
     bf16x8 wh[4], wl[4];
 #pragma unroll
@@ -500,7 +542,7 @@ __global__ __launch_bounds__(V * 2) void gdn_chunk_scan(
       for (int i8 = 0; i8 < 8; ++i8) {
         const int e = (s % 2) * 8 + i8;
         const int i = (s / 2) * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
-        x[i8] = VN[s / 2][e] * sc[S_WU][i];
+        x[i8] = ((float)vh[s][i8] + (float)vl[s][i8]) * sc[S_WU][i];
       }
       split8(x, wh[s], wl[s]);
     }
@@ -510,17 +552,24 @@ __global__ __launch_bounds__(V * 2) void gdn_chunk_scan(
       f32x16 acc = S[kt];
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] *= egl;
-      const bf16_t* rowp = kbT + (kt * 32 + col) * LD64;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 a = perm_frag(rowp, s * 16, hi);
+        const bf16x8 a = kt_frag<LDK>(kb, kt, s, lane);
         acc = mfma32x32x16(a, wh[s], acc);
         acc = mfma32x32x16(a, wl[s], acc);
       }
       S[kt] = acc;
     }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kOU; ++u) {
+      const int i = (tid + u * NTH) / CPV;
+      const u32x4 ov = *(const u32x4*)(vb + i * LDV + och * 8);
+      if (i < nt) *(u32x4*)(out + (row0 + i) * ld_out + (int64_t)hv * V + och * 8) = ov;
+    }
   }
   if (final_state) {
+    const int lane = tid0 & 63, hi = lane >> 5, vcol = wave * 32 + (lane & 31);
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
@@ -544,34 +593,23 @@ int launch_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, int
   int rc = kad_launch_status("gdn_chunk_prep");
   if (rc) return rc;
   hipLaunchKernelGGL((gdn_chunk_scan<K, V>), dim3((unsigned)((int64_t)N * HV)), dim3(V * 2), 0, s,
-                     (const bf16_t*)v, ld_v, (const uint8_t*)ws, state0, sdt, bps, (bf16_t*)out,
-                     ld_out, fin, T, HV, nchunks);
+                     (const bf16_t*)q, (const bf16_t*)k, ld_qk, (const bf16_t*)v, ld_v,
+                     (const uint8_t*)ws, state0, sdt, bps, (bf16_t*)out, ld_out, fin, T, H, HV,
+                     nchunks, hf_norm);
   return kad_launch_status("gdn_chunk_scan");
 }
 
-size_t rec_bytes(int K) { return K == 128 ? ChunkRec<128>::bytes : ChunkRec<64>::bytes; }
-
-}  // namespace
-
-static int64_t chunk_ws_bytes(int N, int T, int HV, int K) {
-  return (int64_t)N * HV * ((T + kC - 1) / kC) * (int64_t)rec_bytes(K);
+int64_t chunk_ws_bytes(int N, int T, int HV) {
+  return (int64_t)N * HV * ((T + kC - 1) / kC) * (int64_t)ChunkRec::bytes;
 }
 
-extern "C" int kad_gdn_chunk_workspace_bytes(int N, int T, int HV, int K, int64_t* bytes) {
-  KAD_REQUIRE(bytes, "null pointer argument");
-  KAD_REQUIRE(N > 0 && T > 0 && HV > 0, "bad dimensions");
-  if (K != 64 && K != 128) KAD_UNSUPPORTED("chunked gated delta supports K in {64, 128}");
-  *bytes = chunk_ws_bytes(N, T, HV, K);
-  return KAD_OK;
-}
-
-extern "C" int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk,
-                             int64_t ld_v, int qkv_dtype, const void* log_decay, int gate_dtype,
-                             const void* beta, int beta_dtype, int64_t ld_gate,
-                             const void* initial_state, int state_dtype, int beams_per_state,
-                             void* out, int64_t ld_out, float* final_state, void* workspace,
-                             int64_t workspace_bytes, int N, int T, int H, int HV, int K, int V,
-                             float scale, int transformers_l2norm, kad_stream_t stream) {
+int chunk_common(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
+                 int qkv_dtype, const void* log_decay, int gate_dtype, const void* beta,
+                 int beta_dtype, int64_t ld_gate, const void* initial_state, int state_dtype,
+                 int beams_per_state, void* out, int64_t ld_out,
+                 float* final_state, void* workspace, int64_t workspace_bytes, int N, int T,
+                 int H, int HV, int K, int V, float scale, int transformers_l2norm,
+                 hipStream_t s) {
   KAD_REQUIRE(q && k && v && log_decay && beta && out && workspace, "null pointer argument");
   KAD_REQUIRE(N > 0 && T > 0 && H > 0 && HV > 0 && HV % H == 0, "bad dimensions");
   KAD_REQUIRE(!initial_state || (beams_per_state > 0 && N % beams_per_state == 0),
@@ -582,14 +620,14 @@ extern "C" int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_
   KAD_REQUIRE(ld_v % 8 == 0 && ((uintptr_t)v % 16) == 0, "v rows must be 16-byte aligned");
   KAD_REQUIRE(ld_qk % 8 == 0 && ((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0,
               "q and k rows must be 16-byte aligned");
+  KAD_REQUIRE(ld_out % 8 == 0 && ((uintptr_t)out % 16) == 0, "out rows must be 16-byte aligned");
   if (qkv_dtype != KAD_DTYPE_BF16) KAD_UNSUPPORTED("chunked gated delta takes bf16 q/k/v");
   if (!((K == 64 || K == 128) && (V == 64 || V == 128)))
     KAD_UNSUPPORTED("chunked gated delta supports K, V in {64, 128}; got K=%d V=%d", K, V);
-  const int64_t need = chunk_ws_bytes(N, T, HV, K);
+  const int64_t need = chunk_ws_bytes(N, T, HV);
   KAD_REQUIRE(workspace_bytes >= need, "workspace of %lld bytes is smaller than %lld",
               (long long)workspace_bytes, (long long)need);
   KAD_REQUIRE(((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
 #define KAD_CHUNK(KK, VV)                                                                      \
   if (K == KK && V == VV)                                                                      \
     return launch_chunk<KK, VV>(q, k, v, ld_qk, ld_v, log_decay, gate_dtype, beta, beta_dtype, \
@@ -602,4 +640,27 @@ extern "C" int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_
   KAD_CHUNK(64, 128)
 #undef KAD_CHUNK
   KAD_UNSUPPORTED("unreachable");
+}
+
+}  // namespace
+
+extern "C" int kad_gdn_chunk_workspace_bytes(int N, int T, int HV, int K, int64_t* bytes) {
+  KAD_REQUIRE(bytes, "null pointer argument");
+  KAD_REQUIRE(N > 0 && T > 0 && HV > 0, "bad dimensions");
+  if (K != 64 && K != 128) KAD_UNSUPPORTED("chunked gated delta supports K in {64, 128}");
+  *bytes = chunk_ws_bytes(N, T, HV);
+  return KAD_OK;
+}
+
+extern "C" int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk,
+                             int64_t ld_v, int qkv_dtype, const void* log_decay, int gate_dtype,
+                             const void* beta, int beta_dtype, int64_t ld_gate,
+                             const void* initial_state, int state_dtype, int beams_per_state,
+                             void* out, int64_t ld_out, float* final_state, void* workspace,
+                             int64_t workspace_bytes, int N, int T, int H, int HV, int K, int V,
+                             float scale, int transformers_l2norm, kad_stream_t stream) {
+  return chunk_common(q, k, v, ld_qk, ld_v, qkv_dtype, log_decay, gate_dtype, beta, beta_dtype,
+                      ld_gate, initial_state, state_dtype, beams_per_state, out, ld_out,
+                      final_state, workspace, workspace_bytes, N, T, H, HV, K, V, scale,
+                      transformers_l2norm, (hipStream_t)stream);
 }
