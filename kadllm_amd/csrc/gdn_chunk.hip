@@ -106,7 +106,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   bf16_t* kb = (bf16_t*)region;
   float* Ar = (float*)region;                         // Ar[i*64 + (j%4)*16 + j/4] = A[i][j]
   float(*Tm)[kC + 1] = (float(*)[kC + 1])(Ar + kC * kC);
-  __shared__ float Gs[kC], bt[kC], kmul[kC], krs[kC], qrs[kC], qmul[kC];
+  __shared__ __attribute__((aligned(16))) float Gs[kC];
+  __shared__ float bt[kC], kmul[kC], krs[kC], qrs[kC], qmul[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x % nchunks;
@@ -157,11 +158,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   }
   __syncthreads();
   if (tid == 0) {
-    float acc = 0.f;
-    for (int i = 0; i < kC; ++i) {  // sequential cumulative sum, as torch.cumsum
-      acc += Gs[i];
-      Gs[i] = acc;
-    }
+    // sequential cumulative sum (torch.cumsum's order on the CPU), in registers
+    float gv[kC];
+#pragma unroll
+    for (int i = 0; i < kC; i += 4) *(float4*)(gv + i) = *(const float4*)(Gs + i);
+#pragma unroll
+    for (int i = 1; i < kC; ++i) gv[i] += gv[i - 1];
+#pragma unroll
+    for (int i = 0; i < kC; i += 4) *(float4*)(Gs + i) = *(const float4*)(gv + i);
   }
   __syncthreads();
   if (tid < kC) {
@@ -337,6 +341,80 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     }
   }
 
+  // the chunk's global data pass through registers into LDS; all loads are
+  // issued before the barrier, so their latency is paid once per chunk (and
+  // the second workgroup on the CU computes meanwhile).  Prefetching the next
+  // chunk instead needs the registers of a second workgroup.
+  constexpr int kRowU = kC * CPR / NTH;               // q/k slices per thread
+  constexpr int kVU = kC * V / 8 / NTH;               // v slices per thread
+  constexpr int kTU = ChunkRec::tf_elems / 8 / NTH;   // T' slices per thread
+  constexpr int kSU = (kScal * kC + NTH - 1) / NTH;
+  static_assert(kRowU * NTH == kC * CPR && kVU * NTH * 8 == kC * V &&
+                    kTU * NTH * 8 == ChunkRec::tf_elems && NTH % CPR == 0,
+                "chunk tiles must split evenly");
+  u32x4 rk[kRowU], rq[kRowU], rv[kVU], rt[kTU];
+  float rs[kSU], krs_u[kRowU], qrs_u[kRowU];
+  auto fetch = [&](int c, int tid) {
+    const int t0 = c * kC, nt = min(kC, T - t0);
+    const int64_t row0 = (int64_t)n * T + t0;
+    const uint8_t* rec = ws + ((size_t)blockIdx.x * nchunks + c) * ChunkRec::bytes;
+    const float* scg = (const float*)(rec + ChunkRec::scal);
+#pragma unroll
+    for (int u = 0; u < kRowU; ++u) {
+      const int e = tid + u * NTH;
+      const int i = e / CPR, ch = e % CPR;
+      const bool live = i < nt;
+      const int64_t off = (row0 + (live ? i : 0)) * ld_qk + (int64_t)h * K + ch * 8;
+      rk[u] = live ? *(const u32x4*)(k + off) : u32x4{0u, 0u, 0u, 0u};
+      rq[u] = live ? *(const u32x4*)(q + off) : u32x4{0u, 0u, 0u, 0u};
+      krs_u[u] = scg[S_KRS * kC + i];
+      qrs_u[u] = scg[S_QRS * kC + i];
+    }
+#pragma unroll
+    for (int u = 0; u < kVU; ++u) {
+      const int e = tid + u * NTH;
+      const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
+      rv[u] = i < nt ? *(const u32x4*)(v + (row0 + i) * ld_v + (int64_t)hv * V + v8)
+                     : u32x4{0u, 0u, 0u, 0u};
+    }
+    const bf16_t* tfg = (const bf16_t*)(rec + ChunkRec::tf);
+#pragma unroll
+    for (int u = 0; u < kTU; ++u) rt[u] = *(const u32x4*)(tfg + (tid + u * NTH) * 8);
+#pragma unroll
+    for (int u = 0; u < kSU; ++u) {
+      const int e = tid + u * NTH;
+      rs[u] = e < kScal * kC ? scg[e] : 0.f;
+    }
+  };
+  // q and k rows normalised with the prep's row scales (bit-identical to the
+  // prep's own k rows)
+  auto stash = [&](int tid) {
+#pragma unroll
+    for (int u = 0; u < kRowU; ++u) {
+      const int e = tid + u * NTH;
+      const int i = e / CPR, ch = e % CPR;
+      if (hf_norm) {
+        hf_l2_apply(rk[u], krs_u[u]);
+        hf_l2_apply(rq[u], qrs_u[u]);
+      }
+      *(u32x4*)(kb + i * LDK + ch * 8) = rk[u];
+      *(u32x4*)(qb + i * LDK + ch * 8) = rq[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kVU; ++u) {
+      const int e = tid + u * NTH;
+      const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
+      *(u32x4*)(vb + i * LDV + v8) = rv[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kTU; ++u) *(u32x4*)(tf + (tid + u * NTH) * 8) = rt[u];
+#pragma unroll
+    for (int u = 0; u < kSU; ++u) {
+      const int e = tid + u * NTH;
+      if (e < kScal * kC) sc[e / kC][e % kC] = rs[u];
+    }
+  };
+
   for (int c = 0; c < nchunks; ++c) {
     // lane-derived indices are recomputed from an opaque copy of the thread
     // id every chunk, so the compiler does not keep dozens of precomputed
@@ -347,75 +425,10 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     const int vcol = wave * 32 + col;  // this lane's value column
     const int t0 = c * kC;
     const int nt = min(kC, T - t0);
-    const uint8_t* rec = ws + ((size_t)blockIdx.x * nchunks + c) * ChunkRec::bytes;
     const int64_t row0 = (int64_t)n * T + t0;
+    fetch(c, tid);
     __syncthreads();  // previous chunk done with LDS
-    {
-      // every global load of the chunk is issued before any LDS store, so the
-      // load latency is paid once per chunk
-      constexpr int kRowU = kC * CPR / NTH;               // q/k slices per thread
-      constexpr int kVU = kC * V / 8 / NTH;               // v slices per thread
-      constexpr int kTU = ChunkRec::tf_elems / 8 / NTH;   // T' slices per thread
-      constexpr int kSU = (kScal * kC + NTH - 1) / NTH;
-      static_assert(kRowU * NTH == kC * CPR && kVU * NTH * 8 == kC * V &&
-                        kTU * NTH * 8 == ChunkRec::tf_elems && NTH % CPR == 0,
-                    "chunk tiles must split evenly");
-      const float* scg = (const float*)(rec + ChunkRec::scal);
-      u32x4 rk[kRowU], rq[kRowU], rv[kVU], rt[kTU];
-      float rs[kSU], krs_u[kRowU], qrs_u[kRowU];
-#pragma unroll
-      for (int u = 0; u < kRowU; ++u) {
-        const int e = tid + u * NTH;
-        const int i = e / CPR, ch = e % CPR;
-        const bool live = i < nt;
-        const int64_t off = (row0 + (live ? i : 0)) * ld_qk + (int64_t)h * K + ch * 8;
-        rk[u] = live ? *(const u32x4*)(k + off) : u32x4{0u, 0u, 0u, 0u};
-        rq[u] = live ? *(const u32x4*)(q + off) : u32x4{0u, 0u, 0u, 0u};
-        krs_u[u] = scg[S_KRS * kC + i];
-        qrs_u[u] = scg[S_QRS * kC + i];
-      }
-#pragma unroll
-      for (int u = 0; u < kVU; ++u) {
-        const int e = tid + u * NTH;
-        const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
-        rv[u] = i < nt ? *(const u32x4*)(v + (row0 + i) * ld_v + (int64_t)hv * V + v8)
-                       : u32x4{0u, 0u, 0u, 0u};
-      }
-      const bf16_t* tfg = (const bf16_t*)(rec + ChunkRec::tf);
-#pragma unroll
-      for (int u = 0; u < kTU; ++u) rt[u] = *(const u32x4*)(tfg + (tid + u * NTH) * 8);
-#pragma unroll
-      for (int u = 0; u < kSU; ++u) {
-        const int e = tid + u * NTH;
-        rs[u] = e < kScal * kC ? scg[e] : 0.f;
-      }
-      // q and k rows, normalised with the prep's row scales (bit-identical
-      // to the prep's own k rows)
-#pragma unroll
-      for (int u = 0; u < kRowU; ++u) {
-        const int e = tid + u * NTH;
-        const int i = e / CPR, ch = e % CPR;
-        if (hf_norm) {
-          hf_l2_apply(rk[u], krs_u[u]);
-          hf_l2_apply(rq[u], qrs_u[u]);
-        }
-        *(u32x4*)(kb + i * LDK + ch * 8) = rk[u];
-        *(u32x4*)(qb + i * LDK + ch * 8) = rq[u];
-      }
-#pragma unroll
-      for (int u = 0; u < kVU; ++u) {
-        const int e = tid + u * NTH;
-        const int i = e / (V / 8), v8 = (e % (V / 8)) * 8;
-        *(u32x4*)(vb + i * LDV + v8) = rv[u];
-      }
-#pragma unroll
-      for (int u = 0; u < kTU; ++u) *(u32x4*)(tf + (tid + u * NTH) * 8) = rt[u];
-#pragma unroll
-      for (int u = 0; u < kSU; ++u) {
-        const int e = tid + u * NTH;
-        if (e < kScal * kC) sc[e / kC][e % kC] = rs[u];
-      }
-    }
+    stash(tid);
     __syncthreads();
 
     // ---- k S and q S for both 32-token tiles, S split hi/lo per k16 step
