@@ -169,8 +169,11 @@ __device__ void row_select_exact(int64_t row,
 }
 
 
-constexpr int kCandCap = 4096;                 // LDS candidate capacity (32 KB)
-constexpr int kSampleCap = kCandCap * 4;       // bf16 sample keys aliasing the candidates
+// LDS candidate capacity: 2048 (16 KB) while about 2K + 256 <= 1024
+// candidates are expected, which leaves room for two workgroups more per CU
+// than 4096 (32 KB); the samples (bf16 keys) and the exact path's 4096-bin
+// histogram alias the same buffer
+constexpr int kCandCapSmall = 2048, kCandCapLarge = 4096;
 constexpr int kLine = 64;                      // logits per 128-byte line
 constexpr int kTargetLines = 128;              // sampled lines per row (~8k samples)
 
@@ -216,13 +219,16 @@ __device__ int wave_rank_bin(const int* hist, int r, int* above) {
 //     threshold into LDS;
 //  3. a radix select over the candidates' keys (ties at the K-th key ranked by
 //     column) emits the row's top K, unordered: the merge stage orders them.
-// If fewer than K or more than kCandCap entries qualify, the exact histogram
-// path runs instead, so the result never depends on the sample.
+// If fewer than K or more than CAP entries qualify, the exact histogram path
+// runs instead, so the result never depends on the sample.
+template <int CAP>
 __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
     const bf16_t* __restrict__ logits, int64_t ld, const uint8_t* __restrict__ mask,
     int64_t ld_mask, const float* __restrict__ parent, int Wp, int V, int K,
     float* __restrict__ cand_key, int* __restrict__ cand_idx, int line_stride, int rank) {
-  __shared__ __attribute__((aligned(16))) uint64_t cand[kCandCap];
+  constexpr int kSampleCap = CAP * 4;   // bf16 sample keys aliasing the candidates
+  static_assert(CAP * 8 >= 4096 * 4, "the exact path's histogram must fit the buffer");
+  __shared__ __attribute__((aligned(16))) uint64_t cand[CAP];
   __shared__ int hist[256];
   __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64], red_smax[kRowThreads / 64];
   __shared__ int sh_count, sh_hi, sh_above, sh_thr;
@@ -332,7 +338,7 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
       const uint32_t u = order16(bits);
       if (u >= thr) {
         const int slot = atomicAdd(&sh_count, 1);
-        if (slot < kCandCap) cand[slot] = ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
+        if (slot < CAP) cand[slot] = ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
       }
     }
   };
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   // log sum exp(v - M) = log(sum exp(v - mref)) + (mref - M)
   const float lse = logf(SE) + (mref - M);
   const int count = sh_count;
-  if (thr == 0 || count < K || count > kCandCap) {
+  if (thr == 0 || count < K || count > CAP) {
     // exact fallback: reuses the candidate buffer as the 4096-bin histogram
     __syncthreads();
     row_select_exact(row, logits, ld, mask, ld_mask, parent, Wp, V, K, cand_key, cand_idx,
@@ -707,9 +713,14 @@ extern "C" int kad_beam_row_select(const void* logits, int64_t ld, const void* m
   const int nlines = (V + kLine - 1) / kLine;
   const int line_stride = nlines > kTargetLines ? nlines / kTargetLines : 1;
   const int rank = (int)kad_cdiv(2 * (int64_t)K + 256, line_stride);
-  hipLaunchKernelGGL(row_select_kernel, dim3(rows), dim3(kRowThreads), 0, (hipStream_t)stream,
-                     (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores, Wp,
-                     V, K, cand_key, cand_idx, line_stride, rank);
+  if (2 * (int64_t)K + 256 <= kCandCapSmall / 2)
+    hipLaunchKernelGGL(row_select_kernel<kCandCapSmall>, dim3(rows), dim3(kRowThreads), 0,
+                       (hipStream_t)stream, (const bf16_t*)logits, ld, (const uint8_t*)mask,
+                       ld_mask, parent_scores, Wp, V, K, cand_key, cand_idx, line_stride, rank);
+  else
+    hipLaunchKernelGGL(row_select_kernel<kCandCapLarge>, dim3(rows), dim3(kRowThreads), 0,
+                       (hipStream_t)stream, (const bf16_t*)logits, ld, (const uint8_t*)mask,
+                       ld_mask, parent_scores, Wp, V, K, cand_key, cand_idx, line_stride, rank);
   return kad_launch_status("row_select_kernel");
 }
 

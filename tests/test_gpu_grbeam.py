@@ -35,7 +35,7 @@ def _check_selection(logits, scores, width, mask=None):
 
 
 @pytest.mark.parametrize("B,Wp,V,W", [(3, 5, 1000, 7), (2, 1, 4096, 8), (2, 8, 33, 200),
-                                      (1, 3, 64, 192)])
+                                      (1, 3, 64, 192), (2, 4, 60000, 300), (2, 3, 60000, 500)])
 def test_select_level_matches_oracle(device, B, Wp, V, W):
     g = torch.Generator().manual_seed(V + W)
     logits = torch.randn(B, Wp, V, generator=g).bfloat16()   # bf16 rounding creates ties
