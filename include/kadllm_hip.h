@@ -115,22 +115,6 @@ int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, 
                         int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                         int epilogue, int tile_config, kad_stream_t stream);
 
-/* The GDN input projection of the prefill with the causal conv fused into
- * the GEMM epilogue: C[M, N] = A W^T and Y[:, :conv_cols] = SiLU(conv4(C[:,
- * :conv_cols])) along the rows of each sequence (M = B * seqlen rows, zero
- * history), exactly as kad_causal_conv_prefill computes it.  C receives its
- * columns >= conv_cols in full, and its first conv_cols columns only on the
- * rows that kad_causal_conv_tile_fixup reads (the first and last 3 rows of
- * every 256-row tile and the last 4 rows of every sequence).  Y lacks the
- * rows r with r % 256 < 3 whose conv taps reach the previous tile; the
- * fix-up completes them.  Replaces the projection and causal_conv1d of the
- * transformers GDN layer the reference prefill runs
- * (src/kadllm/adapters/qwen3_5.py:111).  C, Y and conv_w [conv_cols, 4]
- * 16-byte aligned, row strides multiples of 8; K % 64 == 0. */
-int kad_gemm_bf16_conv(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
-                       int64_t ldc, const void* conv_w, void* Y, int64_t ldy, int conv_cols,
-                       int seqlen, int M, int N, int K, kad_stream_t stream);
-
 /* --------------------------------------------------------------------------
  * Row-wise layer kernels (bf16).  They replace the transformers modules the
  * reference decode calls between its projections (src/kadllm/adapters/
@@ -287,14 +271,6 @@ int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, in
 int kad_causal_conv_prefill(const void* x, int64_t ldx, const void* weight, void* out,
                             int64_t ldo, void* state, int B, int L, int C, int activation_silu,
                             kad_stream_t stream);
-
-/* Completes kad_gemm_bf16_conv: the conv + SiLU output rows whose taps reach
- * the previous 256-row tile, from the raw rows x holds, and (state
- * nullable) the conv state [B, C, 4] of the last 4 inputs.  x/out [B*L, C]
- * row-strided bf16, 16-byte aligned rows; weight [C, 4]. */
-int kad_causal_conv_tile_fixup(const void* x, int64_t ldx, const void* weight, void* out,
-                               int64_t ldo, void* state, int B, int L, int C,
-                               kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
  * MFMA lane-layout self-test (no reference counterpart): C[16x16] = A[16x32]

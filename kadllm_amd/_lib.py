@@ -48,8 +48,6 @@ SIGNATURES = {
     "kad_gdn_chunk_workspace_bytes": "iiiip",
     "kad_gdn_chunk": "ppplli" "pipil" "pii" "plp" "pl" "iiiiii" "fi" "s",
     "kad_causal_conv_prefill": "plpplpiiiis",
-    "kad_causal_conv_tile_fixup": "plpplpiiis",
-    "kad_gemm_bf16_conv": "plpl" "pl" "ppl" "ii" "iii" "s",
     "kad_selftest_mfma16": "ppps",
     "kad_selftest_mfma32": "ppps",
 }

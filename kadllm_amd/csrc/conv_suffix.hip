@@ -234,7 +234,11 @@ __global__ __launch_bounds__(256) void conv_prefill_bf16(
         win[ch][1] = win[ch][2];
         win[ch][2] = win[ch][3];
         win[ch][3] = xv[hh];
-        const float y = conv4_silu(wt[ch], win[ch][0], win[ch][1], win[ch][2], win[ch][3], silu);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc += wt[ch][i] * win[ch][i];
+        float y = round_bf(acc);
+        if (silu) y = silu_f(y);
         packed |= (uint32_t)f2bf(y) << (16 * hh);
       }
       o[e] = packed;
@@ -266,75 +270,6 @@ int launch_scalar(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx_t, const
                      history, (const T*)w, width, (const T*)bias, (T*)out, so_n, so_c, so_t, W,
                      C, T_, total, silu);
   return kad_launch_status("conv_suffix_scalar");
-}
-
-// Completes the conv output of a GEMM whose epilogue ran the conv per
-// 256-row tile (kad_gemm_bf16_conv): rows r with r % 256 < 3 whose taps reach
-// rows of the previous tile (position t = r % L > r % 256).  x holds the raw
-// projection for those rows and the 3 rows before them.  One thread per
-// (row, 8 channels).
-__global__ __launch_bounds__(256) void conv_tile_fixup_bf16(const bf16_t* __restrict__ x,
-                                                           int64_t ldx,
-                                                           const bf16_t* __restrict__ w,
-                                                           bf16_t* __restrict__ out, int64_t ldo,
-                                                           int M, int L, int C) {
-  const int C8 = C / 8;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t cand = idx / C8;  // (tile >= 1, j < 3)
-  const int c0 = (int)(idx % C8) * 8;
-  const int64_t row = (cand / 3 + 1) * 256 + cand % 3;
-  if (row >= M) return;
-  const int t = (int)(row % L), j = (int)(row % 256);
-  if (t <= j) return;  // every tap within the tile: the GEMM epilogue wrote it
-  float wt[8][4];
-  {
-    const u32x4* wp = (const u32x4*)(w + (int64_t)c0 * 4);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const u32x4 r = wp[q];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int flat = q * 8 + e * 2;
-        wt[flat / 4][flat % 4] = __uint_as_float(r[e] << 16);
-        wt[(flat + 1) / 4][(flat + 1) % 4] = __uint_as_float(r[e] & 0xffff0000u);
-      }
-    }
-  }
-  float xs[4][8];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {  // xs[k] = row - 3 + k
-    const bool live = t - 3 + k >= 0;
-    const u32x4 r = live ? *(const u32x4*)(x + (row - 3 + k) * ldx + c0) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xs[k][2 * e] = __uint_as_float(r[e] << 16);
-      xs[k][2 * e + 1] = __uint_as_float(r[e] & 0xffff0000u);
-    }
-  }
-  u32x4 o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float y0 = conv4_silu(wt[2 * e], xs[0][2 * e], xs[1][2 * e], xs[2][2 * e], xs[3][2 * e], true);
-    const float y1 = conv4_silu(wt[2 * e + 1], xs[0][2 * e + 1], xs[1][2 * e + 1],
-                                xs[2][2 * e + 1], xs[3][2 * e + 1], true);
-    o[e] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
-  }
-  *(u32x4*)(out + row * ldo + c0) = o;
-}
-
-// conv state [B, C, 4]: the raw inputs at positions L-4 .. L-1 (zero before 0)
-__global__ __launch_bounds__(256) void conv_state_bf16(const bf16_t* __restrict__ x, int64_t ldx,
-                                                      bf16_t* __restrict__ state, int B, int L,
-                                                      int C) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)B * C) return;
-  const int64_t b = idx / C;
-  const int c = (int)(idx % C);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = L - 4 + j;
-    state[idx * 4 + j] = t >= 0 ? x[(b * L + t) * ldx + c] : (bf16_t)0;
-  }
 }
 
 }  // namespace
@@ -389,32 +324,4 @@ extern "C" int kad_causal_conv_prefill(const void* x, int64_t ldx, const void* w
                      (hipStream_t)stream, (const bf16_t*)x, ldx, (const bf16_t*)weight,
                      (bf16_t*)out, ldo, (bf16_t*)state, B, L, C, activation_silu);
   return kad_launch_status("conv_prefill_bf16");
-}
-
-extern "C" int kad_causal_conv_tile_fixup(const void* x, int64_t ldx, const void* weight,
-                                          void* out, int64_t ldo, void* state, int B, int L,
-                                          int C, kad_stream_t stream) {
-  KAD_REQUIRE(x && weight && out, "null pointer argument");
-  KAD_REQUIRE(B > 0 && L > 0 && C > 0 && C % 8 == 0, "bad dimensions (C %% 8 == 0)");
-  KAD_REQUIRE(ldx >= C && ldo >= C, "row strides smaller than a row");
-  KAD_REQUIRE(ldx % 8 == 0 && ldo % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
-                  ((uintptr_t)out % 16) == 0 && ((uintptr_t)weight % 16) == 0,
-              "16-byte aligned rows required");
-  const int64_t M = (int64_t)B * L;
-  KAD_REQUIRE(M < 0x7fffffff, "too many rows");
-  const int64_t tiles = kad_cdiv(M, 256);
-  if (tiles > 1) {
-    const int64_t total = (tiles - 1) * 3 * (C / 8);
-    hipLaunchKernelGGL(conv_tile_fixup_bf16, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
-                       (hipStream_t)stream, (const bf16_t*)x, ldx, (const bf16_t*)weight,
-                       (bf16_t*)out, ldo, (int)M, L, C);
-    const int rc = kad_launch_status("conv_tile_fixup_bf16");
-    if (rc) return rc;
-  }
-  if (state) {
-    hipLaunchKernelGGL(conv_state_bf16, dim3((unsigned)kad_cdiv((int64_t)B * C, 256)), dim3(256),
-                       0, (hipStream_t)stream, (const bf16_t*)x, ldx, (bf16_t*)state, B, L, C);
-    return kad_launch_status("conv_state_bf16");
-  }
-  return KAD_OK;
 }

@@ -190,21 +190,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
 // across tile shapes.
 constexpr int kT = 256;
 
-// Epilogue of the GDN input projection (internal id, not a tile-config
-// epilogue): the causal width-4 conv + SiLU of the first `cols` output
-// columns along the rows of each sequence of `seqlen` rows, written to y.
-// The raw projection goes to C for columns >= cols, and for columns < cols
-// only on the rows the conv fix-up and the conv state read: the first 3 and
-// last 3 rows of every 256-row tile and the last 4 rows of every sequence.
-constexpr int kEpiConv = 3;
-struct ConvEpi {
-  const bf16_t* w;   // [cols, 4]
-  bf16_t* y;
-  int64_t ldy;
-  int cols;
-  int seqlen;
-};
-
 template <int BN>
 struct Tile256 {
   static constexpr int NJ = BN / 64;                 // 32-column blocks per wave
@@ -316,91 +301,6 @@ __device__ __forceinline__ void epilogue_tile(f32x16 (&acc)[4][Tile256<BN>::NJ],
   }
 }
 
-// Conv epilogue (BN = 256, waves 2 x 2): stage the raw bf16 tile in LDS
-// exactly as the store epilogue does, then every lane takes an 8-column slice
-// of 4 rows per pass; a row's conv taps are the rows above it in the same
-// tile (another wave's staging rows where it crosses row 128).  Rows whose
-// taps reach the previous tile are left to the fix-up kernel.
-__device__ __forceinline__ void epilogue_conv_tile(f32x16 (&acc)[4][4], bf16_t* smem, int lane,
-                                                   int wave, int m0, int n0, bf16_t* C,
-                                                   int64_t ldc, const ConvEpi& ce, int M, int N) {
-  constexpr int kEpiLd = Tile256<256>::EpiLd;
-  const int wm = wave >> 1, wn = wave & 1;
-  bf16_t* ep = smem + wave * 128 * kEpiLd;
-  const int e_row = lane & 31, e_col = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 packed;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          packed[h] = (uint32_t)f2bf(acc[i][j][g * 4 + h * 2]) |
-                      ((uint32_t)f2bf(acc[i][j][g * 4 + h * 2 + 1]) << 16);
-        *(u32x2*)(ep + (i * 32 + e_row) * kEpiLd + j * 32 + g * 8 + e_col) = packed;
-      }
-  __syncthreads();
-  constexpr int kChunks = 16, kRowsPer = 4;  // 128 columns per wave, 8 per lane
-  const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
-  const int col = n0 + wn * 128 + c_col;
-  const bool conv_col = col < ce.cols;
-  float wt[8][4];
-  if (conv_col) {
-    const u32x4* wp = (const u32x4*)(ce.w + (int64_t)col * 4);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const u32x4 r = wp[q];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int flat = q * 8 + e * 2;
-        wt[flat / 4][flat % 4] = __uint_as_float(r[e] << 16);
-        wt[(flat + 1) / 4][(flat + 1) % 4] = __uint_as_float(r[e] & 0xffff0000u);
-      }
-    }
-  }
-  // staging row of tile row q for this lane's columns
-  auto stage_row = [&](int q) -> const bf16_t* {
-    return smem + ((q >> 7) * 2 + wn) * 128 * kEpiLd + (q & 127) * kEpiLd + c_col;
-  };
-#pragma unroll 2
-  for (int r = c_row; r < 128; r += kRowsPer) {
-    const int rt = wm * 128 + r;  // row within the tile
-    const int row = m0 + rt;
-    if (row >= M || col >= N) continue;
-    const u32x4 v = *(const u32x4*)(ep + r * kEpiLd + c_col);
-    const int t = row % ce.seqlen;
-    const bool raw = !conv_col || rt < 3 || rt >= kT - 3 || t >= ce.seqlen - 4;
-    if (raw) *(u32x4*)(C + (int64_t)row * ldc + col) = v;
-    if (conv_col && (rt >= 3 || t <= rt)) {
-      float xs[4][8];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {  // xs[k]: tile row rt - 3 + k, zero before the sequence
-        const bool live = t - 3 + k >= 0;
-        const u32x4 rr = k == 3 ? v
-                         : live ? *(const u32x4*)stage_row(rt - 3 + k)
-                                : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          xs[k][2 * e] = __uint_as_float(rr[e] << 16);
-          xs[k][2 * e + 1] = __uint_as_float(rr[e] & 0xffff0000u);
-        }
-      }
-      u32x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float y0 =
-            conv4_silu(wt[2 * e], xs[0][2 * e], xs[1][2 * e], xs[2][2 * e], xs[3][2 * e], true);
-        const float y1 = conv4_silu(wt[2 * e + 1], xs[0][2 * e + 1], xs[1][2 * e + 1],
-                                    xs[2][2 * e + 1], xs[3][2 * e + 1], true);
-        o[e] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
-      }
-      *(u32x4*)(ce.y + (int64_t)row * ce.ldy + col) = o;
-    }
-  }
-}
-
 // issue order inside one 16-deep step: NM MFMAs, each followed by up to one
 // fragment read (NR in all), and the step's NV global loads and NW LDS writes
 // spread one per MFMA (two when there are at least NM of them)
@@ -443,7 +343,7 @@ template <int EPI, int BN, int MODE>
 __global__ __launch_bounds__(256, 1) void gemm256_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
     bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
-    int group, ConvEpi ce) {
+    int group) {
   using TL = Tile256<BN>;
   constexpr int NJ = TL::NJ, kStage = TL::Stage;
   constexpr int WG = BN / 32;          // W row groups of 8 rows per wave
@@ -586,18 +486,12 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  if constexpr (EPI == kEpiConv) {
-    static_assert(BN == 256, "the conv epilogue runs on 256 x 256 tiles");
-    epilogue_conv_tile(acc, smem, lane, wave, m0, n0, C, ldc, ce, M, N);
-  } else {
-    epilogue_tile<EPI, BN>(acc, smem, lane, wave, m0, n0, C, ldc, R, ldr, M, N);
-  }
+  epilogue_tile<EPI, BN>(acc, smem, lane, wave, m0, n0, C, ldc, R, ldr, M, N);
 }
 
 template <int EPI, int BN, int MODE>
 int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s,
-                ConvEpi ce = ConvEpi{}) {
+                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
   if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
   const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
@@ -607,7 +501,7 @@ int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
   }();
   hipLaunchKernelGGL((gemm256_kernel<EPI, BN, MODE>), dim3((unsigned)nblocks), dim3(256), 0, s,
                      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
-                     (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group, ce);
+                     (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group);
   return kad_launch_status("gemm256_kernel");
 }
 
@@ -888,26 +782,4 @@ extern "C" int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t 
                              int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                              int epilogue, kad_stream_t stream) {
   return kad_gemm_bf16_tiled(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, epilogue, 0, stream);
-}
-
-extern "C" int kad_gemm_bf16_conv(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
-                                  int64_t ldc, const void* conv_w, void* Y, int64_t ldy,
-                                  int conv_cols, int seqlen, int M, int N, int K,
-                                  kad_stream_t stream) {
-  KAD_REQUIRE(A && W && C && conv_w && Y, "null pointer argument");
-  KAD_REQUIRE(M > 0 && N > 0 && K > 0 && seqlen > 0 && M % seqlen == 0,
-              "dimensions must be positive and M a multiple of seqlen");
-  if (K % kBK) KAD_UNSUPPORTED("gemm requires K %% %d == 0, got K=%d", kBK, K);
-  KAD_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0,
-              "lda/ldw must be >= K and multiples of 8");
-  KAD_REQUIRE(((uintptr_t)A | (uintptr_t)W) % 16 == 0, "A and W must be 16-byte aligned");
-  KAD_REQUIRE(conv_cols > 0 && conv_cols <= N && conv_cols % 8 == 0,
-              "conv_cols must be in (0, N] and a multiple of 8");
-  KAD_REQUIRE(ldc >= N && ldy >= conv_cols, "row strides smaller than a row");
-  KAD_REQUIRE(vector_epilogue_ok(C, ldc, nullptr, 0, N, KAD_EPI_STORE) &&
-                  ((uintptr_t)Y % 16) == 0 && ldy % 8 == 0 && ((uintptr_t)conv_w % 16) == 0,
-              "C, Y and the conv weight need 16-byte aligned rows in 8-column units");
-  const ConvEpi ce{(const bf16_t*)conv_w, (bf16_t*)Y, ldy, conv_cols, seqlen};
-  return launch_tile<kEpiConv, 256, 2>(A, lda, W, ldw, C, ldc, nullptr, 0, M, N, K,
-                                       (hipStream_t)stream, ce);
 }

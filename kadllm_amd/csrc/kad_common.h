@@ -73,20 +73,6 @@ template <> struct Elem<float> {
 };
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
-
-// causal width-4 conv of one bf16 channel, x3 the newest tap: the fp32 tap sum
-// rounded to bf16 (the conv module's output), then SiLU.  Every prefill conv
-// path uses this, so their outputs agree bit for bit.
-__device__ __forceinline__ float conv4_silu(const float* w4, float x0, float x1, float x2,
-                                            float x3, bool silu) {
-  float acc = 0.f;
-  acc += w4[0] * x0;
-  acc += w4[1] * x1;
-  acc += w4[2] * x2;
-  acc += w4[3] * x3;
-  const float y = round_bf(acc);
-  return silu ? silu_f(y) : y;
-}
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float softplus_f(float x) {
   // torch softplus (beta 1, threshold 20)

@@ -242,21 +242,12 @@ class Qwen35Runner:
             terminal = li == len(self.layers) - 1
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
-                # input projection with the causal conv fused into the GEMM epilogue;
-                # the fix-up completes the rows whose conv taps cross a 256-row tile
-                # and writes the conv state
-                proj = torch.empty(rows, self.gdn_cols, dtype=torch.bfloat16, device=dev)
+                proj = self._gdn_proj(lyr, n)
                 conv = torch.empty(rows, self.conv_dim, dtype=torch.bfloat16, device=dev)
                 conv_state = torch.empty(B, self.conv_dim, 4, dtype=torch.bfloat16, device=dev)
-                c_in = lyr.w_in.shape[0]
-                _lib.call("kad_gemm_bf16_conv", _lib.ptr(n), n.stride(0), _lib.ptr(lyr.w_in),
-                          lyr.w_in.stride(0), _lib.ptr(proj), proj.stride(0), _lib.ptr(lyr.conv_w),
-                          _lib.ptr(conv), conv.stride(0), self.conv_dim, L, rows, c_in,
-                          n.shape[1], _lib.stream_of(x))
-                layers.gemm(n, lyr.w_ab, out=proj[:, c_in:c_in + lyr.w_ab.shape[0]])
-                _lib.call("kad_causal_conv_tile_fixup", _lib.ptr(proj), proj.stride(0),
+                _lib.call("kad_causal_conv_prefill", _lib.ptr(proj), proj.stride(0),
                           _lib.ptr(lyr.conv_w), _lib.ptr(conv), conv.stride(0),
-                          _lib.ptr(conv_state), B, L, self.conv_dim, _lib.stream_of(x))
+                          _lib.ptr(conv_state), B, L, self.conv_dim, 1, _lib.stream_of(x))
                 g, beta = self._gdn_gates(lyr, proj)
                 o = torch.empty(rows, self.vd, dtype=torch.bfloat16, device=dev)
                 S = torch.empty(B, HV, dk, dv, dtype=torch.float32, device=dev)

@@ -153,41 +153,6 @@ def test_gemm_short_k_pipelines_agree(device, K):
     assert ((outs[1].float() - ref).abs() <= 1e-2 * ref.abs() + 1e-2).all()
 
 
-@pytest.mark.parametrize("B,L", [(3, 300), (40, 5), (2, 1024), (1, 2)])
-def test_gemm_conv_epilogue_matches_gemm_then_conv(device, B, L):
-    """The input projection with the causal conv fused into the GEMM epilogue,
-    completed by the tile fix-up, against the plain GEMM followed by the
-    stand-alone conv kernel: conv output, conv state and the raw z columns
-    bit for bit.  Sequences straddle 256-row tiles (L = 300), many start
-    inside one tile (L = 5), align with tiles (L = 1024) or are shorter
-    than the conv (L = 2)."""
-    from kadllm_amd import _lib
-    M, K, N, CC = B * L, 128, 512, 384
-    g = torch.Generator().manual_seed(B * 1000 + L)
-    a = torch.randn(M, K, generator=g).bfloat16().to(device)
-    w = (torch.randn(N, K, generator=g) * 0.1).bfloat16().to(device)
-    cw = (torch.rand(CC, 4, generator=g) - 0.5).bfloat16().to(device)
-    s = _lib.stream_of(a)
-    raw = torch.empty(M, N, dtype=torch.bfloat16, device=device)
-    _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(raw), N, None, 0,
-              M, N, K, layers.EPI_STORE, 9, s)
-    ref = torch.empty(M, CC, dtype=torch.bfloat16, device=device)
-    ref_state = torch.empty(B, CC, 4, dtype=torch.bfloat16, device=device)
-    _lib.call("kad_causal_conv_prefill", _lib.ptr(raw), N, _lib.ptr(cw), _lib.ptr(ref), CC,
-              _lib.ptr(ref_state), B, L, CC, 1, s)
-    c = torch.zeros(M, N, dtype=torch.bfloat16, device=device)
-    y = torch.zeros(M, CC, dtype=torch.bfloat16, device=device)
-    st = torch.zeros(B, CC, 4, dtype=torch.bfloat16, device=device)
-    _lib.call("kad_gemm_bf16_conv", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), N, _lib.ptr(cw),
-              _lib.ptr(y), CC, CC, L, M, N, K, s)
-    _lib.call("kad_causal_conv_tile_fixup", _lib.ptr(c), N, _lib.ptr(cw), _lib.ptr(y), CC,
-              _lib.ptr(st), B, L, CC, s)
-    torch.cuda.synchronize()
-    assert torch.equal(y.cpu(), ref.cpu()), "conv output differs"
-    assert torch.equal(st.cpu(), ref_state.cpu()), "conv state differs"
-    assert torch.equal(c[:, CC:].cpu(), raw[:, CC:].cpu()), "raw columns differ"
-
-
 def test_gemm_pipelined_tile_rejects_unaligned_output(device):
     from kadllm_amd import _lib
     a = torch.zeros(256, 64, dtype=torch.bfloat16, device=device)
