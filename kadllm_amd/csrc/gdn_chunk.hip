@@ -230,8 +230,12 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
         if (q4 * 4 + 2 < nq) part += av.z * treg[q4 * 4 + 2];
         if (q4 * 4 + 3 < nq) part += av.w * treg[q4 * 4 + 3];
       }
-      part += __shfl_xor(part, 1, 64);
-      part += __shfl_xor(part, 2, 64);
+      // sum over the 4 lanes of the column: DPP quad permutes (xor 1, xor 2)
+      // instead of LDS-routed shuffles on this serial chain
+      part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                            0, __builtin_bit_cast(int, part), 0xB1, 0xF, 0xF, true));
+      part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                            0, __builtin_bit_cast(int, part), 0x4E, 0xF, 0xF, true));
       const float val = Ar[i * kC + (col & 3) * 16 + (col >> 2)] + part;
       if (r == (i & 3)) treg[i >> 2] = val;
     }
