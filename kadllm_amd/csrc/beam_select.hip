@@ -537,19 +537,36 @@ __device__ __forceinline__ bool before(float ka, int ia, float kb, int ib) {
   return ka > kb || (ka == kb && ia < ib);
 }
 
+// Every radix round reads the request's candidate keys again (L2-resident);
+// each thread loads kMergeBatch of them before using any, so that many loads
+// are in flight instead of one.
+constexpr int kMergeBatch = 8;
+
 __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
     const float* __restrict__ cand_key, const int* __restrict__ cand_idx, int ncand, int W,
     int V, float* __restrict__ scores, int64_t* __restrict__ parents,
     int64_t* __restrict__ tokens, uint8_t* __restrict__ valid) {
   __shared__ int hist[256];
   __shared__ uint32_t sh_prefix;
-  __shared__ int sh_need, sh_count;
+  __shared__ int sh_need, sh_count, sh_ties;
   __shared__ float sk[kMaxW];
   __shared__ int si[kMaxW];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
   const float* keys = cand_key + (int64_t)b * ncand;
   const int* idxs = cand_idx + (int64_t)b * ncand;
+  // f(order key, candidate index) over this thread's candidates
+  auto for_each = [&](auto&& f) {
+    int i0 = tid;
+    for (; i0 + (kMergeBatch - 1) * kMergeThreads < ncand; i0 += kMergeBatch * kMergeThreads) {
+      float kv[kMergeBatch];
+#pragma unroll
+      for (int q = 0; q < kMergeBatch; ++q) kv[q] = keys[i0 + q * kMergeThreads];
+#pragma unroll
+      for (int q = 0; q < kMergeBatch; ++q) f(order32(kv[q]), i0 + q * kMergeThreads);
+    }
+    for (int i = i0; i < ncand; i += kMergeThreads) f(order32(keys[i]), i);
+  };
 
   // radix select of the W-th largest key (order32 space), 4 x 8 bits
   uint32_t prefix = 0, pmask = 0;
@@ -557,10 +574,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = tid; i < 256; i += kMergeThreads) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < ncand; i += kMergeThreads) {
-      const uint32_t u = order32(keys[i]);
+    for_each([&](uint32_t u, int) {
       if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
-    }
+    });
     __syncthreads();
     if (tid == 0) {
       int acc = 0, d = 255;
@@ -570,6 +586,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
       }
       sh_prefix = prefix | ((uint32_t)d << shift);
       sh_need = need - acc;
+      sh_ties = hist[d];  // after the last round: the candidates equal to the key
     }
     __syncthreads();
     prefix = sh_prefix;
@@ -578,17 +595,20 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
     __syncthreads();
   }
   const uint32_t kth = prefix;  // order key of the W-th largest
-  // `need` ties at kth are taken, smallest flat index first: radix select on index
-  uint32_t iprefix = 0, imask = 0;
+  // `need` ties at kth are taken, smallest flat index first: radix select on
+  // index, unless every tie is taken
+  uint32_t iprefix = 0xffffffffu, imask = 0;
   int ineed = need;
-  for (int shift = 24; shift >= 0; shift -= 8) {
+  const bool all_ties = need == sh_ties;
+  if (!all_ties) iprefix = 0;
+  for (int shift = 24; shift >= 0 && !all_ties; shift -= 8) {
     for (int i = tid; i < 256; i += kMergeThreads) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < ncand; i += kMergeThreads) {
-      if (order32(keys[i]) != kth) continue;
+    for_each([&](uint32_t k, int i) {
+      if (k != kth) return;
       const uint32_t u = (uint32_t)idxs[i];
       if ((u & imask) == iprefix) atomicAdd(&hist[(u >> shift) & 255], 1);
-    }
+    });
     __syncthreads();
     if (tid == 0) {
       int acc = 0, d = 0;
@@ -610,8 +630,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
   // gather the W winners
   if (tid == 0) sh_count = 0;
   __syncthreads();
-  for (int i = tid; i < ncand; i += kMergeThreads) {
-    const uint32_t u = order32(keys[i]);
+  for_each([&](uint32_t u, int i) {
     const bool take = u > kth || (u == kth && (uint32_t)idxs[i] <= idx_cut);
     if (take) {
       const int slot = atomicAdd(&sh_count, 1);
@@ -620,7 +639,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
         si[slot] = idxs[i];
       }
     }
-  }
+  });
   __syncthreads();
   // pad to a power of two and bitonic-sort by (key desc, idx asc)
   int P = 1;
