@@ -310,7 +310,12 @@ class Qwen35Runner:
         dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
         nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         C = self.conv_dim
-        for lyr, cached in zip(self.layers, prefix_layers):
+        # terminal pruning: the logits read only each beam's last token, so the
+        # last layer's mixer output, o_proj/out_proj and MLP run on those rows
+        # (its K/V or conv/state inputs still cover the whole suffix)
+        x_last = x.view(BW, T, -1)[:, -1]
+        for li, (lyr, cached) in enumerate(zip(self.layers, prefix_layers)):
+            terminal = li == len(self.layers) - 1 and T > 1
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
                 proj = self._gdn_proj(lyr, n)
@@ -329,7 +334,31 @@ class Qwen35Runner:
                           _lib.ptr(beta), 0, HV, _lib.ptr(S), _lib.dtype_code(S.dtype),
                           _lib.ptr(o), self.vd, B, W, T, H_, HV, dk, dv, float(dk ** -0.5),
                           _lib.stream_of(x))
-                self._gdn_finish(lyr, o, proj, x)
+                if terminal:
+                    self._gdn_finish(lyr, o.view(BW, T, -1)[:, -1], proj.view(BW, T, -1)[:, -1],
+                                     x_last)
+                else:
+                    self._gdn_finish(lyr, o, proj, x)
+            elif terminal:
+                proj = layers.gemm(n, lyr.w_qkv)
+                ld = proj.stride(0)
+                # queries of the last token only (position prefix + T - 1), keys and
+                # values of the whole suffix
+                q = torch.empty(BW, 1, nh, hd, dtype=torch.bfloat16, device=dev)
+                k = torch.empty(BW, T, nkv, hd, dtype=torch.bfloat16, device=dev)
+                last_rows = proj.view(BW, T, -1)[:, -1]
+                layers.qk_norm_rope(last_rows, T * ld, 2 * hd, nh, lyr.q_norm, q, (0, nh * hd, hd),
+                                    BW, BW, hd, self.rot, self.inv_freq, prefix_length + T - 1, 1,
+                                    cfg.rms_norm_eps)
+                layers.qk_norm_rope(proj[:, 2 * nh * hd:], ld, hd, nkv, lyr.k_norm, k,
+                                    (0, nkv * hd, hd), R, R, hd, self.rot, self.inv_freq,
+                                    prefix_length, T, cfg.rms_norm_eps)
+                v = proj[:, (2 * nh + nkv) * hd:].as_strided((BW, T, nkv, hd), (T * ld, ld, hd, 1))
+                att = prefix_attention_decode(q, cached[0], cached[1], k, v, W, None,
+                                              hd ** -0.5, gate=last_rows[:, hd:],
+                                              gate_strides=(T * ld, T * ld, 2 * hd))
+                layers.gemm(att.view(BW, nh * hd), lyr.w_o, out=x_last,
+                            epilogue=layers.EPI_RESIDUAL, residual=x_last)
             else:
                 proj = layers.gemm(n, lyr.w_qkv)
                 ld = proj.stride(0)
@@ -347,9 +376,11 @@ class Qwen35Runner:
                                               gate_strides=(T * ld, ld, 2 * hd))
                 layers.gemm(att.view(R, nh * hd), lyr.w_o, out=x,
                             epilogue=layers.EPI_RESIDUAL, residual=x)
-            self._mlp(lyr, x, R)
-        last = x.view(BW, T, -1)[:, -1]
-        hN = layers.rmsnorm(last, self.norm_w, cfg.rms_norm_eps)
+            if terminal:
+                self._mlp(lyr, x_last, BW)
+            else:
+                self._mlp(lyr, x, R)
+        hN = layers.rmsnorm(x_last, self.norm_w, cfg.rms_norm_eps)
         logits = layers.gemm(hN, self.lm_head)
         return logits.view(B, W, -1)
 

@@ -303,6 +303,32 @@ def test_widened_ffn_layers_match_oracle(device):
                        "widened decode")
 
 
+def test_gdn_last_layer_pruned_prefill_and_decode(device):
+    """A model whose last layer is a GDN layer: the pruned last layer (its
+    output gate, out_proj and MLP on the last position only) in the prefill and
+    in a 3-token decode, against the oracle."""
+    import dataclasses
+    cfg = dataclasses.replace(tiny_hybrid_config(), num_hidden_layers=5,
+                              layer_types=("linear_attention", "full_attention",
+                                           "linear_attention", "full_attention",
+                                           "linear_attention"))
+    sd = random_state_dict(cfg, seed=21, dtype=torch.bfloat16)
+    oracle = Qwen35Oracle(cfg, sd)
+    truth = Qwen35Oracle(cfg, {k: v.float() for k, v in sd.items()})
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}))
+    g = torch.Generator().manual_seed(22)
+    ids = torch.randint(0, cfg.vocab_size, (2, 90), generator=g)
+    hist = torch.randint(0, cfg.vocab_size, (2, 5, 3), generator=g)
+    res = adapter.prefill(ids.to(device))
+    logits = adapter.decode(hist.to(device), res.state)
+    torch.cuda.synchronize()
+    ref_logits, ref_state = oracle.prefill(ids)
+    t_logits, t_state = truth.prefill(ids)
+    assert_bf16_parity(res.logits, ref_logits, t_logits, "GDN-last prefill")
+    assert_bf16_parity(logits, oracle.decode(hist, ref_state), truth.decode(hist, t_state),
+                       "GDN-last decode")
+
+
 def test_sid_only_head_search(device, tiny):
     """A head that projects only to a subset of token ids (in arbitrary order):
     logits are the oracle's columns for those ids, the softmax runs over the
