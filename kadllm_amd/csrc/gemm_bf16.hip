@@ -505,6 +505,126 @@ int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
   return kad_launch_status("gemm256_kernel");
 }
 
+// The split-load schedule with 8 waves (2 per SIMD) on a 256 x 256 tile:
+// waves 2 (M) x 4 (N), each a 128 x 64 sub-tile (8 MFMAs per 6 fragment reads
+// per step).  The second wave of each SIMD issues its MFMAs while the other
+// waits on its fragment reads.  The epilogue treats the tile as two 256 x 128
+// halves, each staged in its own LDS region.
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm256w8_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group) {
+  constexpr int BN = 256, NW = 8, WN = 4;
+  constexpr int NJ = BN / (32 * WN);        // 32-column blocks per wave: 2
+  constexpr int kStage = Tile256<BN>::Stage;
+  constexpr int AG = (kT / 8) / NW;         // A row groups (8 rows) per wave: 4
+  constexpr int WGW = (BN / 8) / NW;        // W row groups per wave: 4
+  constexpr int kLoads = AG + WGW;
+  constexpr int NM = 4 * NJ, NR = 4 + NJ;
+  constexpr int kHalfSmem = 4 * 128 * Tile256<128>::EpiLd;
+  constexpr int kSmem = 2 * kStage > 2 * kHalfSmem ? 2 * kStage : 2 * kHalfSmem;
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[kSmem];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int m0, n0;
+  tile_origin(M, N, BN, n_major, group, m0, n0);
+
+  // row groups g = wave + 8 i (8 rows each); lane L -> row g*8 + L/8, LDS
+  // chunk L%8 holding global chunk (L%8) ^ ((row>>1)&7)
+  const int d_row = lane >> 3;
+  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
+  const bf16_t* a_src[AG];
+  const bf16_t* b_src[WGW];
+#pragma unroll
+  for (int i = 0; i < AG; ++i) {
+    const int r = (wave + NW * i) * 8 + d_row;
+    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
+    if (i < WGW) b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
+  }
+  auto issue = [&](int stage, int k0, int i0, int i1) {  // A groups [i0, i1), W likewise
+    bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
+#pragma unroll
+    for (int i = i0; i < i1; ++i) dma16(a_src[i] + k0, base + i * NW * 8 * kBK);
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+      if (i < WGW) dma16(b_src[i] + k0, base + kT * kBK + i * NW * 8 * kBK);
+  };
+
+  const int f_row = lane & 31, f_sw = (lane >> 1) & 7, f_hi = lane >> 5;
+  const int fa_row = (wm * 128 + f_row) * kBK;
+  const int fw_row = kT * kBK + (wn * (BN / WN) + f_row) * kBK;
+  bf16x8 fa[2][4], fw[2][NJ];
+  auto load_frags = [&](int stage, int kk, int slot) {
+    const bf16_t* base = smem + stage * kStage + (((kk * 2 + f_hi) ^ f_sw) * 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[slot][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kBK));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      fw[slot][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kBK));
+  };
+  f32x16 acc[4][NJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
+  auto mfma_step = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x16(fw[slot][j], fa[slot][i], acc[i][j]);
+  };
+
+  const int KT = K / kBK;
+  issue(0, 0, 0, AG);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  load_frags(0, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int stage = kt & 1;
+    const int kn = min(kt + 1, KT - 1) * kBK;
+    issue(stage ^ 1, kn, 0, AG / 2);
+    load_frags(stage, 1, 1);
+    mfma_step(0);
+    interleave_step<NM, NR, kLoads / 2, 0>();
+    issue(stage ^ 1, kn, AG / 2, AG);
+    load_frags(stage, 2, 0);
+    mfma_step(1);
+    interleave_step<NM, NR, kLoads / 2, 0>();
+    load_frags(stage, 3, 1);
+    mfma_step(0);
+    interleave_step<NM, NR, 0, 0>();
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    load_frags(stage ^ 1, 0, 0);
+    mfma_step(1);
+    interleave_step<NM, NR, 0, 0>();
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // two 256 x 128 halves: wave (wm, wn) is wave (wm, wn % 2) of half wn / 2
+  const int half = wn >> 1;
+  epilogue_tile<EPI, 128>(acc, smem + half * kHalfSmem, lane, wm * 2 + (wn & 1), m0,
+                          n0 + half * 128, C, ldc, R, ldr, M, N);
+}
+
+template <int EPI>
+int launch_w8(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+              const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, 256);
+  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  hipLaunchKernelGGL((gemm256w8_kernel<EPI>), dim3((unsigned)nblocks), dim3(512), 0, s,
+                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N, K, n_major, 8);
+  return kad_launch_status("gemm256w8_kernel");
+}
+
 // 256 x BN tile fed through a ring of 4 LDS slots of 32-deep K slices.  The
 // loads of slice t + 3 are issued while slice t is consumed, half in each of
 // its two 16-deep steps and spread between MFMAs, so they have two slices of
@@ -682,18 +802,17 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
        CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8,
        CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10,
-       CFG_128x32 = 11, CFG_256x256_RDFIRST = 12, CFG_256x256_RING = 13 };
+       CFG_128x32 = 11, CFG_256x256_RDFIRST = 12, CFG_256x256_RING = 13, CFG_256x256_W8 = 14 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
-    // the pipelined 256x256 kernel when its tiles still fill every CU (and
-    // the output suits 16-byte stores): the 4-slot ring for K >= 3072, the
-    // reads-first schedule for very wide outputs (the vocabulary head), the
-    // split-load schedule otherwise; then the pipelined 256x128 one;
-    // 128x32 for outputs of at most 32 columns (the GDN gate projection);
-    // 128x128 otherwise (all measured on the decode/prefill shapes)
+    // the pipelined 256x256 kernel with 8 waves when its tiles still fill
+    // every CU (and the output suits 16-byte stores); then the pipelined
+    // 256x128 one; 128x32 for outputs of at most 32 columns (the GDN gate
+    // projection); 128x128 otherwise (all measured on the decode/prefill
+    // shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
     const int64_t tiles128 = kad_cdiv(M, 256) * kad_cdiv(N, 128);
     const bool vec = vector_epilogue_ok(C, ldc, R, ldr, N, EPI);
@@ -704,7 +823,7 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
     else if (tiles256 >= 256)
-      cfg = K >= 3072 ? CFG_256x256_RING : N >= 65536 ? CFG_256x256_RDFIRST : CFG_256x256_SPREAD;
+      cfg = CFG_256x256_W8;
     else if (vec && tiles128 >= 256)
       cfg = CFG_256x128_PIPE;
     else
@@ -735,6 +854,11 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       if (cfg == CFG_256x256_SPREAD)
         return launch_tile<EPI, 256, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       return launch_tile<EPI, 128, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x256_W8:
+      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
+        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
+                        cfg);
+      return launch_w8<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_RDFIRST:
     case CFG_256x256_RING:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
