@@ -505,26 +505,104 @@ int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
   return kad_launch_status("gemm256_kernel");
 }
 
-// The split-load schedule with 8 waves (2 per SIMD) on a 256 x 256 tile:
-// waves 2 (M) x 4 (N), each a 128 x 64 sub-tile (8 MFMAs per 6 fragment reads
-// per step).  The second wave of each SIMD issues its MFMAs while the other
-// waits on its fragment reads.  The epilogue treats the tile as two 256 x 128
-// halves, each staged in its own LDS region.
-template <int EPI>
+// Epilogue of one wave's (NI*32) x (NJ*32) sub-tile through a wave-private
+// LDS region: accumulators packed as bf16 (SwiGLU applied), then 16-byte row
+// stores with the residual add.  acc[i][j][e]: row i*32 + lane%32, column
+// j*32 + (e/4)*8 + (lane/32)*4 + e%4.  No workgroup barrier: the caller has
+// synchronised once after the main loop, and each wave only touches its own
+// region.
+template <int EPI, int NI, int NJ>
+__device__ __forceinline__ void epilogue_sub(f32x16 (&acc)[NI][NJ], bf16_t* ep, int lane,
+                                             int row0, int col0, bf16_t* C, int64_t ldc,
+                                             const bf16_t* R, int64_t ldr, int M, int N) {
+  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? NJ * 16 : NJ * 32;  // output columns
+  constexpr int kLd = kCols + 8;
+  const int e_row = lane & 31, e_col = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    if constexpr (EPI == KAD_EPI_SWIGLU) {
+#pragma unroll
+      for (int j = 0; j < NJ; j += 2) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2 packed;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            uint32_t two = 0;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const int e = g * 4 + h * 2 + q;
+              const float gv = round_bf(acc[i][j][e]);
+              const float uv = round_bf(acc[i][j + 1][e]);
+              two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+            }
+            packed[h] = two;
+          }
+          *(u32x2*)(ep + (i * 32 + e_row) * kLd + (j / 2) * 32 + g * 8 + e_col) = packed;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2 packed;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            packed[h] = (uint32_t)f2bf(acc[i][j][g * 4 + h * 2]) |
+                        ((uint32_t)f2bf(acc[i][j][g * 4 + h * 2 + 1]) << 16);
+          *(u32x2*)(ep + (i * 32 + e_row) * kLd + j * 32 + g * 8 + e_col) = packed;
+        }
+      }
+    }
+  }
+  // the wave's own LDS writes are visible to its later reads (in order)
+  constexpr int kChunks = kCols / 8, kRowsPer = 64 / kChunks;
+  const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
+  const int n_out = EPI == KAD_EPI_SWIGLU ? N / 2 : N;
+#pragma unroll 4
+  for (int r = c_row; r < NI * 32; r += kRowsPer) {
+    const int row = row0 + r, col = col0 + c_col;
+    if (row >= M || col >= n_out) continue;
+    u32x4 v = *(const u32x4*)(ep + r * kLd + c_col);
+    if constexpr (EPI == KAD_EPI_RESIDUAL) {
+      const u32x4 rr = *(const u32x4*)(R + (int64_t)row * ldr + col);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float lo = __uint_as_float(rr[h] << 16) + __uint_as_float(v[h] << 16);
+        const float hi = __uint_as_float(rr[h] & 0xffff0000u) + __uint_as_float(v[h] & 0xffff0000u);
+        v[h] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+      }
+    }
+    *(u32x4*)(C + (int64_t)row * ldc + col) = v;
+  }
+}
+
+// The split-load schedule with 8 waves (2 per SIMD) on a 256 x BN tile:
+// waves WM (M) x 8/WM (N), each an (NI*32) x (NJ*32) sub-tile.  The second
+// wave of each SIMD issues its MFMAs while the other waits on its fragment
+// reads.  BN = 256: waves 2 x 4 of 128 x 64; BN = 128: waves 4 x 2 of 64 x 64.
+template <int BN>
+struct TileW8 {
+  static constexpr int NW = 8, WM = BN == 256 ? 2 : 4, WN = NW / WM;
+  static constexpr int NI = kT / WM / 32, NJ = BN / WN / 32;
+  static constexpr int Stage = (kT + BN) * kBK;
+  static constexpr int AG = (kT / 8) / NW, WGW = (BN / 8) / NW;   // 8-row groups per wave
+  static constexpr int EpiWave = NI * 32 * (NJ * 32 + 8);         // elements per wave
+  static constexpr int Smem = 2 * Stage > NW * EpiWave ? 2 * Stage : NW * EpiWave;
+};
+
+template <int EPI, int BN>
 __global__ __launch_bounds__(512, 1) void gemm256w8_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
     bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
     int group) {
-  constexpr int BN = 256, NW = 8, WN = 4;
-  constexpr int NJ = BN / (32 * WN);        // 32-column blocks per wave: 2
-  constexpr int kStage = Tile256<BN>::Stage;
-  constexpr int AG = (kT / 8) / NW;         // A row groups (8 rows) per wave: 4
-  constexpr int WGW = (BN / 8) / NW;        // W row groups per wave: 4
+  using TW = TileW8<BN>;
+  constexpr int NW = TW::NW, WN = TW::WN, NI = TW::NI, NJ = TW::NJ;
+  constexpr int kStage = TW::Stage, AG = TW::AG, WGW = TW::WGW;
   constexpr int kLoads = AG + WGW;
-  constexpr int NM = 4 * NJ, NR = 4 + NJ;
-  constexpr int kHalfSmem = 4 * 128 * Tile256<128>::EpiLd;
-  constexpr int kSmem = 2 * kStage > 2 * kHalfSmem ? 2 * kStage : 2 * kHalfSmem;
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[kSmem];
+  constexpr int NM = NI * NJ, NR = NI + NJ;
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[TW::Smem];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -544,36 +622,37 @@ __global__ __launch_bounds__(512, 1) void gemm256w8_kernel(
     a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
     if (i < WGW) b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
   }
-  auto issue = [&](int stage, int k0, int i0, int i1) {  // A groups [i0, i1), W likewise
+  // A groups [i0, i1) and W groups [i0 * WGW / AG, i1 * WGW / AG)
+  auto issue = [&](int stage, int k0, int i0, int i1) {
     bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
 #pragma unroll
     for (int i = i0; i < i1; ++i) dma16(a_src[i] + k0, base + i * NW * 8 * kBK);
 #pragma unroll
-    for (int i = i0; i < i1; ++i)
-      if (i < WGW) dma16(b_src[i] + k0, base + kT * kBK + i * NW * 8 * kBK);
+    for (int i = i0 * WGW / AG; i < i1 * WGW / AG; ++i)
+      dma16(b_src[i] + k0, base + kT * kBK + i * NW * 8 * kBK);
   };
 
   const int f_row = lane & 31, f_sw = (lane >> 1) & 7, f_hi = lane >> 5;
-  const int fa_row = (wm * 128 + f_row) * kBK;
-  const int fw_row = kT * kBK + (wn * (BN / WN) + f_row) * kBK;
-  bf16x8 fa[2][4], fw[2][NJ];
+  const int fa_row = (wm * NI * 32 + f_row) * kBK;
+  const int fw_row = kT * kBK + (wn * NJ * 32 + f_row) * kBK;
+  bf16x8 fa[2][NI], fw[2][NJ];
   auto load_frags = [&](int stage, int kk, int slot) {
     const bf16_t* base = smem + stage * kStage + (((kk * 2 + f_hi) ^ f_sw) * 8);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
       fa[slot][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kBK));
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
       fw[slot][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kBK));
   };
-  f32x16 acc[4][NJ];
+  f32x16 acc[NI][NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
   auto mfma_step = [&](int slot) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x16(fw[slot][j], fa[slot][i], acc[i][j]);
   };
@@ -607,19 +686,18 @@ __global__ __launch_bounds__(512, 1) void gemm256w8_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  // two 256 x 128 halves: wave (wm, wn) is wave (wm, wn % 2) of half wn / 2
-  const int half = wn >> 1;
-  epilogue_tile<EPI, 128>(acc, smem + half * kHalfSmem, lane, wm * 2 + (wn & 1), m0,
-                          n0 + half * 128, C, ldc, R, ldr, M, N);
+  const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 32) / 2 : n0 + wn * NJ * 32;
+  epilogue_sub<EPI, NI, NJ>(acc, smem + wave * TW::EpiWave, lane, m0 + wm * NI * 32, col0, C,
+                            ldc, R, ldr, M, N);
 }
 
-template <int EPI>
+template <int EPI, int BN>
 int launch_w8(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
-  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, 256);
+  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
   if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
   const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
-  hipLaunchKernelGGL((gemm256w8_kernel<EPI>), dim3((unsigned)nblocks), dim3(512), 0, s,
+  hipLaunchKernelGGL((gemm256w8_kernel<EPI, BN>), dim3((unsigned)nblocks), dim3(512), 0, s,
                      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
                      (const bf16_t*)R, ldr, M, N, K, n_major, 8);
   return kad_launch_status("gemm256w8_kernel");
@@ -775,6 +853,225 @@ int launch_ring(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
   return kad_launch_status("gemm_ring_kernel");
 }
 
+// 16x16x32 MFMA form of the 8-wave tile.  mfma16x16x32(w, a, c): lane l
+// supplies row l%16 and K elements 8*(l/16) .. +7 of a 32-deep step of each
+// operand; acc[i][j][e] then holds output row i*16 + l%16, column
+// j*16 + 4*(l/16) + e of the wave's sub-tile (4 consecutive columns per lane).
+
+template <int BN>
+struct TileX16 {
+  static constexpr int NW = 8, WM = BN == 256 ? 2 : 4, WN = NW / WM;
+  static constexpr int NI = kT / WM / 16, NJ = BN / WN / 16;      // 16 x 16 blocks per wave
+  static constexpr int Stage = (kT + BN) * kBK;
+  static constexpr int AG = (kT / 8) / NW, WGW = (BN / 8) / NW;   // 8-row groups per wave
+  static constexpr int Cols = NJ * 16;                            // wave sub-tile columns
+  static constexpr int EpiWave = NI * 16 * (Cols + 8);
+  static constexpr int Smem = 2 * Stage > NW * EpiWave ? 2 * Stage : NW * EpiWave;
+};
+
+// Epilogue of one wave's (NI*16) x (NJ*16) sub-tile through a wave-private LDS
+// region, as epilogue_sub.  SwiGLU: the sub-tile's columns are whole 64-column
+// [gate 32 | up 32] groups, blocks 4g, 4g+1 gate and 4g+2, 4g+3 up.
+template <int EPI, int NI, int NJ>
+__device__ __forceinline__ void epilogue_x16(f32x4 (&acc)[NI][NJ], bf16_t* ep, int lane,
+                                             int row0, int col0, bf16_t* C, int64_t ldc,
+                                             const bf16_t* R, int64_t ldr, int M, int N) {
+  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? NJ * 8 : NJ * 16;
+  constexpr int kLd = kCols + 8;
+  const int e_row = lane & 15, e_col = (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    if constexpr (EPI == KAD_EPI_SWIGLU) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if ((j & 3) >= 2) continue;
+        u32x2 packed;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t two = 0;
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const float gv = round_bf(acc[i][j][h * 2 + q]);
+            const float uv = round_bf(acc[i][j + 2][h * 2 + q]);
+            two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+          }
+          packed[h] = two;
+        }
+        *(u32x2*)(ep + (i * 16 + e_row) * kLd + (j >> 2) * 32 + (j & 3) * 16 + e_col) = packed;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        u32x2 packed;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          packed[h] = (uint32_t)f2bf(acc[i][j][h * 2]) | ((uint32_t)f2bf(acc[i][j][h * 2 + 1]) << 16);
+        *(u32x2*)(ep + (i * 16 + e_row) * kLd + j * 16 + e_col) = packed;
+      }
+    }
+  }
+  constexpr int kChunks = kCols / 8, kRowsPer = 64 / kChunks;
+  const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
+  const int n_out = EPI == KAD_EPI_SWIGLU ? N / 2 : N;
+#pragma unroll 4
+  for (int r = c_row; r < NI * 16; r += kRowsPer) {
+    const int row = row0 + r, col = col0 + c_col;
+    if (row >= M || col >= n_out) continue;
+    u32x4 v = *(const u32x4*)(ep + r * kLd + c_col);
+    if constexpr (EPI == KAD_EPI_RESIDUAL) {
+      const u32x4 rr = *(const u32x4*)(R + (int64_t)row * ldr + col);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float lo = __uint_as_float(rr[h] << 16) + __uint_as_float(v[h] << 16);
+        const float hi = __uint_as_float(rr[h] & 0xffff0000u) + __uint_as_float(v[h] & 0xffff0000u);
+        v[h] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+      }
+    }
+    *(u32x4*)(C + (int64_t)row * ldc + col) = v;
+  }
+}
+
+// issue order of a half step: NM MFMAs, the first NR each followed by one
+// fragment read, the NV global loads spread over the rest
+template <int NM, int NR, int NV>
+__device__ __forceinline__ void interleave_x16() {
+#pragma unroll
+  for (int t = 0; t < NM; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (t < NR) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    } else if constexpr (NV > 0) {
+      constexpr int kSlots = NM - NR;
+      const int c = ((t - NR + 1) * NV) / kSlots - ((t - NR) * NV) / kSlots;
+#pragma unroll
+      for (int q = 0; q < c; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// 256 x BN tile, 8 waves, 16x16x32 MFMAs; two 64-deep LDS stages, two 32-deep
+// steps per tile.  One barrier per tile, in the middle of step 1: past it the
+// next tile has landed (each wave waited for its own loads) and every wave has
+// read its last fragments of the current stage, so the loads of the tile
+// after next go out into that stage at once and have a whole tile of time
+// to land.
+template <int EPI, int BN>
+__global__ __launch_bounds__(512, 1) void gemm_x16_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group) {
+  using TX = TileX16<BN>;
+  constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
+  constexpr int kStage = TX::Stage, AG = TX::AG, WGW = TX::WGW;
+  constexpr int kLoads = AG + WGW;
+  constexpr int NM = NI * NJ, NR = NI + NJ;
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[TX::Smem];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int m0, n0;
+  tile_origin(M, N, BN, n_major, group, m0, n0);
+
+  // row groups g = wave + 8 i (8 rows each); lane L -> row g*8 + L/8, LDS
+  // chunk L%8 holding global chunk (L%8) ^ ((row>>1)&7)
+  const int d_row = lane >> 3;
+  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
+  // uniform tile bases plus 32-bit per-lane offsets (a tile spans < 2^31
+  // elements: 256 rows of lda, ldw)
+  const bf16_t* a_base = A + (int64_t)m0 * lda;
+  const bf16_t* b_base = Wt + (int64_t)n0 * ldw;
+  int a_off[AG], b_off[WGW];
+#pragma unroll
+  for (int i = 0; i < AG; ++i) {
+    const int r = (wave + NW * i) * 8 + d_row;
+    a_off[i] = (int)((int64_t)(min(m0 + r, M - 1) - m0) * lda) + d_kc;
+    if (i < WGW) b_off[i] = (int)((int64_t)(min(n0 + r, N - 1) - n0) * ldw) + d_kc;
+  }
+  auto issue = [&](int stage, int k0) {
+    bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
+#pragma unroll
+    for (int i = 0; i < AG; ++i) dma16(a_base + (a_off[i] + k0), base + i * NW * 8 * kBK);
+#pragma unroll
+    for (int i = 0; i < WGW; ++i) dma16(b_base + (b_off[i] + k0), base + kT * kBK + i * NW * 8 * kBK);
+  };
+
+  // fragment lane l: row block_base + l%16, chunk 4*step + l/16, stored at
+  // chunk ^ ((row >> 1) & 7)
+  const int f_row = lane & 15, f_sw = (lane & 15) >> 1, f_q = lane >> 4;
+  const int fa_row = (wm * NI * 16 + f_row) * kBK;
+  const int fw_row = kT * kBK + (wn * NJ * 16 + f_row) * kBK;
+  bf16x8 fa[2][NI], fw[2][NJ];
+  auto load_frags = [&](int stage, int step, int buf) {
+    const bf16_t* base = smem + stage * kStage + (((step * 4 + f_q) ^ f_sw) * 8);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      fw[buf][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 16 * kBK));
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      fa[buf][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 16 * kBK));
+  };
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{};
+  // MFMAs of A blocks [i0, i1)
+  auto mfma_rows = [&](int buf, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x32(fw[buf][j], fa[buf][i], acc[i][j]);
+  };
+
+  // past the last tile the loads re-fetch it, which keeps every iteration's
+  // wait the same
+  const int KT = K / kBK;
+  issue(0, 0);
+  issue(1, min(1, KT - 1) * kBK);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoads));   // tile 0 landed
+  ring_barrier();
+  load_frags(0, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int stage = kt & 1;
+    const int k2 = min(kt + 2, KT - 1) * kBK;
+    load_frags(stage, 1, 1);
+    mfma_rows(0, 0, NI);
+    interleave_x16<NM, NR, 0>();
+    mfma_rows(1, 0, NI / 2);
+    interleave_x16<NM / 2, 0, 0>();
+    // tile kt + 1 landed; every wave is done reading this stage
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+    ring_barrier();
+    load_frags(stage ^ 1, 0, 0);
+    issue(stage, k2);
+    mfma_rows(1, NI / 2, NI);
+    interleave_x16<NM / 2, NR, kLoads>();
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 16) / 2 : n0 + wn * NJ * 16;
+  epilogue_x16<EPI, NI, NJ>(acc, smem + wave * TX::EpiWave, lane, m0 + wm * NI * 16, col0, C,
+                            ldc, R, ldr, M, N);
+}
+
+template <int EPI, int BN>
+int launch_x16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
+  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
+  if ((int64_t)kT * (lda > ldw ? lda : ldw) + K >= 0x7fffffff)
+    KAD_UNSUPPORTED("gemm rows too long for 32-bit tile offsets");
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  hipLaunchKernelGGL((gemm_x16_kernel<EPI, BN>), dim3((unsigned)nblocks), dim3(512), 0, s,
+                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N, K, n_major, 8);
+  return kad_launch_status("gemm_x16_kernel");
+}
+
 // 16-byte epilogue stores need aligned, 8-column-granular outputs
 bool vector_epilogue_ok(const void* C, int64_t ldc, const void* R, int64_t ldr, int N, int epi) {
   const int n_out = epi == KAD_EPI_SWIGLU ? N / 2 : N;
@@ -802,15 +1099,17 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
        CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8,
        CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10,
-       CFG_128x32 = 11, CFG_256x256_RDFIRST = 12, CFG_256x256_RING = 13, CFG_256x256_W8 = 14 };
+       CFG_128x32 = 11, CFG_256x256_RDFIRST = 12, CFG_256x256_RING = 13, CFG_256x256_W8 = 14,
+       CFG_256x128_W8 = 15,
+       CFG_256x256_X16 = 16, CFG_256x128_X16 = 17 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
-    // the pipelined 256x256 kernel with 8 waves when its tiles still fill
-    // every CU (and the output suits 16-byte stores); then the pipelined
-    // 256x128 one; 128x32 for outputs of at most 32 columns (the GDN gate
+    // the 8-wave 256x256 kernel on 16x16x32 MFMAs when its tiles still fill
+    // every CU (and the output suits 16-byte stores); then its 256x128
+    // variant; 128x32 for outputs of at most 32 columns (the GDN gate
     // projection); 128x128 otherwise (all measured on the decode/prefill
     // shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
@@ -823,9 +1122,9 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
     else if (tiles256 >= 256)
-      cfg = CFG_256x256_W8;
+      cfg = CFG_256x256_X16;
     else if (vec && tiles128 >= 256)
-      cfg = CFG_256x128_PIPE;
+      cfg = CFG_256x128_X16;
     else
       cfg = CFG_128x128;
   }
@@ -855,10 +1154,21 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
         return launch_tile<EPI, 256, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       return launch_tile<EPI, 128, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_W8:
+    case CFG_256x128_W8:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
                         cfg);
-      return launch_w8<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_256x256_W8)
+        return launch_w8<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return launch_w8<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x256_X16:
+    case CFG_256x128_X16:
+      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
+        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
+                        cfg);
+      if (cfg == CFG_256x256_X16)
+        return launch_x16<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return launch_x16<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_RDFIRST:
     case CFG_256x256_RING:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))

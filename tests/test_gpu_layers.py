@@ -101,7 +101,7 @@ def test_gemm_tile_configurations_agree(device, epi):
     x = torch.randn(M, n_out, generator=g).bfloat16()
     ad, wd = a.to(device), w.to(device)
     outs = {}
-    cfgs = [c for c in range(1, 15) if not (c == 11 and epi == layers.EPI_SWIGLU)]
+    cfgs = [c for c in range(1, 18) if not (c == 11 and epi == layers.EPI_SWIGLU)]
     for cfg in cfgs:
         c = torch.zeros(M, n_out + 16, dtype=torch.bfloat16, device=device)  # ldc > width
         cv = c[:, :n_out]
@@ -142,7 +142,7 @@ def test_gemm_short_k_pipelines_agree(device, K):
     a = torch.randn(M, K, generator=g).bfloat16().to(device)
     w = (torch.randn(N, K, generator=g) * 0.05).bfloat16().to(device)
     outs = {}
-    for cfg in (1, 7, 9, 12, 13, 14):
+    for cfg in (1, 7, 9, 12, 13, 14, 15, 16, 17):
         c = torch.zeros(M, N, dtype=torch.bfloat16, device=device)
         _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), N, None, 0,
                   M, N, K, layers.EPI_STORE, cfg, _lib.stream_of(a))
