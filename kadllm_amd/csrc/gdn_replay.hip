@@ -70,25 +70,6 @@ __device__ __forceinline__ float dot8_bf16(bf16x8 a, bf16x8 b, float acc) {
 }
 
 template <typename TIN>
-__device__ __forceinline__ void load4(const TIN* p, float* f);
-template <>
-__device__ __forceinline__ void load4<bf16_t>(const bf16_t* p, float* f) {
-  u32x2 r = *(const u32x2*)p;
-  f[0] = __uint_as_float(r[0] << 16);
-  f[1] = __uint_as_float(r[0] & 0xffff0000u);
-  f[2] = __uint_as_float(r[1] << 16);
-  f[3] = __uint_as_float(r[1] & 0xffff0000u);
-}
-template <>
-__device__ __forceinline__ void load4<float>(const float* p, float* f) {
-  f32x4 r = *(const f32x4*)p;
-  f[0] = r[0];
-  f[1] = r[1];
-  f[2] = r[2];
-  f[3] = r[3];
-}
-
-template <typename TIN>
 __device__ __forceinline__ void store4(TIN* p, const float* f);
 template <>
 __device__ __forceinline__ void store4<bf16_t>(bf16_t* p, const float* f) {
@@ -102,6 +83,33 @@ __device__ __forceinline__ void store4<float>(float* p, const float* f) {
   f32x4 r = {f[0], f[1], f[2], f[3]};
   *(f32x4*)p = r;
 }
+
+// four consecutive v elements kept as loaded (the conversion waits for the
+// load, so it happens only where the values are used)
+template <typename TIN>
+struct Raw4;
+template <>
+struct Raw4<bf16_t> {
+  u32x2 r;
+  __device__ __forceinline__ void load(const bf16_t* p) { r = *(const u32x2*)p; }
+  __device__ __forceinline__ void unpack(float* f) const {
+    f[0] = __uint_as_float(r[0] << 16);
+    f[1] = __uint_as_float(r[0] & 0xffff0000u);
+    f[2] = __uint_as_float(r[1] << 16);
+    f[3] = __uint_as_float(r[1] & 0xffff0000u);
+  }
+};
+template <>
+struct Raw4<float> {
+  f32x4 r;
+  __device__ __forceinline__ void load(const float* p) { r = *(const f32x4*)p; }
+  __device__ __forceinline__ void unpack(float* f) const {
+    f[0] = r[0];
+    f[1] = r[1];
+    f[2] = r[2];
+    f[3] = r[3];
+  }
+};
 
 template <int KD, int VD, typename TIN, int kTMax>
 __global__ __launch_bounds__(256) void gdn_replay_kernel(
@@ -154,6 +162,16 @@ __global__ __launch_bounds__(256) void gdn_replay_kernel(
     const bool valid = nl < n_end;
     const int64_t n = (int64_t)b * W + (valid ? nl : n_begin);
 
+    // every load of the group goes out first (v, then q and k, then the
+    // gates), so the group costs one memory round trip
+    Raw4<TIN> vraw[kTMax][MT];
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t)
+      if (t < T)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          vraw[t][mt].load(v + (n * T + t) * ld_v + (int64_t)hv * VD + v0 + mt * 16 + quad * 4);
+
     f32x4 acc_q[kTMax][MT], acc_k[kTMax][MT];
 #pragma unroll
     for (int t = 0; t < kTMax; ++t)
@@ -174,18 +192,47 @@ __global__ __launch_bounds__(256) void gdn_replay_kernel(
       }
     }
 
+    // q and k of every K step are loaded up front too where the registers
+    // allow it (one token); longer suffixes load them step by step, which
+    // keeps two waves per SIMD
+    constexpr bool kHoistQK = kTMax == 1;
+    constexpr int KSH = kHoistQK ? KSTEPS : 1;
+    QKFrag<TIN> fq_all[KSH][kTMax], fk_all[KSH][kTMax];
+    float xq_all[KSH][kTMax][8], xk_all[KSH][kTMax][8];
+    auto load_qk = [&](int ks, int slot) {
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      QKFrag<TIN> fq[kTMax], fk[kTMax];
-      float xq[kTMax][8], xk[kTMax][8];
-#pragma unroll
-      for (int t = 0; t < kTMax; ++t) {
+      for (int t = 0; t < kTMax; ++t)
         if (t < T) {
           const int64_t row = (n * T + t) * ld_qk + (int64_t)h * KD + ks * 32 + quad * 8;
-          fq[t].load(q + row, xq[t]);
-          fk[t].load(k + row, xk[t]);
+          fq_all[slot][t].load(q + row, xq_all[slot][t]);
+          fk_all[slot][t].load(k + row, xk_all[slot][t]);
         }
+    };
+    if constexpr (kHoistQK) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) load_qk(ks, ks);
+    }
+    float et[kTMax], bt[kTMax];
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+      if (t < T) {
+        const int64_t gi = (n * T + t) * ld_gate + hv;
+        et[t] = load_as_float(gdecay, gi, gate_dtype);
+        bt[t] = load_as_float(beta, gi, beta_dtype);
+      } else {
+        et[t] = 0.f;
+        bt[t] = 0.f;
       }
+    }
+
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int slot = kHoistQK ? ks : 0;
+      if constexpr (!kHoistQK) load_qk(ks, 0);
+      QKFrag<TIN>(&fq)[kTMax] = fq_all[slot];
+      QKFrag<TIN>(&fk)[kTMax] = fk_all[slot];
+      float(&xq)[kTMax][8] = xq_all[slot];
+      float(&xk)[kTMax][8] = xk_all[slot];
 #pragma unroll
       for (int t = 0; t < kTMax; ++t) {
         if (t < T) {
@@ -246,19 +293,12 @@ __global__ __launch_bounds__(256) void gdn_replay_kernel(
       }
     }
 
-    float rk[kTMax], rq[kTMax], et[kTMax], bt[kTMax];
+    float rk[kTMax], rq[kTMax];
 #pragma unroll
     for (int t = 0; t < kTMax; ++t) {
       rk[t] = 1.0f / sqrtf(kk[t] + 1e-6f);
       rq[t] = scale / sqrtf(qq[t] + 1e-6f);
-      if (t < T) {
-        const int64_t gi = (n * T + t) * ld_gate + hv;
-        et[t] = expf(load_as_float(gdecay, gi, gate_dtype));
-        bt[t] = load_as_float(beta, gi, beta_dtype);
-      } else {
-        et[t] = 1.f;
-        bt[t] = 0.f;
-      }
+      et[t] = t < T ? expf(et[t]) : 1.f;
     }
 
     float u[kTMax][MT][4];
@@ -275,7 +315,7 @@ __global__ __launch_bounds__(256) void gdn_replay_kernel(
         for (int mt = 0; mt < MT; ++mt) {
           const int vr = v0 + mt * 16 + quad * 4;
           float vt[4], ov[4];
-          load4<TIN>(v + vrow_base * ld_v + (int64_t)hv * VD + vr, vt);
+          vraw[t][mt].unpack(vt);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float recall = gam * (acc_k[t][mt][i] * rk[t]);
