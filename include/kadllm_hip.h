@@ -113,7 +113,8 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
  * of 32-deep K slices, loads three slices ahead; 14 = 9 with 8 waves, 2 per
  * SIMD, each a 128 x 64 sub-tile; 15 = 14 with 256x128 tiles, each wave a
  * 64 x 64 sub-tile; 16, 17 = 14, 15 on 16x16x32 MFMAs with the loads of the
- * tile after next issued mid-tile), for tuning. */
+ * tile after next issued mid-tile; 18, 19 = 16, 17 persistent, one workgroup
+ * per CU walking tiles), for tuning. */
 int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
                         int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                         int epilogue, int tile_config, kad_stream_t stream);

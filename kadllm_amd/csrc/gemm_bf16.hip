@@ -1072,6 +1072,235 @@ int launch_x16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, 
   return kad_launch_status("gemm_x16_kernel");
 }
 
+// Persistent form of the 16x16x32 kernel: one workgroup per CU walks the
+// tiles v = blockIdx.x, + gridDim.x, ... (the same grouped, XCD-aware order).
+// The K slices of successive tiles form one stream through the two LDS
+// stages, so the last two iterations of a tile already load the first two
+// slices of the next one; the epilogue then runs while those loads land
+// (through a small LDS region of its own), and no workgroup is dispatched
+// per tile.
+// Epilogue of the persistent kernel: as epilogue_x16, staged one 16-row
+// block at a time through a small wave-private LDS region (16 x (cols + 8) elements), so that every global
+// store is a 16-byte piece of a full 128-byte row segment.  A wave's LDS
+// accesses complete in order, so no barrier is needed.
+template <int EPI, int NI, int NJ>
+__device__ __forceinline__ void epilogue_x16_chunked(f32x4 (&acc)[NI][NJ], bf16_t* ep, int lane,
+                                                     int row0, int col0, bf16_t* C, int64_t ldc,
+                                                     const bf16_t* R, int64_t ldr, int M, int N) {
+  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? NJ * 8 : NJ * 16;
+  constexpr int kLd = kCols + 8;
+  constexpr int kChunks = kCols / 8, kRowsPer = 64 / kChunks;
+  const int e_row = lane & 15, e_col = (lane >> 4) * 4;
+  const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
+  const int n_out = EPI == KAD_EPI_SWIGLU ? N / 2 : N;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if constexpr (EPI == KAD_EPI_SWIGLU) {
+        if ((j & 3) >= 2) continue;
+        u32x2 packed;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t two = 0;
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const float gv = round_bf(acc[i][j][h * 2 + q]);
+            const float uv = round_bf(acc[i][j + 2][h * 2 + q]);
+            two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+          }
+          packed[h] = two;
+        }
+        *(u32x2*)(ep + e_row * kLd + (j >> 2) * 32 + (j & 3) * 16 + e_col) = packed;
+      } else {
+        u32x2 packed;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          packed[h] = (uint32_t)f2bf(acc[i][j][h * 2]) | ((uint32_t)f2bf(acc[i][j][h * 2 + 1]) << 16);
+        *(u32x2*)(ep + e_row * kLd + j * 16 + e_col) = packed;
+      }
+    }
+#pragma unroll
+    for (int r = c_row; r < 16; r += kRowsPer) {
+      const int row = row0 + i * 16 + r, col = col0 + c_col;
+      u32x4 v = *(const u32x4*)(ep + r * kLd + c_col);
+      if (row >= M || col >= n_out) continue;
+      if constexpr (EPI == KAD_EPI_RESIDUAL) {
+        const u32x4 rr = *(const u32x4*)(R + (int64_t)row * ldr + col);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const float lo = __uint_as_float(rr[h] << 16) + __uint_as_float(v[h] << 16);
+          const float hi =
+              __uint_as_float(rr[h] & 0xffff0000u) + __uint_as_float(v[h] & 0xffff0000u);
+          v[h] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+        }
+      }
+      *(u32x4*)(C + (int64_t)row * ldc + col) = v;
+    }
+  }
+}
+
+template <int EPI, int BN>
+__global__ __launch_bounds__(512, 1) void gemm_x16p_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group, int ntiles) {
+  using TX = TileX16<BN>;
+  constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
+  constexpr int kStage = TX::Stage, AG = TX::AG, WGW = TX::WGW;
+  constexpr int kLoads = AG + WGW;
+  constexpr int NM = NI * NJ, NR = NI + NJ;
+  constexpr int kEpiChunk = 16 * ((EPI == KAD_EPI_SWIGLU ? NJ * 8 : NJ * 16) + 8);
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[2 * kStage + NW * kEpiChunk];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int KT = K / kBK;
+  // this workgroup's tiles: v = blockIdx.x + r * gridDim.x, r < my_tiles
+  const int my_tiles = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int my_slices = my_tiles * KT;
+  auto origin = [&](int r, int& m0, int& n0) {
+    const int v = (int)blockIdx.x + r * (int)gridDim.x;
+    tile_origin_of(xcd_logical_id(v, ntiles), M, N, BN, n_major, group, m0, n0);
+  };
+
+  // DMA rows: groups g = wave + 8 i (8 rows each); lane L -> row g*8 + L/8,
+  // LDS chunk L%8 holding global chunk (L%8) ^ ((row>>1)&7)
+  const int d_row = lane >> 3;
+  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
+  // load cursor: tile ld_r, slice ld_k of it; it stops at the last slice of
+  // the last tile (the loads then re-fetch it, which keeps the wait counts
+  // uniform)
+  int ld_r = 0, ld_k = 0, ld_g = 0;
+  const bf16_t* ld_a = A;
+  const bf16_t* ld_b = Wt;
+  int ld_amax = 0, ld_bmax = 0;
+  auto set_tile = [&](int r) {
+    int m0, n0;
+    origin(r, m0, n0);
+    ld_a = A + (int64_t)m0 * lda + d_kc;
+    ld_b = Wt + (int64_t)n0 * ldw + d_kc;
+    ld_amax = M - 1 - m0;
+    ld_bmax = N - 1 - n0;
+  };
+  auto issue = [&](int slot) {
+    bf16_t* base = smem + (slot & 1) * kStage + wave * 8 * kBK;
+    const int k0 = ld_k * kBK;
+#pragma unroll
+    for (int i = 0; i < AG; ++i) {
+      const int rr = min((wave + NW * i) * 8 + d_row, ld_amax);
+      dma16(ld_a + (int64_t)rr * lda + k0, base + i * NW * 8 * kBK);
+    }
+#pragma unroll
+    for (int i = 0; i < WGW; ++i) {
+      const int rr = min((wave + NW * i) * 8 + d_row, ld_bmax);
+      dma16(ld_b + (int64_t)rr * ldw + k0, base + kT * kBK + i * NW * 8 * kBK);
+    }
+  };
+  auto advance = [&]() {
+    if (++ld_g < my_slices) {
+      if (++ld_k == KT) {
+        ld_k = 0;
+        set_tile(++ld_r);
+      }
+    }
+  };
+
+  const int f_row = lane & 15, f_sw = (lane & 15) >> 1, f_q = lane >> 4;
+  const int fa_row = (wm * NI * 16 + f_row) * kBK;
+  const int fw_row = kT * kBK + (wn * NJ * 16 + f_row) * kBK;
+  bf16x8 fa[2][NI], fw[2][NJ];
+  auto load_frags = [&](int stage, int step, int buf) {
+    const bf16_t* base = smem + stage * kStage + (((step * 4 + f_q) ^ f_sw) * 8);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      fw[buf][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 16 * kBK));
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      fa[buf][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 16 * kBK));
+  };
+  f32x4 acc[NI][NJ];
+  auto mfma_rows = [&](int buf, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x32(fw[buf][j], fa[buf][i], acc[i][j]);
+  };
+
+  if (my_tiles <= 0) return;
+  set_tile(0);
+  issue(0);
+  advance();
+  issue(1);
+  advance();
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoads));   // slice 0 landed
+  ring_barrier();
+  load_frags(0, 0, 0);
+  for (int r = 0; r < my_tiles; ++r) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{};
+    const int g0 = r * KT;
+    for (int kt = 0; kt < KT; ++kt) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int g = g0 + kt, stage = g & 1;
+      load_frags(stage, 1, 1);
+      mfma_rows(0, 0, NI);
+      interleave_x16<NM, NR, 0>();
+      mfma_rows(1, 0, NI / 2);
+      interleave_x16<NM / 2, 0, 0>();
+      // slice g + 1 landed; every wave is done reading this stage
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+      ring_barrier();
+      load_frags(stage ^ 1, 0, 0);
+      issue(g + 2);
+      mfma_rows(1, NI / 2, NI);
+      interleave_x16<NM / 2, NR, kLoads>();
+      advance();
+    }
+    int m0, n0;
+    origin(r, m0, n0);
+    const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 16) / 2 : n0 + wn * NJ * 16;
+    epilogue_x16_chunked<EPI, NI, NJ>(acc, smem + 2 * kStage + wave * kEpiChunk, lane,
+                                      m0 + wm * NI * 16, col0, C, ldc, R, ldr, M, N);
+  }
+  // no LDS write may land after the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int EPI, int BN>
+int launch_x16p(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t ntiles = kad_cdiv(M, kT) * kad_cdiv(N, BN);
+  if (ntiles > 0x7fffffff / 2 || ntiles * (K / kBK) > 0x7fffffff)
+    KAD_UNSUPPORTED("gemm grid too large");
+  // whole XCD rounds of workgroups, so that a workgroup's tiles keep one XCD
+  int grid = device_cu_count();
+  grid -= grid % 8;
+  if (grid <= 0) grid = 8;
+  if (ntiles < grid) grid = (int)ntiles;
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  hipLaunchKernelGGL((gemm_x16p_kernel<EPI, BN>), dim3((unsigned)grid), dim3(512), 0, s,
+                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N, K, n_major, 8, (int)ntiles);
+  return kad_launch_status("gemm_x16p_kernel");
+}
+
 // 16-byte epilogue stores need aligned, 8-column-granular outputs
 bool vector_epilogue_ok(const void* C, int64_t ldc, const void* R, int64_t ldr, int N, int epi) {
   const int n_out = epi == KAD_EPI_SWIGLU ? N / 2 : N;
@@ -1101,15 +1330,17 @@ enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x2
        CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10,
        CFG_128x32 = 11, CFG_256x256_RDFIRST = 12, CFG_256x256_RING = 13, CFG_256x256_W8 = 14,
        CFG_256x128_W8 = 15,
-       CFG_256x256_X16 = 16, CFG_256x128_X16 = 17 };
+       CFG_256x256_X16 = 16, CFG_256x128_X16 = 17, CFG_256x256_X16P = 18,
+       CFG_256x128_X16P = 19 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
     // the 8-wave 256x256 kernel on 16x16x32 MFMAs when its tiles still fill
-    // every CU (and the output suits 16-byte stores); then its 256x128
-    // variant; 128x32 for outputs of at most 32 columns (the GDN gate
+    // every CU (and the output suits 16-byte stores), persistent except for
+    // the SwiGLU epilogue, where both forms measured the same; then the
+    // 256x128 variant; 128x32 for outputs of at most 32 columns (the GDN gate
     // projection); 128x128 otherwise (all measured on the decode/prefill
     // shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
@@ -1122,7 +1353,7 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
     else if (tiles256 >= 256)
-      cfg = CFG_256x256_X16;
+      cfg = EPI == KAD_EPI_SWIGLU ? CFG_256x256_X16 : CFG_256x256_X16P;
     else if (vec && tiles128 >= 256)
       cfg = CFG_256x128_X16;
     else
@@ -1169,6 +1400,14 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       if (cfg == CFG_256x256_X16)
         return launch_x16<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       return launch_x16<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_256x256_X16P:
+    case CFG_256x128_X16P:
+      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
+        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
+                        cfg);
+      if (cfg == CFG_256x256_X16P)
+        return launch_x16p<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return launch_x16p<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_RDFIRST:
     case CFG_256x256_RING:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))

@@ -101,7 +101,7 @@ def test_gemm_tile_configurations_agree(device, epi):
     x = torch.randn(M, n_out, generator=g).bfloat16()
     ad, wd = a.to(device), w.to(device)
     outs = {}
-    cfgs = [c for c in range(1, 18) if not (c == 11 and epi == layers.EPI_SWIGLU)]
+    cfgs = [c for c in range(1, 20) if not (c == 11 and epi == layers.EPI_SWIGLU)]
     for cfg in cfgs:
         c = torch.zeros(M, n_out + 16, dtype=torch.bfloat16, device=device)  # ldc > width
         cv = c[:, :n_out]
@@ -142,15 +142,44 @@ def test_gemm_short_k_pipelines_agree(device, K):
     a = torch.randn(M, K, generator=g).bfloat16().to(device)
     w = (torch.randn(N, K, generator=g) * 0.05).bfloat16().to(device)
     outs = {}
-    for cfg in (1, 7, 9, 12, 13, 14, 15, 16, 17):
+    for cfg in (1, 7, 9, 12, 13, 14, 15, 16, 17, 18, 19):
         c = torch.zeros(M, N, dtype=torch.bfloat16, device=device)
         _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), N, None, 0,
                   M, N, K, layers.EPI_STORE, cfg, _lib.stream_of(a))
         outs[cfg] = c.cpu()
-    for cfg in (7, 9, 12, 13, 14):
+    for cfg in outs:
         assert torch.equal(outs[cfg], outs[1]), f"config {cfg} differs from config 1 at K={K}"
     ref = (a.float() @ w.float().T).cpu()
     assert ((outs[1].float() - ref).abs() <= 1e-2 * ref.abs() + 1e-2).all()
+
+
+@pytest.mark.parametrize("K", [64, 192])
+@pytest.mark.parametrize("epi", [layers.EPI_STORE, layers.EPI_RESIDUAL, layers.EPI_SWIGLU])
+def test_gemm_persistent_tiles_agree(device, K, epi):
+    """The persistent kernels (configs 18, 19) against their one-tile-per-
+    workgroup forms (16, 17) with more tiles than CUs, ragged last tiles in
+    both dimensions, and tiles of one or three K slices, so that the load
+    stream crosses tile boundaries at both stage parities."""
+    from kadllm_amd import _lib
+    M, N = 256 * 17 + 40, 256 * 16 + 64
+    g = torch.Generator().manual_seed(90 + K + epi)
+    a = torch.randn(M, K, generator=g).bfloat16().to(device)
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16().to(device)
+    n_out = N // 2 if epi == layers.EPI_SWIGLU else N
+    x = torch.randn(M, n_out, generator=g).bfloat16().to(device)
+    outs = {}
+    for cfg in (16, 17, 18, 19):
+        c = x.clone() if epi == layers.EPI_RESIDUAL else torch.zeros(M, n_out, dtype=torch.bfloat16,
+                                                                     device=device)
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), n_out,
+                  _lib.ptr(c) if epi == layers.EPI_RESIDUAL else None,
+                  n_out if epi == layers.EPI_RESIDUAL else 0, M, N, K, epi, cfg,
+                  _lib.stream_of(a))
+        torch.cuda.synchronize()
+        outs[cfg] = c.cpu()
+    assert torch.equal(outs[18], outs[16]), f"persistent 256x256 differs at K={K}"
+    assert torch.equal(outs[19], outs[17]), f"persistent 256x128 differs at K={K}"
+    assert torch.equal(outs[16], outs[17])
 
 
 def test_gemm_pipelined_tile_rejects_unaligned_output(device):
