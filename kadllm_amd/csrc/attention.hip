@@ -384,10 +384,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
   const int G = a.H / a.HK;
   const int64_t rows_total = CAUSAL ? (int64_t)a.L * G : (int64_t)a.W * G * a.T;
 
+  // head dim 256: block 0 of a wave holds the 32 query rows whose softmax it
+  // forms, block 1 its partner's (so the odd wave of a pair swaps them)
+  const int swap = DS == 2 ? (wave & 1) : 0;
   // this lane's query row of block qb: token n (batch row), suffix position
   // or prompt position t, head h (recomputed where needed to save registers)
   auto row_of_q = [&](int qb, int64_t& n, int& t, int& h) {
-    int64_t r = (int64_t)qb_blk * ROWS + qgrp * 64 + qb * 32 + col;
+    int64_t r = (int64_t)qb_blk * ROWS + qgrp * 64 + (qb ^ swap) * 32 + col;
     if (r >= rows_total) r = 0;
     int g;
     if (CAUSAL) {
@@ -415,20 +418,25 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
     for (int s = 0; s < KSW; ++s)
       qf[qb][s] = as_bf16x8(*(const u32x4*)(qrow + (dbase * 2 + s) * 16 + hi * 8));
   }
-  // partial scores of the two waves of a query group: written as 32 floats
-  // per lane (8 x 16 bytes, lane-contiguous), read back and added by both
+  // partial suffix scores of the two waves of a query group: v holds n/2
+  // values of block 0 then n/2 of block 1; the partner's block 1 is this
+  // wave's block 0 and the other way round, so the halves are swapped
   float* xbuf = (float*)(smem + AT::xoff);
-  auto exchange = [&](float* v, int n) {  // n <= 32, a multiple of 4
+  auto exchange = [&](float* v, int n) {  // n <= 32, a multiple of 8
     if constexpr (DS == 2) {
       float* mine = xbuf + wave * 64 * 32;
       const float* other = xbuf + (wave ^ 1) * 64 * 32;
 #pragma unroll
       for (int c = 0; c < n / 4; ++c)
         *(f32x4*)(mine + (c * 64 + lane) * 4) = f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
-      __syncthreads();
+      // LDS writes done, then the barrier; the K/V prefetch loads in flight
+      // are not waited for (__syncthreads would wait for them too)
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only
+      tile_barrier();
 #pragma unroll
       for (int c = 0; c < n / 4; ++c) {
-        const f32x4 o = *(const f32x4*)(other + (c * 64 + lane) * 4);
+        const int cp = (c + n / 8) % (n / 4);
+        const f32x4 o = *(const f32x4*)(other + (cp * 64 + lane) * 4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[4 * c + e] += o[e];
       }
@@ -593,18 +601,24 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
+      // head dim 256: each wave completes and exponentiates only its own
+      // block 0 (the partner does block 1), so no score is exponentiated twice
+      constexpr int NQ = DS == 2 ? 1 : 2;
       if constexpr (DS == 2) {
-        float v[32];
+        // send the partial scores of block 1, add the partner's to block 0
+        float* mine = xbuf + wave * 64 * 32;
+        const float* other = xbuf + (wave ^ 1) * 64 * 32;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          v[j] = st[0][j];
-          v[16 + j] = st[1][j];
-        }
-        exchange(v, 32);
+        for (int c = 0; c < 4; ++c)
+          *(f32x4*)(mine + (c * 64 + lane) * 4) =
+              f32x4{st[1][4 * c], st[1][4 * c + 1], st[1][4 * c + 2], st[1][4 * c + 3]};
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only
+        tile_barrier();
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          st[0][j] = v[j];
-          st[1][j] = v[16 + j];
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 o = *(const f32x4*)(other + (c * 64 + lane) * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) st[0][4 * c + e] += o[e];
         }
       }
 
@@ -613,12 +627,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
       // tiles wholly visible to every row of the wave skip the masking
       int lim[2];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      for (int qb = 0; qb < NQ; ++qb)
         lim[qb] = (CAUSAL ? min(kend - 1, pos[qb]) : kend - 1) - k0 - hi * 4;
-      const bool masked = __ballot(min(lim[0], lim[1]) < 27) != 0 || (!CAUSAL && a.mask);
+      const bool masked =
+          __ballot((NQ == 1 ? lim[0] : min(lim[0], lim[1])) < 27) != 0 || (!CAUSAL && a.mask);
       if (masked) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int kj = (j / 4) * 8 + (j % 4);
@@ -630,7 +645,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
       }
       bf16x8 pf[2][2];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < NQ; ++qb) {
         // raw scores: the max is taken before scaling (scale > 0)
         float tmax = -INFINITY;
 #pragma unroll
@@ -650,6 +665,19 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
         }
         psum += __shfl_xor(psum, 32, 64);
         l[qb] += psum;
+      }
+      if constexpr (DS == 2) {
+        // hand P of block 0 to the partner, take the partner's as block 1
+        float* mine = xbuf + wave * 64 * 32 + 4 * 64 * 4;
+        const float* other = xbuf + (wave ^ 1) * 64 * 32 + 4 * 64 * 4;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          *(u32x4*)(mine + (c * 64 + lane) * 4) = __builtin_bit_cast(u32x4, pf[0][c]);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only
+        tile_barrier();
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          pf[1][c] = as_bf16x8(*(const u32x4*)(other + (c * 64 + lane) * 4));
       }
       // O^T[d, query] += V^T[d, keys] P^T[keys, query]; k-step ks covers keys
       // 16ks + {0-3, 8-11} (+4 for the upper half-wave), the order S^T leaves.
@@ -687,10 +715,19 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
       // and this way only tile + 1's (issued an iteration ago) is pending.
       if (tile + 2 < ntiles) issue(tile + 2, (tile + 2) % kStages2);
     }
-    // every wave has finished with the LDS stages; decide together
+    // every wave has finished with the LDS stages; decide together.  Head
+    // dim 256: block 1's row statistics are the partner's block 0 ones
+    if constexpr (DS == 2)
+      *(f32x4*)(xbuf + wave * 64 * 32 + lane * 4) = f32x4{m_ref[0], m_true[0], l[0], 0.f};
     __builtin_amdgcn_s_waitcnt(0);
     if (tid == 0) redo = 0;
     __syncthreads();
+    if constexpr (DS == 2) {
+      const f32x4 o = *(const f32x4*)(xbuf + (wave ^ 1) * 64 * 32 + lane * 4);
+      m_ref[1] = o[0];
+      m_true[1] = o[1];
+      l[1] = o[2];
+    }
     if (__ballot(overflow) != 0 && lane == 0) atomicOr(&redo, 1);
     __syncthreads();
     if (pass == 1 || redo == 0) break;
@@ -725,7 +762,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
           }
       }
     }
-    const int64_t r = (int64_t)qb_blk * ROWS + qgrp * 64 + qb * 32 + col;
+    const int64_t r = (int64_t)qb_blk * ROWS + qgrp * 64 + (qb ^ swap) * 32 + col;
     if (r >= rows_total) continue;
     const float inv = l[qb] > 0.f ? 1.0f / l[qb] : 0.f;
     bf16_t* orow = a.out + n * a.so_n + (int64_t)t * a.so_t + (int64_t)h * a.so_h;
