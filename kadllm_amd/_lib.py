@@ -89,8 +89,9 @@ def load():
 
 
 def stream_of(t):
-    """Raw hipStream_t of torch's current stream on ``t``'s device."""
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """Raw hipStream_t of torch's current stream on ``t``'s device (an int,
+    which ctypes passes for the c_void_p argument)."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def call(name, *args):
@@ -117,9 +118,11 @@ def dtype_code(dtype):
 
 
 def ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    """Device address of a tensor (None for a null pointer); ctypes converts
+    the int for the c_void_p argument."""
+    return t.data_ptr() if t is not None else None
 
 
 def ptr_at(address):
     """A raw device address (e.g. a column offset inside a row-strided buffer)."""
-    return ctypes.c_void_p(address)
+    return address
