@@ -78,7 +78,7 @@ class GemmTimer:
 # WRITE_SIZE over the GEMM dispatches of one search, each scaled by its reading
 # for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the launch
 # count.  Re-measured with the command in profiles/gemm_hbm_traffic_b32_p1024_w256.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 387.1e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 386.2e6
 
 
 def cpu_baseline(cfg, sd_cpu, prefix, beam, depth, threads):
