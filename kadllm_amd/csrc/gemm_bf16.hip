@@ -31,6 +31,13 @@ constexpr int kBK = 64;
 constexpr int kPad = 8;
 constexpr int kLdk = kBK + kPad;  // LDS row stride (elements)
 
+// SiLU of the SwiGLU epilogues: x / (1 + e^-x) with the hardware reciprocal
+// (1 ulp) in place of the IEEE divide, which is most of the epilogue's VALU
+// work; every tile configuration uses it, so they still agree bit for bit
+__device__ __forceinline__ float silu_rcp(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
@@ -137,7 +144,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
           if (row < M) {
             const float gv = round_bf(acc[i][j][e]);
             const float uv = round_bf(acc[i][j + 1][e]);
-            const float s = round_bf(silu_f(gv));
+            const float s = round_bf(silu_rcp(gv));
             C[(int64_t)row * ldc + ocol] = f2bf(s * uv);
           }
         }
@@ -255,7 +262,7 @@ __device__ __forceinline__ void epilogue_tile(f32x16 (&acc)[4][Tile256<BN>::NJ],
               const int e = g * 4 + h * 2 + q;
               const float gv = round_bf(acc[i][j][e]);
               const float uv = round_bf(acc[i][j + 1][e]);
-              two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+              two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
             }
             packed[h] = two;
           }
@@ -534,7 +541,7 @@ __device__ __forceinline__ void epilogue_sub(f32x16 (&acc)[NI][NJ], bf16_t* ep, 
               const int e = g * 4 + h * 2 + q;
               const float gv = round_bf(acc[i][j][e]);
               const float uv = round_bf(acc[i][j + 1][e]);
-              two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+              two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
             }
             packed[h] = two;
           }
@@ -893,7 +900,7 @@ __device__ __forceinline__ void epilogue_x16(f32x4 (&acc)[NI][NJ], bf16_t* ep, i
           for (int q = 0; q < 2; ++q) {
             const float gv = round_bf(acc[i][j][h * 2 + q]);
             const float uv = round_bf(acc[i][j + 2][h * 2 + q]);
-            two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+            two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
           }
           packed[h] = two;
         }
@@ -1107,7 +1114,7 @@ __device__ __forceinline__ void epilogue_x16_chunked(f32x4 (&acc)[NI][NJ], bf16_
           for (int q = 0; q < 2; ++q) {
             const float gv = round_bf(acc[i][j][h * 2 + q]);
             const float uv = round_bf(acc[i][j + 2][h * 2 + q]);
-            two |= (uint32_t)f2bf(round_bf(silu_f(gv)) * uv) << (16 * q);
+            two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
           }
           packed[h] = two;
         }
