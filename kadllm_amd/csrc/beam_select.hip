@@ -542,6 +542,40 @@ __device__ __forceinline__ bool before(float ka, int ia, float kb, int ib) {
 // are in flight instead of one.
 constexpr int kMergeBatch = 8;
 
+// Run by one full wave: the bin d at which the running count of hist,
+// taken from bin 255 down (DESC) or from bin 0 up, first reaches need, and
+// the count before it -- as the serial scan that stops at the last bin
+// without testing it.  Lane l holds the 4 bins 4l.. in scan order; returns
+// true in the one lane that found d.
+template <bool DESC>
+__device__ __forceinline__ bool pick_bin(const int* hist, int need, int lane, int& d_out,
+                                         int& acc_out) {
+  int b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = hist[DESC ? 255 - 4 * lane - i : 4 * lane + i];
+  const int s = b[0] + b[1] + b[2] + b[3];
+  int incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  const unsigned long long hit = __ballot(incl >= need);
+  const int L = hit ? __ffsll((long long)hit) - 1 : 63;
+  if (lane == L) {
+    int acc = incl - s, d = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d = DESC ? 255 - 4 * L - i : 4 * L + i;
+      if (d == (DESC ? 0 : 255) || acc + b[i] >= need) break;
+      acc += b[i];
+    }
+    d_out = d;
+    acc_out = acc;
+  }
+  return lane == L;  // the lane that holds the result
+}
+
 __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
     const float* __restrict__ cand_key, const int* __restrict__ cand_idx, int ncand, int W,
     int V, float* __restrict__ scores, int64_t* __restrict__ parents,
@@ -578,15 +612,13 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
       if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
     });
     __syncthreads();
-    if (tid == 0) {
-      int acc = 0, d = 255;
-      for (; d > 0; --d) {
-        if (acc + hist[d] >= need) break;
-        acc += hist[d];
+    if (tid < 64) {
+      int d = 0, acc = 0;
+      if (pick_bin<true>(hist, need, tid, d, acc)) {
+        sh_prefix = prefix | ((uint32_t)d << shift);
+        sh_need = need - acc;
+        sh_ties = hist[d];  // after the last round: the candidates equal to the key
       }
-      sh_prefix = prefix | ((uint32_t)d << shift);
-      sh_need = need - acc;
-      sh_ties = hist[d];  // after the last round: the candidates equal to the key
     }
     __syncthreads();
     prefix = sh_prefix;
@@ -610,14 +642,12 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
       if ((u & imask) == iprefix) atomicAdd(&hist[(u >> shift) & 255], 1);
     });
     __syncthreads();
-    if (tid == 0) {
-      int acc = 0, d = 0;
-      for (; d < 255; ++d) {
-        if (acc + hist[d] >= ineed) break;
-        acc += hist[d];
+    if (tid < 64) {
+      int d = 0, acc = 0;
+      if (pick_bin<false>(hist, ineed, tid, d, acc)) {
+        sh_prefix = iprefix | ((uint32_t)d << shift);
+        sh_need = ineed - acc;
       }
-      sh_prefix = iprefix | ((uint32_t)d << shift);
-      sh_need = ineed - acc;
     }
     __syncthreads();
     iprefix = sh_prefix;
