@@ -158,7 +158,7 @@ def main():
     torch.cuda.synchronize()
 
     timer = GemmTimer()
-    timer.reserve(400 * a.steps * a.depth)
+    timer.reserve(128 * a.steps * a.depth)   # GEMM launches: about 115 per level
     layers.set_launch_timer(timer)
     times, outputs = [], []
     torch.cuda.synchronize()

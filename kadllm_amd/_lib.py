@@ -88,10 +88,15 @@ def load():
     return lib
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t):
     """Raw hipStream_t of torch's current stream on ``t``'s device (an int,
     which ctypes passes for the c_void_p argument)."""
-    return torch._C._cuda_getCurrentRawStream(t.get_device())
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def call(name, *args):
