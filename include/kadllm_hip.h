@@ -55,7 +55,7 @@ int kad_abi_version(void);
  * Layout (element strides): q/k (n,t,h,i) at [(n*T+t)*ld_qk + h*K + i];
  * v/out (n,t,hv,j) at [(n*T+t)*ld_v + hv*V + j] (ld_out for out);
  * log_decay/beta (n,t,hv) at [(n*T+t)*ld_gate + hv];
- * state contiguous [B, HV, K, V].  Supported: K, V in {64, 128}; T <= 4.
+ * state contiguous [B, HV, K, V].  Supported: K, V in {64, 128}; T <= 8.
  */
 int kad_gdn_suffix_replay(const void* q, const void* k, const void* v, int64_t ld_qk,
                           int64_t ld_v, int qkv_dtype, const void* log_decay,
@@ -72,9 +72,9 @@ int kad_gdn_suffix_replay(const void* q, const void* k, const void* v, int64_t l
  * y[n,c,t] = act( sum_{i<width} w[c,i] * window[n,c,t+i] ),
  * window = [state[n/W, c, history-(width-1) .. history-1] || x[n, c, 0..T-1]].
  * x, state, out are strided [n, c, t] views (strides in elements); weight is
- * contiguous [C, width].  All tensors share `dtype`.  act = SiLU if
- * activation_silu else identity; bias (nullable, [C]) is added before act.
- * Supported: width <= 4 (width-1 <= history).
+ * contiguous [C, width].  All tensors share `dtype` (bf16, fp16, fp32).
+ * act = SiLU if activation_silu else identity; bias (nullable, [C]) is added
+ * before act.  Supported: width <= 64 (width-1 <= history).
  */
 int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
                            const void* state, int64_t ss_b, int64_t ss_c, int64_t ss_t,
@@ -169,7 +169,7 @@ int kad_embedding(const int64_t* ids, const void* table, void* out, int64_t rows
  * keys with prefix_mask[b, key] == 0 excluded when the mask is given) and to
  * suffix keys j <= t of its own beam (suffix_k/v [B*W, T, HK, D]).  One
  * softmax over both (equal to the reference's LSE merge); out = bf16(o),
- * times bf16(sigmoid(gate)) when gated.  Strides in elements.  T <= 4;
+ * times bf16(sigmoid(gate)) when gated.  Strides in elements.  T <= 8;
  * D in {64, 128, 256}; prefix_mask is uint8/bool [B, L].
  */
 int kad_prefix_attention_decode(
@@ -185,7 +185,7 @@ int kad_prefix_attention_decode(
  * of kad_prefix_attention_decode with T = Tk, which lets a level that extends
  * cached suffixes by one token (src/kadllm/grbeam.py:76-77, where the
  * reference replays the whole suffix, src/kadllm/adapters/qwen3_5.py:216) skip
- * the queries of the cached tokens.  Tq <= Tk <= 4. */
+ * the queries of the cached tokens.  Tq <= Tk <= 8. */
 int kad_prefix_attention_decode_ex(
     const void* q, int64_t sq_n, int64_t sq_t, int64_t sq_h, const void* prefix_k,
     const void* prefix_v, int64_t sp_b, int64_t sp_l, int64_t sp_h, const void* suffix_k,
@@ -211,21 +211,22 @@ int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, int64_t sq_
  * (parent * V + token); torch.topk leaves that order unspecified.
  *
  * kad_beam_row_select    per beam row r (rows = B * Wp, row stride ld of the
- *                        bf16 logits; mask uint8 [rows, V] (ld_mask) or null):
- *                        writes the row's K = min(W, V) best candidates,
+ *                        logits, dtype logits_dtype: bf16, fp16 or fp32; mask
+ *                        uint8 [rows, V] (ld_mask) or null): writes the row's
+ *                        K = min(W, V) best candidates,
  *                        key = ((x - max_r) - log sum exp(x - max_r)) + parent[r]
  *                        (-inf where masked) and flat index (r % Wp) * V + c,
  *                        to cand_key / cand_idx [rows, K].
  * kad_beam_merge_select  per request b: the W best of its ncand = Wp * K
  *                        candidates, sorted by (key desc, index asc): scores
  *                        [B, W] fp32, parents = index / V, tokens = index % V
- *                        (int64), valid = isfinite(score) (uint8).  W <= 1024.
+ *                        (int64), valid = isfinite(score) (uint8).  W <= 16384.
  * kad_beam_history       out[b, w, :] = [history[b, parents[b, w], :step], tokens[b, w]]
  *                        (history [B, Wp, step] int64, out [B, W, step + 1]).
  */
-int kad_beam_row_select(const void* logits, int64_t ld, const void* mask, int64_t ld_mask,
-                        const float* parent_scores, int rows, int Wp, int V, int K,
-                        float* cand_key, int* cand_idx, kad_stream_t stream);
+int kad_beam_row_select(const void* logits, int logits_dtype, int64_t ld, const void* mask,
+                        int64_t ld_mask, const float* parent_scores, int rows, int Wp, int V,
+                        int K, float* cand_key, int* cand_idx, kad_stream_t stream);
 int kad_beam_merge_select(const float* cand_key, const int* cand_idx, int B, int ncand, int W,
                           int V, float* scores, int64_t* parents, int64_t* tokens, void* valid,
                           kad_stream_t stream);
@@ -275,6 +276,41 @@ int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, in
 int kad_causal_conv_prefill(const void* x, int64_t ldx, const void* weight, void* out,
                             int64_t ldo, void* state, int B, int L, int C, int activation_silu,
                             kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * General-shape kernels: any head dimension <= 256, any suffix length, bf16,
+ * fp16 or fp32 tensors, fp32 arithmetic.  They serve the shapes the kernels
+ * above do not: the reference operators take any shape and dtype
+ * (src/kadllm/ops.py:70-163,252-341), and its toy model runs 8-wide heads in
+ * fp32 over whole prompts (src/kadllm/adapters/reference.py:56-91).
+ *
+ * kad_gdn_recurrent      the token-by-token gated delta rule of ops.py:139-163
+ *                        (src/kadllm/ops.py:70-163, gated_delta): layouts as
+ *                        kad_gdn_suffix_replay with n in [0, N); q, k
+ *                        L2-normalised in fp32 (q / sqrt(sum q^2 + 1e-6) *
+ *                        scale); initial_state [N / beams_per_state, HV, K, V]
+ *                        (nullable: zeros); final_state fp32 [N, HV, K, V]
+ *                        (nullable); out in the q/k/v dtype.  K <= 256.
+ * kad_attention_general  kad_prefix_attention_decode_ex's contract (queries
+ *                        are the last Tq of Tk suffix tokens; Tk = Tq is the
+ *                        reference operator, src/kadllm/ops.py:252-341) for
+ *                        any Tq <= Tk, L >= 0 and D <= 256, all tensors of
+ *                        `dtype`; fully masked rows give zeros.
+ */
+int kad_gdn_recurrent(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
+                      int qkv_dtype, const void* log_decay, int gate_dtype, const void* beta,
+                      int beta_dtype, int64_t ld_gate, const void* initial_state,
+                      int state_dtype, int beams_per_state, void* out, int64_t ld_out,
+                      float* final_state, int N, int T, int H, int HV, int K, int V, float scale,
+                      kad_stream_t stream);
+int kad_attention_general(
+    const void* q, int64_t sq_n, int64_t sq_t, int64_t sq_h, const void* prefix_k,
+    const void* prefix_v, int64_t sp_b, int64_t sp_l, int64_t sp_h, const void* suffix_k,
+    int64_t ssk_n, int64_t ssk_t, int64_t ssk_h, const void* suffix_v, int64_t ssv_n,
+    int64_t ssv_t, int64_t ssv_h, const void* prefix_mask, const void* gate, int64_t sg_n,
+    int64_t sg_t, int64_t sg_h, void* out, int64_t so_n, int64_t so_t, int64_t so_h, int B,
+    int W, int Tq, int Tk, int H, int HK, int L, int D, int dtype, float scale,
+    kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
  * MFMA lane-layout self-test (no reference counterpart): C[16x16] = A[16x32]

@@ -41,7 +41,9 @@ SIGNATURES = {
     "kad_prefix_attention_decode_ex": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiiii" "f"
                                       "s",
     "kad_attention_prefill": "plll" "pplll" "plll" "plll" "iiiii" "f" "s",
-    "kad_beam_row_select": "plplpiiiipps",
+    "kad_beam_row_select": "pilplpiiiipps",
+    "kad_gdn_recurrent": "ppplli" "pipil" "pii" "plp" "iiiiiif" "s",
+    "kad_attention_general": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiiiii" "f" "s",
     "kad_beam_merge_select": "ppiiiipppps",
     "kad_beam_history": "piipppiis",
     "kad_gather_beam_rows": "pli" "pli" "i" "l" "p" "iii" "s",

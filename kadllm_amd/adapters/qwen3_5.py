@@ -119,8 +119,6 @@ class Qwen35GRBeamAdapter:
             raise ValueError("prefix belongs to a different adapter")
         if history.ndim != 3 or min(history.shape) < 1 or history.shape[0] != state.batch:
             raise ValueError("history must be nonempty [B,W,T] matching the prefix")
-        if history.shape[2] > 4:
-            raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
         return self._runner.decode(history, state.layers, state.length)
 
     @classmethod
@@ -172,8 +170,6 @@ class Qwen35GRBeamAdapter:
         T = history.shape[2]
         if (cache is None and T != 1) or (cache is not None and T != cache.T + 1):
             raise ValueError("history must extend the cached suffixes by exactly one token")
-        if history.shape[2] > 4:
-            raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
         if cache is not None and (parents.shape != history.shape[:2] or parents.device != history.device):
             raise ValueError("parents must be [B, W] on the history's device")
         tokens = history[:, :, -1].contiguous()

@@ -4,6 +4,9 @@ import torch
 
 from . import _lib
 
+# longest per-beam suffix the MFMA decode kernel folds in (kad_prefix_attention_decode_ex)
+MFMA_MAX_SUFFIX = 8
+
 
 def _inner_contiguous(t):
     """Return t if its last dim is contiguous and its other strides are multiples of 8."""
@@ -19,12 +22,16 @@ def prefix_attention_decode(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_widt
     tokens; Tk = T is the reference operator); optional bool prefix_mask [B,L];
     optional gate [B*W,T,H*D] (output multiplied by sigmoid(gate)), or any
     tensor whose data pointer is head 0's gate with element strides
-    ``gate_strides`` = (beam, token, head).  Returns [B*W,T,H,D] bf16."""
-    if q.dtype != torch.bfloat16:
-        raise RuntimeError("HIP prefix attention supports bf16 inputs")
+    ``gate_strides`` = (beam, token, head).  Returns [B*W,T,H,D] in q's dtype.
+    bf16 with head dims 64/128/256 and suffixes of at most 8 tokens run the
+    MFMA kernel (kad_prefix_attention_decode_ex); every other shape and dtype
+    the general kernel (kad_attention_general)."""
     BW, T, H, D = q.shape
     Tk = suffix_k.shape[1]
     B, L, HK, _ = prefix_k.shape
+    if q.dtype != torch.bfloat16 or D not in (64, 128, 256) or Tk > MFMA_MAX_SUFFIX:
+        return prefix_attention_general(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_width,
+                                        prefix_mask, scale, gate, out, gate_strides)
     q = _inner_contiguous(q)
     suffix_k = _inner_contiguous(suffix_k)
     if L:
@@ -56,6 +63,43 @@ def prefix_attention_decode(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_widt
               *suffix_v.stride()[:3], _lib.ptr(mask), _lib.ptr(gate), *g_strides,
               _lib.ptr(out), *out.stride()[:3], B, beam_width, T, Tk, H, HK, L, D, float(scale),
               _lib.stream_of(q))
+    return out
+
+
+def prefix_attention_general(q, prefix_k, prefix_v, suffix_k, suffix_v, beam_width, prefix_mask,
+                             scale, gate=None, out=None, gate_strides=None):
+    """The contract of prefix_attention_decode for every shape and dtype the
+    specialised kernel does not take (kad_attention_general): any head dim up
+    to 256, any suffix length, bf16/fp16/fp32.  Strides are passed through;
+    prefix K and V must share theirs (copied otherwise)."""
+    BW, T, H, D = q.shape
+    Tk = suffix_k.shape[1]
+    B, L, HK, _ = prefix_k.shape
+    if L and prefix_k.stride() != prefix_v.stride():
+        prefix_k, prefix_v = prefix_k.contiguous(), prefix_v.contiguous()
+    mask = prefix_mask.contiguous().view(torch.uint8) if prefix_mask is not None else None
+    if gate is not None and gate_strides is not None:
+        g_strides = tuple(gate_strides)
+    elif gate is not None:
+        if gate.shape != (BW, T, H * D) or gate.dtype != q.dtype:
+            raise ValueError("gate must be [B*W, T, H*D] in the query dtype")
+        if gate.stride(-1) != 1:
+            gate = gate.contiguous()
+        g_strides = (gate.stride(0), gate.stride(1), D)
+    else:
+        g_strides = (0, 0, 0)
+    if out is None:
+        out = torch.empty(BW, T, H, D, dtype=q.dtype, device=q.device)
+    for t in (q, suffix_k, suffix_v, out) + ((prefix_k,) if L else ()):
+        if t.stride(-1) != 1:
+            raise ValueError("attention tensors need a contiguous last dimension")
+    pk_strides = prefix_k.stride()[:3] if L else (0, 0, 0)
+    _lib.call("kad_attention_general", _lib.ptr(q), *q.stride()[:3],
+              _lib.ptr(prefix_k if L else None), _lib.ptr(prefix_v if L else None), *pk_strides,
+              _lib.ptr(suffix_k), *suffix_k.stride()[:3], _lib.ptr(suffix_v),
+              *suffix_v.stride()[:3], _lib.ptr(mask), _lib.ptr(gate), *g_strides,
+              _lib.ptr(out), *out.stride()[:3], B, beam_width, T, Tk, H, HK, L, D,
+              _lib.dtype_code(q.dtype), float(scale), _lib.stream_of(q))
     return out
 
 

@@ -6,24 +6,21 @@
 // Prefill replaces the causal SDPA attention of the transformers forward the
 // reference prefill runs (qwen3_5.py:111).
 //
-// Work unit: one (request b, KV head kh) and a block of 128 query rows, one
-// 32-row slice per wave (4 waves, each with the full register file: the 32
-// query rows and the 32 x D output accumulator stay in registers).  Decode rows are ordered (beam, q-head in
-// the group, suffix token); every row of a request/KV-head shares one prefix
-// K/V, so a K tile and a transposed V tile of 64 keys are staged in LDS once
-// per workgroup and consumed by all 128 rows (double-buffered, next tile
-// fetched into registers while the current one is used).
+// Work unit: one (request b, KV head kh) and a block of query rows (256, or
+// 128 for head dim 256), 4 waves of 64 rows.  Decode rows are ordered (beam,
+// q-head in the group, suffix token); every row of a request/KV-head shares
+// one prefix K/V, so each 32-key K and V tile is staged in LDS once per
+// workgroup and consumed by all its rows.
 //
 // Scores are formed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_bf16, A = K
-// tile, B = the wave's 32 query rows held in registers for the whole kernel),
-// so each lane owns one query column: the running max needs one cross-lane
-// exchange per tile.  P is rounded to bf16 and O^T += V^T P^T accumulates in
-// fp32 registers (the key order inside each MFMA K-step is the order the S^T
-// output layout leaves in the lane; the V^T fragment is read in that order).
-// The causal per-beam suffix (T <= 4 keys) is folded in first, with fp32 dot
-// products, as the initial online-softmax state; the result equals the
-// reference's LSE merge of the prefix and suffix partitions (ops.py:243-249).
-// A fully masked prefix contributes nothing, as in ops.py:229-240.
+// tile, B = the wave's query rows held in registers for the whole kernel),
+// so each lane owns one query column.  P is rounded to bf16 and
+// O^T += V^T P^T accumulates in fp32 registers.  The causal per-beam suffix
+// (up to 8 keys: a 4-key fold, and an 8-key one for longer suffixes) is
+// folded in first, with fp32 dot products, as the initial softmax state; the
+// result equals the reference's LSE merge of the prefix and suffix
+// partitions (ops.py:243-249).  A fully masked prefix contributes nothing, as
+// in ops.py:229-240.
 //
 // CAUSAL (prefill) mode: rows are (position, q-head in group) of one
 // sequence, keys are the same sequence's K/V and key j is visible to a row at
@@ -33,18 +30,9 @@
 
 namespace {
 
-constexpr int kKeys = 64;       // keys per tile
-constexpr int kRows = 128;      // query rows per workgroup (4 waves x 32)
 constexpr int kThreads = 256;
-
-template <int D>
-struct AttnSmem {
-  static constexpr int kLd = D + 8;          // K tile row stride (elements)
-  static constexpr int vLd = kKeys + 4;      // V^T tile row stride (elements)
-  static constexpr int kSize = kKeys * kLd;  // elements
-  static constexpr int vSize = D * vLd;
-  static constexpr int stage = kSize + vSize;
-};
+// suffix keys folded per beam row (decode): 4, or 8 for longer suffixes
+constexpr int kSuffixFold = 4, kSuffixFoldLong = 8;
 
 struct AttnArgs {
   const bf16_t* q; int64_t sq_n, sq_t, sq_h;
@@ -58,257 +46,6 @@ struct AttnArgs {
   int nqblk;
   int Tk, qoff;           // suffix keys per beam; query t is suffix position t + qoff
 };
-
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
-  using SM = AttnSmem<D>;
-  constexpr int KS = D / 16;   // k16 steps over the head dim
-  constexpr int DT = D / 32;   // 32-row d tiles of O^T
-  constexpr int K_TOT = kKeys * (D / 8), V_TOT = (kKeys / 2) * (D / 8);
-  constexpr int K_CH = (K_TOT + kThreads - 1) / kThreads;  // K chunks per thread
-  constexpr int V_CH = (V_TOT + kThreads - 1) / kThreads;  // V key-pair chunks per thread
-  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hi = lane >> 5, col = lane & 31;
-  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int qb = lid % a.nqblk;
-  const int bk = lid / a.nqblk;
-  const int kh = bk % a.HK, b = bk / a.HK;
-  const int G = a.H / a.HK;
-  const int64_t rows_total = CAUSAL ? (int64_t)a.L * G : (int64_t)a.W * G * a.T;
-
-  // ---- this lane's query row
-  const int64_t r = (int64_t)qb * kRows + wave * 32 + col;
-  const bool rvalid = r < rows_total;
-  const int64_t rr = rvalid ? r : 0;
-  int t, g, pos;
-  int64_t n;
-  if (CAUSAL) {
-    pos = (int)(rr / G);
-    g = (int)(rr % G);
-    t = pos;
-    n = b;  // q is [B, L, H, D]: sq_n = batch stride, sq_t = position stride
-  } else {
-    t = (int)(rr % a.T);
-    const int64_t wg = rr / a.T;
-    g = (int)(wg % G);
-    n = (int64_t)b * a.W + wg / G;
-    pos = 0;
-  }
-  const int h = kh * G + g;
-  const bf16_t* qrow = a.q + n * a.sq_n + (int64_t)t * a.sq_t + (int64_t)h * a.sq_h;
-  bf16x8 qf[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) qf[s] = as_bf16x8(*(const u32x4*)(qrow + s * 16 + hi * 8));
-
-  const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
-  float m = -INFINITY, l = 0.f;
-  f32x16 O[DT];
-#pragma unroll
-  for (int i = 0; i < DT; ++i) O[i] = f32x16{};
-
-  // ---- causal suffix of this beam (decode): keys j <= t of the same beam
-  if (!CAUSAL) {
-    float sc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sc[j] = -INFINITY;
-      if (j < a.Tk) {
-        const bf16_t* krow = a.sk + n * a.ssk_n + (int64_t)j * a.ssk_t + (int64_t)kh * a.ssk_h;
-        float part = 0.f;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const u32x4 kv = *(const u32x4*)(krow + s * 16 + hi * 8);
-          const bf16x8 kb = as_bf16x8(kv);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) part += (float)qf[s][i] * (float)kb[i];
-        }
-        part += __shfl_xor(part, 32, 64);
-        if (j <= t + a.qoff) sc[j] = part * sl2;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) m = fmaxf(m, sc[j]);
-    float pj[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pj[j] = sc[j] == -INFINITY ? 0.f : exp2f(sc[j] - m);
-      l += pj[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < a.Tk && pj[j] != 0.f) {
-        const bf16_t* vrow = a.sv + n * a.ssv_n + (int64_t)j * a.ssv_t + (int64_t)kh * a.ssv_h;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const int d0 = dt * 32 + gq * 8 + hi * 4;
-            const u32x2 v2 = *(const u32x2*)(vrow + d0);
-            O[dt][gq * 4 + 0] += pj[j] * __uint_as_float(v2[0] << 16);
-            O[dt][gq * 4 + 1] += pj[j] * __uint_as_float(v2[0] & 0xffff0000u);
-            O[dt][gq * 4 + 2] += pj[j] * __uint_as_float(v2[1] << 16);
-            O[dt][gq * 4 + 3] += pj[j] * __uint_as_float(v2[1] & 0xffff0000u);
-          }
-      }
-    }
-  }
-
-  // ---- prefix keys [0, kend)
-  int kend = a.L;
-  if (CAUSAL) {
-    const int64_t rlast = min((int64_t)(qb + 1) * kRows, rows_total) - 1;
-    kend = (int)(rlast / G) + 1;
-  }
-  const int ntiles = (kend + kKeys - 1) / kKeys;
-  const bf16_t* pkb = a.pk + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
-  const bf16_t* pvb = a.pv + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
-
-  u32x4 kreg[K_CH], vreg[V_CH][2];
-  auto fetch = [&](int tile) {
-    const int k0 = tile * kKeys;
-#pragma unroll
-    for (int i = 0; i < K_CH; ++i) {
-      const int c = tid + i * kThreads;
-      if (K_TOT % kThreads && c >= K_TOT) break;
-      const int key = c / (D / 8), ch = c % (D / 8);
-      const int kk = min(k0 + key, a.L - 1);
-      kreg[i] = *(const u32x4*)(pkb + (int64_t)kk * a.sp_l + ch * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < V_CH; ++i) {
-      const int c = tid + i * kThreads;
-      if (V_TOT % kThreads && c >= V_TOT) break;
-      const int kp = c / (D / 8), ch = c % (D / 8);
-      const int k1 = min(k0 + 2 * kp, a.L - 1), k2 = min(k0 + 2 * kp + 1, a.L - 1);
-      vreg[i][0] = *(const u32x4*)(pvb + (int64_t)k1 * a.sp_l + ch * 8);
-      vreg[i][1] = *(const u32x4*)(pvb + (int64_t)k2 * a.sp_l + ch * 8);
-    }
-  };
-  auto stash = [&](int buf) {
-    bf16_t* ks = smem + buf * SM::stage;
-    bf16_t* vs = ks + SM::kSize;
-#pragma unroll
-    for (int i = 0; i < K_CH; ++i) {
-      const int c = tid + i * kThreads;
-      if (K_TOT % kThreads && c >= K_TOT) break;
-      const int key = c / (D / 8), ch = c % (D / 8);
-      *(u32x4*)(ks + key * SM::kLd + ch * 8) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_CH; ++i) {
-      const int c = tid + i * kThreads;
-      if (V_TOT % kThreads && c >= V_TOT) break;
-      const int kp = c / (D / 8), ch = c % (D / 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t x0 = vreg[i][0][e], x1 = vreg[i][1][e];
-        // V^T[d][key pair]: two keys per 32-bit word
-        *(uint32_t*)(vs + (ch * 8 + 2 * e) * SM::vLd + 2 * kp) = (x0 & 0xffffu) | (x1 << 16);
-        *(uint32_t*)(vs + (ch * 8 + 2 * e + 1) * SM::vLd + 2 * kp) =
-            (x0 >> 16) | (x1 & 0xffff0000u);
-      }
-    }
-  };
-
-  if (ntiles > 0) {
-    fetch(0);
-    stash(0);
-  }
-  __syncthreads();
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
-    if (tile + 1 < ntiles) fetch(tile + 1);
-    const bf16_t* ks = smem + buf * SM::stage;
-    const bf16_t* vs = ks + SM::kSize;
-    // S^T[key, query] for 64 keys (two 32-key m-tiles)
-    f32x16 st[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + (mt * 32 + col) * SM::kLd + s * 16 + hi * 8));
-        st[mt] = mfma32x32x16(kf, qf[s], st[mt]);
-      }
-    }
-    const int k0 = tile * kKeys;
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = k0 + mt * 32 + (j / 4) * 8 + hi * 4 + (j % 4);
-        bool ok = key < kend;
-        if (CAUSAL) ok = ok && key <= pos;
-        else if (a.mask) ok = ok && a.mask[(int64_t)b * a.L + min(key, a.L - 1)] != 0;
-        const float v = ok ? st[mt][j] * sl2 : -INFINITY;
-        st[mt][j] = v;
-        tmax = fmaxf(tmax, v);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mnew = fmaxf(m, tmax);
-    const float alpha = (m == -INFINITY) ? (mnew == -INFINITY ? 1.f : 0.f) : exp2f(m - mnew);
-    float psum = 0.f;
-    bf16x8 pf[4];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float p = (st[mt][j] == -INFINITY) ? 0.f : exp2f(st[mt][j] - mnew);
-        psum += p;
-        pf[mt * 2 + j / 8][j % 8] = (__bf16)p;
-      }
-    psum += __shfl_xor(psum, 32, 64);
-    l = l * alpha + psum;
-    m = mnew;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) O[dt][j] *= alpha;
-    // O^T[d, query] += V^T[d, keys] P^T[keys, query]; K-step s covers keys
-    // 16s..16s+15 in the lane order {0-3, 8-11} (+4 for the upper half-wave)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16_t* vp = vs + (dt * 32 + col) * SM::vLd + s * 16 + hi * 4;
-        const u32x2 lo = *(const u32x2*)vp;
-        const u32x2 up = *(const u32x2*)(vp + 8);
-        const u32x4 vv = {lo[0], lo[1], up[0], up[1]};
-        O[dt] = mfma32x32x16(as_bf16x8(vv), pf[s], O[dt]);
-      }
-    }
-    if (tile + 1 < ntiles) stash(buf ^ 1);
-    __syncthreads();
-  }
-
-  if (!rvalid) return;
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
-  bf16_t* orow = a.out + n * a.so_n + (int64_t)t * a.so_t + (int64_t)h * a.so_h;
-  const bf16_t* grow =
-      a.gate ? a.gate + n * a.sg_n + (int64_t)t * a.sg_t + (int64_t)h * a.sg_h : nullptr;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const int d0 = dt * 32 + gq * 8 + hi * 4;
-      float o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = round_bf(O[dt][gq * 4 + i] * inv);
-      if (grow) {
-        const u32x2 g2 = *(const u32x2*)(grow + d0);
-        const float gv[4] = {__uint_as_float(g2[0] << 16), __uint_as_float(g2[0] & 0xffff0000u),
-                             __uint_as_float(g2[1] << 16), __uint_as_float(g2[1] & 0xffff0000u)};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = o[i] * round_bf(sigmoid_f(gv[i]));
-      }
-      u32x2 packed;
-      packed[0] = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
-      packed[1] = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
-      *(u32x2*)(orow + d0) = packed;
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Attention with 64 query rows per wave (two 32-row MFMA column blocks), so
@@ -361,7 +98,7 @@ typedef __attribute__((address_space(3))) void attn_lds_t;
 typedef __attribute__((address_space(1))) void attn_global_t;
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int NSUF>
 __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
   using AT = Attn2<D>;
   constexpr int KS = D / 16;   // k16 steps over the head dim
@@ -527,22 +264,22 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
   // scores are formed first (they set m_ref in decode) and their V rows are
   // added in the epilogue, so that O is only ever touched by MFMAs in the loop.
   float m_ref[2] = {-INFINITY, -INFINITY};
-  float sc[2][4];
+  float sc[2][NSUF];  // suffix scores (decode), key j of the beam
   if (!CAUSAL) {
-    float part[8];
+    float part[2 * NSUF];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) part[qb * 4 + j] = suffix_part(qb, j);
-    exchange(part, 8);
+      for (int j = 0; j < NSUF; ++j) part[qb * NSUF + j] = suffix_part(qb, j);
+    exchange(part, 2 * NSUF);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       int64_t n;
       int t, h;
       row_of_q(qb, n, t, h);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sc[qb][j] = j < a.Tk && j <= t + a.qoff ? part[qb * 4 + j] * sl2 : -INFINITY;
+      for (int j = 0; j < NSUF; ++j) {
+        sc[qb][j] = j < a.Tk && j <= t + a.qoff ? part[qb * NSUF + j] * sl2 : -INFINITY;
         m_ref[qb] = fmaxf(m_ref[qb], sc[qb][j]);
       }
     }
@@ -550,7 +287,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sc[qb][j] = -INFINITY;
+      for (int j = 0; j < NSUF; ++j) sc[qb][j] = -INFINITY;
   }
   float m_true[2] = {m_ref[0], m_ref[1]};
   float l[2];
@@ -561,7 +298,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
     for (int qb = 0; qb < 2; ++qb) {
       l[qb] = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NSUF; ++j)
         if (sc[qb][j] != -INFINITY) l[qb] += exp2f(sc[qb][j] - m_ref[qb]);
 #pragma unroll
       for (int i = 0; i < DT; ++i) O[qb][i] = f32x16{};
@@ -744,7 +481,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
     row_of_q(qb, n, t, h);
     if (!CAUSAL) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NSUF; ++j) {
         const float sj = sc[qb][j];
         if (sj == -INFINITY) continue;
         const float pj = exp2f(sj - m_ref[qb]);
@@ -791,7 +528,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
   }
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int NSUF>
 int launch_attn2(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
   a.nqblk = (int)kad_cdiv(rows, Attn2<D>::ROWS);
   const int64_t nblocks = bh * a.nqblk;
@@ -799,42 +536,33 @@ int launch_attn2(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
   const size_t lds = Attn2<D>::lds;
   static bool configured = false;
   if (!configured) {
-    if (hipFuncSetAttribute((const void*)attn2_kernel<D, CAUSAL>,
+    if (hipFuncSetAttribute((const void*)attn2_kernel<D, CAUSAL, NSUF>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
       kad_set_error("attention: cannot reserve %zu bytes of LDS", lds);
       return KAD_ERR_HIP;
     }
     configured = true;
   }
-  hipLaunchKernelGGL((attn2_kernel<D, CAUSAL>), dim3((unsigned)nblocks), dim3(kThreads), lds, s,
+  hipLaunchKernelGGL((attn2_kernel<D, CAUSAL, NSUF>), dim3((unsigned)nblocks), dim3(kThreads), lds, s,
                      a);
   return kad_launch_status("attn2_kernel");
 }
 
-template <int D, bool CAUSAL>
-int launch_attn(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
-  const size_t lds = 2 * AttnSmem<D>::stage * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute((const void*)attention_kernel<D, CAUSAL>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-      kad_set_error("attention: cannot reserve %zu bytes of LDS", lds);
-      return KAD_ERR_HIP;
-    }
-    configured = true;
-  }
-  hipLaunchKernelGGL((attention_kernel<D, CAUSAL>), dim3((unsigned)nblocks), dim3(kThreads), lds,
-                     s, a);
-  return kad_launch_status("attention_kernel");
+// rows: query rows per (request, KV head); bh: number of (request, KV head)
+// (the fold of up to 8 suffix keys is its own instantiation: a row's
+// arithmetic is the same in both, the keys past Tk scoring -inf)
+template <bool CAUSAL, int NSUF>
+int dispatch_d(int D, const AttnArgs& a, int64_t rows, int64_t bh, hipStream_t s) {
+  if (D == 256) return launch_attn2<256, CAUSAL, NSUF>(a, rows, bh, s);
+  if (D == 128) return launch_attn2<128, CAUSAL, NSUF>(a, rows, bh, s);
+  if (D == 64) return launch_attn2<64, CAUSAL, NSUF>(a, rows, bh, s);
+  KAD_UNSUPPORTED("attention supports head dim 64, 128, 256; got %d", D);
 }
 
-// rows: query rows per (request, KV head); bh: number of (request, KV head)
 template <bool CAUSAL>
 int dispatch(int D, const AttnArgs& a, int64_t rows, int64_t bh, hipStream_t s) {
-  if (D == 256) return launch_attn2<256, CAUSAL>(a, rows, bh, s);
-  if (D == 128) return launch_attn2<128, CAUSAL>(a, rows, bh, s);
-  if (D == 64) return launch_attn2<64, CAUSAL>(a, rows, bh, s);
-  KAD_UNSUPPORTED("attention supports head dim 64, 128, 256; got %d", D);
+  if (!CAUSAL && a.Tk > kSuffixFold) return dispatch_d<CAUSAL, kSuffixFoldLong>(D, a, rows, bh, s);
+  return dispatch_d<CAUSAL, kSuffixFold>(D, a, rows, bh, s);
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -853,7 +581,9 @@ extern "C" int kad_prefix_attention_decode_ex(
   KAD_REQUIRE(B > 0 && W > 0 && Tq > 0 && Tq <= Tk && H > 0 && HK > 0 && L >= 0 && D > 0,
               "bad dimensions");
   KAD_REQUIRE(H % HK == 0, "H must be divisible by HK");
-  if (Tk > 4) KAD_UNSUPPORTED("prefix attention supports suffixes of <= 4 tokens, got %d", Tk);
+  if (Tk > kSuffixFoldLong)
+    KAD_UNSUPPORTED("prefix attention supports suffixes of <= %d tokens, got %d", kSuffixFoldLong,
+                    Tk);
   KAD_REQUIRE(scale > 0.f && scale < INFINITY, "scale must be positive and finite");
   KAD_REQUIRE(al16(q) && al16(suffix_k) && (L == 0 || (al16(prefix_k) && al16(prefix_v))),
               "q, suffix_k and prefix K/V must be 16-byte aligned");

@@ -531,7 +531,9 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
 
 // ---------------------------------------------------------------------------
 constexpr int kMergeThreads = 1024;
-constexpr int kMaxW = 1024;
+// widest level: the winners and their sort buffer (the next power of two of
+// W entries, 8 bytes each) live in dynamic LDS, 128 KB at W = 16384
+constexpr int kMaxW = 16384;
 
 __device__ __forceinline__ bool before(float ka, int ia, float kb, int ib) {
   return ka > kb || (ka == kb && ia < ib);
@@ -576,15 +578,112 @@ __device__ __forceinline__ bool pick_bin(const int* hist, int need, int lane, in
   return lane == L;  // the lane that holds the result
 }
 
+// Rows of fp32 or fp16 logits (the reference upcasts any float dtype before
+// its log-softmax, src/kadllm/grbeam.py:91), one workgroup per row, exact:
+// the row max, the sum of exp(x - max), four 8-bit radix rounds over the
+// order keys of the row's scores key = ((x - max) - lse) + parent (-inf where
+// masked) for the K-th largest, then one pass that emits every key above it
+// and the first ties in column order.  Each pass recomputes the keys with the
+// same operations, so every pass sees the same values.
+__global__ __launch_bounds__(kRowThreads) void row_select_float_kernel(
+    const void* __restrict__ logits, int dtype, int64_t ld, const uint8_t* __restrict__ mask,
+    int64_t ld_mask, const float* __restrict__ parent, int Wp, int V, int K,
+    float* __restrict__ cand_key, int* __restrict__ cand_idx) {
+  __shared__ int hist[256];
+  __shared__ int scan_tmp[kRowThreads / 64];
+  __shared__ float red[kRowThreads / 64];
+  __shared__ uint32_t sh_prefix;
+  __shared__ int sh_need, sh_emit;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t xrow = row * ld;
+  const uint8_t* mk = mask ? mask + row * ld_mask : nullptr;
+
+  float m = -INFINITY;
+  for (int c = tid; c < V; c += kRowThreads) m = fmaxf(m, load_as_float(logits, xrow + c, dtype));
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  float M = -INFINITY;
+  for (int w = 0; w < kRowThreads / 64; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+  float se = 0.f;
+  for (int c = tid; c < V; c += kRowThreads) se += expf(load_as_float(logits, xrow + c, dtype) - M);
+  se = wave_sum(se);
+  if (lane == 0) red[wave] = se;
+  if (tid == 0) sh_emit = 0;
+  __syncthreads();
+  float SE = 0.f;
+  for (int w = 0; w < kRowThreads / 64; ++w) SE += red[w];
+  const float lse = logf(SE);
+  const float p = parent[row];
+  auto key_at = [&](int c) -> float {
+    const bool ok = mk ? mk[c] != 0 : true;
+    return ok ? ((load_as_float(logits, xrow + c, dtype) - M) - lse) + p : -INFINITY;
+  };
+
+  uint32_t prefix = 0, pmask = 0;
+  int need = K;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0;  // kRowThreads == 256 bins
+    __syncthreads();
+    for (int c = tid; c < V; c += kRowThreads) {
+      const uint32_t u = order32(key_at(c));
+      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      int d = 0, acc = 0;
+      if (pick_bin<true>(hist, need, tid, d, acc)) {
+        sh_prefix = prefix | ((uint32_t)d << shift);
+        sh_need = need - acc;
+      }
+    }
+    __syncthreads();
+    prefix = sh_prefix;
+    need = sh_need;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+  const uint32_t kth = prefix;  // the K-th largest key; `need` of its ties are taken
+  const int r_local = (int)(row % Wp);
+  float* ck = cand_key + row * K;
+  int* ci = cand_idx + row * K;
+  int ties_taken = 0;
+  for (int c0 = 0; c0 < V; c0 += kRowThreads) {
+    const int c = c0 + tid;
+    float key = -INFINITY;
+    uint32_t u = 0;
+    if (c < V) {
+      key = key_at(c);
+      u = order32(key);
+    }
+    const bool above = c < V && u > kth;
+    const bool tie = c < V && u == kth;
+    int tot = 0;
+    const int rank = block_exclusive_scan(tie ? 1 : 0, scan_tmp, &tot);
+    if (above || (tie && ties_taken + rank < need)) {
+      const int slot = atomicAdd(&sh_emit, 1);
+      if (slot < K) {  // exactly K entries qualify; the bound only guards memory
+        ck[slot] = key;
+        ci[slot] = r_local * V + c;
+      }
+    }
+    ties_taken += tot;
+  }
+}
+
 __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
     const float* __restrict__ cand_key, const int* __restrict__ cand_idx, int ncand, int W,
     int V, float* __restrict__ scores, int64_t* __restrict__ parents,
-    int64_t* __restrict__ tokens, uint8_t* __restrict__ valid) {
+    int64_t* __restrict__ tokens, uint8_t* __restrict__ valid, int cap) {
   __shared__ int hist[256];
   __shared__ uint32_t sh_prefix;
   __shared__ int sh_need, sh_count, sh_ties;
-  __shared__ float sk[kMaxW];
-  __shared__ int si[kMaxW];
+  // cap = the next power of two >= W keys, then as many indices
+  extern __shared__ __attribute__((aligned(16))) float merge_lds[];
+  float* sk = merge_lds;
+  int* si = (int*)(merge_lds + cap);
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
   const float* keys = cand_key + (int64_t)b * ncand;
@@ -664,7 +763,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
     const bool take = u > kth || (u == kth && (uint32_t)idxs[i] <= idx_cut);
     if (take) {
       const int slot = atomicAdd(&sh_count, 1);
-      if (slot < kMaxW) {
+      if (slot < cap) {
         sk[slot] = keys[i];
         si[slot] = idxs[i];
       }
@@ -748,29 +847,70 @@ __global__ __launch_bounds__(256) void gather_beam_rows_kernel(
   *(u32x4*)(dst + (n * dst_rows_per_beam + t) * ld_dst + c * 16) = v;
 }
 
-}  // namespace
-
-extern "C" int kad_beam_row_select(const void* logits, int64_t ld, const void* mask,
-                                   int64_t ld_mask, const float* parent_scores, int rows, int Wp,
-                                   int V, int K, float* cand_key, int* cand_idx,
-                                   kad_stream_t stream) {
-  KAD_REQUIRE(logits && parent_scores && cand_key && cand_idx, "null pointer argument");
-  KAD_REQUIRE(rows > 0 && Wp > 0 && rows % Wp == 0 && V > 0 && ld >= V, "bad dimensions");
-  KAD_REQUIRE(K >= 1 && K <= V, "K must be in [1, V]");
-  KAD_REQUIRE((int64_t)Wp * V < 0x7fffffff, "Wp * V must fit in int32 flat indices");
+int launch_row_select(const void* logits, int logits_dtype, int64_t ld, const void* mask,
+                      int64_t ld_mask, const float* parent_scores, int rows, int Wp, int V,
+                      int K, float* cand_key, int* cand_idx, hipStream_t s) {
+  if (logits_dtype != KAD_DTYPE_BF16) {
+    hipLaunchKernelGGL(row_select_float_kernel, dim3(rows), dim3(kRowThreads), 0, s, logits,
+                       logits_dtype, ld, (const uint8_t*)mask, ld_mask, parent_scores, Wp, V, K,
+                       cand_key, cand_idx);
+    return kad_launch_status("row_select_float_kernel");
+  }
   // sample ~kTargetLines lines; rank chosen so that rank * line_stride >= 2K + 256
   const int nlines = (V + kLine - 1) / kLine;
   const int line_stride = nlines > kTargetLines ? nlines / kTargetLines : 1;
   const int rank = (int)kad_cdiv(2 * (int64_t)K + 256, line_stride);
   if (2 * (int64_t)K + 256 <= kCandCapSmall / 2)
-    hipLaunchKernelGGL(row_select_kernel<kCandCapSmall>, dim3(rows), dim3(kRowThreads), 0,
-                       (hipStream_t)stream, (const bf16_t*)logits, ld, (const uint8_t*)mask,
-                       ld_mask, parent_scores, Wp, V, K, cand_key, cand_idx, line_stride, rank);
+    hipLaunchKernelGGL(row_select_kernel<kCandCapSmall>, dim3(rows), dim3(kRowThreads), 0, s,
+                       (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores,
+                       Wp, V, K, cand_key, cand_idx, line_stride, rank);
   else
-    hipLaunchKernelGGL(row_select_kernel<kCandCapLarge>, dim3(rows), dim3(kRowThreads), 0,
-                       (hipStream_t)stream, (const bf16_t*)logits, ld, (const uint8_t*)mask,
-                       ld_mask, parent_scores, Wp, V, K, cand_key, cand_idx, line_stride, rank);
+    hipLaunchKernelGGL(row_select_kernel<kCandCapLarge>, dim3(rows), dim3(kRowThreads), 0, s,
+                       (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores,
+                       Wp, V, K, cand_key, cand_idx, line_stride, rank);
   return kad_launch_status("row_select_kernel");
+}
+
+int launch_merge(const float* cand_key, const int* cand_idx, int B, int ncand, int W, int V,
+                 float* scores, int64_t* parents, int64_t* tokens, void* valid, hipStream_t s) {
+  int cap = 1;
+  while (cap < W) cap <<= 1;
+  const size_t lds = (size_t)cap * 8;
+  if (lds > 64 * 1024) {
+    // beyond the default 64 KB of dynamic LDS per workgroup (the CU has 160 KB)
+    const hipError_t e = hipFuncSetAttribute((const void*)merge_select_kernel,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)lds);
+    if (e != hipSuccess) {
+      kad_set_error("merge_select_kernel: cannot raise its LDS limit to %zu bytes: %s", lds,
+                    hipGetErrorString(e));
+      return KAD_ERR_HIP;
+    }
+  }
+  hipLaunchKernelGGL(merge_select_kernel, dim3(B), dim3(kMergeThreads), lds, s, cand_key, cand_idx,
+                     ncand, W, V, scores, parents, tokens, (uint8_t*)valid, cap);
+  return kad_launch_status("merge_select_kernel");
+}
+
+int check_logits_dtype(int dtype) {
+  KAD_REQUIRE(dtype == KAD_DTYPE_BF16 || dtype == KAD_DTYPE_F16 || dtype == KAD_DTYPE_F32,
+              "unknown logits dtype code %d", dtype);
+  return KAD_OK;
+}
+
+}  // namespace
+
+extern "C" int kad_beam_row_select(const void* logits, int logits_dtype, int64_t ld,
+                                   const void* mask, int64_t ld_mask, const float* parent_scores,
+                                   int rows, int Wp, int V, int K, float* cand_key, int* cand_idx,
+                                   kad_stream_t stream) {
+  KAD_REQUIRE(logits && parent_scores && cand_key && cand_idx, "null pointer argument");
+  KAD_REQUIRE(rows > 0 && Wp > 0 && rows % Wp == 0 && V > 0 && ld >= V, "bad dimensions");
+  KAD_REQUIRE(K >= 1 && K <= V, "K must be in [1, V]");
+  KAD_REQUIRE((int64_t)Wp * V < 0x7fffffff, "Wp * V must fit in int32 flat indices");
+  if (const int rc = check_logits_dtype(logits_dtype)) return rc;
+  return launch_row_select(logits, logits_dtype, ld, mask, ld_mask, parent_scores, rows, Wp, V, K,
+                           cand_key, cand_idx, (hipStream_t)stream);
 }
 
 extern "C" int kad_beam_merge_select(const float* cand_key, const int* cand_idx, int B, int ncand,
@@ -779,9 +919,8 @@ extern "C" int kad_beam_merge_select(const float* cand_key, const int* cand_idx,
   KAD_REQUIRE(cand_key && cand_idx && scores && parents && tokens && valid, "null pointer argument");
   KAD_REQUIRE(B > 0 && W > 0 && ncand >= W && V > 0, "bad dimensions (need ncand >= W)");
   if (W > kMaxW) KAD_UNSUPPORTED("beam width %d exceeds %d", W, kMaxW);
-  hipLaunchKernelGGL(merge_select_kernel, dim3(B), dim3(kMergeThreads), 0, (hipStream_t)stream,
-                     cand_key, cand_idx, ncand, W, V, scores, parents, tokens, (uint8_t*)valid);
-  return kad_launch_status("merge_select_kernel");
+  return launch_merge(cand_key, cand_idx, B, ncand, W, V, scores, parents, tokens, valid,
+                      (hipStream_t)stream);
 }
 
 extern "C" int kad_beam_history(const int64_t* history, int Wp, int step, const int64_t* parents,

@@ -21,7 +21,7 @@ int kad_launch_status(const char* what) {
 }
 
 extern "C" const char* kad_last_error(void) { return g_last_error; }
-extern "C" int kad_abi_version(void) { return 1; }
+extern "C" int kad_abi_version(void) { return 2; }
 
 // ---------------------------------------------------------------------------
 // MFMA operand-layout self-test.  One wave loads row-major A, B into the

@@ -30,6 +30,24 @@ __global__ __launch_bounds__(256) void conv_suffix_scalar(
   const int c = (int)(idx % C);
   const int64_t n = idx / C;
   const int64_t b = n / W;
+  if (width > 4) {
+    // wide kernels: each output reads its window straight from the prefix
+    // taps and the suffix, taps in weight order as the width-4 path
+    const float bv = bias ? ld(bias + c) : 0.f;
+    for (int t = 0; t < T_; ++t) {
+      float acc = bv;
+      for (int i = 0; i < width; ++i) {
+        const int p = t + i - (width - 1);  // < 0: prefix tap history + p
+        const float xv = p < 0 ? ld(state + b * ss_b + (int64_t)c * ss_c + (int64_t)(history + p) * ss_t)
+                               : ld(x + n * sx_n + (int64_t)c * sx_c + (int64_t)p * sx_t);
+        acc += ld(w + (int64_t)c * width + i) * xv;
+      }
+      float y = round_to_dtype(acc, Elem<T>::code);
+      if (silu) y = silu_f(y);
+      out[n * so_n + (int64_t)c * so_c + (int64_t)t * so_t] = Elem<T>::from_f(y);
+    }
+    return;
+  }
   float win[4] = {0.f, 0.f, 0.f, 0.f};  // win[3] is the newest tap
   float wt[4] = {0.f, 0.f, 0.f, 0.f};
   for (int i = 0; i < width; ++i) wt[4 - width + i] = ld(w + (int64_t)c * width + i);
@@ -282,7 +300,7 @@ extern "C" int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c,
                                       int activation_silu, kad_stream_t stream) {
   KAD_REQUIRE(x && state && weight && out, "null pointer argument");
   KAD_REQUIRE(B > 0 && W > 0 && C > 0 && T > 0 && width > 0, "dimensions must be positive");
-  if (width > 4) KAD_UNSUPPORTED("causal conv supports width <= 4, got %d", width);
+  if (width > 64) KAD_UNSUPPORTED("causal conv supports width <= 64, got %d", width);
   KAD_REQUIRE(history >= width - 1, "state history %d shorter than width-1", history);
   KAD_REQUIRE((int64_t)B * W * C < ((int64_t)1 << 40), "problem too large");
   hipStream_t s = (hipStream_t)stream;
@@ -307,7 +325,11 @@ extern "C" int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c,
     return launch_scalar<float>(x, sx_n, sx_c, sx_t, state, ss_b, ss_c, ss_t, history, weight,
                                 width, bias, out, so_n, so_c, so_t, B, W, C, T, activation_silu,
                                 s);
-  KAD_UNSUPPORTED("causal conv supports bf16 and fp32, got dtype %d", dtype);
+  if (dtype == KAD_DTYPE_F16)
+    return launch_scalar<_Float16>(x, sx_n, sx_c, sx_t, state, ss_b, ss_c, ss_t, history, weight,
+                                   width, bias, out, so_n, so_c, so_t, B, W, C, T,
+                                   activation_silu, s);
+  KAD_UNSUPPORTED("causal conv supports bf16, fp16 and fp32, got dtype %d", dtype);
 }
 
 extern "C" int kad_causal_conv_prefill(const void* x, int64_t ldx, const void* weight, void* out,

@@ -27,7 +27,7 @@
 
 namespace {
 
-constexpr int kTLimit = 4;  // longest suffix the replay handles
+constexpr int kTLimit = 8;  // longest suffix the replay handles
 
 template <typename TIN>
 struct QKFrag;
@@ -364,6 +364,10 @@ int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, in
   KAD_REPLAY_T(2)
   KAD_REPLAY_T(3)
   KAD_REPLAY_T(4)
+  KAD_REPLAY_T(5)
+  KAD_REPLAY_T(6)
+  KAD_REPLAY_T(7)
+  KAD_REPLAY_T(8)
 #undef KAD_REPLAY_T
   kad_set_error("gdn replay supports suffixes of 1..%d tokens, got %d", kTLimit, T);
   return KAD_ERR_UNSUPPORTED;

@@ -71,6 +71,11 @@ template <> struct Elem<float> {
   __device__ static __forceinline__ float to_f(float v) { return v; }
   __device__ static __forceinline__ float from_f(float f) { return f; }
 };
+template <> struct Elem<_Float16> {
+  static constexpr int code = KAD_DTYPE_F16;
+  __device__ static __forceinline__ float to_f(_Float16 v) { return (float)v; }
+  __device__ static __forceinline__ _Float16 from_f(float f) { return (_Float16)f; }
+};
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }

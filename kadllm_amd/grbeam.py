@@ -48,18 +48,30 @@ class GRBeamResult:
 Constraint = Callable[[torch.Tensor, torch.Tensor], torch.Tensor]
 
 
+# Widest level the merge kernel sorts in LDS (kad_beam_merge_select).
+MAX_WIDTH = 16384
+
+
+def _check_widths(widths):
+    if any(w > MAX_WIDTH for w in widths):
+        raise ValueError(f"beam widths above {MAX_WIDTH} are not supported by the HIP selection")
+
+
 def select_level(logits, scores, width, mask=None):
     """One selection level on the GPU (src/kadllm/grbeam.py:89-104).
 
-    logits [B, Wp, V] bf16 (last dim contiguous), scores [B, Wp] fp32, mask
+    logits [B, Wp, V] bf16, fp16 or fp32 (last dim contiguous; the key is
+    computed in fp32 as the reference's .float().log_softmax), scores [B, Wp] fp32, mask
     [B, Wp, V] bool or None; a mask that is one [V] row broadcast to every beam
     row (an ``expand``-ed view, row stride 0) is read in place.  Returns
     (scores [B, width] fp32, parents, tokens [B, width] int64, valid [B, width]
     bool).
     """
     B, Wp, V = logits.shape
-    if logits.dtype != torch.bfloat16:
-        raise RuntimeError("HIP beam selection takes bf16 logits")
+    if logits.dtype not in _lib.DTYPE_CODES:
+        raise RuntimeError("HIP beam selection takes bf16, fp16 or fp32 logits")
+    if width > MAX_WIDTH:
+        raise ValueError(f"beam width {width} exceeds the HIP selection limit {MAX_WIDTH}")
     if not logits.is_cuda:
         raise RuntimeError("HIP beam selection needs logits on a ROCm device")
     if logits.stride(2) != 1 or logits.stride(0) != Wp * logits.stride(1):
@@ -74,12 +86,15 @@ def select_level(logits, scores, width, mask=None):
     if mask is not None:
         if mask.shape != logits.shape or mask.dtype != torch.bool:
             raise ValueError("mask must be a bool tensor shaped like the logits")
+        if mask.device != dev:
+            raise ValueError("constraint mask must be on the logits' device")
         if mask.stride(2) == 1 and mask.stride(0) == Wp * mask.stride(1) and mask.is_cuda:
             m, ld_mask = mask.view(torch.uint8), mask.stride(1)
         else:
             m = mask.contiguous().view(torch.uint8)
     stream = _lib.stream_of(logits)
-    _lib.call("kad_beam_row_select", _lib.ptr(logits), logits.stride(1), _lib.ptr(m),
+    _lib.call("kad_beam_row_select", _lib.ptr(logits), _lib.dtype_code(logits.dtype),
+              logits.stride(1), _lib.ptr(m),
               ld_mask, _lib.ptr(parent), rows, Wp, V, K, _lib.ptr(cand_key), _lib.ptr(cand_idx),
               stream)
     new_scores = torch.empty(B, width, dtype=torch.float32, device=dev)
@@ -109,6 +124,8 @@ def select_level_grouped(logits, scores, groups, width, mask=None):
     if mask is not None:
         if mask.shape != logits.shape or mask.dtype != torch.bool:
             raise ValueError("mask must be a bool tensor shaped like the logits")
+        if mask.device != logits.device:
+            raise ValueError("constraint mask must be on the logits' device")
         if mask.stride(2) == 1 and mask.stride(0) == Wp * mask.stride(1):
             mk = mask.as_strided((B * groups, rpg, V), (rpg * mask.stride(1), mask.stride(1), 1))
         else:
@@ -163,6 +180,7 @@ def grbeam_search(
         not isinstance(w, int) or isinstance(w, bool) or w < 1 for w in widths
     ):
         raise ValueError("widths must contain positive integers")
+    _check_widths(widths)
     prefill = adapter.prefill(input_ids)
     B = input_ids.shape[0]
     if prefill.logits.ndim != 2 or prefill.logits.shape[0] != B:
@@ -192,6 +210,8 @@ def grbeam_search(
             mask = allowed(history, logits)
             if mask.shape != logits.shape or mask.dtype != torch.bool:
                 raise ValueError("constraint must return a bool mask matching logits")
+            if mask.device != logits.device:
+                raise ValueError("constraint mask must be on the logits' device")
         if width > history.shape[1] * V:
             raise ValueError("beam width exceeds the number of candidate slots")
         scores, parents, tokens, valid = select_level(logits, scores, width, mask)
@@ -226,6 +246,7 @@ def conditional_search(
             raise ValueError("widths must contain positive integers")
     if input_ids.ndim != 2 or min(input_ids.shape) < 1:
         raise ValueError("input_ids must be nonempty [B, prompt_length]")
+    _check_widths(list(coarse_widths) + list(fine_widths))
     prefill = adapter.prefill(input_ids)
     B = input_ids.shape[0]
     V = prefill.logits.shape[-1]
@@ -250,6 +271,8 @@ def conditional_search(
             mask = allowed(history, logits)
             if mask.dtype != torch.bool:
                 raise ValueError("constraint must return a bool mask")
+            if mask.device != logits.device:
+                raise ValueError("constraint mask must be on the logits' device")
             mask = mask.expand(logits.shape)
         if kind is None:
             if width > history.shape[1] * V:

@@ -74,7 +74,8 @@ def _gdn_launch(config):
         )
 
 
-REPLAY_MAX_T = 4
+# longest suffix of the factored replay kernel (kad_gdn_suffix_replay)
+REPLAY_MAX_T = 8
 
 
 def gated_delta(q, k, v, log_decay, beta, shared_state, *, beam_width: int = 1,
@@ -89,9 +90,11 @@ def gated_delta(q, k, v, log_decay, beta, shared_state, *, beam_width: int = 1,
     [B*W,T,HV,V] in v's dtype; with ``return_final_state`` also the per-beam
     final state [B*W,HV,K,V] fp32 (use W=1 to build a shared prefix).
 
-    Suffixes of up to 4 tokens run the factored replay kernel
-    (kad_gdn_suffix_replay); longer ones and final-state requests run the
-    chunked kernel (kad_gdn_chunk).
+    Key and value dims of 64 or 128 run the specialised kernels: suffixes of
+    up to 8 tokens the factored replay (kad_gdn_suffix_replay), longer bf16
+    ones and final-state requests the chunked kernel (kad_gdn_chunk).  Every
+    other shape and dtype (fp16, fp32 beyond the replay, head dims up to 256)
+    runs the token-by-token recurrence kernel (kad_gdn_recurrent).
     """
     _width(beam_width)
     _gdn_launch(triton_config)
@@ -118,12 +121,15 @@ def gated_delta(q, k, v, log_decay, beta, shared_state, *, beam_width: int = 1,
         raise ValueError("Triton decode does not return a final state")
     if triton_config is not None and (backend == "torch" or return_final_state):
         raise ValueError("triton_config requires the Triton execution path")
-    if q.dtype == torch.float16:
-        raise RuntimeError("HIP gated_delta supports bf16 and fp32 q/k/v")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     log_decay, beta = log_decay.contiguous(), beta.contiguous()
     shared_state = shared_state.contiguous()
     B = BW // beam_width
+    specialised = K in (64, 128) and V in (64, 128)
+    if not specialised or q.dtype == torch.float16 or (
+            q.dtype == torch.float32 and (T > REPLAY_MAX_T or return_final_state)):
+        return gdn_recurrent(q, k, v, log_decay, beta, shared_state, beam_width=beam_width,
+                             scale=scale, want_final=return_final_state)
     if T <= REPLAY_MAX_T and not return_final_state:
         out = torch.empty_like(v)
         _lib.call("kad_gdn_suffix_replay", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), H * K, HV * V,
@@ -136,6 +142,26 @@ def gated_delta(q, k, v, log_decay, beta, shared_state, *, beam_width: int = 1,
     out, final = gdn_chunk(q, k, v, log_decay, beta, shared_state, beam_width=beam_width,
                            scale=scale, want_final=return_final_state)
     return (out, final) if return_final_state else out
+
+
+def gdn_recurrent(q, k, v, log_decay, beta, shared_state, *, beam_width=1, scale=None,
+                  want_final=False):
+    """The per-token gated delta rule of src/kadllm/ops.py:139-163 on the GPU
+    (kad_gdn_recurrent) for contiguous q, k [N,T,H,K], v [N,T,HV,V], gates
+    [N,T,HV], shared_state [N/beam_width,HV,K,V] or None (zeros).  Returns out
+    [N,T,HV,V] in v's dtype, or (out, final fp32 [N,HV,K,V]) with want_final."""
+    N, T, H, K = q.shape
+    HV, V = v.shape[-2:]
+    scale = K ** -0.5 if scale is None else scale
+    out = torch.empty_like(v)
+    final = torch.empty(N, HV, K, V, dtype=torch.float32, device=v.device) if want_final else None
+    st = shared_state
+    _lib.call("kad_gdn_recurrent", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), H * K, HV * V,
+              _lib.dtype_code(q.dtype), _lib.ptr(log_decay), _lib.dtype_code(log_decay.dtype),
+              _lib.ptr(beta), _lib.dtype_code(beta.dtype), HV, _lib.ptr(st),
+              _lib.dtype_code(st.dtype) if st is not None else 2, beam_width, _lib.ptr(out),
+              HV * V, _lib.ptr(final), N, T, H, HV, K, V, float(scale), _lib.stream_of(v))
+    return (out, final) if want_final else out
 
 
 def causal_conv1d(x, shared_state, weight, *, beam_width: int = 1, bias=None,
@@ -168,10 +194,8 @@ def causal_conv1d(x, shared_state, weight, *, beam_width: int = 1, bias=None,
     if activation not in (None, "silu"):
         raise ValueError("activation must be None or silu")
     _backend(backend, tensors)
-    if width > 4:
-        raise RuntimeError("HIP short convolution supports width <= 4")
-    if x.dtype == torch.float16:
-        raise RuntimeError("HIP short convolution supports bf16 and fp32")
+    if (width != 4 or bias is not None or activation != "silu") and backend == "triton":
+        raise ValueError("Triton short-conv requires width=4, SiLU, and no bias")
     weight = weight.contiguous()
     bias = None if bias is None else bias.contiguous()
     out = torch.empty(BW, C, T, dtype=x.dtype, device=x.device)

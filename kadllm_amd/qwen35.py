@@ -26,12 +26,28 @@ import torch
 
 from . import _lib, layers
 from .attention import attention_prefill, prefix_attention_decode
+from .ops import REPLAY_MAX_T
 
 _BLOCK = 32  # gate/up interleave granularity of the SwiGLU epilogue
 
 
 def _round_up(x, m):
     return (x + m - 1) // m * m
+
+
+def reject_biases(cfg, state_dict):
+    """The packed projections carry no bias.  Qwen3.5 has none
+    (attention_bias=False, bias-free GDN projections and conv); a checkpoint
+    that holds one would be applied by the reference adapter's modules
+    (src/kadllm/adapters/qwen3_5.py:146,181-188,202 and the conv1d.bias it
+    passes to causal_conv1d), so it is refused here rather than dropped."""
+    if getattr(cfg, "attention_bias", False):
+        raise ValueError("attention_bias=True checkpoints are not supported by the HIP runner")
+    biased = sorted(k for k in state_dict
+                    if k.endswith(".bias") and (".self_attn." in k or ".linear_attn." in k
+                                                or ".mlp." in k))
+    if biased:
+        raise ValueError(f"the HIP runner has no projection biases; checkpoint holds {biased[:3]}")
 
 
 @dataclass
@@ -109,6 +125,7 @@ class Qwen35Runner:
         H = cfg.hidden_size
         if H % 64:
             raise ValueError("hidden size must be a multiple of 64 for the GEMM kernels")
+        reject_biases(cfg, state_dict)
         self.embed = get("embed_tokens.weight")
         head = lm_head_weight if lm_head_weight is not None else state_dict.get("lm_head.weight")
         self.lm_head = (self.embed if head is None else
@@ -185,6 +202,28 @@ class Qwen35Runner:
         o = self.conv_dim + self.vd
         return layers.gdn_gates(proj[:, o:o + hv], proj[:, o + hv:o + 2 * hv], lyr.A_log,
                                 lyr.dt_bias)
+
+    def _gdn_replay(self, conv, g, beta, S, o, B, W, T):
+        """Each beam's T suffix tokens applied to its request's prefix state S
+        (q, k, v are column ranges of the conv output rows).  Up to 8 tokens
+        the factored MFMA replay, whose arithmetic for a token does not depend
+        on how many follow it (so a cached suffix extended by one token gives
+        the stateless replay's bits); longer suffixes the per-token recurrence
+        (kad_gdn_recurrent), the reference torch path's arithmetic in fp32."""
+        cfg = self.cfg
+        H_, HV = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+        dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+        C = self.conv_dim
+        base, es = conv.data_ptr(), conv.element_size()
+        args = (_lib.ptr(conv), _lib.ptr_at(base + self.kd * es), _lib.ptr_at(base + 2 * self.kd * es),
+                C, C, 0, _lib.ptr(g), 2, _lib.ptr(beta), 0, HV, _lib.ptr(S),
+                _lib.dtype_code(S.dtype))
+        if T <= REPLAY_MAX_T:
+            _lib.call("kad_gdn_suffix_replay", *args, _lib.ptr(o), self.vd, B, W, T, H_, HV, dk,
+                      dv, float(dk ** -0.5), _lib.stream_of(conv))
+        else:
+            _lib.call("kad_gdn_recurrent", *args, W, _lib.ptr(o), self.vd, None, B * W, T, H_, HV,
+                      dk, dv, float(dk ** -0.5), _lib.stream_of(conv))
 
     def _gdn_finish(self, lyr, o, proj, x):
         cfg = self.cfg
@@ -328,12 +367,7 @@ class Qwen35Runner:
                 g, beta = self._gdn_gates(lyr, proj)
                 o = torch.empty(R, self.vd, dtype=torch.bfloat16, device=dev)
                 S = cached[1]
-                base, es = conv.data_ptr(), conv.element_size()
-                _lib.call("kad_gdn_suffix_replay", _lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
-                          _lib.ptr_at(base + 2 * self.kd * es), C, C, 0, _lib.ptr(g), 2,
-                          _lib.ptr(beta), 0, HV, _lib.ptr(S), _lib.dtype_code(S.dtype),
-                          _lib.ptr(o), self.vd, B, W, T, H_, HV, dk, dv, float(dk ** -0.5),
-                          _lib.stream_of(x))
+                self._gdn_replay(conv, g, beta, S, o, B, W, T)
                 if terminal:
                     self._gdn_finish(lyr, o.view(BW, T, -1)[:, -1], proj.view(BW, T, -1)[:, -1],
                                      x_last)
@@ -410,8 +444,6 @@ class Qwen35Runner:
         BW = B * W
         T = 1 if cache is None else cache.T + 1
         Wp = 1 if cache is None else cache.W
-        if T > 4:
-            raise ValueError("the HIP replay kernels handle suffixes of at most 4 tokens")
         dev = self.device
         parents = parents.to(torch.int64).contiguous() if cache is not None else None
         x = layers.embedding(tokens, self.embed)
@@ -444,12 +476,7 @@ class Qwen35Runner:
                           _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, stream)
                 g, beta = self._gdn_gates(lyr, proj)
                 o = torch.empty(BW * T, self.vd, dtype=torch.bfloat16, device=dev)
-                base, es = conv.data_ptr(), conv.element_size()
-                _lib.call("kad_gdn_suffix_replay", _lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
-                          _lib.ptr_at(base + 2 * self.kd * es), C, C, 0, _lib.ptr(g), 2,
-                          _lib.ptr(beta), 0, HV, _lib.ptr(cached[1]),
-                          _lib.dtype_code(cached[1].dtype), _lib.ptr(o), self.vd, B, W, T, H_,
-                          HV, dk, dv, float(dk ** -0.5), stream)
+                self._gdn_replay(conv, g, beta, cached[1], o, B, W, T)
                 o_new = o.view(BW, T, self.vd)[:, T - 1]
                 z_new = pv[:, T - 1, C:C + self.vd]
                 y = layers.rmsnorm_gated(o_new, z_new, lyr.norm_w, cfg.rms_norm_eps, HV)

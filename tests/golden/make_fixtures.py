@@ -16,6 +16,14 @@ grbeam_tiny_fp32.npz
     [8, 8, 8].  Stores the prompt, prefill logits, every decode call's
     history and logits, the prefix tensors, final tokens and scores.
 
+reference_lm_fp32.npz
+    The reference's own toy adapter ``ReferenceHybridLM`` (torch backends,
+    fp32): for each case, the state dict after ``torch.manual_seed(seed)``
+    construction, the prompt, prefill logits, every decode call's history
+    and logits, and the final tokens, scores and valid flags.  Case 0 is the
+    README example (vocabulary 32, prompts [2, 5], widths [2, 3, 4]); case 1
+    a wider model (vocabulary 64, hidden 32, 4 heads) over 6 levels.
+
 ops_bf16.npz
     Bit-level outputs of the reference torch operators in bf16 on small
     seeded inputs (gated_delta, causal_conv1d, prefix_attention), pinning
@@ -93,6 +101,53 @@ def make_grbeam_tiny():
     print("grbeam_tiny_fp32: tokens", result.tokens.tolist())
 
 
+def make_reference_lm():
+    from kadllm import grbeam_search
+    from kadllm.adapters import ReferenceHybridLM
+
+    cases = [dict(seed=0, vocab=32, hidden=16, heads=2, batch=2, prompt=5, widths=[2, 3, 4]),
+             dict(seed=1, vocab=64, hidden=32, heads=4, batch=3, prompt=9,
+                  widths=[4, 6, 5, 8, 3, 7])]
+    arrays = {}
+    for ci, c in enumerate(cases):
+        torch.manual_seed(c["seed"])
+        model = ReferenceHybridLM(vocab_size=c["vocab"], hidden_size=c["hidden"],
+                                  num_heads=c["heads"]).eval()
+        gen = torch.Generator().manual_seed(c["seed"])
+        ids = torch.randint(0, c["vocab"], (c["batch"], c["prompt"]), generator=gen)
+        calls = []
+        decode, prefill = model.decode, model.prefill
+        captured = {}
+
+        def recording_decode(history, state, decode=decode, calls=calls):
+            logits = decode(history, state)
+            calls.append((history.clone(), logits.clone()))
+            return logits
+
+        def recording_prefill(input_ids, prefill=prefill, captured=captured):
+            out = prefill(input_ids)
+            captured["logits"] = out.logits.clone()
+            return out
+
+        model.decode, model.prefill = recording_decode, recording_prefill
+        result = grbeam_search(model, ids, c["widths"])
+        p = f"c{ci}_"
+        arrays[p + "config"] = np.array([c["vocab"], c["hidden"], c["heads"]])
+        arrays[p + "widths"] = np.array(c["widths"])
+        arrays[p + "input_ids"] = ids.numpy()
+        arrays[p + "prefill_logits"] = _bits(captured["logits"])
+        arrays[p + "tokens"] = result.tokens.numpy()
+        arrays[p + "scores"] = _bits(result.scores)
+        arrays[p + "valid"] = result.valid.numpy()
+        for step, (hist, logits) in enumerate(calls, start=1):
+            arrays[p + f"decode{step}_history"] = hist.numpy()
+            arrays[p + f"decode{step}_logits"] = _bits(logits)
+        for name, t in model.state_dict().items():
+            arrays[p + "w:" + name] = _bits(t)
+        print(f"reference_lm case {ci}: tokens shape", tuple(result.tokens.shape))
+    np.savez_compressed(os.path.join(HERE, "reference_lm_fp32.npz"), **arrays)
+
+
 def make_ops_bf16():
     from kadllm.ops import causal_conv1d, gated_delta, prefix_attention
 
@@ -140,6 +195,7 @@ def make_ops_bf16():
 if __name__ == "__main__":
     sys.path.insert(0, REFERENCE_SRC)
     torch.set_num_threads(4)
+    which = sys.argv[1:] or ["grbeam_tiny", "ops_bf16", "reference_lm"]
     with torch.no_grad():
-        make_grbeam_tiny()
-        make_ops_bf16()
+        for name in which:
+            globals()["make_" + name]()

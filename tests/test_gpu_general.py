@@ -1,0 +1,209 @@
+"""General-shape kernels (kad_gdn_recurrent, kad_attention_general, wide conv,
+fp32/fp16 selection, beams above 1024) and the reference's toy model on them,
+against the oracle and the reference's own outputs."""
+
+import pytest
+import torch
+
+from kadllm_amd import grbeam_search, ops
+from kadllm_amd.attention import prefix_attention_decode
+from kadllm_amd.grbeam import select_level
+from _fixtures import gdn_inputs
+from conftest import assert_close_rel, assert_selection_gap_aware
+from oracle import grbeam_ref, ops_ref
+from test_oracle_reference_lm import reference_lm_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _on(device, *ts):
+    return [t.to(device) if t is not None else None for t in ts]
+
+
+@pytest.mark.parametrize("dtype,B,W,T,H,HV,K,V", [
+    (torch.float32, 2, 3, 7, 2, 2, 8, 8),
+    (torch.float32, 1, 4, 6, 1, 2, 128, 128),
+    (torch.bfloat16, 2, 2, 5, 2, 4, 32, 48),
+    (torch.float16, 2, 3, 3, 2, 2, 64, 64),
+    (torch.float32, 1, 2, 2, 1, 1, 256, 70),
+])
+def test_gated_delta_general_matches_oracle(device, dtype, B, W, T, H, HV, K, V):
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, dtype=dtype, seed=T + K)
+    expected = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W)
+    S_dev = S.to(device)
+    got = ops.gated_delta(*_on(device, q, k, v, g, beta), S_dev, beam_width=W)
+    assert got.dtype == dtype
+    if dtype == torch.float32:
+        torch.testing.assert_close(got.cpu(), expected, atol=2e-5, rtol=1e-4)
+    else:
+        assert_close_rel(got, expected, rtol=1e-2, atol_frac=4e-3, name="gdn general")
+    assert torch.equal(S_dev.cpu(), S)  # the prefix is read, never written
+
+
+@pytest.mark.parametrize("dtype,K,V", [(torch.float32, 8, 8), (torch.float32, 64, 64),
+                                       (torch.bfloat16, 16, 40)])
+def test_gated_delta_final_state_general(device, dtype, K, V):
+    B, W, T, H, HV = 2, 1, 9, 2, 2
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, dtype=dtype, seed=3)
+    eo, ef = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W, return_final_state=True)
+    go, gf = ops.gated_delta(*_on(device, q, k, v, g, beta, S), beam_width=W,
+                             return_final_state=True)
+    torch.testing.assert_close(gf.cpu(), ef, atol=2e-5, rtol=1e-4)
+    if dtype == torch.float32:
+        torch.testing.assert_close(go.cpu(), eo, atol=2e-5, rtol=1e-4)
+    else:
+        assert_close_rel(go, eo, rtol=1e-2, atol_frac=4e-3, name="gdn final")
+
+
+def _attn_inputs(B, W, T, H, HK, L, D, dtype, seed, Tk=None):
+    g = torch.Generator().manual_seed(seed)
+    Tk = T if Tk is None else Tk
+    q = torch.randn(B * W, T, H, D, generator=g).to(dtype)
+    pk = torch.randn(B, L, HK, D, generator=g).to(dtype)
+    pv = torch.randn(B, L, HK, D, generator=g).to(dtype)
+    sk = torch.randn(B * W, Tk, HK, D, generator=g).to(dtype)
+    sv = torch.randn(B * W, Tk, HK, D, generator=g).to(dtype)
+    return q, pk, pv, sk, sv
+
+
+@pytest.mark.parametrize("dtype,B,W,T,H,HK,L,D", [
+    (torch.float32, 2, 1, 5, 2, 2, 0, 8),       # a whole prompt, no prefix
+    (torch.float32, 2, 3, 3, 4, 2, 17, 48),
+    (torch.bfloat16, 1, 4, 6, 8, 2, 40, 256),   # suffix longer than the MFMA kernel's 4
+    (torch.float16, 2, 2, 2, 4, 4, 33, 64),
+    (torch.bfloat16, 2, 2, 3, 2, 1, 9, 96),     # head dim outside 64/128/256
+])
+def test_prefix_attention_general_matches_oracle(device, dtype, B, W, T, H, HK, L, D):
+    q, pk, pv, sk, sv = _attn_inputs(B, W, T, H, HK, L, D, dtype, seed=L + D)
+    mask = None
+    if L:
+        mask = torch.rand(B, L, generator=torch.Generator().manual_seed(5)) > 0.3
+        mask[-1] = False  # a request whose prefix is fully masked
+    expected = ops_ref.prefix_attention(q, pk, pv, sk, sv, beam_width=W, prefix_mask=mask)
+    got = ops.prefix_attention(*_on(device, q, pk, pv, sk, sv), beam_width=W,
+                               prefix_mask=_on(device, mask)[0])
+    if dtype == torch.float32:
+        torch.testing.assert_close(got.cpu(), expected, atol=2e-5, rtol=1e-4)
+    else:
+        assert_close_rel(got, expected, rtol=1e-2, atol_frac=4e-3, name="attention general")
+
+
+def test_prefix_attention_general_query_offset_and_gate(device):
+    """Queries that are the last Tq of Tk suffix tokens equal the last rows of
+    the full Tk-token attention; a gate multiplies by its rounded sigmoid."""
+    B, W, H, HK, L, D, Tk, Tq = 2, 3, 4, 2, 20, 128, 7, 2
+    q, pk, pv, sk, sv = _attn_inputs(B, W, Tk, H, HK, L, D, torch.bfloat16, seed=9)
+    full = ops_ref.prefix_attention(q, pk, pv, sk, sv, beam_width=W)
+    gate = torch.randn(B * W, Tq, H * D, generator=torch.Generator().manual_seed(2)).to(
+        torch.bfloat16)
+    got = prefix_attention_decode(*_on(device, q[:, Tk - Tq:].contiguous(), pk, pv, sk, sv), W,
+                                  None, D ** -0.5, gate=gate.to(device))
+    expected = (full[:, Tk - Tq:].float().reshape(B * W, Tq, H * D)
+                * torch.sigmoid(gate.float()).bfloat16().float()).bfloat16()
+    assert_close_rel(got.reshape(B * W, Tq, H * D), expected, rtol=1e-2, atol_frac=4e-3,
+                     name="attention offset+gate")
+
+
+@pytest.mark.parametrize("dtype,width,bias", [(torch.float32, 6, True), (torch.float16, 5, False),
+                                              (torch.bfloat16, 8, True), (torch.float32, 3, True)])
+def test_causal_conv1d_any_width(device, dtype, width, bias):
+    g = torch.Generator().manual_seed(width)
+    B, W, C, T = 2, 3, 24, 4
+    x = torch.randn(B * W, C, T, generator=g).to(dtype)
+    st = torch.randn(B, C, width + 1, generator=g).to(dtype)
+    w = (torch.rand(C, width, generator=g) - 0.5).to(dtype)
+    b = torch.randn(C, generator=g).to(dtype) if bias else None
+    expected = ops_ref.causal_conv1d(x.float(), st.float(), w.float(), beam_width=W,
+                                     bias=None if b is None else b.float())
+    got = ops.causal_conv1d(*_on(device, x, st, w), beam_width=W, bias=_on(device, b)[0])
+    tol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]
+    torch.testing.assert_close(got.float().cpu(), expected, atol=tol, rtol=tol)
+
+
+def test_triton_conv_backend_requires_width4_silu_nobias(device):
+    x = torch.randn(2, 8, 2, device=device, dtype=torch.bfloat16)
+    st = torch.randn(2, 8, 3, device=device, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="Triton short-conv requires width=4, SiLU, and no bias"):
+        ops.causal_conv1d(x, st, torch.randn(8, 3, device=device, dtype=torch.bfloat16),
+                          backend="triton")
+    with pytest.raises(ValueError, match="Triton short-conv"):
+        ops.causal_conv1d(x, st, torch.randn(8, 4, device=device, dtype=torch.bfloat16),
+                          activation=None, backend="triton")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_select_float_logits_matches_oracle(device, dtype):
+    g = torch.Generator().manual_seed(11)
+    B, Wp, V, width = 3, 5, 1000, 7
+    logits = (torch.randn(B, Wp, V, generator=g) * 3).to(dtype)
+    scores = torch.randn(B, Wp, generator=g)
+    mask = torch.rand(B, Wp, V, generator=g) > 0.2
+    for m in (None, mask):
+        es, ep, et = grbeam_ref.level_select(logits, scores, width, m)
+        s, p, t, valid = select_level(*_on(device, logits, scores), width,
+                                      None if m is None else m.to(device))
+        assert torch.equal(p.cpu(), ep) and torch.equal(t.cpu(), et)
+        torch.testing.assert_close(s.cpu(), es, atol=1e-5, rtol=1e-6)
+        assert bool(valid.all())
+
+
+@pytest.mark.parametrize("B,Wp,V,width", [(2, 4, 2048, 3000), (1, 16, 4096, 16384)])
+def test_select_beams_above_1024(device, B, Wp, V, width):
+    """Widths past the 1024 the merge once held, up to its LDS limit.  Judged
+    gap-aware against fp64 keys: thousands of picks sit within fp32 noise of
+    picks from other rows, whose order rounding decides."""
+    g = torch.Generator().manual_seed(width)
+    logits = torch.randn(B, Wp, V, generator=g).bfloat16()
+    scores = torch.randn(B, Wp, generator=g)
+    s, p, t, valid = select_level(*_on(device, logits, scores), width)
+    keys = logits.double().log_softmax(-1) + scores.double()[..., None]
+    assert_selection_gap_aware(s, p, t, keys, width, delta=2e-5, name=f"W={width}")
+    assert bool(valid.all())
+
+
+def test_reference_hybrid_lm_readme_example(device):
+    """README.md:254-266: ReferenceHybridLM(vocab_size=32), prompts [2, 5],
+    widths [2, 3, 4] gives tokens [2, 4, 3]."""
+    from kadllm import grbeam_search as search
+    from kadllm.adapters import ReferenceHybridLM
+
+    torch.manual_seed(0)
+    model = ReferenceHybridLM(vocab_size=32).to(device).eval()
+    prompts = torch.randint(0, 32, (2, 5), device=device)
+    with torch.inference_mode():
+        result = search(model, prompts, widths=[2, 3, 4])
+    assert tuple(result.tokens.shape) == (2, 4, 3)
+    assert bool(result.valid.all())
+
+
+@pytest.mark.parametrize("ci", [0, 1])
+def test_reference_hybrid_lm_matches_reference_outputs(device, ci):
+    """The HIP toy model with the reference's weights reproduces the reference's
+    search: tokens exactly, scores and every level's logits within fp32 noise."""
+    from kadllm.adapters import ReferenceHybridLM
+
+    c = reference_lm_case(ci)
+    model = ReferenceHybridLM(vocab_size=c["vocab"], hidden_size=c["hidden"],
+                              num_heads=c["heads"])
+    model.load_state_dict(c["sd"])
+    model = model.to(device).eval()
+    seen = []
+    decode = model.decode
+
+    def recording(history, state):
+        out = decode(history, state)
+        seen.append((history.cpu(), out.cpu()))
+        return out
+
+    model.decode = recording
+    result = grbeam_search(model, c["ids"].to(device), c["widths"])
+    with torch.no_grad():
+        pre = model.prefill(c["ids"].to(device))
+    torch.testing.assert_close(pre.logits.cpu(), c["prefill_logits"], atol=1e-4, rtol=1e-4)
+    assert len(seen) == len(c["calls"])
+    for (h, got), (eh, expected) in zip(seen, c["calls"]):
+        assert torch.equal(h, eh)
+        torch.testing.assert_close(got, expected, atol=1e-4, rtol=1e-4)
+    assert torch.equal(result.tokens.cpu(), c["tokens"])
+    torch.testing.assert_close(result.scores.cpu(), c["scores"], atol=1e-4, rtol=1e-5)
+    assert torch.equal(result.valid.cpu(), c["valid"])

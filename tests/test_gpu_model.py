@@ -80,7 +80,7 @@ def test_tiny_prefill_matches_oracle(device, tiny):
             assert_logits_close(b, rb, f"layer {i} V", rel=1e-2)
 
 
-@pytest.mark.parametrize("T", [1, 2, 3])
+@pytest.mark.parametrize("T", [1, 2, 3, 5, 6])
 def test_tiny_decode_matches_oracle(device, tiny, T):
     cfg, oracle, adapter = tiny
     g = torch.Generator().manual_seed(T)
@@ -189,11 +189,45 @@ def _incremental_matches_stateless(adapter, state, B, widths, V, device, seed):
 
 
 def test_incremental_decode_equals_stateless_tiny(device, tiny):
-    """Suffix dedup across levels: exactly the stateless replay's logits, T = 1..4."""
+    """Suffix dedup across levels: exactly the stateless replay's logits, T = 1..7
+    (past 4 tokens both run the per-token recurrence and the general attention)."""
     cfg, _, adapter = tiny
     ids = torch.randint(0, cfg.vocab_size, (3, 50), generator=torch.Generator().manual_seed(21))
     res = adapter.prefill(ids.to(device))
-    _incremental_matches_stateless(adapter, res.state, 3, [5, 7, 6, 9], cfg.vocab_size, device, 22)
+    _incremental_matches_stateless(adapter, res.state, 3, [5, 7, 6, 9, 4, 3, 5],
+                                   cfg.vocab_size, device, 22)
+
+
+def test_tiny_grbeam_depth7_teacher_forced(device, tiny):
+    """A 7-token search (the depth of the reference's README.md:125 runs; the
+    reference has no depth limit, src/kadllm/grbeam.py:75-77): every level's
+    logits against the oracle, the selection equal to the oracle's on the GPU's
+    own logits."""
+    cfg, oracle, adapter = tiny
+    g = torch.Generator().manual_seed(17)
+    B = 2
+    ids = torch.randint(0, cfg.vocab_size, (B, 64), generator=g)
+    widths = [6, 6, 5, 6, 4, 5, 6]
+    result = grbeam_search(adapter, ids.to(device), widths)
+    torch.cuda.synchronize()
+    toks = result.tokens.cpu()
+    assert toks.shape == (B, 6, 7) and result.valid.all()
+    pre_logits, state = oracle.prefill(ids)
+    _, t_state = adapter.truth.prefill(ids)
+    gpu_pre = adapter.prefill(ids.to(device))
+    scores = torch.zeros(B, 1)
+    history = torch.empty(B, 1, 0, dtype=torch.int64)
+    logits = gpu_pre.logits.cpu()[:, None]
+    for step, w in enumerate(widths):
+        if step:
+            logits = adapter.decode(history.to(device), gpu_pre.state).cpu()
+            assert_bf16_parity(logits, oracle.decode(history, state),
+                               adapter.truth.decode(history, t_state), f"level-{step} logits")
+        scores, parents, tokens = grbeam_ref.level_select(logits, scores, w)
+        history = torch.cat((history.gather(1, parents[..., None].expand(B, w, step)),
+                             tokens[..., None]), -1)
+    assert torch.equal(history, toks), "GPU search differs from its own teacher-forced replay"
+    assert torch.allclose(result.scores.cpu(), scores, atol=1e-4)
 
 
 def test_incremental_decode_equals_stateless_08b(device):
@@ -205,6 +239,11 @@ def test_incremental_decode_equals_stateless_08b(device):
     ids = torch.randint(0, cfg.vocab_size, (4, 64), generator=torch.Generator().manual_seed(5))
     res = adapter.prefill(ids.to(device))
     _incremental_matches_stateless(adapter, res.state, 4, [256, 256], cfg.vocab_size, device, 6)
+    # deeper suffixes (5..7 tokens), where the replay and the attention's
+    # suffix fold run their long-suffix instantiations in every layer
+    res2 = adapter.prefill(ids[:2].to(device))
+    _incremental_matches_stateless(adapter, res2.state, 2, [8, 8, 8, 8, 8, 8, 8],
+                                   cfg.vocab_size, device, 7)
 
 
 def test_search_with_and_without_incremental_decode(device, tiny):

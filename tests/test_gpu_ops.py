@@ -44,6 +44,10 @@ GDN_CASES = [
     (2, 20, 1, 4, 4, 128, 64),
     (2, 33, 4, 2, 2, 64, 128),
     (1, 1, 1, 1, 1, 64, 64),
+    (2, 40, 5, 16, 16, 128, 128),    # suffixes past 4 tokens: 5..8
+    (1, 17, 6, 2, 4, 64, 64),
+    (2, 24, 7, 4, 4, 128, 128),
+    (1, 130, 8, 2, 2, 128, 64),
 ]
 
 
@@ -62,7 +66,8 @@ def test_gdn_replay_bf16_matches_oracle(device, case):
     assert_close_rel(out.cpu(), expected, rtol=1e-2, atol_frac=2e-3, name=f"gdn {case}")
 
 
-@pytest.mark.parametrize("case", [(2, 7, 3, 2, 4, 64, 64), (1, 16, 4, 4, 4, 128, 128)])
+@pytest.mark.parametrize("case", [(2, 7, 3, 2, 4, 64, 64), (1, 16, 4, 4, 4, 128, 128),
+                                  (1, 9, 8, 2, 2, 128, 128)])
 def test_gdn_replay_fp32_matches_oracle(device, case):
     B, W, T, H, HV, K, V = case
     q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, dtype=torch.float32, seed=3)
@@ -135,9 +140,15 @@ def test_gdn_replay_closed_form_beta_zero(device):
     assert_close_rel(out.cpu(), expected.float(), rtol=1e-4, atol_frac=1e-4, name="beta=0")
 
 
-def test_gdn_rejects_long_suffix_on_replay_limits(device):
+def test_gdn_head_dims_outside_the_replay_and_the_limit(device):
+    """Head dims the replay does not take run the per-token recurrence kernel;
+    key dims past its 256 raise (KadLibraryError, a RuntimeError)."""
     q, k, v, g, beta, S = gdn_inputs(1, 2, 2, 1, 1, 96, 96)
-    with pytest.raises(RuntimeError):
+    out = ops.gated_delta(*_to(device, q, k, v, g, beta, S), beam_width=2)
+    expected = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=2)
+    assert_close_rel(out, expected, rtol=1e-2, atol_frac=4e-3, name="K=V=96")
+    q, k, v, g, beta, S = gdn_inputs(1, 2, 2, 1, 1, 320, 64)
+    with pytest.raises(RuntimeError, match="key dims <= 256"):
         ops.gated_delta(*_to(device, q, k, v, g, beta, S), beam_width=2)
 
 

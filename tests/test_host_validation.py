@@ -1,0 +1,65 @@
+"""Host-side argument checks that run before any kernel launch (CPU only)."""
+
+import pytest
+import torch
+
+from kadllm_amd import conditional_search, grbeam_search
+from kadllm_amd.grbeam import MAX_WIDTH, PrefillResult
+from kadllm_amd.qwen35 import reject_biases
+
+
+class _MetaAdapter:
+    """Returns logits on the meta device (no data, no kernels) and counts calls."""
+
+    def __init__(self, V=16):
+        self.V = V
+        self.prefills = 0
+
+    def prefill(self, ids):
+        self.prefills += 1
+        return PrefillResult(torch.empty(ids.shape[0], self.V, device="meta"), None)
+
+    def decode(self, history, state):
+        raise AssertionError("decode must not be reached")
+
+
+def test_width_above_limit_raises_before_prefill():
+    a = _MetaAdapter()
+    ids = torch.zeros(1, 3, dtype=torch.int64)
+    with pytest.raises(ValueError, match="not supported by the HIP selection"):
+        grbeam_search(a, ids, [4, MAX_WIDTH + 1])
+    with pytest.raises(ValueError, match="not supported by the HIP selection"):
+        conditional_search(a, ids, [4], [MAX_WIDTH + 1])
+    assert a.prefills == 0
+
+
+def test_constraint_mask_on_another_device_raises():
+    """A mask on another device than the logits would hand the kernel a
+    foreign pointer; it is refused before selection."""
+    a = _MetaAdapter()
+    ids = torch.zeros(2, 3, dtype=torch.int64)
+
+    def allowed(history, logits):
+        return torch.ones(logits.shape, dtype=torch.bool)  # CPU, logits are on meta
+
+    with pytest.raises(ValueError, match="logits' device"):
+        grbeam_search(a, ids, [2], allowed=allowed)
+    with pytest.raises(ValueError, match="logits' device"):
+        conditional_search(a, ids, [2], [2], allowed=allowed)
+
+
+def test_checkpoint_biases_are_refused():
+    sd = {"layers.0.self_attn.q_proj.weight": torch.zeros(1),
+          "layers.0.self_attn.q_proj.bias": torch.zeros(1)}
+    with pytest.raises(ValueError, match="no projection biases"):
+        reject_biases(object(), sd)
+    sd = {"layers.0.linear_attn.conv1d.bias": torch.zeros(1)}
+    with pytest.raises(ValueError, match="no projection biases"):
+        reject_biases(object(), sd)
+
+    class Cfg:
+        attention_bias = True
+
+    with pytest.raises(ValueError, match="attention_bias"):
+        reject_biases(Cfg(), {})
+    reject_biases(object(), {"layers.0.input_layernorm.weight": torch.zeros(1)})
