@@ -230,6 +230,20 @@ int kad_beam_row_select(const void* logits, int logits_dtype, int64_t ld, const 
 int kad_beam_merge_select(const float* cand_key, const int* cand_idx, int B, int ncand, int W,
                           int V, float* scores, int64_t* parents, int64_t* tokens, void* valid,
                           kad_stream_t stream);
+/* Allocation-free selection: kad_beam_row_select then kad_beam_merge_select
+ * (same arguments, same results bit for bit) with the candidates kept in a
+ * 32 MiB device array inside the library instead of caller workspace, so the
+ * call makes no hipMalloc and no other allocation.  No counterpart in the
+ * reference: it serves callers that cannot allocate (code under stream
+ * capture, tight serving loops).  Limit: B * Wp * min(W, V) <= 4,194,304
+ * candidates (e.g. 32 requests x 256 beams x 256), else KAD_ERR_UNSUPPORTED.
+ * Each GPU has one such array for the life of the process, shared by every
+ * call on it: calls that overlap on one GPU (different streams or host
+ * threads) race and must be serialised by the caller. */
+int kad_beam_select_noalloc(const void* logits, int logits_dtype, int64_t ld, const void* mask,
+                            int64_t ld_mask, const float* parent_scores, int B, int Wp, int V,
+                            int W, float* scores, int64_t* parents, int64_t* tokens, void* valid,
+                            kad_stream_t stream);
 int kad_beam_history(const int64_t* history, int Wp, int step, const int64_t* parents,
                      const int64_t* tokens, int64_t* out, int B, int W, kad_stream_t stream);
 /* Per-token rows cached for a level's beams follow the beams' parents into the

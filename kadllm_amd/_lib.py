@@ -42,6 +42,7 @@ SIGNATURES = {
                                       "s",
     "kad_attention_prefill": "plll" "pplll" "plll" "plll" "iiiii" "f" "s",
     "kad_beam_row_select": "pilplpiiiipps",
+    "kad_beam_select_noalloc": "pilplpiiiipppps",
     "kad_gdn_recurrent": "ppplli" "pipil" "pii" "plp" "iiiiiif" "s",
     "kad_attention_general": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiiiii" "f" "s",
     "kad_beam_merge_select": "ppiiiipppps",

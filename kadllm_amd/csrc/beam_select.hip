@@ -24,6 +24,11 @@
 
 #include "kad_common.h"
 
+#include <mutex>
+
+// Scratch of kad_beam_select_noalloc (32 MiB per GPU; see scratch_address).
+static __device__ __align__(256) uint8_t scratch[32ll << 20];
+
 namespace {
 
 constexpr int kRowThreads = 256;
@@ -898,6 +903,43 @@ int check_logits_dtype(int dtype) {
   return KAD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free selection (kad_beam_select_noalloc): the
+// per-row candidates (keys, then flat indices) live in this file-scope device
+// array, one copy per GPU for the life of the process.  Host code never uses
+// the array's name as an address: scratch_address() asks the runtime for the
+// current device's copy once and keeps it.
+constexpr int64_t kSelectScratchBytes = 32ll << 20;
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+static_assert(sizeof(scratch) == kSelectScratchBytes, "scratch size");
+
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    kad_set_error("hipGetDevice failed: %s", hipGetErrorString(e));
+    return KAD_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) KAD_UNSUPPORTED("device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      kad_set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      return KAD_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KAD_OK;
+}
+
 }  // namespace
 
 extern "C" int kad_beam_row_select(const void* logits, int logits_dtype, int64_t ld,
@@ -921,6 +963,40 @@ extern "C" int kad_beam_merge_select(const float* cand_key, const int* cand_idx,
   if (W > kMaxW) KAD_UNSUPPORTED("beam width %d exceeds %d", W, kMaxW);
   return launch_merge(cand_key, cand_idx, B, ncand, W, V, scores, parents, tokens, valid,
                       (hipStream_t)stream);
+}
+
+extern "C" int kad_beam_select_noalloc(const void* logits, int logits_dtype, int64_t ld,
+                                       const void* mask, int64_t ld_mask,
+                                       const float* parent_scores, int B, int Wp, int V, int W,
+                                       float* scores, int64_t* parents, int64_t* tokens,
+                                       void* valid, kad_stream_t stream) {
+  KAD_REQUIRE(logits && parent_scores && scores && parents && tokens && valid,
+              "null pointer argument");
+  KAD_REQUIRE(B > 0 && Wp > 0 && V > 0 && W > 0 && ld >= V, "bad dimensions");
+  KAD_REQUIRE((int64_t)Wp * V < 0x7fffffff, "Wp * V must fit in int32 flat indices");
+  KAD_REQUIRE((int64_t)W <= (int64_t)Wp * V, "beam width exceeds the number of candidate slots");
+  if (W > kMaxW) KAD_UNSUPPORTED("beam width %d exceeds %d", W, kMaxW);
+  if (const int rc = check_logits_dtype(logits_dtype)) return rc;
+  const int K = W < V ? W : V;
+  const int64_t rows = (int64_t)B * Wp;
+  const int64_t ncand = rows * K;
+  const int64_t key_bytes = (ncand * 4 + 255) / 256 * 256;
+  if (key_bytes + ncand * 4 > kSelectScratchBytes)
+    KAD_UNSUPPORTED("allocation-free selection holds at most %lld candidates "
+                    "(B * Wp * min(W, V) = %lld); use kad_beam_row_select + "
+                    "kad_beam_merge_select with caller workspace",
+                    (long long)(kSelectScratchBytes / 8), (long long)ncand);
+  KAD_REQUIRE(rows < 0x7fffffffLL, "too many beam rows");
+  void* base = nullptr;
+  if (const int rc = scratch_address(&base)) return rc;
+  float* cand_key = (float*)base;
+  int* cand_idx = (int*)((uint8_t*)base + key_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  // the row stage writes exactly K candidates per row, so nothing is cleared
+  if (const int rc = launch_row_select(logits, logits_dtype, ld, mask, ld_mask, parent_scores,
+                                       (int)rows, Wp, V, K, cand_key, cand_idx, s))
+    return rc;
+  return launch_merge(cand_key, cand_idx, B, Wp * K, W, V, scores, parents, tokens, valid, s);
 }
 
 extern "C" int kad_beam_history(const int64_t* history, int Wp, int step, const int64_t* parents,
