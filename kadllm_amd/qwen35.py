@@ -176,6 +176,10 @@ class Qwen35Runner:
                 self.layers.append(_AttnLayer(w_qkv=w_qkv, q_norm=get(a + "q_norm.weight"),
                                               k_norm=get(a + "k_norm.weight"),
                                               w_o=get(a + "o_proj.weight"), **common))
+        # optional observer: trace(phase, layer, x) after each layer with a copy
+        # of the residual stream rows (the last position only past a pruned
+        # last layer); phase is "prefill", "decode" or "step"
+        self.trace = None
         rot = int(cfg.head_dim * cfg.partial_rotary_factor)
         self.rot = rot
         self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=torch.float) / rot))
@@ -331,6 +335,8 @@ class Qwen35Runner:
                 self._mlp(lyr, x_last, B)
             else:
                 self._mlp(lyr, x, rows)
+            if self.trace is not None:
+                self.trace("prefill", li, (x_last if terminal else x).clone())
         hN = layers.rmsnorm(x_last, self.norm_w, cfg.rms_norm_eps)
         logits = layers.gemm(hN, self.lm_head)
         return logits, tuple(snap)
@@ -414,6 +420,8 @@ class Qwen35Runner:
                 self._mlp(lyr, x_last, BW)
             else:
                 self._mlp(lyr, x, R)
+            if self.trace is not None:
+                self.trace("decode", li, (x_last if terminal else x).clone())
         hN = layers.rmsnorm(x_last, self.norm_w, cfg.rms_norm_eps)
         logits = layers.gemm(hN, self.lm_head)
         return logits.view(B, W, -1)
@@ -508,6 +516,8 @@ class Qwen35Runner:
                             residual=x)
                 new_layers.append((k_all, v_all))
             self._mlp(lyr, x, BW)
+            if self.trace is not None:
+                self.trace("step", li, x.clone())
         hN = layers.rmsnorm(x, self.norm_w, cfg.rms_norm_eps)
         logits = layers.gemm(hN, self.lm_head)
         return logits.view(B, W, -1), DecodeCache(T, W, tuple(new_layers))

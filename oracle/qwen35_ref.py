@@ -151,52 +151,64 @@ class Qwen35Oracle:
         return q, k, v, gate.reshape(rows, length, -1)
 
     # -- full forward / prefill --------------------------------------------
+    def forward_layer(self, i, x, cos, sin):
+        """Layer i of the full causal forward on x [B,L,H]: (x after the layer,
+        its prefix snapshot (conv state, S) or (K, V))."""
+        cfg = self.cfg
+        B, L = x.shape[:2]
+        kind = cfg.layer_types[i]
+        n = rms_norm(x, self._p(f"layers.{i}.input_layernorm.weight"), cfg.rms_norm_eps)
+        if kind == "linear_attention":
+            qkv, z, beta, g = self._gdn_projections(i, n)
+            pre = qkv.transpose(1, 2)                                   # [B,C,L]
+            ks = cfg.linear_conv_kernel_dim
+            padded = F.pad(pre, (max(0, ks - L), 0)) if L < ks else pre
+            conv_state = padded[..., -ks:].clone()
+            wconv = self._p(f"layers.{i}.linear_attn.conv1d.weight")    # [C,1,ks]
+            y = F.conv1d(pre.to(wconv.dtype), wconv, None, padding=ks - 1,
+                         groups=pre.shape[1])[..., :L]
+            y = F.silu(y).to(pre.dtype).transpose(1, 2)
+            q, k, v = self._split_qkv(y, B, L)
+            rep = cfg.linear_num_value_heads // cfg.linear_num_key_heads
+            if rep > 1:
+                q = q.repeat_interleave(rep, dim=2)
+                k = k.repeat_interleave(rep, dim=2)
+            o, S = ops_ref.chunk_gated_delta(q, k, v, g, beta)
+            mixed = self._gdn_finish(i, o, z, B, L)
+            snap = (conv_state, S)
+        else:
+            q, k, v, gate = self._attn_projections(i, n, cos, sin)
+            vt = v.transpose(1, 2)                                      # [B,HK,L,D]
+            rep = cfg.num_attention_heads // cfg.num_key_value_heads
+            qf = q.float()
+            kf = k.float().repeat_interleave(rep, dim=1)
+            vf = vt.float().repeat_interleave(rep, dim=1)
+            s = qf @ kf.transpose(-1, -2) * (cfg.head_dim ** -0.5)
+            causal = torch.ones(L, L, dtype=torch.bool).tril()
+            s = s.masked_fill(~causal, -torch.inf)
+            a = (s.softmax(-1) @ vf).to(x.dtype)                        # [B,H,L,D]
+            a = a.transpose(1, 2).reshape(B, L, -1) * gate.sigmoid()
+            mixed = F.linear(a, self._p(f"layers.{i}.self_attn.o_proj.weight"))
+            snap = (k.transpose(1, 2), vt.transpose(1, 2))             # [B,L,HK,D] views
+        x = x + mixed
+        n2 = rms_norm(x, self._p(f"layers.{i}.post_attention_layernorm.weight"),
+                      cfg.rms_norm_eps)
+        return x + self._mlp(i, n2), snap
+
+    def prompt_rope(self, B, L, dtype):
+        pos = torch.arange(L)[None].expand(B, L)
+        return rope_cos_sin(self.cfg, pos, dtype)
+
     def forward(self, input_ids):
         """Full causal forward.  Returns (final-normed hidden [B,L,H], snapshot)."""
         cfg = self.cfg
         B, L = input_ids.shape
         x = F.embedding(input_ids, self._p("embed_tokens.weight"))
-        pos = torch.arange(L)[None].expand(B, L)
-        cos, sin = rope_cos_sin(cfg, pos, x.dtype)
+        cos, sin = self.prompt_rope(B, L, x.dtype)
         snap = []
-        for i, kind in enumerate(cfg.layer_types):
-            n = rms_norm(x, self._p(f"layers.{i}.input_layernorm.weight"), cfg.rms_norm_eps)
-            if kind == "linear_attention":
-                qkv, z, beta, g = self._gdn_projections(i, n)
-                pre = qkv.transpose(1, 2)                                   # [B,C,L]
-                ks = cfg.linear_conv_kernel_dim
-                padded = F.pad(pre, (max(0, ks - L), 0)) if L < ks else pre
-                conv_state = padded[..., -ks:].clone()
-                wconv = self._p(f"layers.{i}.linear_attn.conv1d.weight")    # [C,1,ks]
-                y = F.conv1d(pre.to(wconv.dtype), wconv, None, padding=ks - 1,
-                             groups=pre.shape[1])[..., :L]
-                y = F.silu(y).to(pre.dtype).transpose(1, 2)
-                q, k, v = self._split_qkv(y, B, L)
-                rep = cfg.linear_num_value_heads // cfg.linear_num_key_heads
-                if rep > 1:
-                    q = q.repeat_interleave(rep, dim=2)
-                    k = k.repeat_interleave(rep, dim=2)
-                o, S = ops_ref.chunk_gated_delta(q, k, v, g, beta)
-                mixed = self._gdn_finish(i, o, z, B, L)
-                snap.append((conv_state, S))
-            else:
-                q, k, v, gate = self._attn_projections(i, n, cos, sin)
-                vt = v.transpose(1, 2)                                      # [B,HK,L,D]
-                rep = cfg.num_attention_heads // cfg.num_key_value_heads
-                qf = q.float()
-                kf = k.float().repeat_interleave(rep, dim=1)
-                vf = vt.float().repeat_interleave(rep, dim=1)
-                s = qf @ kf.transpose(-1, -2) * (cfg.head_dim ** -0.5)
-                causal = torch.ones(L, L, dtype=torch.bool).tril()
-                s = s.masked_fill(~causal, -torch.inf)
-                a = (s.softmax(-1) @ vf).to(x.dtype)                        # [B,H,L,D]
-                a = a.transpose(1, 2).reshape(B, L, -1) * gate.sigmoid()
-                mixed = F.linear(a, self._p(f"layers.{i}.self_attn.o_proj.weight"))
-                snap.append((k.transpose(1, 2), vt.transpose(1, 2)))       # [B,L,HK,D] views
-            x = x + mixed
-            n2 = rms_norm(x, self._p(f"layers.{i}.post_attention_layernorm.weight"),
-                          cfg.rms_norm_eps)
-            x = x + self._mlp(i, n2)
+        for i in range(len(cfg.layer_types)):
+            x, s = self.forward_layer(i, x, cos, sin)
+            snap.append(s)
         x = rms_norm(x, self._p("norm.weight"), cfg.rms_norm_eps)
         return x, tuple(snap)
 
@@ -212,34 +224,48 @@ class Qwen35Oracle:
         return logits, OraclePrefix(input_ids.shape[1], input_ids.shape[0], snap)
 
     # -- suffix replay ------------------------------------------------------
+    def suffix_rope(self, rows, length, T, dtype):
+        pos = torch.arange(length, length + T)[None].expand(rows, T)
+        return rope_cos_sin(self.cfg, pos, dtype)
+
+    def decode_layer(self, i, x, cached, W, cos, sin):
+        """Layer i of the suffix replay on x [B*W,T,H] against the prefix entry
+        ``cached`` of that layer; returns x after the layer."""
+        cfg = self.cfg
+        rows, T = x.shape[:2]
+        kind = cfg.layer_types[i]
+        n = rms_norm(x, self._p(f"layers.{i}.input_layernorm.weight"), cfg.rms_norm_eps)
+        if kind == "linear_attention":
+            qkv, z, beta, g = self._gdn_projections(i, n)
+            wconv = self._p(f"layers.{i}.linear_attn.conv1d.weight").squeeze(1)
+            mixed = ops_ref.causal_conv1d(qkv.transpose(1, 2), cached[0], wconv,
+                                          beam_width=W).transpose(1, 2)
+            q, k, v = self._split_qkv(mixed, rows, T)
+            o = ops_ref.gated_delta(q, k, v, g, beta, cached[1], beam_width=W)
+            mixed = self._gdn_finish(i, o, z, rows, T)
+        else:
+            q, k, v, gate = self._attn_projections(i, n, cos, sin)
+            o = ops_ref.prefix_attention(q.transpose(1, 2), cached[0], cached[1],
+                                         k.transpose(1, 2), v, beam_width=W,
+                                         scale=cfg.head_dim ** -0.5)
+            o = o.reshape(rows, T, -1) * gate.sigmoid()
+            mixed = F.linear(o, self._p(f"layers.{i}.self_attn.o_proj.weight"))
+        x = x + mixed
+        n2 = rms_norm(x, self._p(f"layers.{i}.post_attention_layernorm.weight"),
+                      cfg.rms_norm_eps)
+        return x + self._mlp(i, n2)
+
+    def head(self, h):
+        """Final RMSNorm and LM head of hidden rows [..., H]."""
+        h = rms_norm(h, self._p("norm.weight"), self.cfg.rms_norm_eps)
+        return F.linear(h, self.lm_head_weight())
+
     def decode(self, history, state):
         """Reference decode (qwen3_5.py:204-235): replay [B,W,T] suffixes -> [B,W,V]."""
-        cfg = self.cfg
         B, W, T = history.shape
         rows = B * W
         x = F.embedding(history.reshape(rows, T), self._p("embed_tokens.weight"))
-        pos = torch.arange(state.length, state.length + T)[None].expand(rows, T)
-        cos, sin = rope_cos_sin(cfg, pos, x.dtype)
-        for i, (kind, cached) in enumerate(zip(cfg.layer_types, state.layers)):
-            n = rms_norm(x, self._p(f"layers.{i}.input_layernorm.weight"), cfg.rms_norm_eps)
-            if kind == "linear_attention":
-                qkv, z, beta, g = self._gdn_projections(i, n)
-                wconv = self._p(f"layers.{i}.linear_attn.conv1d.weight").squeeze(1)
-                mixed = ops_ref.causal_conv1d(qkv.transpose(1, 2), cached[0], wconv,
-                                              beam_width=W).transpose(1, 2)
-                q, k, v = self._split_qkv(mixed, rows, T)
-                o = ops_ref.gated_delta(q, k, v, g, beta, cached[1], beam_width=W)
-                mixed = self._gdn_finish(i, o, z, rows, T)
-            else:
-                q, k, v, gate = self._attn_projections(i, n, cos, sin)
-                o = ops_ref.prefix_attention(q.transpose(1, 2), cached[0], cached[1],
-                                             k.transpose(1, 2), v, beam_width=W,
-                                             scale=cfg.head_dim ** -0.5)
-                o = o.reshape(rows, T, -1) * gate.sigmoid()
-                mixed = F.linear(o, self._p(f"layers.{i}.self_attn.o_proj.weight"))
-            x = x + mixed
-            n2 = rms_norm(x, self._p(f"layers.{i}.post_attention_layernorm.weight"),
-                          cfg.rms_norm_eps)
-            x = x + self._mlp(i, n2)
-        h = rms_norm(x[:, -1], self._p("norm.weight"), cfg.rms_norm_eps)
-        return F.linear(h, self.lm_head_weight()).reshape(B, W, -1)
+        cos, sin = self.suffix_rope(rows, state.length, T, x.dtype)
+        for i, cached in enumerate(state.layers):
+            x = self.decode_layer(i, x, cached, W, cos, sin)
+        return self.head(x[:, -1]).reshape(B, W, -1)
