@@ -327,6 +327,43 @@ int kad_attention_general(
     kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
+ * fp32 models.  The reference adapter runs any float model (src/kadllm/
+ * adapters/qwen3_5.py:40-104 wraps the transformers model in its own dtype)
+ * and states its fixed-history accuracy for fp32 runs (README.md:152).  These
+ * are the projections and row-wise ops of kad_gemm_bf16 / kad_rmsnorm ...
+ * in fp32 with no intermediate rounding (same argument meaning, fp32
+ * tensors); attention and gated delta of an fp32 model use the general-shape
+ * kernels above, the conv kad_causal_conv_suffix.
+ *
+ * kad_gemm_f32           C = A W^T (v_mfma_f32_16x16x4_f32), epilogues as
+ *                        kad_gemm_bf16 (SwiGLU: silu(g) u of interleaved
+ *                        [gate 32 | up 32] W rows, N % 64 == 0)
+ * kad_rmsnorm_f32        y = x rsqrt(mean x^2 + eps) (w_offset + w)
+ * kad_rmsnorm_gated_f32  y = w (x rsqrt(mean x^2 + eps)) silu(z) per head
+ * kad_gdn_gates_f32      g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
+ * kad_qk_norm_rope_f32   kad_qk_norm_rope with fp32 cos/sin and no rounding
+ * kad_embedding_f32      out[r] = table[ids[r]]
+ */
+int kad_gemm_f32(const float* A, int64_t lda, const float* W, int64_t ldw, float* C, int64_t ldc,
+                 const float* R, int64_t ldr, int M, int N, int K, int epilogue,
+                 kad_stream_t stream);
+int kad_rmsnorm_f32(const float* x, int64_t ldx, const float* w, float w_offset, float* y,
+                    int64_t ldy, int64_t rows, int D, float eps, kad_stream_t stream);
+int kad_rmsnorm_gated_f32(const float* x, int64_t ldx, const float* z, int64_t ldz,
+                          const float* w, float* y, int64_t ldy, int64_t rows, int heads, int D,
+                          float eps, kad_stream_t stream);
+int kad_gdn_gates_f32(const float* a, int64_t lda, const float* b, int64_t ldb,
+                      const float* A_log, const float* dt_bias, float* g, float* beta,
+                      int64_t rows, int HV, kad_stream_t stream);
+int kad_qk_norm_rope_f32(const float* src, int64_t ld_src, int64_t src_head_stride, int heads,
+                         const float* w, float* dst, int64_t period, int64_t s_b, int64_t s_t,
+                         int64_t s_h, int64_t rows, int D, int rot, const float* inv_freq,
+                         int64_t pos0, int64_t pos_period, float eps, int do_norm,
+                         kad_stream_t stream);
+int kad_embedding_f32(const int64_t* ids, const float* table, float* out, int64_t rows, int D,
+                      int64_t vocab, kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
  * MFMA lane-layout self-test (no reference counterpart): C[16x16] = A[16x32]
  * B[32x16] (bf16 in, fp32 out, all row-major) computed by one wave with the
  * operand layout the kernels above assume for v_mfma_f32_16x16x32_bf16, and
@@ -334,6 +371,8 @@ int kad_attention_general(
  */
 int kad_selftest_mfma16(const void* a, const void* b, float* c, kad_stream_t stream);
 int kad_selftest_mfma32(const void* a, const void* b, float* c, kad_stream_t stream);
+/* the same for v_mfma_f32_16x16x4_f32 (fp32 A 16x4, B 4x16, C 16x16) */
+int kad_selftest_mfma_f32(const float* a, const float* b, float* c, kad_stream_t stream);
 
 #ifdef __cplusplus
 }

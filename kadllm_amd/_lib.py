@@ -51,6 +51,13 @@ SIGNATURES = {
     "kad_gdn_chunk_workspace_bytes": "iiiip",
     "kad_gdn_chunk": "ppplli" "pipil" "pii" "plp" "pl" "iiiiii" "fi" "s",
     "kad_causal_conv_prefill": "plpplpiiiis",
+    "kad_gemm_f32": "plplplpl" "iiii" "s",
+    "kad_rmsnorm_f32": "plpfpllifs",
+    "kad_rmsnorm_gated_f32": "plplpplliifs",
+    "kad_gdn_gates_f32": "plplpppplis",
+    "kad_qk_norm_rope_f32": "plli" "pp" "lllll" "ii" "p" "ll" "f" "i" "s",
+    "kad_embedding_f32": "ppplils",
+    "kad_selftest_mfma_f32": "ppps",
     "kad_selftest_mfma16": "ppps",
     "kad_selftest_mfma32": "ppps",
 }

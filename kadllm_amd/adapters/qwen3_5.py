@@ -11,7 +11,9 @@ construction, into fused bf16 device buffers, and both prefill and decode run
 the native HIP kernels (kadllm_amd.qwen35.Qwen35Runner).  The backend
 arguments keep their reference names and validation; every accepted value
 runs the single HIP implementation.  The prefix is request-sized and is never
-written by decode.  Models must be bf16 and on one ROCm device.
+written by decode.  Models must be on one ROCm device, in bf16 (the packed
+bf16 kernels, with the transformers bf16 rounding points) or fp32 (fp32
+kernels throughout, kadllm_amd.qwen35_f32).
 """
 
 from dataclasses import dataclass
@@ -22,6 +24,7 @@ from ..config import Qwen35Config
 from ..grbeam import PrefillResult
 from ..ops import _gdn_launch
 from ..qwen35 import LMHead, Qwen35Runner, Qwen35TextModel
+from ..qwen35_f32 import Qwen35RunnerF32
 
 
 @dataclass(frozen=True)
@@ -77,8 +80,12 @@ class Qwen35GRBeamAdapter:
         if gdn_triton_config is not None and gdn_backend != "triton":
             raise ValueError("gdn_triton_config requires gdn_backend='triton'")
         dtypes = {p.dtype for module in (text_model, lm_head) for p in module.parameters()}
-        if dtypes != {torch.bfloat16}:
-            raise TypeError("the HIP GRBeam path runs bf16 models; convert with .to(torch.bfloat16)")
+        if dtypes == {torch.bfloat16}:
+            runner = Qwen35Runner
+        elif dtypes == {torch.float32}:
+            runner = Qwen35RunnerF32
+        else:
+            raise TypeError("the HIP GRBeam path runs bf16 or fp32 models; convert with .to()")
         if device.type != "cuda":
             raise RuntimeError("the HIP GRBeam path needs the model on a ROCm device")
         self.layer_types = tuple(cfg.layer_types)
@@ -88,9 +95,12 @@ class Qwen35GRBeamAdapter:
         self.gdn_triton_config = gdn_triton_config
         self.config = cfg if native else Qwen35Config.from_hf(cfg)
         self.device = device
-        self._runner = Qwen35Runner(self.config, text_model.state_dict(),
-                                    lm_head_weight=lm_head.weight, device=device,
-                                    head_tokens=head_tokens)
+        self._runner = runner(self.config, text_model.state_dict(),
+                              lm_head_weight=lm_head.weight, device=device,
+                              head_tokens=head_tokens)
+        if runner is Qwen35RunnerF32:
+            # fp32 models replay the whole suffix at every level, as the reference does
+            self.decode_incremental = None
         # logits column -> token id for a SID-only head (None: the full vocabulary)
         self.vocab_ids = self._runner.head_ids
         self._owner = object()
@@ -136,12 +146,13 @@ class Qwen35GRBeamAdapter:
         from ..formats import prefix_layers_from_cache
 
         layers = []
+        act = self._runner.dtype
         for kind, (a, b) in zip(self.layer_types,
                                 prefix_layers_from_cache(cache, self.layer_types)):
             if kind == "linear_attention":
-                layers.append((a.to(self.device, torch.bfloat16), b.to(self.device, torch.float32)))
+                layers.append((a.to(self.device, act), b.to(self.device, torch.float32)))
             else:
-                layers.append((a.to(self.device, torch.bfloat16), b.to(self.device, torch.bfloat16)))
+                layers.append((a.to(self.device, act), b.to(self.device, act)))
         batch = layers[0][0].shape[0]
         return Qwen35Prefix(int(length), batch, self._owner, tuple(layers))
 

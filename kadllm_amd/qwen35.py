@@ -111,6 +111,8 @@ class Qwen35Runner:
     head_tokens[c], and the softmax of a search runs over that sub-vocabulary.
     """
 
+    dtype = torch.bfloat16
+
     def __init__(self, cfg, state_dict, lm_head_weight=None, device=None, head_tokens=None):
         self.cfg = cfg
         self.device = torch.device(device) if device is not None else \

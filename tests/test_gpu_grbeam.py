@@ -156,7 +156,8 @@ def test_conv_prefill_and_state(device, L):
     xd = x.to(device).reshape(B * L, C)
     out = torch.empty(B * L, C, dtype=torch.bfloat16, device=device)
     st = torch.empty(B, C, 4, dtype=torch.bfloat16, device=device)
-    _lib.call("kad_causal_conv_prefill", _lib.ptr(xd), C, _lib.ptr(w.to(device)), _lib.ptr(out), C,
+    wd = w.to(device)   # held until the kernel has read it
+    _lib.call("kad_causal_conv_prefill", _lib.ptr(xd), C, _lib.ptr(wd), _lib.ptr(out), C,
               _lib.ptr(st), B, L, C, 1, _lib.stream_of(xd))
     torch.cuda.synchronize()
     pre = x.transpose(1, 2)
