@@ -86,7 +86,12 @@ def build_hf_text_model(cfg, state_dict):
         model = Qwen3_5TextModel(hf_cfg)
     finally:
         torch.set_default_dtype(torch_default)
+    # as from_pretrained(dtype=...) leaves it: parameters in `dtype`, the
+    # rotary inverse frequencies (a non-persistent buffer) in fp32
+    inv, inv0 = model.rotary_emb.inv_freq.clone(), model.rotary_emb.original_inv_freq.clone()
     model = model.to(dtype=dtype, device=device)
+    model.rotary_emb.inv_freq = inv.to(device)
+    model.rotary_emb.original_inv_freq = inv0.to(device)
     missing, unexpected = model.load_state_dict(
         {k: v for k, v in state_dict.items() if k != "lm_head.weight"}, strict=False)
     missing = [m for m in missing if "rotary_emb" not in m]

@@ -8,7 +8,11 @@ layer pre-norm residual blocks (Gated DeltaNet :432-543 or gated attention
 prompt token.  The prefix snapshot matches qwen3_5.py:113-129: per GDN layer
 (conv state = last kernel-size pre-conv inputs [B,C,4], recurrent state
 fp32 [B,HV,K,V]); per attention layer (K post-norm post-RoPE, V), exposed as
-[B,L,HK,D] views of [B,HK,L,D] storage.
+[B,L,HK,D] views of [B,HK,L,D] storage.  The prompt's attention is the
+causal SDPA call the transformers forward makes with
+attn_implementation="sdpa" (the reference's runner, benchmarks/grbeam.py:213).
+Pinned bit for bit in bf16 and to 1e-5 in fp32 against the reference's own
+search outputs (tests/golden/grbeam_tiny_*.npz).
 
 Decode follows Qwen35GRBeamAdapter.decode/_linear/_attention
 (src/kadllm/adapters/qwen3_5.py:144-235) with the oracle operators of
@@ -180,13 +184,13 @@ class Qwen35Oracle:
             q, k, v, gate = self._attn_projections(i, n, cos, sin)
             vt = v.transpose(1, 2)                                      # [B,HK,L,D]
             rep = cfg.num_attention_heads // cfg.num_key_value_heads
-            qf = q.float()
-            kf = k.float().repeat_interleave(rep, dim=1)
-            vf = vt.float().repeat_interleave(rep, dim=1)
-            s = qf @ kf.transpose(-1, -2) * (cfg.head_dim ** -0.5)
-            causal = torch.ones(L, L, dtype=torch.bool).tril()
-            s = s.masked_fill(~causal, -torch.inf)
-            a = (s.softmax(-1) @ vf).to(x.dtype)                        # [B,H,L,D]
+            # the causal SDPA call of the transformers forward the reference
+            # runs (attn_implementation="sdpa", benchmarks/grbeam.py:213;
+            # HF-q35 682-695), in the model dtype: its internal rounding is
+            # part of the reference's bf16 prefill
+            a = F.scaled_dot_product_attention(q, k.repeat_interleave(rep, dim=1),
+                                               vt.repeat_interleave(rep, dim=1), is_causal=True,
+                                               scale=cfg.head_dim ** -0.5)   # [B,H,L,D]
             a = a.transpose(1, 2).reshape(B, L, -1) * gate.sigmoid()
             mixed = F.linear(a, self._p(f"layers.{i}.self_attn.o_proj.weight"))
             snap = (k.transpose(1, 2), vt.transpose(1, 2))             # [B,L,HK,D] views

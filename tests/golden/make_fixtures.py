@@ -16,6 +16,10 @@ grbeam_tiny_fp32.npz
     [8, 8, 8].  Stores the prompt, prefill logits, every decode call's
     history and logits, the prefix tensors, final tokens and scores.
 
+grbeam_tiny_bf16.npz
+    The same run with the model in bf16 (bf16 arrays as uint16 bits): the
+    reference's bf16 rounding, in its transformers prefill and its own decode.
+
 reference_lm_fp32.npz
     The reference's own toy adapter ``ReferenceHybridLM`` (torch backends,
     fp32): for each case, the state dict after ``torch.manual_seed(seed)``
@@ -49,7 +53,11 @@ def _bits(t):
     return t.detach().contiguous().numpy()
 
 
-def make_grbeam_tiny():
+def make_grbeam_tiny_bf16():
+    make_grbeam_tiny(torch.bfloat16, "grbeam_tiny_bf16.npz")
+
+
+def make_grbeam_tiny(dtype=torch.float32, name="grbeam_tiny_fp32.npz"):
     from kadllm import grbeam_search
     from kadllm.adapters import Qwen35GRBeamAdapter
 
@@ -57,7 +65,7 @@ def make_grbeam_tiny():
     from kadllm_amd.weights import build_hf_text_model, random_state_dict
 
     cfg = tiny_hybrid_config()
-    sd = random_state_dict(cfg, seed=0, dtype=torch.float32)
+    sd = random_state_dict(cfg, seed=0, dtype=dtype)
     model, head = build_hf_text_model(cfg, sd)
     adapter = Qwen35GRBeamAdapter(model, head)
     gen = torch.Generator().manual_seed(0)
@@ -97,8 +105,8 @@ def make_grbeam_tiny():
     for i, (a, b) in enumerate(captured["state"].layers):
         arrays[f"prefix{i}_a"] = _bits(a)
         arrays[f"prefix{i}_b"] = _bits(b)
-    np.savez_compressed(os.path.join(HERE, "grbeam_tiny_fp32.npz"), **arrays)
-    print("grbeam_tiny_fp32: tokens", result.tokens.tolist())
+    np.savez_compressed(os.path.join(HERE, name), **arrays)
+    print(name, "tokens", result.tokens.tolist())
 
 
 def make_reference_lm():
@@ -195,7 +203,7 @@ def make_ops_bf16():
 if __name__ == "__main__":
     sys.path.insert(0, REFERENCE_SRC)
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["grbeam_tiny", "ops_bf16", "reference_lm"]
+    which = sys.argv[1:] or ["grbeam_tiny", "grbeam_tiny_bf16", "ops_bf16", "reference_lm"]
     with torch.no_grad():
         for name in which:
             globals()["make_" + name]()

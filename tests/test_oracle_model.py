@@ -82,6 +82,40 @@ def test_oracle_decode_equals_full_forward(dtype):
                 assert err <= tol * full.abs().max().item(), (b, w, err)
 
 
+def test_oracle_bf16_is_bit_exact_to_reference_bf16_run():
+    """The reference's grbeam_search + Qwen35GRBeamAdapter on the tiny model in
+    bf16 (tests/golden/grbeam_tiny_bf16.npz: the transformers bf16 prefill
+    loaded as from_pretrained(dtype=bf16) leaves it, and the reference's own
+    bf16 decode): prefill logits, every prefix tensor, both decode levels'
+    logits, tokens and scores, bit for bit.  This pins the oracle's bf16
+    rounding points (RMSNorm cast, RMSNormGated order, RoPE cos/sin cast,
+    the conv's rounding before SiLU, the fp32 state, SDPA) at model level."""
+    from _fixtures import bf16_from_bits
+    f = load_npz("grbeam_tiny_bf16.npz")
+    cfg = tiny_hybrid_config()
+    orc = Qwen35Oracle(cfg, random_state_dict(cfg, seed=0, dtype=torch.bfloat16))
+
+    def t(name):
+        a = f[name]
+        return bf16_from_bits(a) if a.dtype == np.uint16 else torch.from_numpy(a)
+
+    ids = t("input_ids")
+    with torch.no_grad():
+        logits, state = orc.prefill(ids)
+        assert torch.equal(logits, t("prefill_logits"))
+        for i, (a, b) in enumerate(state.layers):
+            assert torch.equal(a, t(f"prefix{i}_a")), f"prefix {i} a"
+            assert torch.equal(b, t(f"prefix{i}_b")), f"prefix {i} b"
+        for step in (1, 2):
+            assert torch.equal(orc.decode(t(f"decode{step}_history"), state),
+                               t(f"decode{step}_logits")), f"decode {step}"
+        tokens, scores, valid, _ = grbeam_ref.grbeam_search(_OracleAdapter(orc), ids,
+                                                            [int(w) for w in f["widths"]])
+    assert torch.equal(tokens, t("tokens"))
+    assert torch.equal(scores, t("scores"))
+    assert torch.equal(valid, t("valid"))
+
+
 def test_oracle_reproduces_reference_search():
     """Tokens, scores, prefill/decode logits and prefix tensors of the reference
     search on the tiny fp32 model (config 1 of the workload family)."""
