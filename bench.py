@@ -1,26 +1,44 @@
-"""GRBeam end-to-end benchmark on one MI355X.
+"""GRBeam benchmarks on one MI355X.
 
-Workload (the reference's headline configuration): a Qwen3.5-0.8B-shaped
-hybrid model (24 layers [3x Gated DeltaNet, 1x gated attention] x 6, hidden
-1024, vocabulary 248320, tied embeddings) with random bf16 weights, batch 32,
-prompts of 1024 uniform-random token ids, beam 256, 3 output tokens over the
-full vocabulary.  One step is one ``grbeam_search`` call on the batch with the
-reference's timing protocol (src/kadllm benchmarks/grbeam.py:266-330): output
-token 1 from prefill, two decode calls, selection, synchronisation and the
-copy of the tokens to the host are all inside the timed region; every step's
-output is validated to hold 256 distinct fixed-depth sequences per request.
+Default workload (the reference's headline configuration): a
+Qwen3.5-0.8B-shaped hybrid model (24 layers [3x Gated DeltaNet, 1x gated
+attention] x 6, hidden 1024, vocabulary 248320, tied embeddings) with random
+bf16 weights, batch 32, prompts of 1024 uniform-random token ids, beam 256,
+3 output tokens over the full vocabulary.  One step is one ``grbeam_search``
+call on the batch with the reference's timing protocol (src/kadllm
+benchmarks/grbeam.py:266-330): output token 1 from prefill, two decode calls,
+selection, synchronisation and the copy of the tokens to the host are all
+inside the timed region; every step's output is validated to hold 256
+distinct fixed-depth sequences per request.
 
 Printed: one JSON line with requests/s (= batch * steps / elapsed), the
-roofline of the dominant kernel (the bf16 MFMA GEMM: algorithmic flops of all
-GEMM launches in the timed steps divided by their summed durations from HIP
-events recorded on the launch stream) and the CPU baseline (the oracle
-restatement of the reference torch path on this host, one request).
+roofline of the dominant kernel (the bf16 MFMA GEMM), a per-kernel table
+("kernels": launches, time, achieved GB/s or TFLOP/s and roofline fraction
+per kernel class, from HIP events around every launch in extra untimed
+steps), per-step host / enqueue / device times, memory peaks, and the CPU
+baseline (the oracle restatement of the reference torch path on this host's
+cores, one request, timed twice).
+
+Other modes:
+  --protocol reference   3 processes x (3 warmups + 5 timed calls), latency
+                         mean with a 95% CI over process means and the sampled
+                         device-memory peak (README.md:116,119)
+  --workload ops_gdn     isolated GDN suffix replay and conv4 (configuration 2)
+  --workload ops_attention  isolated prefix-shared attention, T = 1, 2, 3
+                         (configuration 3)
+  --workload conditional_sid  two-level SID search (configuration 5)
+  --depth 7 --batch 4    the reference's 7-token runs (README.md:125)
 """
 
 import argparse
 import json
+import math
 import os
+import platform
+import statistics
+import subprocess
 import sys
+import threading
 import time
 
 import torch
@@ -31,6 +49,14 @@ sys.path.insert(0, ROOT)
 METRIC = "requests/s at B32/prefix1024/beam256/3 tok; per-kernel HBM GB/s & MFMA util"
 H800_REQ_S = 36.08          # reference README, 1x H800, same workload
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+T975 = {1: 12.706, 2: 4.303, 3: 3.182, 4: 2.776, 5: 2.571, 6: 2.447, 7: 2.365, 9: 2.262}
+
+# HBM bytes per GEMM launch of the default workload: rocprofv3 FETCH_SIZE and
+# WRITE_SIZE over the GEMM dispatches of one search, each scaled by its reading
+# for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the launch
+# count.  Re-measured with the command in profiles/gemm_hbm_traffic_b32_p1024_w256.md.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 386.2e6
 
 
 def validate_output(tokens, batch, width, depth):
@@ -43,50 +69,173 @@ def validate_output(tokens, batch, width, depth):
         raise ValueError("search did not return the requested distinct fixed-depth beams")
 
 
-class GemmTimer:
-    """Records a HIP event pair around every GEMM launch (torch's current stream,
-    the stream the GEMM is launched on).  The events are created before the
-    timed region (`reserve`), so that the timed loop only records them."""
+# ---------------------------------------------------------------------------
+# per-kernel accounting: algorithmic HBM bytes and flops of each C-ABI call,
+# from its arguments (each input and output counted once)
+
+def _es(code):
+    return 4 if code == 2 else 2
+
+
+def kernel_work(name, a):
+    """(kernel class, bound, algorithmic bytes, algorithmic flops) of one call."""
+    if name == "kad_gemm_bf16":
+        M, N, K, epi = a[8], a[9], a[10], a[11]
+        n_out = N // 2 if epi == 2 else N
+        return "gemm", "mfma", 2 * (M * K + N * K + M * n_out + (M * n_out if a[6] else 0)), \
+            2 * M * N * K
+    if name in ("kad_gdn_suffix_replay", "kad_gdn_recurrent"):
+        if name == "kad_gdn_suffix_replay":
+            B, W, T, H, HV, K, V = a[15:22]
+            BW, sdt = B * W, a[12]
+        else:
+            BW, T, H, HV, K, V = a[17:23]
+            B, sdt = BW // max(a[13], 1), a[12]
+        es = _es(a[5])
+        nbytes = BW * T * (2 * H * K + 2 * HV * V) * es + B * HV * K * V * _es(sdt) \
+            + BW * T * HV * 6
+        label = "gdn_replay" if name == "kad_gdn_suffix_replay" else "gdn_recurrent"
+        return label, "hbm", nbytes, BW * HV * 2 * T * 2 * K * V
+    if name == "kad_causal_conv_suffix":
+        B, W, C, T, dt = a[16], a[17], a[18], a[19], a[20]
+        return "conv_suffix", "hbm", (2 * B * W * C * T + B * C * 3 + C * 4) * _es(dt), \
+            8 * B * W * C * T
+    if name in ("kad_prefix_attention_decode_ex", "kad_prefix_attention_decode"):
+        if name.endswith("_ex"):
+            B, W, Tq, Tk, H, HK, L, D = a[26:34]
+        else:
+            B, W, Tq, H, HK, L, D = a[26:33]
+            Tk = Tq
+        rows = B * W * Tq * H
+        nbytes = 2 * (3 * rows * D + 2 * B * L * HK * D + 2 * B * W * Tk * HK * D)
+        return "attention_decode", "mfma", nbytes, 4 * rows * (L + Tk) * D
+    if name == "kad_attention_prefill":
+        B, L, H, HK, D = a[17:22]
+        return "attention_prefill", "mfma", 2 * (3 * B * L * H * D + 2 * B * L * HK * D), \
+            4 * B * H * D * L * (L + 1) // 2
+    if name == "kad_gdn_chunk":
+        N, T, H, HV, K, V = a[19:25]
+        return "gdn_chunk", "hbm", N * T * (2 * H * K + 2 * HV * V) * 2 + N * HV * K * V * 4, \
+            None
+    if name == "kad_causal_conv_prefill":
+        B, L, C = a[6], a[7], a[8]
+        return "conv_prefill", "hbm", 2 * B * L * C * 2 + B * C * 4 * 2 + C * 8, None
+    if name == "kad_beam_row_select":
+        rows, V, K = a[6], a[8], a[9]
+        return "row_select", "hbm", rows * V * _es(a[1]) + rows * K * 8, None
+    if name == "kad_beam_merge_select":
+        return "merge_select", "hbm", a[2] * a[3] * 8, None
+    if name == "kad_gather_beam_rows":
+        return "gather_rows", "hbm", 2 * a[9] * a[10] * a[6] * a[7], None
+    if name == "kad_rmsnorm":
+        return "rowwise", "hbm", 4 * a[6] * a[7], None
+    if name == "kad_rmsnorm_gated":
+        return "rowwise", "hbm", 6 * a[7] * a[8] * a[9], None
+    if name in ("kad_qk_norm_rope", "kad_scatter_heads"):
+        rows, heads, D = (a[10], a[3], a[11]) if name == "kad_qk_norm_rope" else (a[9], a[2], a[3])
+        return "rowwise", "hbm", 4 * rows * heads * D, None
+    if name == "kad_embedding":
+        return "rowwise", "hbm", 4 * a[3] * a[4], None
+    if name == "kad_gdn_gates":
+        return "rowwise", "hbm", 10 * a[8] * a[9], None
+    return "other", "hbm", None, None
+
+
+class KernelProfiler:
+    """C-ABI call hook: a HIP event pair around every launch, on the stream the
+    launch goes to (torch's current stream), grouped by kernel class."""
 
     def __init__(self):
-        self.events = []
-        self.pool = []
+        self.records = []
 
-    def reserve(self, n):
-        self.pool.extend(torch.cuda.Event(enable_timing=True) for _ in range(2 * n))
-
-    def __call__(self, launch, flops, nbytes):
-        if len(self.pool) >= 2:
-            e1, e0 = self.pool.pop(), self.pool.pop()
-        else:
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
+    def __call__(self, name, args, launch):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         launch()
         e1.record()
-        self.events.append((e0, e1, flops, nbytes))
+        self.records.append((kernel_work(name, args), e0, e1))
 
-    def summary(self):
+    def table(self, steps):
         torch.cuda.synchronize()
-        ms = sum(e0.elapsed_time(e1) for e0, e1, _, _ in self.events)
-        flops = sum(f for _, _, f, _ in self.events)
-        nbytes = sum(b for _, _, _, b in self.events)
-        return ms, flops, nbytes, len(self.events)
+        agg = {}
+        for (label, bound, nbytes, flops), e0, e1 in self.records:
+            r = agg.setdefault(label, dict(bound=bound, launches=0, ms=0.0, bytes=0, flops=0,
+                                           have_bytes=True, have_flops=True))
+            r["launches"] += 1
+            r["ms"] += e0.elapsed_time(e1)
+            r["have_bytes"] &= nbytes is not None
+            r["have_flops"] &= flops is not None
+            r["bytes"] += nbytes or 0
+            r["flops"] += flops or 0
+        out = {}
+        for label, r in sorted(agg.items(), key=lambda kv: -kv[1]["ms"]):
+            sec = r["ms"] * 1e-3
+            e = {"bound": r["bound"], "launches_per_step": r["launches"] // steps,
+                 "ms_per_step": round(r["ms"] / steps, 3),
+                 "avg_us": round(1000 * r["ms"] / r["launches"], 2)}
+            if r["have_bytes"] and sec > 0:
+                e["GB/s"] = round(r["bytes"] / sec / 1e9, 1)
+                e["hbm_frac"] = round(e["GB/s"] / PEAK_HBM_GBS, 4)
+            if r["have_flops"] and sec > 0 and r["flops"]:
+                e["TFLOP/s"] = round(r["flops"] / sec / 1e12, 2)
+                e["mfma_frac"] = round(e["TFLOP/s"] / PEAK_BF16_TFLOPS, 4)
+            e["frac"] = e.get("mfma_frac" if r["bound"] == "mfma" else "hbm_frac")
+            e["bytes_per_launch"] = r["bytes"] // r["launches"] if r["have_bytes"] else None
+            e["flops_per_launch"] = r["flops"] // r["launches"] if r["have_flops"] else None
+            out[label] = e
+        return out
 
 
-# HBM bytes per GEMM launch of this workload: rocprofv3 FETCH_SIZE and
-# WRITE_SIZE over the GEMM dispatches of one search, each scaled by its reading
-# for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the launch
-# count.  Re-measured with the command in profiles/gemm_hbm_traffic_b32_p1024_w256.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 386.2e6
+class DeviceMemorySampler:
+    """Whole-device memory in use (total - free), sampled every 100 ms in a
+    thread, as the reference samples nvidia-smi (benchmarks/grbeam.py:125-141)."""
+
+    def __init__(self, interval=0.1):
+        self.interval, self.peak = interval, 0
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self):
+        while not self._stop.is_set():
+            free, total = torch.cuda.mem_get_info()
+            self.peak = max(self.peak, total - free)
+            self._stop.wait(self.interval)
+
+    def __enter__(self):
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._thread.join(timeout=3)
 
 
-def cpu_baseline(cfg, sd_cpu, prefix, beam, depth, threads):
-    """Oracle search on the host for one request of the workload; returns requests/s."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def host_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline_search(cfg, sd_cpu, prefix, beam, depth, repeats):
+    """Oracle search on the host, one request of the workload, `repeats` times,
+    on every core this process may use; returns (requests/s, seconds list)."""
     from oracle import grbeam_ref
     from oracle.qwen35_ref import Qwen35Oracle
 
-    torch.set_num_threads(threads)
+    torch.set_num_threads(host_cores())
     oracle = Qwen35Oracle(cfg, sd_cpu)
 
     class _Adapter:
@@ -97,51 +246,32 @@ def cpu_baseline(cfg, sd_cpu, prefix, beam, depth, threads):
             return oracle.decode(history, state)
 
     ids = torch.randint(0, cfg.vocab_size, (1, prefix), generator=torch.Generator().manual_seed(1))
-    t0 = time.perf_counter()
-    with torch.no_grad():
-        tokens, _, _, _ = grbeam_ref.grbeam_search(_Adapter(), ids, [beam] * depth)
-    tokens.tolist()
-    dt = time.perf_counter() - t0
-    return 1.0 / dt, dt
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            tokens, _, _, _ = grbeam_ref.grbeam_search(_Adapter(), ids, [beam] * depth)
+        tokens.tolist()
+        times.append(time.perf_counter() - t0)
+    return 1.0 / statistics.mean(times), times
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=32)
-    ap.add_argument("--prefix", type=int, default=1024)
-    ap.add_argument("--beam", type=int, default=256)
-    ap.add_argument("--depth", type=int, default=3)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=16)
-    ap.add_argument("--prompts", choices=("uniform", "pattern"), default="uniform",
-                    help="uniform: uniform-random prompt ids (default); pattern: the reference "
-                         "runner's prompts, token i of request r = 10 + (i + 17 r) % 100")
-    ap.add_argument("--workload", choices=("grbeam", "conditional_sid"), default="grbeam",
-                    help="grbeam: the headline full-vocabulary search (default); "
-                         "conditional_sid: B8, prefix 4096, coarse widths [32, 32] over the full "
-                         "vocabulary, then 16 children per coarse beam for 2 tokens with "
-                         "candidates restricted to a seeded 8192-id subset")
-    a = ap.parse_args()
-    if a.workload == "conditional_sid":
-        return conditional_sid(a)
-    if a.gpus != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {a.gpus}); "
-              "requests shard across GPUs with no exchange, see the design notes", file=sys.stderr)
-        sys.exit(2)
-
-    from kadllm_amd import grbeam_search, layers
+def build_model(dev):
     from kadllm_amd.adapters import Qwen35GRBeamAdapter, native_model
     from kadllm_amd.config import qwen35_08b_config
     from kadllm_amd.weights import random_state_dict
 
-    dev = torch.device("cuda:0")
     cfg = qwen35_08b_config()
     sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16, device=dev)
-    model, head = native_model(cfg, sd)
-    adapter = Qwen35GRBeamAdapter(model, head)
+    return cfg, sd, Qwen35GRBeamAdapter(*native_model(cfg, sd))
+
+
+# ---------------------------------------------------------------------------
+def grbeam(a):
+    from kadllm_amd import _lib, grbeam_search
+
+    dev = torch.device("cuda:0")
+    cfg, sd, adapter = build_model(dev)
     if a.prompts == "pattern":   # benchmarks/grbeam.py:254-257
         r = torch.arange(a.batch)[:, None]
         ids = (10 + (torch.arange(a.prefix)[None, :] + 17 * r) % 100).to(dev)
@@ -149,45 +279,75 @@ def main():
         ids = torch.randint(0, cfg.vocab_size, (a.batch, a.prefix),
                             generator=torch.Generator().manual_seed(0)).to(dev)
     widths = [a.beam] * a.depth
+    enqueue = []
 
     def run():
-        return grbeam_search(adapter, ids, widths).tokens.tolist()
-
-    for _ in range(a.warmup):
-        validate_output(run(), a.batch, a.beam, a.depth)
-    torch.cuda.synchronize()
-
-    timer = GemmTimer()
-    timer.reserve(128 * a.steps * a.depth)   # GEMM launches: about 115 per level
-    layers.set_launch_timer(timer)
-    times, outputs = [], []
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for _ in range(a.steps):
         t0 = time.perf_counter()
-        outputs.append(run())
+        res = grbeam_search(adapter, ids, widths)
+        enqueue.append(time.perf_counter() - t0)   # the host has issued every launch
+        return res.tokens.tolist()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(a.steps)]
+    with DeviceMemorySampler() as mem:
+        for _ in range(a.warmup):
+            validate_output(run(), a.batch, a.beam, a.depth)
         torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t_start
-    layers.set_launch_timer(None)
+        torch.cuda.reset_peak_memory_stats()
+        enqueue.clear()
+        times, outputs = [], []
+        torch.cuda.synchronize()
+        t_start = time.perf_counter()
+        for e0, e1 in ev:
+            t0 = time.perf_counter()
+            e0.record()
+            outputs.append(run())
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t_start
+    gpu_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
     for out in outputs:
         validate_output(out, a.batch, a.beam, a.depth)
-    gemm_ms, gemm_flops, gemm_bytes, n_gemm = timer.summary()
-    achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12  # TFLOP/s
+    memory = {"device_peak_gib": round(mem.peak / 2**30, 2),
+              "torch_peak_allocated_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+              "torch_peak_reserved_gib": round(torch.cuda.max_memory_reserved() / 2**30, 2)}
     value = a.batch * a.steps / elapsed
+
+    kernels, roofline = None, None
+    if a.profile_steps:
+        prof = KernelProfiler()
+        _lib.set_call_hook(prof)
+        try:
+            for _ in range(a.profile_steps):
+                validate_output(run(), a.batch, a.beam, a.depth)
+        finally:
+            _lib.set_call_hook(None)
+        kernels = prof.table(a.profile_steps)
+        g = kernels.get("gemm")
+        default = (a.batch, a.prefix, a.beam, a.depth) == (32, 1024, 256, 3)
+        if g:
+            roofline = {"kernel": "bf16 MFMA GEMM (all launches)", "bound": "mfma",
+                        "achieved": g["TFLOP/s"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": g["mfma_frac"],
+                        "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH if default else None,
+                        "algorithmic_bytes_per_launch": g["bytes_per_launch"],
+                        "launches_per_step": g["launches_per_step"],
+                        "gemm_ms_per_step": g["ms_per_step"]}
 
     cpu = None
     if not a.no_cpu_baseline:
         sd_cpu = {k: v.cpu() for k, v in sd.items()}
-        threads = min(a.cpu_threads, os.cpu_count() or 1)
-        rps, dt = cpu_baseline(cfg, sd_cpu, a.prefix, a.beam, a.depth, threads)
-        cpu = {"value": round(rps, 6), "unit": "requests/s", "cores": threads, "kind": "port",
+        rps, secs = cpu_baseline_search(cfg, sd_cpu, a.prefix, a.beam, a.depth, a.cpu_repeats)
+        cpu = {"value": round(rps, 6), "unit": "requests/s", "cores": host_cores(),
+               "kind": "port", "cpu_model": cpu_model(),
                "sample": f"1 request (prefix {a.prefix}, beam {a.beam}, {a.depth} tokens, full "
                          f"vocabulary) through the oracle restatement of the reference torch "
-                         f"path, bf16 weights, {dt:.1f} s"}
+                         f"path, bf16 weights, timed {len(secs)} times: "
+                         + ", ".join(f"{s:.1f}" for s in secs) + " s"}
 
-    workload_default = (a.batch, a.prefix, a.beam, a.depth) == (32, 1024, 256, 3)
+    default = (a.batch, a.prefix, a.beam, a.depth) == (32, 1024, 256, 3)
     line = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -198,7 +358,7 @@ def main():
         "ms_per_step": round(1000 * elapsed / a.steps, 3),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(value / H800_REQ_S, 3) if workload_default else None,
+        "vs_baseline": round(value / H800_REQ_S, 3) if default else None,
         "dtype": "bf16",
         "data": "synthetic (random-init weights, " + (
             "uniform-random prompt ids)" if a.prompts == "uniform"
@@ -207,36 +367,251 @@ def main():
                                f"W{a.beam} depth{a.depth} full-vocab",
                    "batch": a.batch, "prefix": a.prefix, "beam": a.beam, "depth": a.depth,
                    "vocab": cfg.vocab_size, "layers": cfg.num_hidden_layers},
-        "roofline": {"kernel": "bf16 MFMA GEMM (all launches)", "bound": "mfma",
-                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH if workload_default else None,
-                     "algorithmic_bytes_per_launch": round(gemm_bytes / n_gemm),
-                     "launches_per_step": n_gemm // a.steps,
-                     "gemm_ms_per_step": round(gemm_ms / a.steps, 3)},
+        "roofline": roofline,
         "cpu_baseline": cpu,
+        "kernels": kernels,
+        "memory": memory,
         "step_ms": [round(1000 * t, 2) for t in times],
+        "step_gpu_ms": [round(t, 2) for t in gpu_ms],
+        "step_enqueue_ms": [round(1000 * t, 2) for t in enqueue[:a.steps]],
     }
     print(json.dumps(line), flush=True)
+    return line
+
+
+def reference_protocol(a):
+    """3 processes x (3 warmups + 5 timed calls): latency mean with a 95% CI
+    over the process means, requests/s = batch / mean latency, and the sampled
+    whole-device memory peak (README.md:116,119; benchmarks/grbeam.py:315-363)."""
+    child = [sys.executable, os.path.abspath(__file__), "--steps", str(a.steps),
+             "--warmup", str(a.warmup), "--batch", str(a.batch), "--prefix", str(a.prefix),
+             "--beam", str(a.beam), "--depth", str(a.depth), "--prompts", a.prompts,
+             "--no-cpu-baseline", "--profile-steps", "0"]
+    means, peaks, lines = [], [], []
+    for p in range(a.processes):
+        res = subprocess.run(child, capture_output=True, text=True, timeout=900)
+        if res.returncode != 0:
+            sys.stderr.write(res.stderr)
+            raise SystemExit(f"process {p} failed with {res.returncode}")
+        line = json.loads(res.stdout.strip().splitlines()[-1])
+        lines.append(line)
+        means.append(statistics.mean(line["step_ms"]))
+        peaks.append(line["memory"]["device_peak_gib"])
+        print(f"process {p}: mean {means[-1]:.2f} ms over {len(line['step_ms'])} calls",
+              file=sys.stderr, flush=True)
+    n = len(means)
+    mean = statistics.mean(means)
+    ci = T975.get(n - 1, 1.96) * statistics.stdev(means) / math.sqrt(n) if n > 1 else None
+    value = a.batch / (mean / 1000)
+    default = (a.batch, a.prefix, a.beam, a.depth) == (32, 1024, 256, 3)
+    out = dict(lines[0])
+    out.update({
+        "value": round(value, 3), "steps": a.steps * n, "warmup": a.warmup,
+        "ms_per_step": round(mean, 3),
+        "vs_baseline": round(value / H800_REQ_S, 3) if default else None,
+        "protocol": {"processes": n, "warmups_per_process": a.warmup,
+                     "timed_calls_per_process": a.steps, "latency_ms": round(mean, 3),
+                     "ci95_ms": round(ci, 3) if ci is not None else None,
+                     "process_mean_ms": [round(m, 3) for m in means],
+                     "device_peak_gib": max(peaks)},
+        "step_ms": [t for line in lines for t in line["step_ms"]],
+        "step_gpu_ms": [t for line in lines for t in line["step_gpu_ms"]],
+    })
+    out.pop("kernels", None)
+    print(json.dumps(out), flush=True)
+
+
+# ---------------------------------------------------------------------------
+def _time_calls(fn, iters):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e-3   # seconds per call
+
+
+def _rel_check(actual, expected, name, rtol=1e-2, atol_frac=3e-3):
+    a_, e_ = actual.detach().double().cpu(), expected.detach().double().cpu()
+    bad = (a_ - e_).abs() > rtol * e_.abs() + atol_frac * e_.abs().max()
+    if bool(bad.any()):
+        raise SystemExit(f"{name}: {int(bad.sum())} elements outside tolerance")
+    return ((a_ - e_).norm() / e_.norm()).item()
+
+
+def _op_line(metric, value, unit, config, roofline, cpu, extra):
+    line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": extra.pop("iters"),
+            "warmup": 3, "ms_per_step": extra.pop("ms"), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) inputs, as the workload describes)",
+            "config": config, "roofline": roofline, "cpu_baseline": cpu}
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+def ops_gdn(a):
+    """Configuration 2: GDN suffix replay (S [32,16,128,128] fp32 ~ N(0, 0.02^2),
+    q/k/v [8192,3,16,128] bf16 ~ N(0,1), g = -softplus(N(0,1)), beta =
+    sigmoid(N(0,1)), 256 beams per request) and the width-4 conv over the same
+    beams (state [32,6144,3], x [8192,6144,3], w ~ U(-1/2,1/2)), each checked
+    against the oracle on 2 requests and timed over repeated calls; the prefix
+    tensors are compared bit for bit before and after."""
+    import torch.nn.functional as F
+
+    from kadllm_amd import ops
+    from oracle import ops_ref
+
+    dev = torch.device("cuda:0")
+    B, W, T, H, HV, K, V, C = 32, 256, 3, 16, 16, 128, 128, 6144
+    BW = B * W
+    g = torch.Generator(device=dev).manual_seed(0)
+    S = torch.randn(B, HV, K, V, generator=g, device=dev) * 0.02
+    q = torch.randn(BW, T, H, K, generator=g, device=dev).bfloat16()
+    k = torch.randn(BW, T, H, K, generator=g, device=dev).bfloat16()
+    v = torch.randn(BW, T, HV, V, generator=g, device=dev).bfloat16()
+    gate = -F.softplus(torch.randn(BW, T, HV, generator=g, device=dev))
+    beta = torch.sigmoid(torch.randn(BW, T, HV, generator=g, device=dev)).bfloat16()
+    S0 = S.clone()
+    out = ops.gated_delta(q, k, v, gate, beta, S, beam_width=W)
+    rows = torch.cat((torch.arange(0, W), torch.arange((B - 1) * W, B * W)))
+    ref = ops_ref.gated_delta(*(t[rows].cpu() for t in (q, k, v, gate, beta)),
+                              S[[0, B - 1]].cpu(), beam_width=W)
+    err = _rel_check(out[rows], ref, "gdn replay")
+    sec = _time_calls(lambda: ops.gated_delta(q, k, v, gate, beta, S, beam_width=W), a.op_iters)
+    if not torch.equal(S, S0):
+        raise SystemExit("gdn replay wrote the prefix state")
+    nbytes = BW * T * (2 * H * K + 2 * HV * V) * 2 + B * HV * K * V * 4 + BW * T * HV * 6
+    flops = BW * HV * 2 * T * 2 * K * V
+    cpu = None
+    if not a.no_cpu_baseline:
+        torch.set_num_threads(host_cores())
+        args1 = [t[:W].cpu() for t in (q, k, v, gate, beta)] + [S[:1].cpu()]
+        t0 = time.perf_counter()
+        ops_ref.gated_delta(*args1, beam_width=W)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(nbytes / B / dt / 1e9, 3), "unit": "GB/s", "cores": host_cores(),
+               "kind": "port", "cpu_model": cpu_model(),
+               "sample": f"1 of the 32 requests (256 beams) through the oracle's per-request "
+                         f"fp32 recurrence, {dt:.2f} s"}
+    gbs = nbytes / sec / 1e9
+    _op_line("GDN suffix replay, configuration 2: achieved HBM GB/s", round(gbs, 1), "GB/s",
+             {"workload": "gdn_replay B32 W256 T3 H16 HV16 K128 V128 (bf16 q/k/v, fp32 S)"},
+             {"kernel": "gdn_replay_kernel<128,128,bf16,3>", "bound": "hbm",
+              "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+              "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+              "algorithmic_bytes_per_launch": nbytes,
+              "mfma_tflops": round(flops / sec / 1e12, 2),
+              "mfma_frac": round(flops / sec / 1e12 / PEAK_BF16_TFLOPS, 4)},
+             cpu, {"iters": a.op_iters, "ms": round(sec * 1e3, 4), "us_per_call": round(sec * 1e6, 2),
+                   "rel_l2_vs_oracle": err})
+
+    # conv4 over the same beams, the reference runner's [BW, C, T] layout and
+    # the model's token-major rows
+    xs = torch.randn(BW, C, T, generator=g, device=dev).bfloat16()
+    st = torch.randn(B, C, 3, generator=g, device=dev).bfloat16()
+    w = (torch.rand(C, 4, generator=g, device=dev) - 0.5).bfloat16()
+    st0 = st.clone()
+    nbytes = (2 * BW * C * T + B * C * 3 + C * 4) * 2
+    for layout in ("reference [BW, C, T]", "token-major [BW, T, C]"):
+        x = xs if layout.startswith("reference") else xs.transpose(1, 2).contiguous().transpose(1, 2)
+        y = ops.causal_conv1d(x, st, w, beam_width=W)
+        ref = ops_ref.causal_conv1d(x[rows].cpu(), st[[0, B - 1]].cpu(), w.cpu(), beam_width=W)
+        err = _rel_check(y[rows], ref, "conv", rtol=1.6e-2, atol_frac=1e-3)
+        sec = _time_calls(lambda: ops.causal_conv1d(x, st, w, beam_width=W), a.op_iters)
+        if not torch.equal(st, st0):
+            raise SystemExit("conv wrote the prefix state")
+        cpu = None
+        if not a.no_cpu_baseline:
+            x1 = x[:W].cpu()
+            t0 = time.perf_counter()
+            ops_ref.causal_conv1d(x1, st[:1].cpu(), w.cpu(), beam_width=W)
+            dt = time.perf_counter() - t0
+            cpu = {"value": round(nbytes / B / dt / 1e9, 3), "unit": "GB/s",
+                   "cores": host_cores(), "kind": "port", "cpu_model": cpu_model(),
+                   "sample": f"1 of the 32 requests through the oracle's per-request conv1d, "
+                             f"{dt:.3f} s"}
+        gbs = nbytes / sec / 1e9
+        _op_line(f"conv4 suffix, configuration 2, {layout}: achieved HBM GB/s", round(gbs, 1),
+                 "GB/s", {"workload": f"conv4 B32 W256 C6144 T3 bf16, x {layout}"},
+                 {"kernel": "conv_suffix", "bound": "hbm", "achieved": round(gbs, 1),
+                  "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                  "traffic": None, "algorithmic_bytes_per_launch": nbytes},
+                 cpu, {"iters": a.op_iters, "ms": round(sec * 1e3, 4),
+                       "us_per_call": round(sec * 1e6, 2), "rel_l2_vs_oracle": err})
+
+
+def ops_attention(a):
+    """Configuration 3: prefix-shared gated GQA decode attention, 32 requests x
+    256 beams, 8 q heads / 2 KV heads x 256, prefix 1024, suffix T = 1, 2, 3,
+    output sigmoid gate; all inputs bf16 ~ N(0,1), scale 1/16.  Checked against
+    the oracle on 2 requests, then timed."""
+    from kadllm_amd import ops
+    from oracle import ops_ref
+
+    dev = torch.device("cuda:0")
+    B, W, H, HK, L, D = 32, 256, 8, 2, 1024, 256
+    BW = B * W
+    g = torch.Generator(device=dev).manual_seed(0)
+    pk = torch.randn(B, L, HK, D, generator=g, device=dev).bfloat16()
+    pv = torch.randn(B, L, HK, D, generator=g, device=dev).bfloat16()
+    pk0, pv0 = pk.clone(), pv.clone()
+    rows = torch.cat((torch.arange(0, W), torch.arange((B - 1) * W, B * W)))
+    for T in (1, 2, 3):
+        q = torch.randn(BW, T, H, D, generator=g, device=dev).bfloat16()
+        sk = torch.randn(BW, T, HK, D, generator=g, device=dev).bfloat16()
+        sv = torch.randn(BW, T, HK, D, generator=g, device=dev).bfloat16()
+        gate = torch.randn(BW, T, H * D, generator=g, device=dev).bfloat16()
+
+        def call():
+            return ops.prefix_attention(q, pk, pv, sk, sv, beam_width=W, scale=1 / 16, gate=gate)
+
+        out = call()
+        ref = ops_ref.prefix_attention(q[rows].cpu(), pk[[0, B - 1]].cpu(), pv[[0, B - 1]].cpu(),
+                                       sk[rows].cpu(), sv[rows].cpu(), beam_width=W, scale=1 / 16)
+        ref = (ref.float().reshape(2 * W, T, H * D)
+               * torch.sigmoid(gate[rows].cpu().float()).bfloat16().float()).bfloat16()
+        err = _rel_check(out[rows].reshape(2 * W, T, H * D), ref, "attention")
+        sec = _time_calls(call, a.op_iters)
+        if not (torch.equal(pk, pk0) and torch.equal(pv, pv0)):
+            raise SystemExit("attention wrote the prefix K/V")
+        flops = 4 * BW * T * H * (L + T) * D
+        nbytes = 2 * (3 * BW * T * H * D + 2 * B * L * HK * D + 2 * BW * T * HK * D)
+        tfs = flops / sec / 1e12
+        cpu = None
+        if not a.no_cpu_baseline:
+            torch.set_num_threads(host_cores())
+            t0 = time.perf_counter()
+            ops_ref.prefix_attention(q[:W].cpu(), pk[:1].cpu(), pv[:1].cpu(), sk[:W].cpu(),
+                                     sv[:W].cpu(), beam_width=W, scale=1 / 16)
+            dt = time.perf_counter() - t0
+            cpu = {"value": round(flops / B / dt / 1e12, 4), "unit": "TFLOP/s",
+                   "cores": host_cores(), "kind": "port", "cpu_model": cpu_model(),
+                   "sample": f"1 of the 32 requests through the oracle's fp32 folded-beam "
+                             f"attention, {dt:.2f} s"}
+        _op_line(f"prefix-shared gated GQA attention, configuration 3, T={T}: achieved TFLOP/s",
+                 round(tfs, 2), "TFLOP/s",
+                 {"workload": f"prefix_attention B32 W256 H8 HK2 D256 L1024 T{T} gated bf16"},
+                 {"kernel": f"attn2_kernel<256,false>", "bound": "mfma", "achieved": round(tfs, 2),
+                  "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(tfs / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "algorithmic_flops_per_launch": flops, "algorithmic_bytes_per_launch": nbytes,
+                  "hbm_GBps": round(nbytes / sec / 1e9, 1),
+                  "hbm_frac": round(nbytes / sec / 1e9 / PEAK_HBM_GBS, 4)},
+                 cpu, {"iters": a.op_iters, "ms": round(sec * 1e3, 4),
+                       "us_per_call": round(sec * 1e6, 2), "rel_l2_vs_oracle": err})
 
 
 def conditional_sid(a):
     """Two-level conditional semantic-ID search (no reference runner exists for it;
     vs_baseline is null).  One step is one conditional_search call on the batch,
     tokens copied to the host, inside the timed region."""
-    if a.gpus != 1:
-        print("bench.py runs on one GPU", file=sys.stderr)
-        sys.exit(2)
     from kadllm_amd import conditional_search
-    from kadllm_amd.adapters import Qwen35GRBeamAdapter, native_model
-    from kadllm_amd.config import qwen35_08b_config
-    from kadllm_amd.weights import random_state_dict
 
     B, P, coarse, fine, n_sub = 8, 4096, [32, 32], [16, 16], 8192
     dev = torch.device("cuda:0")
-    cfg = qwen35_08b_config()
-    sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16, device=dev)
-    adapter = Qwen35GRBeamAdapter(*native_model(cfg, sd))
+    cfg, _, adapter = build_model(dev)
     ids = torch.randint(0, cfg.vocab_size, (B, P), generator=torch.Generator().manual_seed(0)).to(dev)
     sub = torch.zeros(cfg.vocab_size, dtype=torch.bool)
     sub[torch.randperm(cfg.vocab_size, generator=torch.Generator().manual_seed(0))[:n_sub]] = True
@@ -255,7 +630,11 @@ def conditional_sid(a):
         validate_output(run(), B, width, len(coarse) + len(fine))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    outs = [run() for _ in range(a.steps)]
+    times, outs = [], []
+    for _ in range(a.steps):
+        t1 = time.perf_counter()
+        outs.append(run())
+        times.append(time.perf_counter() - t1)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     for out in outs:
@@ -270,7 +649,42 @@ def conditional_sid(a):
         "config": {"workload": f"conditional_sid qwen3.5-0.8B-shaped B{B} P{P} coarse{coarse} "
                                f"fine{fine}x{coarse[-1]} subset{n_sub}",
                    "batch": B, "prefix": P, "coarse_widths": coarse, "fine_widths": fine},
-        "roofline": None, "cpu_baseline": None}), flush=True)
+        "roofline": None, "cpu_baseline": None,
+        "step_ms": [round(1000 * t, 2) for t in times]}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--prefix", type=int, default=1024)
+    ap.add_argument("--beam", type=int, default=256)
+    ap.add_argument("--depth", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-repeats", type=int, default=2)
+    ap.add_argument("--profile-steps", type=int, default=2,
+                    help="untimed steps after the timed ones with every launch timed")
+    ap.add_argument("--prompts", choices=("uniform", "pattern"), default="uniform",
+                    help="uniform: uniform-random prompt ids (default); pattern: the reference "
+                         "runner's prompts, token i of request r = 10 + (i + 17 r) %% 100")
+    ap.add_argument("--protocol", choices=("single", "reference"), default="single")
+    ap.add_argument("--processes", type=int, default=3)
+    ap.add_argument("--op-iters", type=int, default=50)
+    ap.add_argument("--workload",
+                    choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention"),
+                    default="grbeam")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {a.gpus}); "
+              "requests shard across GPUs with no exchange, see the design notes", file=sys.stderr)
+        sys.exit(2)
+    if a.protocol == "reference":
+        return reference_protocol(a)
+    return {"grbeam": grbeam, "conditional_sid": conditional_sid, "ops_gdn": ops_gdn,
+            "ops_attention": ops_attention}[a.workload](a)
 
 
 if __name__ == "__main__":

@@ -109,13 +109,32 @@ def stream_of(t):
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def call(name, *args):
-    """Invoke entry point ``name``; raise KadLibraryError on a nonzero code."""
-    lib = load()
+_call_hook = None
+
+
+def set_call_hook(hook):
+    """Install (or clear with None) ``hook(name, args, launch)``, which every
+    call makes instead of invoking entry point ``name`` directly; the hook
+    must call ``launch()`` once (e.g. between two HIP events, for per-kernel
+    timing)."""
+    global _call_hook
+    _call_hook = hook
+
+
+def _invoke(lib, name, args):
     rc = getattr(lib, name)(*args)
     if rc != KAD_OK:
         msg = lib.kad_last_error().decode(errors="replace")
         raise KadLibraryError(f"{name} failed ({ERRORS.get(rc, rc)}): {msg}")
+
+
+def call(name, *args):
+    """Invoke entry point ``name``; raise KadLibraryError on a nonzero code."""
+    lib = load()
+    if _call_hook is None:
+        _invoke(lib, name, args)
+    else:
+        _call_hook(name, args, lambda: _invoke(lib, name, args))
 
 
 def gdn_chunk_workspace(N, T, HV, K, device):

@@ -11,18 +11,6 @@ from . import _lib
 
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
 
-_launch_timer = None
-
-
-def set_launch_timer(timer):
-    """Install (or clear with None) a callable ``timer(launch, flops, nbytes)``
-    that wraps every GEMM launch, e.g. to bracket it with HIP events for
-    roofline figures; nbytes = the launch's algorithmic HBM bytes (A, W, the
-    output and the residual each once)."""
-    global _launch_timer
-    _launch_timer = timer
-
-
 def gemm(a, w, out=None, *, epilogue=EPI_STORE, residual=None):
     """out[M, N'] = epilogue(a[M, K] @ w[N, K]^T) (bf16, fp32 accumulate).
 
@@ -36,17 +24,9 @@ def gemm(a, w, out=None, *, epilogue=EPI_STORE, residual=None):
     if out is None:
         out = torch.empty(M, n_out, dtype=torch.bfloat16, device=a.device)
     r = residual
-
-    def launch():
-        _lib.call("kad_gemm_bf16", _lib.ptr(a), a.stride(0), _lib.ptr(w), w.stride(0),
-                  _lib.ptr(out), out.stride(0), _lib.ptr(r), r.stride(0) if r is not None else 0,
-                  M, N, K, epilogue, _lib.stream_of(a))
-
-    if _launch_timer is None:
-        launch()
-    else:
-        nbytes = 2 * (M * K + N * K + M * n_out + (M * n_out if r is not None else 0))
-        _launch_timer(launch, 2 * M * N * K, nbytes)
+    _lib.call("kad_gemm_bf16", _lib.ptr(a), a.stride(0), _lib.ptr(w), w.stride(0), _lib.ptr(out),
+              out.stride(0), _lib.ptr(r), r.stride(0) if r is not None else 0, M, N, K, epilogue,
+              _lib.stream_of(a))
     return out
 
 

@@ -198,7 +198,12 @@ def causal_conv1d(x, shared_state, weight, *, beam_width: int = 1, bias=None,
         raise ValueError("Triton short-conv requires width=4, SiLU, and no bias")
     weight = weight.contiguous()
     bias = None if bias is None else bias.contiguous()
-    out = torch.empty(BW, C, T, dtype=x.dtype, device=x.device)
+    # [BW, C, T] in x's layout: token-major x (channels contiguous, as a
+    # projection's rows give it) gets a token-major result
+    if x.stride() == (T * C, 1, C):
+        out = torch.empty(BW, T, C, dtype=x.dtype, device=x.device).transpose(1, 2)
+    else:
+        out = torch.empty(BW, C, T, dtype=x.dtype, device=x.device)
     _lib.call("kad_causal_conv_suffix", _lib.ptr(x), *x.stride(), _lib.ptr(shared_state),
               *shared_state.stride(), shared_state.shape[-1], _lib.ptr(weight), width,
               _lib.ptr(bias), _lib.ptr(out), *out.stride(), BW // beam_width, beam_width, C, T,
