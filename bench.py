@@ -15,7 +15,8 @@ Printed: one JSON line with requests/s (= batch * steps / elapsed), the
 roofline of the dominant kernel (the bf16 MFMA GEMM), a per-kernel table
 ("kernels": launches, time, achieved GB/s or TFLOP/s and roofline fraction
 per kernel class, from HIP events around every launch in extra untimed
-steps), per-step host / enqueue / device times, memory peaks, and the CPU
+steps), per-step host / enqueue / device times (device: from the step's start
+to its last kernel), memory peaks, and the CPU
 baseline (the oracle restatement of the reference torch path on this host's
 cores, one request, timed twice).
 
@@ -27,10 +28,13 @@ Other modes:
   --workload ops_attention  isolated prefix-shared attention, T = 1, 2, 3
                          (configuration 3)
   --workload conditional_sid  two-level SID search (configuration 5)
+  --workload hbm_copy    a 1 GiB device copy: measured streaming bandwidth and
+                         the calibration of rocprofv3's FETCH/WRITE_SIZE
   --depth 7 --batch 4    the reference's 7-token runs (README.md:125)
 """
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -55,7 +59,7 @@ T975 = {1: 12.706, 2: 4.303, 3: 3.182, 4: 2.776, 5: 2.571, 6: 2.447, 7: 2.365, 9
 # HBM bytes per GEMM launch of the default workload: rocprofv3 FETCH_SIZE and
 # WRITE_SIZE over the GEMM dispatches of one search, each scaled by its reading
 # for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the launch
-# count.  Re-measured with the command in profiles/gemm_hbm_traffic_b32_p1024_w256.md.
+# count.  Re-measured with the commands in profiles/hbm_traffic_and_busy_b32_p1024_w256.md.
 GEMM_TRAFFIC_BYTES_PER_LAUNCH = 386.2e6
 
 
@@ -281,10 +285,12 @@ def grbeam(a):
     widths = [a.beam] * a.depth
     enqueue = []
 
-    def run():
+    def run(done=None):
         t0 = time.perf_counter()
         res = grbeam_search(adapter, ids, widths)
         enqueue.append(time.perf_counter() - t0)   # the host has issued every launch
+        if done is not None:
+            done.record()                          # after the search's last kernel
         return res.tokens.tolist()
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -294,6 +300,14 @@ def grbeam(a):
             validate_output(run(), a.batch, a.beam, a.depth)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
+        # The tokens' host copy (.tolist(), inside the timed region as in the
+        # reference) builds ~33k Python objects, which periodically triggers a
+        # full garbage collection over the whole interpreter heap (~35 ms).
+        # As a serving process would, move the long-lived start-up objects
+        # out of the collector's reach; new garbage is still collected.
+        if not a.no_gc_freeze:
+            gc.collect()
+            gc.freeze()
         enqueue.clear()
         times, outputs = [], []
         torch.cuda.synchronize()
@@ -301,8 +315,7 @@ def grbeam(a):
         for e0, e1 in ev:
             t0 = time.perf_counter()
             e0.record()
-            outputs.append(run())
-            e1.record()
+            outputs.append(run(e1))
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t0)
         torch.cuda.synchronize()
@@ -603,6 +616,25 @@ def ops_attention(a):
                        "us_per_call": round(sec * 1e6, 2), "rel_l2_vs_oracle": err})
 
 
+def hbm_copy(a):
+    """A 1 GiB device-to-device copy (torch's copy kernel), repeated: the
+    bandwidth a plain streaming kernel reaches on this board, and the known
+    byte count against which rocprofv3's FETCH_SIZE / WRITE_SIZE readings of
+    the other kernels are scaled."""
+    dev = torch.device("cuda:0")
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    sec = _time_calls(lambda: dst.copy_(src), a.op_iters)
+    gbs = 2 * n / sec / 1e9
+    _op_line("device copy 1 GiB: achieved HBM GB/s (read + write)", round(gbs, 1), "GB/s",
+             {"workload": "hbm_copy 1 GiB uint8"},
+             {"kernel": "copy", "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+              "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": 2 * n,
+              "algorithmic_bytes_per_launch": 2 * n}, None,
+             {"iters": a.op_iters, "ms": round(sec * 1e3, 4), "us_per_call": round(sec * 1e6, 2)})
+
+
 def conditional_sid(a):
     """Two-level conditional semantic-ID search (no reference runner exists for it;
     vs_baseline is null).  One step is one conditional_search call on the batch,
@@ -665,6 +697,8 @@ def main():
     ap.add_argument("--depth", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=2)
+    ap.add_argument("--no-gc-freeze", action="store_true",
+                    help="leave the start-up heap to Python's full garbage collections")
     ap.add_argument("--profile-steps", type=int, default=2,
                     help="untimed steps after the timed ones with every launch timed")
     ap.add_argument("--prompts", choices=("uniform", "pattern"), default="uniform",
@@ -674,7 +708,7 @@ def main():
     ap.add_argument("--processes", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=50)
     ap.add_argument("--workload",
-                    choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention"),
+                    choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention", "hbm_copy"),
                     default="grbeam")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -684,7 +718,7 @@ def main():
     if a.protocol == "reference":
         return reference_protocol(a)
     return {"grbeam": grbeam, "conditional_sid": conditional_sid, "ops_gdn": ops_gdn,
-            "ops_attention": ops_attention}[a.workload](a)
+            "ops_attention": ops_attention, "hbm_copy": hbm_copy}[a.workload](a)
 
 
 if __name__ == "__main__":
