@@ -27,6 +27,8 @@ Other modes:
   --workload ops_gdn     isolated GDN suffix replay and conv4 (configuration 2)
   --workload ops_attention  isolated prefix-shared attention, T = 1, 2, 3
                          (configuration 3)
+  --workload ops_gemm    every GEMM shape of the headline search alone, beside
+                         torch.matmul (hipBLASLt) on the same operands
   --workload conditional_sid  two-level SID search (configuration 5)
   --workload hbm_copy    a 1 GiB device copy: measured streaming bandwidth and
                          the calibration of rocprofv3's FETCH/WRITE_SIZE
@@ -616,6 +618,94 @@ def ops_attention(a):
                        "us_per_call": round(sec * 1e6, 2), "rel_l2_vs_oracle": err})
 
 
+# The GEMMs of one search at B32 / prefix 1024 / beam 256 / 3 tokens on the
+# 0.8B model: (name, M, N, K, epilogue, dispatches per search).  Prefill runs
+# every layer on 32 x 1024 rows (the last layer's attention output, o_proj and
+# MLP only on the 32 last rows, which take the small-M kernel and are left
+# out here), each of the two decode levels on 32 x 256.
+GEMM_SHAPES = (
+    ("prefill gdn in_proj", 32768, 8192, 1024, 0, 18),
+    ("prefill attn qkv", 32768, 5120, 1024, 0, 5),
+    ("prefill last attn layer kv", 32768, 1024, 1024, 0, 1),
+    ("prefill mlp gate_up (SwiGLU)", 32768, 7168, 1024, 2, 23),
+    ("prefill mixer out (residual)", 32768, 1024, 2048, 1, 23),
+    ("prefill mlp down (residual)", 32768, 1024, 3584, 1, 23),
+    ("decode gdn in_proj", 8192, 8192, 1024, 0, 36),
+    ("decode attn qkv", 8192, 5120, 1024, 0, 12),
+    ("decode mlp gate_up (SwiGLU)", 8192, 7168, 1024, 2, 48),
+    ("decode mixer out (residual)", 8192, 1024, 2048, 1, 48),
+    ("decode mlp down (residual)", 8192, 1024, 3584, 1, 48),
+    ("decode lm head", 8192, 248320, 1024, 0, 2),
+)
+
+
+def ops_gemm(a):
+    """The bf16 GEMM shapes of the headline search, one at a time, through
+    kad_gemm_bf16 (automatic tile choice, fused epilogue) and, beside it, the
+    same product through torch's F.linear (hipBLASLt, no epilogue), both timed
+    with events over --op-iters back-to-back calls.  Inputs ~ N(0,1), weights
+    ~ N(0, 0.05^2); each result is checked against F.linear on 64 rows."""
+    from torch.nn import functional as F
+
+    from kadllm_amd import layers
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    total = {"ours_s": 0.0, "lib_s": 0.0, "flops": 0.0}
+    for name, M, N, K, epi, count in GEMM_SHAPES:
+        x = torch.randn(M, K, generator=g, device=dev).bfloat16()
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.05).bfloat16()
+        n_out = N // 2 if epi == layers.EPI_SWIGLU else N
+        out = torch.randn(M, n_out, generator=g, device=dev).bfloat16()
+        res0 = out[:64].clone()
+        if epi == layers.EPI_RESIDUAL:
+            call = lambda: layers.gemm(x, w, out=out, epilogue=epi, residual=out)  # noqa: E731
+        else:
+            call = lambda: layers.gemm(x, w, out=out, epilogue=epi)  # noqa: E731
+        call()
+        torch.cuda.synchronize()
+        prod = F.linear(x[:64], w).float()
+        if epi == layers.EPI_SWIGLU:
+            gu = prod.bfloat16().float().view(64, N // 64, 2, 32)
+            expect = (F.silu(gu[:, :, 0]).bfloat16().float() * gu[:, :, 1]).reshape(64, n_out)
+        elif epi == layers.EPI_RESIDUAL:
+            expect = res0.float() + prod.bfloat16().float()
+        else:
+            expect = prod
+        _rel_check(out[:64].float(), expect, name, rtol=2e-2, atol_frac=1e-2)
+        sec = _time_calls(call, a.op_iters)
+        lib = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        lib_sec = _time_calls(lambda: torch.matmul(x, w.t(), out=lib), a.op_iters)
+        flops = 2.0 * M * N * K
+        nbytes = 2 * (M * K + N * K + M * n_out * (2 if epi == layers.EPI_RESIDUAL else 1))
+        tfs, lib_tfs = flops / sec / 1e12, flops / lib_sec / 1e12
+        total["ours_s"] += count * sec
+        total["lib_s"] += count * lib_sec
+        total["flops"] += count * flops
+        _op_line(f"bf16 GEMM {name}: achieved TFLOP/s", round(tfs, 1), "TFLOP/s",
+                 {"workload": f"gemm M{M} N{N} K{K} epilogue {epi}"},
+                 {"kernel": "gemm (automatic tile choice)", "bound": "mfma",
+                  "achieved": round(tfs, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(tfs / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "algorithmic_flops_per_launch": flops, "algorithmic_bytes_per_launch": nbytes},
+                 None, {"iters": a.op_iters, "ms": round(sec * 1e3, 4),
+                        "us_per_call": round(sec * 1e6, 2), "dispatches_per_search": count,
+                        "hipblaslt_us_per_call": round(lib_sec * 1e6, 2),
+                        "hipblaslt_tflops": round(lib_tfs, 1),
+                        "vs_hipblaslt": round(lib_sec / sec, 3)})
+        del x, w, out, lib
+        torch.cuda.empty_cache()
+    tfs = total["flops"] / total["ours_s"] / 1e12
+    _op_line("bf16 GEMMs of one headline search, dispatch-weighted: achieved TFLOP/s",
+             round(tfs, 1), "TFLOP/s", {"workload": "gemm shapes of grbeam B32 P1024 W256 3 tokens"},
+             {"kernel": "gemm (automatic tile choice)", "bound": "mfma", "achieved": round(tfs, 1),
+              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tfs / PEAK_BF16_TFLOPS, 4),
+              "traffic": None}, None,
+             {"iters": a.op_iters, "ms": round(total["ours_s"] * 1e3, 3),
+              "hipblaslt_ms": round(total["lib_s"] * 1e3, 3),
+              "hipblaslt_tflops": round(total["flops"] / total["lib_s"] / 1e12, 1)})
+
+
 def hbm_copy(a):
     """A 1 GiB device-to-device copy (torch's copy kernel), repeated: the
     bandwidth a plain streaming kernel reaches on this board, and the known
@@ -708,7 +798,8 @@ def main():
     ap.add_argument("--processes", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=50)
     ap.add_argument("--workload",
-                    choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention", "hbm_copy"),
+                    choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention", "ops_gemm",
+                             "hbm_copy"),
                     default="grbeam")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -718,7 +809,8 @@ def main():
     if a.protocol == "reference":
         return reference_protocol(a)
     return {"grbeam": grbeam, "conditional_sid": conditional_sid, "ops_gdn": ops_gdn,
-            "ops_attention": ops_attention, "hbm_copy": hbm_copy}[a.workload](a)
+            "ops_attention": ops_attention, "ops_gemm": ops_gemm,
+            "hbm_copy": hbm_copy}[a.workload](a)
 
 
 if __name__ == "__main__":

@@ -101,20 +101,15 @@ int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx
 int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
                   const void* R, int64_t ldr, int M, int N, int K, int epilogue,
                   kad_stream_t stream);
-/* Same with an explicit tile configuration (0 = automatic choice as
- * kad_gemm_bf16; 1 = 32x256, 2 = 128x128, 3 = 128x256, 4 = 256x256 with 4
- * waves; 5 = 256x256 and 6 = 256x128 with 8 waves; 7 = 256x256 with 4 waves,
- * fragment double-buffering and a 16-byte store epilogue, which needs 16-byte
- * aligned C (and R) with ldc, ldr and the output width multiples of 8; 8 = the
- * same with register-staged instead of direct-to-LDS loads; 9 = 7 with the
- * next tile's loads split over two K steps; 10 = 9 with 256x128 tiles;
- * 11 = 128x32 with 4 waves, no SwiGLU epilogue; 12 = 9 with each K step's
- * fragment reads issued before its loads; 13 = 256x256 through a 4-slot ring
- * of 32-deep K slices, loads three slices ahead; 14 = 9 with 8 waves, 2 per
- * SIMD, each a 128 x 64 sub-tile; 15 = 14 with 256x128 tiles, each wave a
- * 64 x 64 sub-tile; 16, 17 = 14, 15 on 16x16x32 MFMAs with the loads of the
- * tile after next issued mid-tile; 18, 19 = 16, 17 persistent, one workgroup
- * per CU walking tiles), for tuning. */
+/* Same with an explicit tile configuration, the forms the automatic choice
+ * picks from (0 = automatic choice as kad_gemm_bf16; 1 = 32x256 with 4 waves;
+ * 2 = 128x128 with 4 waves; 5 = 256x256 with 8 waves; 11 = 128x32 with 4
+ * waves, no SwiGLU epilogue; 16 = 256x256 and 17 = 256x128 with 8 waves on
+ * 16x16x32 MFMAs, direct-to-LDS loads and a 16-byte store epilogue, which
+ * needs 16-byte aligned C (and R) with ldc, ldr and the output width multiples
+ * of 8; 18 = 16 persistent, one workgroup per CU walking the tiles).  Every
+ * configuration accumulates K in the same order, so all give bit-identical
+ * results; other numbers are rejected (KAD_ERR_UNSUPPORTED). */
 int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
                         int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                         int epilogue, int tile_config, kad_stream_t stream);

@@ -169,11 +169,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
   }
 }
 
-// 256 x BN tiles (BN = 256 or 128), 4 waves (2 x 2), each wave a 128 x BN/2
-// sub-tile: 4 * BN/64 MFMA 32x32x16 per 16-deep K step against 4 + BN/64
-// fragment loads.  256x256 gives the highest MFMA-to-LDS ratio the
-// 512-register file allows (a second wave per SIMD would halve it); 256x128
-// fills the chip on narrow outputs (N = 1024 at M = 8192 is 256 tiles).
+// 256 x BN tiles (BN = 256 or 128) for the large GEMMs.
 //
 // Operand tiles move HBM -> LDS with global_load_lds_dwordx4 (no register
 // staging): one wave instruction writes 64 x 16 bytes contiguously, i.e. 8
@@ -182,12 +178,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
 // consecutive rows at one chunk) hit 16 distinct 16-byte bank groups; each
 // lane of a load therefore fetches the global chunk that belongs at its LDS
 // slot.  Two stages of 64-deep K: tile kt+1 is in flight while tile kt feeds
-// the MFMAs.  Each 16-deep step is its own scheduling region with its MFMAs
-// interleaved with the next step's fragment reads and the next tile's loads
-// (MODE 0: all in step 0; MODE 2: split over steps 0 and 1, which measured
-// 2-5% faster).  MODE 1 stages the same loads through registers
-// (global_load_dwordx4 in step 0, ds_write_b128 in step 2 to the same
-// swizzled positions).
+// the MFMAs.
 //
 // Operands are swapped (weight rows are the MFMA's A operand), so each lane's
 // accumulators hold 4 consecutive output columns: the epilogue packs them 8
@@ -196,14 +187,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
 // configuration accumulates K in the same order, so results are bit-identical
 // across tile shapes.
 constexpr int kT = 256;
-
-template <int BN>
-struct Tile256 {
-  static constexpr int NJ = BN / 64;                 // 32-column blocks per wave
-  static constexpr int Stage = (kT + BN) * kBK;      // elements per stage: A rows then W rows
-  static constexpr int EpiLd = BN / 2 + 8;           // epilogue LDS row stride (elements)
-  static constexpr int Smem = 2 * Stage > 4 * 128 * EpiLd ? 2 * Stage : 4 * 128 * EpiLd;
-};
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
@@ -233,505 +216,6 @@ __device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
   __builtin_amdgcn_global_load_lds((global_void_t*)g, (lds_void_t*)lds_block, 16, 0, 0);
 }
 
-// Epilogue.  acc[i][j][e]: row m = i*32 + lane%32, column
-// n = j*32 + (e/4)*8 + (lane/32)*4 + e%4 of the wave's 128 x BN/2 sub-tile
-// (waves 2 x 2).  The accumulators go through LDS (smem free on entry) and
-// leave as 16-byte row stores, fusing the residual add or SwiGLU.
-template <int EPI, int BN>
-__device__ __forceinline__ void epilogue_tile(f32x16 (&acc)[4][Tile256<BN>::NJ], bf16_t* smem,
-                                              int lane, int wave, int m0, int n0, bf16_t* C,
-                                              int64_t ldc, const bf16_t* R, int64_t ldr, int M,
-                                              int N) {
-  constexpr int NJ = Tile256<BN>::NJ, kEpiLd = Tile256<BN>::EpiLd;
-  const int wm = wave >> 1, wn = wave & 1;
-  bf16_t* ep = smem + wave * 128 * kEpiLd;
-  const int e_row = lane & 31, e_col = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if constexpr (EPI == KAD_EPI_SWIGLU) {
-#pragma unroll
-      for (int j = 0; j < NJ; j += 2) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          u32x2 packed;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            uint32_t two = 0;
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const int e = g * 4 + h * 2 + q;
-              const float gv = round_bf(acc[i][j][e]);
-              const float uv = round_bf(acc[i][j + 1][e]);
-              two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
-            }
-            packed[h] = two;
-          }
-          *(u32x2*)(ep + (i * 32 + e_row) * kEpiLd + (j / 2) * 32 + g * 8 + e_col) = packed;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          u32x2 packed;
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            packed[h] = (uint32_t)f2bf(acc[i][j][g * 4 + h * 2]) |
-                        ((uint32_t)f2bf(acc[i][j][g * 4 + h * 2 + 1]) << 16);
-          *(u32x2*)(ep + (i * 32 + e_row) * kEpiLd + j * 32 + g * 8 + e_col) = packed;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? BN / 4 : BN / 2;  // wave sub-tile output columns
-  constexpr int kChunks = kCols / 8, kRowsPer = 64 / kChunks;
-  const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
-  const int out_n0 = EPI == KAD_EPI_SWIGLU ? n0 / 2 + wn * kCols : n0 + wn * kCols;
-  const int n_out = EPI == KAD_EPI_SWIGLU ? N / 2 : N;
-#pragma unroll 4
-  for (int r = c_row; r < 128; r += kRowsPer) {
-    const int row = m0 + wm * 128 + r, col = out_n0 + c_col;
-    if (row >= M || col >= n_out) continue;
-    u32x4 v = *(const u32x4*)(ep + r * kEpiLd + c_col);
-    if constexpr (EPI == KAD_EPI_RESIDUAL) {
-      const u32x4 rr = *(const u32x4*)(R + (int64_t)row * ldr + col);
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const float lo = __uint_as_float(rr[h] << 16) + __uint_as_float(v[h] << 16);
-        const float hi = __uint_as_float(rr[h] & 0xffff0000u) + __uint_as_float(v[h] & 0xffff0000u);
-        v[h] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-      }
-    }
-    *(u32x4*)(C + (int64_t)row * ldc + col) = v;
-  }
-}
-
-// issue order inside one 16-deep step: NM MFMAs, each followed by up to one
-// fragment read (NR in all), and the step's NV global loads and NW LDS writes
-// spread one per MFMA (two when there are at least NM of them)
-template <int NM, int NR, int NV, int NW>
-__device__ __forceinline__ void interleave_step() {
-  constexpr int PV = NV >= NM ? 2 : 1, PW = NW >= NM ? 2 : 1;
-#pragma unroll
-  for (int t = 0; t < NM; ++t) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (t < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    if (t * PV < NV) __builtin_amdgcn_sched_group_barrier(0x020, PV, 0);
-    if (t * PW < NW) __builtin_amdgcn_sched_group_barrier(0x200, PW, 0);
-  }
-  __builtin_amdgcn_sched_barrier(0);  // steps are separate scheduling regions
-}
-
-// issue order inside one 16-deep step when the step's fragment reads come
-// before its global loads in program order (the loads write LDS, so they
-// cannot be hoisted above reads that might alias): NR MFMAs each followed by
-// one fragment read, then the NV global loads spread evenly over the
-// remaining NM - NR MFMAs
-template <int NM, int NR, int NV>
-__device__ __forceinline__ void interleave_reads_then_loads() {
-#pragma unroll
-  for (int t = 0; t < NM; ++t) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (t < NR) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    } else {
-      constexpr int kSlots = NM - NR;
-      const int c = ((t - NR + 1) * NV) / kSlots - ((t - NR) * NV) / kSlots;
-#pragma unroll
-      for (int q = 0; q < c; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-template <int EPI, int BN, int MODE>
-__global__ __launch_bounds__(256, 1) void gemm256_kernel(
-    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
-    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
-    int group) {
-  using TL = Tile256<BN>;
-  constexpr int NJ = TL::NJ, kStage = TL::Stage;
-  constexpr int WG = BN / 32;          // W row groups of 8 rows per wave
-  constexpr bool DMA = MODE != 1;
-  constexpr int NM = 4 * NJ, NR = 4 + NJ;  // MFMAs and fragment reads per step
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[TL::Smem];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  int m0, n0;
-  tile_origin(M, N, BN, n_major, group, m0, n0);
-
-  // this wave loads row groups g = wave + 4 i (8 rows each) of both tiles;
-  // lane L -> row g*8 + L/8, LDS chunk L%8, global chunk (L%8) ^ ((row>>1)&7)
-  const int d_row = lane >> 3;
-  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
-  const bf16_t* a_src[8];
-  const bf16_t* b_src[WG];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = (wave + 4 * i) * 8 + d_row;
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
-    if (i < WG) b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
-  }
-  // row groups [i0, i1) of the A tile and [i0 * WG / 8, i1 * WG / 8) of the W tile
-  auto issue = [&](int stage, int k0, int i0, int i1) {
-    bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
-#pragma unroll
-    for (int i = i0; i < i1; ++i) dma16(a_src[i] + k0, base + i * 32 * kBK);
-#pragma unroll
-    for (int i = i0 * WG / 8; i < i1 * WG / 8; ++i)
-      dma16(b_src[i] + k0, base + kT * kBK + i * 32 * kBK);
-  };
-  u32x4 ra[DMA ? 1 : 8], rb[DMA ? 1 : WG];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
-      ra[i] = *(const u32x4*)(a_src[i] + k0);
-      if (i < WG) rb[i] = *(const u32x4*)(b_src[i] + k0);
-    }
-  };
-  auto stash = [&](int stage) {
-    bf16_t* base = smem + stage * kStage + wave * 8 * kBK + lane * 8;
-#pragma unroll
-    for (int i = 0; i < (DMA ? 0 : 8); ++i) {
-      *(u32x4*)(base + i * 32 * kBK) = ra[i];
-      if (i < WG) *(u32x4*)(base + kT * kBK + i * 32 * kBK) = rb[i];
-    }
-  };
-
-  // fragments: lane reads row lane%32 of a 32-row block at K chunk
-  // kk*2 + lane/32, stored at chunk ^ ((row >> 1) & 7)
-  const int f_row = lane & 31, f_sw = (lane >> 1) & 7, f_hi = lane >> 5;
-  const int fa_row = (wm * 128 + f_row) * kBK;
-  const int fw_row = kT * kBK + (wn * (BN / 2) + f_row) * kBK;
-  bf16x8 fa[2][4], fw[2][NJ];
-  auto load_frags = [&](int stage, int kk, int slot) {
-    const bf16_t* base = smem + stage * kStage + (((kk * 2 + f_hi) ^ f_sw) * 8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      fa[slot][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kBK));
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      fw[slot][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kBK));
-  };
-
-  f32x16 acc[4][NJ];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
-  auto mfma_step = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x16(fw[slot][j], fa[slot][i], acc[i][j]);
-  };
-
-  constexpr int kLoads = 8 + WG;  // global loads per wave per K tile
-  const int KT = K / kBK;
-  if constexpr (DMA) {
-    issue(0, 0, 0, 8);
-  } else {
-    fetch(0);
-    stash(0);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  load_frags(0, 0, 0);
-  for (int kt = 0; kt < KT; ++kt) {
-    __builtin_amdgcn_sched_barrier(0);
-    const int stage = kt & 1;
-    // loads of the next tile (the last iteration re-fetches the final tile,
-    // keeping the loop body one basic block)
-    const int kn = min(kt + 1, KT - 1) * kBK;
-    if constexpr (MODE == 4) {
-      load_frags(stage, 1, 1);
-      issue(stage ^ 1, kn, 0, 4);
-      mfma_step(0);
-      interleave_reads_then_loads<NM, NR, kLoads / 2>();
-      load_frags(stage, 2, 0);
-      issue(stage ^ 1, kn, 4, 8);
-      mfma_step(1);
-      interleave_reads_then_loads<NM, NR, kLoads / 2>();
-    } else if constexpr (MODE == 2) {
-      issue(stage ^ 1, kn, 0, 4);
-      load_frags(stage, 1, 1);
-      mfma_step(0);
-      interleave_step<NM, NR, kLoads / 2, 0>();
-      issue(stage ^ 1, kn, 4, 8);
-      load_frags(stage, 2, 0);
-      mfma_step(1);
-      interleave_step<NM, NR, kLoads / 2, 0>();
-    } else {
-      if constexpr (DMA)
-        issue(stage ^ 1, kn, 0, 8);
-      else
-        fetch(kn);
-      load_frags(stage, 1, 1);
-      mfma_step(0);
-      interleave_step<NM, NR, kLoads, 0>();
-      load_frags(stage, 2, 0);
-      mfma_step(1);
-      interleave_step<NM, NR, 0, 0>();
-    }
-    load_frags(stage, 3, 1);
-    if constexpr (!DMA) stash(stage ^ 1);  // nobody reads the idle stage
-    mfma_step(0);
-    interleave_step<NM, NR, 0, DMA ? 0 : kLoads>();
-    // step 3: every read of this stage and the next tile's writes have
-    // completed once all waves pass the barrier; prefetch the next stage's
-    // step 0
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    load_frags(stage ^ 1, 0, 0);
-    mfma_step(1);
-    interleave_step<NM, NR, 0, 0>();
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  epilogue_tile<EPI, BN>(acc, smem, lane, wave, m0, n0, C, ldc, R, ldr, M, N);
-}
-
-template <int EPI, int BN, int MODE>
-int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
-  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
-  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
-  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
-  static const int group = [] {
-    const char* e = getenv("KAD_GEMM_GROUP");
-    return e ? atoi(e) : 8;
-  }();
-  hipLaunchKernelGGL((gemm256_kernel<EPI, BN, MODE>), dim3((unsigned)nblocks), dim3(256), 0, s,
-                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
-                     (const bf16_t*)R, ldr, M, N, K, n_major, group < 1 ? 1 : group);
-  return kad_launch_status("gemm256_kernel");
-}
-
-// Epilogue of one wave's (NI*32) x (NJ*32) sub-tile through a wave-private
-// LDS region: accumulators packed as bf16 (SwiGLU applied), then 16-byte row
-// stores with the residual add.  acc[i][j][e]: row i*32 + lane%32, column
-// j*32 + (e/4)*8 + (lane/32)*4 + e%4.  No workgroup barrier: the caller has
-// synchronised once after the main loop, and each wave only touches its own
-// region.
-template <int EPI, int NI, int NJ>
-__device__ __forceinline__ void epilogue_sub(f32x16 (&acc)[NI][NJ], bf16_t* ep, int lane,
-                                             int row0, int col0, bf16_t* C, int64_t ldc,
-                                             const bf16_t* R, int64_t ldr, int M, int N) {
-  constexpr int kCols = EPI == KAD_EPI_SWIGLU ? NJ * 16 : NJ * 32;  // output columns
-  constexpr int kLd = kCols + 8;
-  const int e_row = lane & 31, e_col = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    if constexpr (EPI == KAD_EPI_SWIGLU) {
-#pragma unroll
-      for (int j = 0; j < NJ; j += 2) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          u32x2 packed;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            uint32_t two = 0;
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const int e = g * 4 + h * 2 + q;
-              const float gv = round_bf(acc[i][j][e]);
-              const float uv = round_bf(acc[i][j + 1][e]);
-              two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
-            }
-            packed[h] = two;
-          }
-          *(u32x2*)(ep + (i * 32 + e_row) * kLd + (j / 2) * 32 + g * 8 + e_col) = packed;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          u32x2 packed;
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            packed[h] = (uint32_t)f2bf(acc[i][j][g * 4 + h * 2]) |
-                        ((uint32_t)f2bf(acc[i][j][g * 4 + h * 2 + 1]) << 16);
-          *(u32x2*)(ep + (i * 32 + e_row) * kLd + j * 32 + g * 8 + e_col) = packed;
-        }
-      }
-    }
-  }
-  // the wave's own LDS writes are visible to its later reads (in order)
-  constexpr int kChunks = kCols / 8, kRowsPer = 64 / kChunks;
-  const int c_row = lane / kChunks, c_col = (lane % kChunks) * 8;
-  const int n_out = EPI == KAD_EPI_SWIGLU ? N / 2 : N;
-#pragma unroll 4
-  for (int r = c_row; r < NI * 32; r += kRowsPer) {
-    const int row = row0 + r, col = col0 + c_col;
-    if (row >= M || col >= n_out) continue;
-    u32x4 v = *(const u32x4*)(ep + r * kLd + c_col);
-    if constexpr (EPI == KAD_EPI_RESIDUAL) {
-      const u32x4 rr = *(const u32x4*)(R + (int64_t)row * ldr + col);
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const float lo = __uint_as_float(rr[h] << 16) + __uint_as_float(v[h] << 16);
-        const float hi = __uint_as_float(rr[h] & 0xffff0000u) + __uint_as_float(v[h] & 0xffff0000u);
-        v[h] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-      }
-    }
-    *(u32x4*)(C + (int64_t)row * ldc + col) = v;
-  }
-}
-
-// The split-load schedule with 8 waves (2 per SIMD) on a 256 x BN tile:
-// waves WM (M) x 8/WM (N), each an (NI*32) x (NJ*32) sub-tile.  The second
-// wave of each SIMD issues its MFMAs while the other waits on its fragment
-// reads.  BN = 256: waves 2 x 4 of 128 x 64; BN = 128: waves 4 x 2 of 64 x 64.
-template <int BN>
-struct TileW8 {
-  static constexpr int NW = 8, WM = BN == 256 ? 2 : 4, WN = NW / WM;
-  static constexpr int NI = kT / WM / 32, NJ = BN / WN / 32;
-  static constexpr int Stage = (kT + BN) * kBK;
-  static constexpr int AG = (kT / 8) / NW, WGW = (BN / 8) / NW;   // 8-row groups per wave
-  static constexpr int EpiWave = NI * 32 * (NJ * 32 + 8);         // elements per wave
-  static constexpr int Smem = 2 * Stage > NW * EpiWave ? 2 * Stage : NW * EpiWave;
-};
-
-template <int EPI, int BN>
-__global__ __launch_bounds__(512, 1) void gemm256w8_kernel(
-    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
-    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
-    int group) {
-  using TW = TileW8<BN>;
-  constexpr int NW = TW::NW, WN = TW::WN, NI = TW::NI, NJ = TW::NJ;
-  constexpr int kStage = TW::Stage, AG = TW::AG, WGW = TW::WGW;
-  constexpr int kLoads = AG + WGW;
-  constexpr int NM = NI * NJ, NR = NI + NJ;
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[TW::Smem];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  int m0, n0;
-  tile_origin(M, N, BN, n_major, group, m0, n0);
-
-  // row groups g = wave + 8 i (8 rows each); lane L -> row g*8 + L/8, LDS
-  // chunk L%8 holding global chunk (L%8) ^ ((row>>1)&7)
-  const int d_row = lane >> 3;
-  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
-  const bf16_t* a_src[AG];
-  const bf16_t* b_src[WGW];
-#pragma unroll
-  for (int i = 0; i < AG; ++i) {
-    const int r = (wave + NW * i) * 8 + d_row;
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
-    if (i < WGW) b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
-  }
-  // A groups [i0, i1) and W groups [i0 * WGW / AG, i1 * WGW / AG)
-  auto issue = [&](int stage, int k0, int i0, int i1) {
-    bf16_t* base = smem + stage * kStage + wave * 8 * kBK;
-#pragma unroll
-    for (int i = i0; i < i1; ++i) dma16(a_src[i] + k0, base + i * NW * 8 * kBK);
-#pragma unroll
-    for (int i = i0 * WGW / AG; i < i1 * WGW / AG; ++i)
-      dma16(b_src[i] + k0, base + kT * kBK + i * NW * 8 * kBK);
-  };
-
-  const int f_row = lane & 31, f_sw = (lane >> 1) & 7, f_hi = lane >> 5;
-  const int fa_row = (wm * NI * 32 + f_row) * kBK;
-  const int fw_row = kT * kBK + (wn * NJ * 32 + f_row) * kBK;
-  bf16x8 fa[2][NI], fw[2][NJ];
-  auto load_frags = [&](int stage, int kk, int slot) {
-    const bf16_t* base = smem + stage * kStage + (((kk * 2 + f_hi) ^ f_sw) * 8);
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      fa[slot][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kBK));
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      fw[slot][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kBK));
-  };
-  f32x16 acc[NI][NJ];
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
-  auto mfma_step = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x16(fw[slot][j], fa[slot][i], acc[i][j]);
-  };
-
-  const int KT = K / kBK;
-  issue(0, 0, 0, AG);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  load_frags(0, 0, 0);
-  for (int kt = 0; kt < KT; ++kt) {
-    __builtin_amdgcn_sched_barrier(0);
-    const int stage = kt & 1;
-    const int kn = min(kt + 1, KT - 1) * kBK;
-    issue(stage ^ 1, kn, 0, AG / 2);
-    load_frags(stage, 1, 1);
-    mfma_step(0);
-    interleave_step<NM, NR, kLoads / 2, 0>();
-    issue(stage ^ 1, kn, AG / 2, AG);
-    load_frags(stage, 2, 0);
-    mfma_step(1);
-    interleave_step<NM, NR, kLoads / 2, 0>();
-    load_frags(stage, 3, 1);
-    mfma_step(0);
-    interleave_step<NM, NR, 0, 0>();
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    load_frags(stage ^ 1, 0, 0);
-    mfma_step(1);
-    interleave_step<NM, NR, 0, 0>();
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 32) / 2 : n0 + wn * NJ * 32;
-  epilogue_sub<EPI, NI, NJ>(acc, smem + wave * TW::EpiWave, lane, m0 + wm * NI * 32, col0, C,
-                            ldc, R, ldr, M, N);
-}
-
-template <int EPI, int BN>
-int launch_w8(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-              const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
-  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
-  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
-  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
-  hipLaunchKernelGGL((gemm256w8_kernel<EPI, BN>), dim3((unsigned)nblocks), dim3(512), 0, s,
-                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
-                     (const bf16_t*)R, ldr, M, N, K, n_major, 8);
-  return kad_launch_status("gemm256w8_kernel");
-}
-
-// 256 x BN tile fed through a ring of 4 LDS slots of 32-deep K slices.  The
-// loads of slice t + 3 are issued while slice t is consumed, half in each of
-// its two 16-deep steps and spread between MFMAs, so they have two slices of
-// time to land and never arrive in a burst.  One barrier per slice, in its
-// middle: past it, slice t + 1 has landed (each wave waits for its own loads
-// with a partial vmcnt, the barrier makes every wave's part visible) and
-// every wave has finished reading slice t - 1, whose slot the next loads
-// reuse.
-constexpr int kRK = 32;    // K depth of a slot
-constexpr int kRing = 4;   // slots
-
-template <int BN>
-struct Ring256 {
-  static constexpr int NJ = BN / 64;              // 32-column blocks per wave
-  static constexpr int WG = BN / 64;              // W 16-row groups per wave
-  static constexpr int Loads = 4 + WG;            // DMA instructions per wave per slot
-  static constexpr int Slot = (kT + BN) * kRK;    // elements per slot: A rows then W rows
-  static constexpr int Smem = kRing * Slot > 4 * 128 * Tile256<BN>::EpiLd
-                                  ? kRing * Slot
-                                  : 4 * 128 * Tile256<BN>::EpiLd;
-};
-
 // workgroup barrier without __syncthreads' wait for every outstanding load;
 // the empty asm statements keep LDS accesses on their side of it
 __device__ __forceinline__ void ring_barrier() {
@@ -743,122 +227,6 @@ __device__ __forceinline__ void ring_barrier() {
 // s_waitcnt vmcnt(n) lgkmcnt(0), expcnt not waited (vmcnt is bits 3:0 and
 // 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int wait_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
-
-template <int EPI, int BN>
-__global__ __launch_bounds__(256, 1) void gemm_ring_kernel(
-    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
-    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
-    int group) {
-  using RL = Ring256<BN>;
-  constexpr int NJ = RL::NJ, WG = RL::WG, kLoads = RL::Loads, kSlot = RL::Slot;
-  constexpr int NM = 4 * NJ, NR = 4 + NJ;   // MFMAs and fragment reads per step
-  constexpr int kHalf = kLoads / 2;
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[RL::Smem];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  int m0, n0;
-  tile_origin(M, N, BN, n_major, group, m0, n0);
-
-  // one DMA instruction fills 16 rows of 64 bytes; this wave loads the
-  // 16-row groups g = wave + 4 i of the A slice (i < 4) and of the W slice
-  // (i < WG).  Lane L -> row g*16 + L/4, LDS chunk L%4 holding global chunk
-  // (L%4) ^ (L/16): a row's 16-byte chunk c sits at c ^ ((row >> 2) & 3)
-  const int d_row = lane >> 2;
-  const int d_kc = ((lane & 3) ^ (lane >> 4)) * 8;
-  const bf16_t* a_src[4];
-  const bf16_t* b_src[WG];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (wave + 4 * i) * 16 + d_row;
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + d_kc;
-    if (i < WG) b_src[i] = Wt + (int64_t)min(n0 + r, N - 1) * ldw + d_kc;
-  }
-  // loads [j0, j1) of one slot: j < 4 are A groups, the rest W groups
-  auto issue = [&](int slot, int k0, int j0, int j1) {
-    bf16_t* base = smem + slot * kSlot + wave * 16 * kRK;
-#pragma unroll
-    for (int j = j0; j < j1; ++j) {
-      if (j < 4)
-        dma16(a_src[j] + k0, base + j * 64 * kRK);
-      else
-        dma16(b_src[j - 4] + k0, base + kT * kRK + (j - 4) * 64 * kRK);
-    }
-  };
-
-  // fragments: lane reads row lane%32 of a 32-row block at K chunk
-  // step*2 + lane/32, stored at chunk ^ ((row >> 2) & 3)
-  const int f_row = lane & 31, f_sw = (lane >> 2) & 3, f_hi = lane >> 5;
-  const int fa_row = (wm * 128 + f_row) * kRK;
-  const int fw_row = kT * kRK + (wn * (BN / 2) + f_row) * kRK;
-  bf16x8 fa[2][4], fw[2][NJ];
-  auto load_frags = [&](int slot, int step, int buf) {
-    const bf16_t* base = smem + slot * kSlot + (((step * 2 + f_hi) ^ f_sw) * 8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      fa[buf][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 32 * kRK));
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      fw[buf][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 32 * kRK));
-  };
-
-  f32x16 acc[4][NJ];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
-  auto mfma_step = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x16(fw[buf][j], fa[buf][i], acc[i][j]);
-  };
-
-  // past the last slice the loads re-fetch it, which keeps every
-  // iteration's wait counts the same
-  const int KT = K / kRK;
-  issue(0, 0, 0, kLoads);
-  issue(1, min(1, KT - 1) * kRK, 0, kLoads);
-  issue(2, min(2, KT - 1) * kRK, 0, kLoads);
-  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * kLoads));   // slice 0 landed
-  ring_barrier();
-  load_frags(0, 0, 0);
-  for (int t = 0; t < KT; ++t) {
-    __builtin_amdgcn_sched_barrier(0);
-    const int slot = t & (kRing - 1), slot3 = (t + 3) & (kRing - 1);
-    const int k3 = min(t + 3, KT - 1) * kRK;
-    load_frags(slot, 1, 1);
-    issue(slot3, k3, 0, kHalf);
-    mfma_step(0);
-    interleave_reads_then_loads<NM, NR, kHalf>();
-    // slice t + 1 landed: only slice t + 2's loads and the first half of
-    // slice t + 3's may still be in flight
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoads + kHalf));
-    ring_barrier();
-    load_frags((t + 1) & (kRing - 1), 0, 0);
-    issue(slot3, k3, kHalf, kLoads);
-    mfma_step(1);
-    interleave_reads_then_loads<NM, NR, kLoads - kHalf>();
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  epilogue_tile<EPI, BN>(acc, smem, lane, wave, m0, n0, C, ldc, R, ldr, M, N);
-}
-
-template <int EPI, int BN>
-int launch_ring(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
-  if (K % kRK) KAD_UNSUPPORTED("ring gemm needs K %% 32 == 0, got %d", K);
-  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
-  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
-  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
-  hipLaunchKernelGGL((gemm_ring_kernel<EPI, BN>), dim3((unsigned)nblocks), dim3(256), 0, s,
-                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
-                     (const bf16_t*)R, ldr, M, N, K, n_major, 8);
-  return kad_launch_status("gemm_ring_kernel");
-}
 
 // 16x16x32 MFMA form of the 8-wave tile.  mfma16x16x32(w, a, c): lane l
 // supplies row l%16 and K elements 8*(l/16) .. +7 of a 32-deep step of each
@@ -948,7 +316,7 @@ __device__ __forceinline__ void interleave_x16() {
     if (t < NR) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     } else if constexpr (NV > 0) {
-      constexpr int kSlots = NM - NR;
+      constexpr int kSlots = NM > NR ? NM - NR : 1;
       const int c = ((t - NR + 1) * NV) / kSlots - ((t - NR) * NV) / kSlots;
 #pragma unroll
       for (int q = 0; q < c; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
@@ -1331,14 +699,10 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
   return kad_launch_status("gemm_bf16_kernel");
 }
 
-// tile configurations (tile_config argument of kad_gemm_bf16_tiled)
-enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_128x256 = 3, CFG_256x256 = 4,
-       CFG_256x256_8W = 5, CFG_256x128_8W = 6, CFG_256x256_PIPE = 7, CFG_256x256_PIPE_REG = 8,
-       CFG_256x256_SPREAD = 9, CFG_256x128_PIPE = 10,
-       CFG_128x32 = 11, CFG_256x256_RDFIRST = 12, CFG_256x256_RING = 13, CFG_256x256_W8 = 14,
-       CFG_256x128_W8 = 15,
-       CFG_256x256_X16 = 16, CFG_256x128_X16 = 17, CFG_256x256_X16P = 18,
-       CFG_256x128_X16P = 19 };
+// tile configurations (tile_config argument of kad_gemm_bf16_tiled): the
+// forms the automatic choice uses; the numbers are part of the C ABI
+enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_128x32 = 11,
+       CFG_256x256_X16 = 16, CFG_256x128_X16 = 17, CFG_256x256_X16P = 18 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
@@ -1373,58 +737,19 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       if (EPI == KAD_EPI_SWIGLU) KAD_UNSUPPORTED("tile configuration 11 has no SwiGLU epilogue");
       return launch<128, 32, 4, 1, EPI == KAD_EPI_SWIGLU ? KAD_EPI_STORE : EPI>(
           A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_128x256: return launch<128, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_256x256: return launch<256, 256, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_8W:
       return launch<256, 256, 2, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_256x256_PIPE:
-    case CFG_256x256_PIPE_REG:
-    case CFG_256x256_SPREAD:
-    case CFG_256x128_PIPE:
-      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
-        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
-                        cfg);
-      if (cfg == CFG_256x256_PIPE)
-        return launch_tile<EPI, 256, 0>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      if (cfg == CFG_256x256_PIPE_REG)
-        return launch_tile<EPI, 256, 1>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      if (cfg == CFG_256x256_SPREAD)
-        return launch_tile<EPI, 256, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      return launch_tile<EPI, 128, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_256x256_W8:
-    case CFG_256x128_W8:
-      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
-        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
-                        cfg);
-      if (cfg == CFG_256x256_W8)
-        return launch_w8<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      return launch_w8<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_X16:
     case CFG_256x128_X16:
+    case CFG_256x256_X16P:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
                         cfg);
       if (cfg == CFG_256x256_X16)
         return launch_x16<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      return launch_x16<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_256x256_X16P:
-    case CFG_256x128_X16P:
-      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
-        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
-                        cfg);
-      if (cfg == CFG_256x256_X16P)
-        return launch_x16p<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      return launch_x16p<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_256x256_RDFIRST:
-    case CFG_256x256_RING:
-      if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
-        KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
-                        cfg);
-      if (cfg == CFG_256x256_RDFIRST)
-        return launch_tile<EPI, 256, 4>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      return launch_ring<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_256x128_8W:
-      return launch<256, 128, 4, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_256x128_X16)
+        return launch_x16<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      return launch_x16p<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     default: KAD_UNSUPPORTED("unknown gemm tile configuration %d", cfg);
   }
 }
