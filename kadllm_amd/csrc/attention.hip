@@ -26,6 +26,8 @@
 // sequence, keys are the same sequence's K/V and key j is visible to a row at
 // position p iff j <= p; no suffix.
 
+#include <type_traits>
+
 #include "kad_common.h"
 
 namespace {
@@ -548,12 +550,519 @@ int launch_attn2(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
   return kad_launch_status("attn2_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Head dim 256: one wave per 32 query rows over the whole head dim (128 rows
+// per workgroup, 4 waves, one per SIMD), software-pipelined over key tiles.
+// Iteration t runs the softmax of tile t on the VALU while the MFMAs of tile
+// t+1's scores S^T = K Q^T execute (interleaved step by step), then
+// O^T += V^T P^T for tile t, with the second half of tile t's exponentials
+// and the loads of tile t+3 between its MFMAs.  No wave depends on another's
+// scores, so the only barrier per tile is the one that frees an LDS stage.
+// K/V tiles move HBM -> LDS by global_load_lds_dwordx4 into a ring of 4
+// stages, three tiles ahead (per-lane source offsets computed once); the V^T
+// transpose reads are written as inline assembly with their own waits, so
+// that they do not wait for those loads (the compiler makes the
+// ds_read_b64_tr_b16 builtin wait for every LDS DMA in flight).  The
+// epilogue transposes O through LDS, so that the suffix V rows, the gate and
+// the output move as whole 512-byte rows.  Per row the arithmetic is fixed:
+// the score is one MFMA chain over the 256-d dot product, the suffix dot
+// products a sequential fp32 sum, whatever the launch shape.
+constexpr int kStages3 = 4;
+
+struct Attn3 {
+  static constexpr int D = 256, CPR = D / 8, ROWS = 128;
+  static constexpr int tile = kKeys2 * D, stage = 2 * tile;
+  static constexpr int LOADS = CPR / 8;               // DMA instructions per wave per K (or V) tile
+  static constexpr int EpiLd = D + 4;                 // fp32 row stride of the epilogue transpose
+  static constexpr int stage_bytes = kStages3 * stage * 2;
+  static constexpr int epi_bytes = ROWS * EpiLd * 4;
+  static constexpr int info_off = stage_bytes > epi_bytes ? stage_bytes : epi_bytes;  // bytes
+  static constexpr int kInfo = 16;                    // per-row words: 1/l, suffix weights, offsets
+  static constexpr int lds = info_off + ROWS * kInfo * 4;
+};
+
+// max and sum of a value over lanes l and l ^ 32 (both lanes get the same bits)
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// one ds_read_b64_tr_b16 whose result may be used only after an
+// s_waitcnt lgkmcnt(N) issued by the caller through tr_wait
+__device__ __forceinline__ u32x2 tr_read(const bf16_t* p) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"((uint32_t)(uintptr_t)p) : "memory");
+  return r;
+}
+// lgkmcnt(N) (vmcnt and expcnt not waited), tied to the fragment registers so
+// that their uses stay after it
+template <int N>
+__device__ __forceinline__ void tr_wait(u32x2& a, u32x2& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
+template <bool CAUSAL, int NSUF>
+__global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
+  constexpr int D = 256, KS = D / 16, DT = D / 32, ROWS = Attn3::ROWS, CPR = Attn3::CPR;
+  constexpr int LOADS = Attn3::LOADS;
+  static_assert(NSUF + 1 <= 10, "row info too small");
+  extern __shared__ __attribute__((aligned(1024))) bf16_t smem[];
+  __shared__ int redo;
+  float* info = (float*)((char*)smem + Attn3::info_off);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hi = lane >> 5, col = lane & 31;
+  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int qb_blk = lid % a.nqblk;
+  const int bk = lid / a.nqblk;
+  const int kh = bk % a.HK, b = bk / a.HK;
+  const int G = a.H / a.HK;
+  const int64_t rows_total = CAUSAL ? (int64_t)a.L * G : (int64_t)a.W * G * a.T;
+
+  // query row r of this (request, KV head): batch row n, suffix (or prompt)
+  // position t, head h
+  auto row_of = [&](int64_t r, int64_t& n, int& t, int& h) {
+    int g;
+    if (CAUSAL) {
+      t = (int)(r / G);
+      g = (int)(r % G);
+      n = b;
+    } else {
+      t = (int)(r % a.T);
+      const int64_t wg = r / a.T;
+      g = (int)(wg % G);
+      n = (int64_t)b * a.W + wg / G;
+    }
+    h = kh * G + g;
+  };
+  const int64_t r_lane = (int64_t)qb_blk * ROWS + wave * 32 + col;
+  int64_t n;
+  int t, h;
+  row_of(r_lane < rows_total ? r_lane : 0, n, t, h);
+  bf16x8 qf[KS];
+  {
+    const bf16_t* qrow = a.q + n * a.sq_n + (int64_t)t * a.sq_t + (int64_t)h * a.sq_h;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = as_bf16x8(*(const u32x4*)(qrow + s * 16 + hi * 8));
+  }
+  const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
+
+  // ---- prefix key range and the DMA plan: instruction k of a wave covers
+  // tile rows (wave + 4k) * 2 + lane / 32, 16-byte chunk lane % 32 of each
+  int kend = a.L;
+  if (CAUSAL) {
+    const int64_t rlast = min((int64_t)(qb_blk + 1) * ROWS, rows_total) - 1;
+    kend = (int)(rlast / G) + 1;
+  }
+  const int ntiles = (kend + kKeys2 - 1) / kKeys2;
+  const bf16_t* pkb = a.pk + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
+  const bf16_t* pvb = a.pv + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
+  const int d_row = lane / CPR, d_pc = lane % CPR;
+  int dk_off[LOADS], dv_off[LOADS];   // element offsets from the tile's first key
+#pragma unroll
+  for (int k = 0; k < LOADS; ++k) {
+    const int r = (wave + 4 * k) * (64 / CPR) + d_row;
+    dk_off[k] = r * (int)a.sp_l + (d_pc ^ (r & 15)) * 8;
+    dv_off[k] = r * (int)a.sp_l + (d_pc ^ ((r & 3) * 4)) * 8;
+  }
+  // loads of one tile: K and V row sources from the tile's first key (rows
+  // past the prefix, in its last tile, repeat its last key) and the wave's
+  // destination in the tile's stage
+  struct TileLoad {
+    const bf16_t* kb;
+    const bf16_t* vb;
+    bf16_t* dst;
+    bool full;
+    int k0;
+  };
+  auto tile_load = [&](int tile) {
+    TileLoad tl;
+    tl.k0 = tile * kKeys2;
+    tl.full = tl.k0 + kKeys2 <= a.L;
+    tl.kb = pkb + (int64_t)tl.k0 * a.sp_l;
+    tl.vb = pvb + (int64_t)tl.k0 * a.sp_l;
+    tl.dst = smem + (tile % kStages3) * Attn3::stage + wave * 64 * 8;
+    return tl;
+  };
+  auto issue_one = [&](const TileLoad& tl, int k) {
+    bf16_t* kd = tl.dst + k * 4 * 64 * 8;
+    if (tl.full) {
+      __builtin_amdgcn_global_load_lds((attn_global_t*)(tl.kb + dk_off[k]), (attn_lds_t*)kd, 16, 0,
+                                       0);
+      __builtin_amdgcn_global_load_lds((attn_global_t*)(tl.vb + dv_off[k]),
+                                       (attn_lds_t*)(kd + Attn3::tile), 16, 0, 0);
+    } else {
+      const int r = (wave + 4 * k) * (64 / CPR) + d_row;
+      const int64_t key = min(tl.k0 + r, a.L - 1);
+      __builtin_amdgcn_global_load_lds(
+          (attn_global_t*)(pkb + key * a.sp_l + (d_pc ^ (r & 15)) * 8), (attn_lds_t*)kd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (attn_global_t*)(pvb + key * a.sp_l + (d_pc ^ ((r & 3) * 4)) * 8),
+          (attn_lds_t*)(kd + Attn3::tile), 16, 0, 0);
+    }
+  };
+  auto issue = [&](int tile) {
+    const TileLoad tl = tile_load(tile);
+#pragma unroll
+    for (int k = 0; k < LOADS; ++k) issue_one(tl, k);
+  };
+  // K fragment offsets (A operand, 32 keys x 16 d; row col, logical chunk
+  // 2s + hi stored at chunk ^ (row & 15)) and V^T transpose-read offsets, as
+  // in attn2_kernel for head dim 256
+  int k_off[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) k_off[s] = col * D + ((2 * s + hi) ^ (col & 15)) * 8;
+  int v_off[4];
+  {
+    const int grp = lane >> 4, gi = lane & 15;
+    const int v_row = 4 * (grp >> 1) + (gi >> 2);
+    const int v_dq = (grp & 1) * 16 + (gi & 3) * 4;
+    const int v_sw = (v_row & 3) * 4;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int d = dt * 32 + v_dq;
+      v_off[dt] = v_row * D + (((d >> 3) ^ v_sw) * 8) + (d & 7);
+    }
+  }
+
+  // suffix scores (decode): sequential fp32 dot products over the head dim
+  float m_ref = -INFINITY;
+  float sc[NSUF];
+#pragma unroll
+  for (int j = 0; j < NSUF; ++j) sc[j] = -INFINITY;
+  if (!CAUSAL) {
+#pragma unroll
+    for (int j = 0; j < NSUF; ++j) {
+      if (j >= a.Tk) continue;
+      const bf16_t* krow = a.sk + n * a.ssk_n + (int64_t)j * a.ssk_t + (int64_t)kh * a.ssk_h;
+      float part = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 kb = as_bf16x8(*(const u32x4*)(krow + s * 16 + hi * 8));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part += (float)qf[s][i] * (float)kb[i];
+      }
+      part += __shfl_xor(part, 32, 64);
+      if (j <= t + a.qoff) {
+        sc[j] = part * sl2;
+        m_ref = fmaxf(m_ref, sc[j]);
+      }
+    }
+  }
+
+  // Softmax with a fixed reference, as attn2_kernel: p = 2^(s - m_ref), m_ref
+  // the first max the row sees; a row whose later scores exceed it by more
+  // than 2^64 makes the workgroup run the key loop again with its true max
+  // (so the first pass needs no clamp: its p can only exceed 2^64 when that
+  // pass is discarded).
+  float m_true = m_ref;
+  float l = 0.f;
+  f32x16 O[DT];
+  const int pos = t;
+  auto kfrag = [&](const bf16_t* ks, int s) {
+    return as_bf16x8(*(const u32x4*)(ks + k_off[s & 7] + (s >> 3) * 128));
+  };
+  for (int pass = 0; pass < 2; ++pass) {
+    bool overflow = false;
+    l = 0.f;
+#pragma unroll
+    for (int j = 0; j < NSUF; ++j)
+      if (sc[j] != -INFINITY) l += exp2f(sc[j] - m_ref);
+#pragma unroll
+    for (int i = 0; i < DT; ++i) O[i] = f32x16{};
+
+    if (ntiles > 0) {
+      issue(0);
+      if (ntiles > 1) issue(1);
+      if (ntiles > 2) issue(2);
+      // tile 0 landed (the later ones stay in flight)
+      if (ntiles > 2)
+        __builtin_amdgcn_s_waitcnt(0x0070 | ((4 * LOADS) & 0xF) | (((4 * LOADS) >> 4) << 14));
+      else if (ntiles > 1)
+        __builtin_amdgcn_s_waitcnt(0x0070 | ((2 * LOADS) & 0xF) | (((2 * LOADS) >> 4) << 14));
+      else
+        __builtin_amdgcn_s_waitcnt(0x0070);
+      tile_barrier();
+      f32x16 st0 = f32x16{}, st1 = f32x16{};
+      {
+        bf16x8 kf[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) kf[s] = kfrag(smem, s);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          st0 = mfma32x32x16(kf[s & 3], qf[s], st0);
+          if (s + 4 < KS) kf[s & 3] = kfrag(smem, s + 4);
+        }
+      }
+      // one key tile: st holds its scores; with kNext, the scores of tile + 1
+      // go to st_next.  Straight-line code apart from the rare prefix mask
+      // and the load issue, so that the accumulators keep their registers.
+      auto step = [&](const int tile, f32x16& st, f32x16& st_next, auto next_c) {
+        constexpr bool kNext = decltype(next_c)::value;
+        // tile + 1 landed (tile + 2 may still be in flight); every wave has
+        // finished iteration tile - 1, whose stage the loads of tile + 3 reuse
+        if (tile + 2 < ntiles)
+          __builtin_amdgcn_s_waitcnt(0x0070 | ((2 * LOADS) & 0xF) | (((2 * LOADS) >> 4) << 14));
+        else
+          __builtin_amdgcn_s_waitcnt(0x0070);
+        tile_barrier();
+        const int k0 = tile * kKeys2;
+        if (!CAUSAL && a.mask) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int kj = (j / 4) * 8 + (j % 4);
+            if (a.mask[(int64_t)b * a.L + min(k0 + hi * 4 + kj, a.L - 1)] == 0) st[j] = -INFINITY;
+          }
+        }
+        // keys of this tile a lane sees: k0 + hi*4 + kj, kj = (j/4)*8 + j%4 <= 27
+        const int lim = (CAUSAL ? min(kend - 1, pos) : kend - 1) - k0 - hi * 4;
+        bf16x8 pf[2];
+        float tmax = -INFINITY, tmax_o = 0.f, nm = 0.f, psum = 0.f;
+        // VALU work of score step s: masking and the row max over 4 scores
+        // (s < 4), the max across the half-waves (4, 5), then the
+        // exponentials of keys 0-7 (6..13); keys 8-15 follow in the PV steps
+        auto softmax_step = [&](int s) {
+          if (s < 4) {
+#pragma unroll
+            for (int j = 4 * s; j < 4 * s + 4; ++j) {
+              const int kj = (j / 4) * 8 + (j % 4);
+              st[j] = kj <= lim ? st[j] : -INFINITY;
+              tmax = fmaxf(tmax, st[j]);
+            }
+          } else if (s == 4) {
+            tmax_o = xor32_max(tmax);
+          } else if (s == 5) {
+            tmax = tmax_o * sl2;
+            m_ref = m_ref == -INFINITY ? tmax : m_ref;
+            m_true = fmaxf(m_true, tmax);
+            overflow |= tmax > m_ref + 64.0f;
+            nm = m_ref == -INFINITY ? 0.f : -m_ref;
+          } else if (s < 14) {
+            const int j = s - 6;
+            const float p = __builtin_amdgcn_exp2f(fmaf(st[j], sl2, nm));
+            psum += p;
+            pf[0][j] = (__bf16)p;
+          }
+        };
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kNext) {
+          const bf16_t* ks = smem + ((tile + 1) % kStages3) * Attn3::stage;
+          bf16x8 kf[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) kf[s] = kfrag(ks, s);
+          st_next = f32x16{};
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            st_next = mfma32x32x16(kf[s & 3], qf[s], st_next);
+            if (s + 4 < KS) kf[s & 3] = kfrag(ks, s + 4);
+            softmax_step(s);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+#pragma unroll
+          for (int s = 0; s < KS; ++s) softmax_step(s);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // the loads of tile + 3 go into the stage of tile - 1 (free since the
+        // barrier above), spread over the PV steps below so that the four
+        // waves' loads do not queue up at once; the transpose reads do not
+        // wait for them
+        const bool load3 = tile + 3 < ntiles;
+        const TileLoad tl3 = tile_load(tile + 3);
+
+        // ---- O^T[d, query] += V^T[d, keys] P^T[keys, query] for tile; k-step
+        // ks2 covers keys 16ks2 + {0-3, 8-11} (+4 for the upper half-wave);
+        // each fragment's two transpose reads go out three fragments ahead,
+        // and the exponentials of keys 8-15 run under the first 8 MFMAs
+        const bf16_t* vs = smem + (tile % kStages3) * Attn3::stage + Attn3::tile;
+        auto vaddr = [&](int f, int rd) {
+          const int ks2 = f / DT, dg = f % DT;
+          return vs + v_off[dg & 3] + (dg >> 2) * 128 + (16 * ks2 + 8 * rd) * D;
+        };
+        constexpr int NF = 2 * DT, AHEAD = 3;
+        u32x2 vlo[AHEAD + 1], vup[AHEAD + 1];
+#pragma unroll
+        for (int f = 0; f < AHEAD; ++f) {
+          vlo[f] = tr_read(vaddr(f, 0));
+          vup[f] = tr_read(vaddr(f, 1));
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const int cur = f % (AHEAD + 1);
+          if (f + AHEAD < NF) {
+            const int nxt = (f + AHEAD) % (AHEAD + 1);
+            vlo[nxt] = tr_read(vaddr(f + AHEAD, 0));
+            vup[nxt] = tr_read(vaddr(f + AHEAD, 1));
+            tr_wait<2 * AHEAD>(vlo[cur], vup[cur]);
+          } else if (f + 2 == NF) {
+            tr_wait<2>(vlo[cur], vup[cur]);
+          } else if (f + 1 == NF) {
+            tr_wait<0>(vlo[cur], vup[cur]);
+          } else {
+            tr_wait<4>(vlo[cur], vup[cur]);
+          }
+          const bf16x8 vf = as_bf16x8(u32x4{vlo[cur][0], vlo[cur][1], vup[cur][0], vup[cur][1]});
+          O[f % DT] = mfma32x32x16(vf, pf[f / DT], O[f % DT]);
+          if (f < 8) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(st[8 + f], sl2, nm));
+            psum += p;
+            pf[1][f] = (__bf16)p;
+          }
+          if (f == 8) l += xor32_sum(psum);
+          if (f % 4 == 2 && load3) issue_one(tl3, f / 4);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      using yes = std::integral_constant<bool, true>;
+      using no = std::integral_constant<bool, false>;
+      int tile = 0;
+      for (; tile + 2 < ntiles; tile += 2) {
+        step(tile, st0, st1, yes{});
+        step(tile + 1, st1, st0, yes{});
+      }
+      if (tile + 1 < ntiles) {
+        step(tile, st0, st1, yes{});
+        step(tile + 1, st1, st0, no{});
+      } else {
+        step(tile, st0, st1, no{});
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (tid == 0) redo = 0;
+    __syncthreads();
+    if (__ballot(overflow) != 0 && lane == 0) atomicOr(&redo, 1);
+    __syncthreads();
+    if (pass == 1 || redo == 0) break;
+    m_ref = m_true;
+    __syncthreads();
+  }
+
+  // ---- epilogue: O^T goes through LDS (the stages are free: every wave
+  // passed the barrier after its last load and read), then each wave writes
+  // its 32 rows one 512-byte row at a time, 4 elements per lane, 8 rows'
+  // loads in flight together: the suffix keys' V rows (decode), the
+  // normalisation, the gate, the store.  Row info (1/l, the suffix keys'
+  // weights, -1 for a key the row does not see, and the row's offsets) comes
+  // from the lane that owns the row.
+  float* ep = (float*)smem + wave * 32 * Attn3::EpiLd;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d0 = dt * 32 + gq * 8 + hi * 4;
+      *(f32x4*)(ep + col * Attn3::EpiLd + d0) =
+          f32x4{O[dt][gq * 4], O[dt][gq * 4 + 1], O[dt][gq * 4 + 2], O[dt][gq * 4 + 3]};
+    }
+  if (hi == 0) {
+    float* ri = info + (wave * 32 + col) * Attn3::kInfo;
+    ri[0] = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int j = 0; j < NSUF; ++j) ri[1 + j] = sc[j] == -INFINITY ? -1.f : exp2f(sc[j] - m_ref);
+    int64_t* ro = (int64_t*)(ri + 10);
+    ro[0] = n * a.so_n + (int64_t)t * a.so_t + (int64_t)h * a.so_h;
+    ro[1] = n * a.sg_n + (int64_t)t * a.sg_t + (int64_t)h * a.sg_h;
+    ro[2] = n * a.ssv_n + (int64_t)kh * a.ssv_h;
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): a wave reads only its own rows
+  const int d0 = lane * 4;
+  const int64_t row0 = (int64_t)qb_blk * ROWS + wave * 32;
+  const int nrows = (int)min<int64_t>(32, rows_total - row0);
+  const int tk = CAUSAL ? 0 : min(a.Tk, NSUF);
+  // rows of 4 elements per lane, 8 rows' loads in flight together; the
+  // gate's sigmoid takes the hardware reciprocal (1 ulp) in place of the
+  // IEEE divide, the bulk of this VALU-bound tail
+  auto rows = [&](auto gated_c) {
+    constexpr bool kGated = decltype(gated_c)::value;
+    constexpr int RB = 8;
+    for (int rb = 0; rb < nrows; rb += RB) {
+      u32x2 gv[RB], vv[RB][NSUF];
+      int64_t oo[RB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int rr = min(rb + i, nrows - 1);
+        const int64_t* ro = (const int64_t*)(info + (wave * 32 + rr) * Attn3::kInfo + 10);
+        oo[i] = ro[0];
+        if constexpr (kGated) gv[i] = *(const u32x2*)(a.gate + ro[1] + d0);
+#pragma unroll
+        for (int j = 0; j < NSUF; ++j)
+          if (j < tk) vv[i][j] = *(const u32x2*)(a.sv + ro[2] + (int64_t)j * a.ssv_t + d0);
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int rr = rb + i;
+        if (rr >= nrows) break;
+        const float* ri = info + (wave * 32 + rr) * Attn3::kInfo;
+        const f32x4 ov = *(const f32x4*)(ep + rr * Attn3::EpiLd + d0);
+        float o[4] = {ov[0], ov[1], ov[2], ov[3]};
+#pragma unroll
+        for (int j = 0; j < NSUF; ++j) {
+          if (j >= tk) break;
+          const float pj = ri[1 + j];   // -1: the key is not visible to the row
+          if (pj < 0.f) continue;
+          o[0] += pj * __uint_as_float(vv[i][j][0] << 16);
+          o[1] += pj * __uint_as_float(vv[i][j][0] & 0xffff0000u);
+          o[2] += pj * __uint_as_float(vv[i][j][1] << 16);
+          o[3] += pj * __uint_as_float(vv[i][j][1] & 0xffff0000u);
+        }
+        const float inv = ri[0];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = round_bf(o[e] * inv);
+        if constexpr (kGated) {
+          const float g4[4] = {__uint_as_float(gv[i][0] << 16),
+                               __uint_as_float(gv[i][0] & 0xffff0000u),
+                               __uint_as_float(gv[i][1] << 16),
+                               __uint_as_float(gv[i][1] & 0xffff0000u)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = o[e] * round_bf(__builtin_amdgcn_rcpf(1.0f + __expf(-g4[e])));
+        }
+        u32x2 packed;
+        packed[0] = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
+        packed[1] = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
+        *(u32x2*)(a.out + oo[i] + d0) = packed;
+      }
+    }
+  };
+  if (a.gate)
+    rows(std::integral_constant<bool, true>{});
+  else
+    rows(std::integral_constant<bool, false>{});
+}
+
+template <bool CAUSAL, int NSUF>
+int launch_attn3(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
+  if ((int64_t)kKeys2 * a.sp_l >= 0x7fffffff)
+    KAD_UNSUPPORTED("attention: prefix key stride %lld too large", (long long)a.sp_l);
+  a.nqblk = (int)kad_cdiv(rows, Attn3::ROWS);
+  const int64_t nblocks = bh * a.nqblk;
+  KAD_REQUIRE(nblocks < 0x7fffffff, "grid too large");
+  const size_t lds = Attn3::lds;
+  static bool configured = false;
+  if (!configured) {
+    if (hipFuncSetAttribute((const void*)attn3_kernel<CAUSAL, NSUF>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+      kad_set_error("attention: cannot reserve %zu bytes of LDS", lds);
+      return KAD_ERR_HIP;
+    }
+    configured = true;
+  }
+  hipLaunchKernelGGL((attn3_kernel<CAUSAL, NSUF>), dim3((unsigned)nblocks), dim3(kThreads), lds, s,
+                     a);
+  return kad_launch_status("attn3_kernel");
+}
+
 // rows: query rows per (request, KV head); bh: number of (request, KV head)
 // (the fold of up to 8 suffix keys is its own instantiation: a row's
 // arithmetic is the same in both, the keys past Tk scoring -inf)
 template <bool CAUSAL, int NSUF>
 int dispatch_d(int D, const AttnArgs& a, int64_t rows, int64_t bh, hipStream_t s) {
-  if (D == 256) return launch_attn2<256, CAUSAL, NSUF>(a, rows, bh, s);
+  if (D == 256) return launch_attn3<CAUSAL, NSUF>(a, rows, bh, s);
   if (D == 128) return launch_attn2<128, CAUSAL, NSUF>(a, rows, bh, s);
   if (D == 64) return launch_attn2<64, CAUSAL, NSUF>(a, rows, bh, s);
   KAD_UNSUPPORTED("attention supports head dim 64, 128, 256; got %d", D);
