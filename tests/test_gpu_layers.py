@@ -343,6 +343,36 @@ def test_prefix_attention_wide_score_range(device, D):
     assert_close_rel(out.cpu(), exp, rtol=1e-2, atol_frac=4e-3, name="wide-range attention")
 
 
+@pytest.mark.parametrize("B,W,T,L", [(2, 5, 6, 77), (1, 3, 8, 0), (2, 4, 5, 19), (1, 2, 2, 33)])
+def test_prefix_attention_d256_suffix_fold_and_ragged_prefix(device, B, W, T, L):
+    """Head dim 256 with the 8-key suffix fold (T > 4), no prefix, a prefix
+    shorter than one 32-key tile and ragged last tiles, against fp64."""
+    H, HK, D = 8, 2, 256
+    q, pk, pv, sk, sv = _attn_inputs(B, W, T, H, HK, L, D, seed=300 + L + T)
+    exp = ops_ref.prefix_attention(q, pk, pv, sk, sv, beam_width=W, compute=torch.float64)
+    dev = [t.to(device) for t in (q, pk, pv, sk, sv)]
+    out = ops.prefix_attention(*dev, beam_width=W)
+    torch.cuda.synchronize()
+    assert_close_rel(out.cpu(), exp, rtol=1e-2, atol_frac=4e-3, name="d256 attention")
+
+
+@pytest.mark.parametrize("Tk,Tq", [(5, 1), (7, 3), (3, 2)])
+def test_prefix_attention_d256_query_offset_is_bitwise(device, Tk, Tq):
+    """Queries that are the last Tq of Tk suffix tokens give, bit for bit, the
+    last Tq rows of the full Tk-token call: a row's arithmetic does not depend
+    on how many rows the launch holds (what the cached-suffix decode needs)."""
+    from kadllm_amd.attention import prefix_attention_decode
+    B, W, H, HK, L, D = 2, 6, 8, 2, 70, 256
+    q, pk, pv, sk, sv = _attn_inputs(B, W, Tk, H, HK, L, D, seed=400 + Tk)
+    gate = torch.randn(B * W, Tk, H * D, generator=torch.Generator().manual_seed(Tk)).bfloat16()
+    qd, pkd, pvd, skd, svd, gd = (t.to(device) for t in (q, pk, pv, sk, sv, gate))
+    full = prefix_attention_decode(qd, pkd, pvd, skd, svd, W, None, D ** -0.5, gate=gd)
+    tail = prefix_attention_decode(qd[:, Tk - Tq:].contiguous(), pkd, pvd, skd, svd, W, None,
+                                   D ** -0.5, gate=gd[:, Tk - Tq:].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(tail.cpu(), full[:, Tk - Tq:].cpu())
+
+
 @pytest.mark.parametrize("B,L,H,HK,D", [(2, 100, 8, 2, 256), (1, 1024, 8, 2, 256), (2, 37, 4, 1, 64)])
 def test_attention_prefill_causal(device, B, L, H, HK, D):
     g = torch.Generator().manual_seed(L)
