@@ -5,7 +5,9 @@
 // prefix taps (state[b, c, history-3 ..]) and the weights are read by every
 // beam of the request and stay in L2.  Rounding follows the reference torch
 // path: the convolution result is rounded to the tensor dtype, then SiLU is
-// applied and rounded again (for fp32 both roundings are exact).
+// applied and rounded again (for fp32 both roundings are exact).  The decode
+// kernels take SiLU with the hardware reciprocal (silu_fast: they are
+// VALU-bound); the prefill kernel keeps the IEEE divide.
 //
 // Two paths: a vectorised one when channels are contiguous in x and out
 // (8 channels per thread, 16-byte accesses; the [rows, T, C] layout produced by
@@ -43,7 +45,7 @@ __global__ __launch_bounds__(256) void conv_suffix_scalar(
         acc += ld(w + (int64_t)c * width + i) * xv;
       }
       float y = round_to_dtype(acc, Elem<T>::code);
-      if (silu) y = silu_f(y);
+      if (silu) y = silu_fast(y);
       out[n * so_n + (int64_t)c * so_c + (int64_t)t * so_t] = Elem<T>::from_f(y);
     }
     return;
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(256) void conv_suffix_scalar(
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc += wt[i] * win[i];
     float y = round_to_dtype(acc, Elem<T>::code);
-    if (silu) y = silu_f(y);
+    if (silu) y = silu_fast(y);
     out[n * so_n + (int64_t)c * so_c + (int64_t)t * so_t] = Elem<T>::from_f(y);
   }
 }
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc += wt[ch][i] * win[ch][i];
         float y = round_bf(acc);
-        if (silu) y = silu_f(y);
+        if (silu) y = silu_fast(y);
         packed |= (uint32_t)f2bf(y) << (16 * hh);
       }
       o[e] = packed;

@@ -4,7 +4,8 @@
 // reference decode calls (src/kadllm/adapters/qwen3_5.py:161-176,184-189,
 // 216-226,234-235):
 //   rmsnorm        Qwen3_5RMSNorm: y = bf16(x * rsqrt(mean x^2 + eps) * (1 + w))
-//   rmsnorm_gated  Qwen3_5RMSNormGated: y = bf16(bf16(w * bf16(x r)) * silu(z))
+//   rmsnorm_gated  Qwen3_5RMSNormGated: y = bf16(bf16(w * bf16(x r)) * silu(z)), SiLU
+//                  with the hardware reciprocal (the kernel is VALU-bound)
 //   gdn_gates      g = -exp(A_log) softplus(a + dt_bias) (fp32); beta = bf16(sigmoid(b))
 //   qk_norm_rope   per-head RMSNorm(1+w) then rotate-half RoPE on the first
 //                  `rot` dims with bf16 cos/sin, every op rounded to bf16
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(
     for (int i = 0; i < 8; ++i) {
       const float nrm = round_bf(f[i] * r);
       const float wn = round_bf(wv[i] * nrm);
-      f[i] = wn * silu_f(zv[i]);
+      f[i] = wn * silu_fast(zv[i]);
     }
     *(u32x4*)(y + tok * ldy + (int64_t)hh * D + off) = pack8(f);
   }
