@@ -104,10 +104,11 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
 /* Same with an explicit tile configuration, the forms the automatic choice
  * picks from (0 = automatic choice as kad_gemm_bf16; 1 = 32x256 with 4 waves;
  * 2 = 128x128 with 4 waves; 5 = 256x256 with 8 waves; 11 = 128x32 with 4
- * waves, no SwiGLU epilogue; 16 = 256x256 and 17 = 256x128 with 8 waves on
- * 16x16x32 MFMAs, direct-to-LDS loads and a 16-byte store epilogue, which
- * needs 16-byte aligned C (and R) with ldc, ldr and the output width multiples
- * of 8; 18 = 16 persistent, one workgroup per CU walking the tiles).  Every
+ * waves, no SwiGLU epilogue; 16 = 256x256 with 8 waves on 16x16x32 MFMAs,
+ * direct-to-LDS loads and a 16-byte store epilogue, which needs 16-byte
+ * aligned C (and R) with ldc, ldr and the output width multiples of 8;
+ * 18 = 16 persistent, one workgroup per CU walking the tiles; 19 = 16's
+ * design on 128x128 tiles with 4 waves, two workgroups per CU).  Every
  * configuration accumulates K in the same order, so all give bit-identical
  * results; other numbers are rejected (KAD_ERR_UNSUPPORTED). */
 int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,

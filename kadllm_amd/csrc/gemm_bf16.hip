@@ -191,25 +191,25 @@ constexpr int kT = 256;
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
 
-// Origin of this workgroup's 256 x BN tile.  Grouped order: `group`
+// Origin of this workgroup's BM x BN tile.  Grouped order: `group`
 // consecutive tiles along the outer dimension share each inner-dimension
 // tile, so an XCD's resident tiles form a 2-D block and both operands are
 // reused from its L2.
-__device__ __forceinline__ void tile_origin_of(int lid, int M, int N, int BN, int n_major,
+__device__ __forceinline__ void tile_origin_of(int lid, int M, int N, int BM, int BN, int n_major,
                                               int group, int& m0, int& n0) {
-  const int mtiles = (M + kT - 1) / kT, ntiles = (N + BN - 1) / BN;
+  const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN;
   const int nx = n_major ? ntiles : mtiles, ny = n_major ? mtiles : ntiles;
   const int gx0 = (lid / (group * ny)) * group, gs = min(nx - gx0, group);
   const int within = lid % (group * ny);
   const int tx = gx0 + within % gs, ty = within / gs;
   const int mi = n_major ? ty : tx, ni = n_major ? tx : ty;
-  m0 = mi * kT;
+  m0 = mi * BM;
   n0 = ni * BN;
 }
 
-__device__ __forceinline__ void tile_origin(int M, int N, int BN, int n_major, int group, int& m0,
-                                           int& n0) {
-  tile_origin_of(xcd_logical_id(blockIdx.x, gridDim.x), M, N, BN, n_major, group, m0, n0);
+__device__ __forceinline__ void tile_origin(int M, int N, int BM, int BN, int n_major, int group,
+                                           int& m0, int& n0) {
+  tile_origin_of(xcd_logical_id(blockIdx.x, gridDim.x), M, N, BM, BN, n_major, group, m0, n0);
 }
 
 __device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
@@ -228,21 +228,27 @@ __device__ __forceinline__ void ring_barrier() {
 // 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int wait_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
 
-// 16x16x32 MFMA form of the 8-wave tile.  mfma16x16x32(w, a, c): lane l
-// supplies row l%16 and K elements 8*(l/16) .. +7 of a 32-deep step of each
-// operand; acc[i][j][e] then holds output row i*16 + l%16, column
+// 16x16x32 MFMA tiles: BM x BN per workgroup, WM x WN waves (an even count,
+// so that a wave's DMA rows keep its swizzle phase).  mfma16x16x32(w, a, c):
+// lane l supplies row l%16 and K elements 8*(l/16) .. +7 of a 32-deep step of
+// each operand; acc[i][j][e] then holds output row i*16 + l%16, column
 // j*16 + 4*(l/16) + e of the wave's sub-tile (4 consecutive columns per lane).
+// 256 x 256 with 2 x 4 waves is the large-shape tile (two waves per SIMD);
+// 128 x 128 with 2 x 2 waves runs two workgroups per CU (64 KB of LDS each),
+// whose barriers then do not stall each other.
 
-template <int BN>
+template <int BM_, int BN_, int WM_, int WN_>
 struct TileX16 {
-  static constexpr int NW = 8, WM = BN == 256 ? 2 : 4, WN = NW / WM;
-  static constexpr int NI = kT / WM / 16, NJ = BN / WN / 16;      // 16 x 16 blocks per wave
-  static constexpr int Stage = (kT + BN) * kBK;
-  static constexpr int AG = (kT / 8) / NW, WGW = (BN / 8) / NW;   // 8-row groups per wave
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NW = WM * WN;
+  static constexpr int NI = BM / WM / 16, NJ = BN / WN / 16;      // 16 x 16 blocks per wave
+  static constexpr int Stage = (BM + BN) * kBK;
+  static constexpr int AG = (BM / 8) / NW, WGW = (BN / 8) / NW;   // 8-row groups per wave
   static constexpr int Cols = NJ * 16;                            // wave sub-tile columns
   static constexpr int EpiWave = NI * 16 * (Cols + 8);
   static constexpr int Smem = 2 * Stage > NW * EpiWave ? 2 * Stage : NW * EpiWave;
+  static_assert(NW % 2 == 0 && AG * NW * 8 == BM && WGW * NW * 8 == BN, "tile/wave mismatch");
 };
+using Tile256 = TileX16<256, 256, 2, 4>;
 
 // Epilogue of one wave's (NI*16) x (NJ*16) sub-tile through a wave-private LDS
 // region, as epilogue_sub.  SwiGLU: the sub-tile's columns are whole 64-column
@@ -333,12 +339,12 @@ __device__ __forceinline__ void interleave_x16() {
 // stage at once, and step 1's MFMAs cover them and the next tile's step-0
 // fragment reads.  (With the barrier in the middle of step 1, only 16 MFMAs
 // per wave followed it: 3.6% slower over the search's shapes.)
-template <int EPI, int BN>
-__global__ __launch_bounds__(512, 1) void gemm_x16_kernel(
+template <int EPI, class TX>
+__global__ __launch_bounds__(64 * TX::NW) void gemm_x16_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
     bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
     int group) {
-  using TX = TileX16<BN>;
+  constexpr int BM = TX::BM, BN = TX::BN;
   constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
   constexpr int kStage = TX::Stage, AG = TX::AG, WGW = TX::WGW;
   constexpr int kLoads = AG + WGW;
@@ -349,7 +355,7 @@ __global__ __launch_bounds__(512, 1) void gemm_x16_kernel(
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   int m0, n0;
-  tile_origin(M, N, BN, n_major, group, m0, n0);
+  tile_origin(M, N, BM, BN, n_major, group, m0, n0);
 
   // row groups g = wave + 8 i (8 rows each); lane L -> row g*8 + L/8, LDS
   // chunk L%8 holding global chunk (L%8) ^ ((row>>1)&7)
@@ -371,14 +377,14 @@ __global__ __launch_bounds__(512, 1) void gemm_x16_kernel(
 #pragma unroll
     for (int i = 0; i < AG; ++i) dma16(a_base + (a_off[i] + k0), base + i * NW * 8 * kBK);
 #pragma unroll
-    for (int i = 0; i < WGW; ++i) dma16(b_base + (b_off[i] + k0), base + kT * kBK + i * NW * 8 * kBK);
+    for (int i = 0; i < WGW; ++i) dma16(b_base + (b_off[i] + k0), base + BM * kBK + i * NW * 8 * kBK);
   };
 
   // fragment lane l: row block_base + l%16, chunk 4*step + l/16, stored at
   // chunk ^ ((row >> 1) & 7)
   const int f_row = lane & 15, f_sw = (lane & 15) >> 1, f_q = lane >> 4;
   const int fa_row = (wm * NI * 16 + f_row) * kBK;
-  const int fw_row = kT * kBK + (wn * NJ * 16 + f_row) * kBK;
+  const int fw_row = BM * kBK + (wn * NJ * 16 + f_row) * kBK;
   bf16x8 fa[2][NI], fw[2][NJ];
   auto load_frags = [&](int stage, int step, int buf) {
     const bf16_t* base = smem + stage * kStage + (((step * 4 + f_q) ^ f_sw) * 8);
@@ -434,15 +440,15 @@ __global__ __launch_bounds__(512, 1) void gemm_x16_kernel(
                             ldc, R, ldr, M, N);
 }
 
-template <int EPI, int BN>
+template <int EPI, class TX>
 int launch_x16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
                const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
-  const int64_t nblocks = kad_cdiv(M, kT) * kad_cdiv(N, BN);
+  const int64_t nblocks = kad_cdiv(M, TX::BM) * kad_cdiv(N, TX::BN);
   if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
-  if ((int64_t)kT * (lda > ldw ? lda : ldw) + K >= 0x7fffffff)
+  if ((int64_t)TX::BM * (lda > ldw ? lda : ldw) + K >= 0x7fffffff)
     KAD_UNSUPPORTED("gemm rows too long for 32-bit tile offsets");
   const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
-  hipLaunchKernelGGL((gemm_x16_kernel<EPI, BN>), dim3((unsigned)nblocks), dim3(512), 0, s,
+  hipLaunchKernelGGL((gemm_x16_kernel<EPI, TX>), dim3((unsigned)nblocks), dim3(64 * TX::NW), 0, s,
                      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
                      (const bf16_t*)R, ldr, M, N, K, n_major, 8);
   return kad_launch_status("gemm_x16_kernel");
@@ -521,7 +527,7 @@ __global__ __launch_bounds__(512, 1) void gemm_x16p_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
     bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
     int group, int ntiles) {
-  using TX = TileX16<BN>;
+  using TX = TileX16<256, BN, 2, 4>;
   constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
   constexpr int kStage = TX::Stage, AG = TX::AG, WGW = TX::WGW;
   constexpr int kLoads = AG + WGW;
@@ -538,7 +544,7 @@ __global__ __launch_bounds__(512, 1) void gemm_x16p_kernel(
   const int my_slices = my_tiles * KT;
   auto origin = [&](int r, int& m0, int& n0) {
     const int v = (int)blockIdx.x + r * (int)gridDim.x;
-    tile_origin_of(xcd_logical_id(v, ntiles), M, N, BN, n_major, group, m0, n0);
+    tile_origin_of(xcd_logical_id(v, ntiles), M, N, kT, BN, n_major, group, m0, n0);
   };
 
   // DMA rows: groups g = wave + 8 i (8 rows each); lane L -> row g*8 + L/8,
@@ -702,7 +708,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled): the
 // forms the automatic choice uses; the numbers are part of the C ABI
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_128x32 = 11,
-       CFG_256x256_X16 = 16, CFG_256x128_X16 = 17, CFG_256x256_X16P = 18 };
+       CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
@@ -711,11 +717,13 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     // the 8-wave 256x256 kernel on 16x16x32 MFMAs when its tiles still fill
     // every CU (and the output suits 16-byte stores), persistent except for
     // the SwiGLU epilogue, where both forms measured the same; then the
-    // 256x128 variant; 128x32 for outputs of at most 32 columns (the GDN gate
-    // projection); 128x128 otherwise (all measured on the decode/prefill
-    // shapes)
+    // 128x128 form, two workgroups per CU, when its tiles fill two rounds
+    // (N = 1,024 at M = 8,192: 5-7% faster than 8-wave 256x128 tiles, and
+    // 14% slower than 256x256 where those fill the chip); 128x32 for outputs
+    // of at most 32 columns (the GDN gate projection); the register-staged
+    // 128x128 kernel otherwise (all measured on the decode/prefill shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
-    const int64_t tiles128 = kad_cdiv(M, 256) * kad_cdiv(N, 128);
+    const int64_t tiles128 = kad_cdiv(M, 128) * kad_cdiv(N, 128);
     const bool vec = vector_epilogue_ok(C, ldc, R, ldr, N, EPI);
     if (M <= 64)
       cfg = CFG_32x256;
@@ -725,8 +733,8 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       cfg = CFG_256x256_8W;
     else if (tiles256 >= 256)
       cfg = EPI == KAD_EPI_SWIGLU ? CFG_256x256_X16 : CFG_256x256_X16P;
-    else if (vec && tiles128 >= 256)
-      cfg = CFG_256x128_X16;
+    else if (vec && tiles128 >= 512)
+      cfg = CFG_128x128_X16;
     else
       cfg = CFG_128x128;
   }
@@ -740,15 +748,16 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_256x256_8W:
       return launch<256, 256, 2, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_X16:
-    case CFG_256x128_X16:
     case CFG_256x256_X16P:
+    case CFG_128x128_X16:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
                         cfg);
       if (cfg == CFG_256x256_X16)
-        return launch_x16<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      if (cfg == CFG_256x128_X16)
-        return launch_x16<EPI, 128>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+        return launch_x16<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_128x128_X16)
+        return launch_x16<EPI, TileX16<128, 128, 2, 2>>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K,
+                                                        s);
       return launch_x16p<EPI, 256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     default: KAD_UNSUPPORTED("unknown gemm tile configuration %d", cfg);
   }
