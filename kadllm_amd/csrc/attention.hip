@@ -576,9 +576,7 @@ struct Attn3 {
   static constexpr int EpiLd = D + 4;                 // fp32 row stride of the epilogue transpose
   static constexpr int stage_bytes = kStages3 * stage * 2;
   static constexpr int epi_bytes = ROWS * EpiLd * 4;
-  static constexpr int info_off = stage_bytes > epi_bytes ? stage_bytes : epi_bytes;  // bytes
-  static constexpr int kInfo = 16;                    // per-row words: 1/l, suffix weights, offsets
-  static constexpr int lds = info_off + ROWS * kInfo * 4;
+  static constexpr int lds = stage_bytes > epi_bytes ? stage_bytes : epi_bytes;  // bytes
 };
 
 // max and sum of a value over lanes l and l ^ 32 (both lanes get the same bits)
@@ -611,10 +609,8 @@ template <bool CAUSAL, int NSUF>
 __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
   constexpr int D = 256, KS = D / 16, DT = D / 32, ROWS = Attn3::ROWS, CPR = Attn3::CPR;
   constexpr int LOADS = Attn3::LOADS;
-  static_assert(NSUF + 1 <= 10, "row info too small");
   extern __shared__ __attribute__((aligned(1024))) bf16_t smem[];
   __shared__ int redo;
-  float* info = (float*)((char*)smem + Attn3::info_off);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hi = lane >> 5, col = lane & 31;
@@ -947,9 +943,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
   // passed the barrier after its last load and read), then each wave writes
   // its 32 rows one 512-byte row at a time, 4 elements per lane, 8 rows'
   // loads in flight together: the suffix keys' V rows (decode), the
-  // normalisation, the gate, the store.  Row info (1/l, the suffix keys'
-  // weights, -1 for a key the row does not see, and the row's offsets) comes
-  // from the lane that owns the row.
+  // normalisation, the gate, the store.  A row's scalars (1/l, the suffix
+  // keys' weights, its offsets) come from the lane that owns it by readlane,
+  // and the code is branch-free but for the store of rows past the end.
   float* ep = (float*)smem + wave * 32 * Attn3::EpiLd;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -959,26 +955,34 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
       *(f32x4*)(ep + col * Attn3::EpiLd + d0) =
           f32x4{O[dt][gq * 4], O[dt][gq * 4 + 1], O[dt][gq * 4 + 2], O[dt][gq * 4 + 3]};
     }
-  if (hi == 0) {
-    float* ri = info + (wave * 32 + col) * Attn3::kInfo;
-    ri[0] = l > 0.f ? 1.0f / l : 0.f;
+  // this lane's row: 1/l, the suffix weights (0 for a key the row does not
+  // see) and the offsets of its output, gate and suffix V rows
+  const float inv_l = l > 0.f ? 1.0f / l : 0.f;
+  float pw[NSUF];
 #pragma unroll
-    for (int j = 0; j < NSUF; ++j) ri[1 + j] = sc[j] == -INFINITY ? -1.f : exp2f(sc[j] - m_ref);
-    int64_t* ro = (int64_t*)(ri + 10);
-    ro[0] = n * a.so_n + (int64_t)t * a.so_t + (int64_t)h * a.so_h;
-    ro[1] = n * a.sg_n + (int64_t)t * a.sg_t + (int64_t)h * a.sg_h;
-    ro[2] = n * a.ssv_n + (int64_t)kh * a.ssv_h;
-  }
+  for (int j = 0; j < NSUF; ++j) pw[j] = sc[j] == -INFINITY ? 0.f : exp2f(sc[j] - m_ref);
+  const int64_t off_o = n * a.so_n + (int64_t)t * a.so_t + (int64_t)h * a.so_h;
+  const int64_t off_g = n * a.sg_n + (int64_t)t * a.sg_t + (int64_t)h * a.sg_h;
+  const int64_t off_v = n * a.ssv_n + (int64_t)kh * a.ssv_h;
+  auto row_i64 = [&](int64_t v, int r) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, r);
+    const uint32_t hi32 = __builtin_amdgcn_readlane((uint32_t)(v >> 32), r);
+    return (int64_t)(((uint64_t)hi32 << 32) | lo);
+  };
+  // the builtin takes and returns int: a float goes through as its bits
+  auto lane_f32 = [](float v, int r) {
+    return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), r));
+  };
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): a wave reads only its own rows
   const int d0 = lane * 4;
   const int64_t row0 = (int64_t)qb_blk * ROWS + wave * 32;
   const int nrows = (int)min<int64_t>(32, rows_total - row0);
   const int tk = CAUSAL ? 0 : min(a.Tk, NSUF);
-  // rows of 4 elements per lane, 8 rows' loads in flight together; the
-  // gate's sigmoid takes the hardware reciprocal (1 ulp) in place of the
-  // IEEE divide, the bulk of this VALU-bound tail
-  auto rows = [&](auto gated_c) {
+  // the gate's sigmoid takes the hardware reciprocal (1 ulp) in place of
+  // the IEEE divide, the bulk of this VALU-bound tail
+  auto rows = [&](auto gated_c, auto suffix_c) {
     constexpr bool kGated = decltype(gated_c)::value;
+    constexpr bool kSuffix = decltype(suffix_c)::value;
     constexpr int RB = 8;
     for (int rb = 0; rb < nrows; rb += RB) {
       u32x2 gv[RB], vv[RB][NSUF];
@@ -986,31 +990,31 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const int rr = min(rb + i, nrows - 1);
-        const int64_t* ro = (const int64_t*)(info + (wave * 32 + rr) * Attn3::kInfo + 10);
-        oo[i] = ro[0];
-        if constexpr (kGated) gv[i] = *(const u32x2*)(a.gate + ro[1] + d0);
+        oo[i] = row_i64(off_o, rr);
+        if constexpr (kGated) gv[i] = *(const u32x2*)(a.gate + row_i64(off_g, rr) + d0);
+        if constexpr (kSuffix) {
+          const bf16_t* vrow = a.sv + row_i64(off_v, rr) + d0;
 #pragma unroll
-        for (int j = 0; j < NSUF; ++j)
-          if (j < tk) vv[i][j] = *(const u32x2*)(a.sv + ro[2] + (int64_t)j * a.ssv_t + d0);
+          for (int j = 0; j < NSUF; ++j)   // keys past Tk repeat the last one (weight 0)
+            vv[i][j] = *(const u32x2*)(vrow + (int64_t)min(j, tk - 1) * a.ssv_t);
+        }
       }
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
-        const int rr = rb + i;
-        if (rr >= nrows) break;
-        const float* ri = info + (wave * 32 + rr) * Attn3::kInfo;
+        const int rr = min(rb + i, nrows - 1);
         const f32x4 ov = *(const f32x4*)(ep + rr * Attn3::EpiLd + d0);
         float o[4] = {ov[0], ov[1], ov[2], ov[3]};
+        if constexpr (kSuffix) {
 #pragma unroll
-        for (int j = 0; j < NSUF; ++j) {
-          if (j >= tk) break;
-          const float pj = ri[1 + j];   // -1: the key is not visible to the row
-          if (pj < 0.f) continue;
-          o[0] += pj * __uint_as_float(vv[i][j][0] << 16);
-          o[1] += pj * __uint_as_float(vv[i][j][0] & 0xffff0000u);
-          o[2] += pj * __uint_as_float(vv[i][j][1] << 16);
-          o[3] += pj * __uint_as_float(vv[i][j][1] & 0xffff0000u);
+          for (int j = 0; j < NSUF; ++j) {
+            const float pj = lane_f32(pw[j], rr);
+            o[0] += pj * __uint_as_float(vv[i][j][0] << 16);
+            o[1] += pj * __uint_as_float(vv[i][j][0] & 0xffff0000u);
+            o[2] += pj * __uint_as_float(vv[i][j][1] << 16);
+            o[3] += pj * __uint_as_float(vv[i][j][1] & 0xffff0000u);
+          }
         }
-        const float inv = ri[0];
+        const float inv = lane_f32(inv_l, rr);
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = round_bf(o[e] * inv);
         if constexpr (kGated) {
@@ -1025,14 +1029,17 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
         u32x2 packed;
         packed[0] = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
         packed[1] = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
-        *(u32x2*)(a.out + oo[i] + d0) = packed;
+        if (rb + i < nrows) *(u32x2*)(a.out + oo[i] + d0) = packed;
       }
     }
   };
-  if (a.gate)
-    rows(std::integral_constant<bool, true>{});
-  else
-    rows(std::integral_constant<bool, false>{});
+  using yes = std::integral_constant<bool, true>;
+  using no = std::integral_constant<bool, false>;
+  if (a.gate) {
+    if (tk > 0) rows(yes{}, yes{}); else rows(yes{}, no{});
+  } else {
+    if (tk > 0) rows(no{}, yes{}); else rows(no{}, no{});
+  }
 }
 
 template <bool CAUSAL, int NSUF>
