@@ -120,28 +120,51 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
 
   // ---- k rows (normalised into LDS) and the q row scales: wave w handles
   // rows 16w..16w+15, RPI rows per instruction (lane -> row lane / CPR,
-  // 16-byte slice lane % CPR)
+  // 16-byte slice lane % CPR).  Every load (rows past the sequence end read
+  // its last row and are zeroed) goes out before the first use, so the
+  // chunk pays one memory round trip.
   {
+    constexpr int NIT = 16 / RPI;
     const int rsub = lane / CPR, ch = lane % CPR;
+    u32x4 kr[NIT], qr[NIT];
 #pragma unroll
-    for (int it = 0; it < 16 / RPI; ++it) {
+    for (int it = 0; it < NIT; ++it) {
       const int i = wave * 16 + it * RPI + rsub;
-      const bool live = i < nt;
-      const int64_t off = ((int64_t)n * T + t0 + (live ? i : 0)) * ld_qk + (int64_t)h * K + ch * 8;
-      u32x4 kr = live ? *(const u32x4*)(k + off) : u32x4{0, 0, 0, 0};
-      const u32x4 qr = live ? *(const u32x4*)(q + off) : u32x4{0, 0, 0, 0};
-      const float kss = row_sumsq<CPR>(kr, hf_norm);
-      const float qss = row_sumsq<CPR>(qr, hf_norm);
+      const int64_t off = ((int64_t)n * T + t0 + min(i, nt - 1)) * ld_qk + (int64_t)h * K + ch * 8;
+      kr[it] = *(const u32x4*)(k + off);
+      qr[it] = *(const u32x4*)(q + off);
+    }
+    // the gate scalars after the rows: their dtype conversion waits on them
+    const int gt = min(tid, nt - 1);
+    const int64_t gi = ((int64_t)n * T + t0 + gt) * ld_gate + hv;
+    float gv = 0.f, bv = 0.f;
+    if (tid < kC) {
+      gv = load_as_float(g, gi, gdt);
+      bv = load_as_float(beta, gi, bdt);
+    }
+    if (tid < kC) {
+      Gs[tid] = tid < nt ? gv : 0.f;
+      bt[tid] = tid < nt ? bv : 0.f;
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int i = wave * 16 + it * RPI + rsub;
+      if (i >= nt) {
+        kr[it] = u32x4{0, 0, 0, 0};
+        qr[it] = u32x4{0, 0, 0, 0};
+      }
+      const float kss = row_sumsq<CPR>(kr[it], hf_norm);
+      const float qss = row_sumsq<CPR>(qr[it], hf_norm);
       float km = 1.f, kr_s = 1.f, qr_s = 1.f, qm = scale;
       if (hf_norm) {
         kr_s = hf_l2_rs(kss);
         qr_s = hf_l2_rs(qss);
-        hf_l2_apply(kr, kr_s);
+        hf_l2_apply(kr[it], kr_s);
       } else {
         km = 1.0f / sqrtf(kss + 1e-6f);
         qm = scale / sqrtf(qss + 1e-6f);
       }
-      *(u32x4*)(kb + i * LD + ch * 8) = kr;
+      *(u32x4*)(kb + i * LD + ch * 8) = kr[it];
       if (ch == 0) {
         kmul[i] = km;
         krs[i] = kr_s;
@@ -149,12 +172,6 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
         qmul[i] = qm;
       }
     }
-  }
-  if (tid < kC) {
-    const bool live = tid < nt;
-    const int64_t gi = ((int64_t)n * T + t0 + (live ? tid : 0)) * ld_gate + hv;
-    Gs[tid] = live ? load_as_float(g, gi, gdt) : 0.f;
-    bt[tid] = live ? load_as_float(beta, gi, bdt) : 0.f;
   }
   __syncthreads();
   if (tid == 0) {
@@ -215,20 +232,34 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
     float treg[16];
 #pragma unroll
     for (int qq = 0; qq < 16; ++qq) treg[qq] = 0.f;
+    // row i's A values (this lane's residue part and the column's own entry)
+    // are read while row i - 1 is being computed: the chain then waits only
+    // on its own arithmetic and the two DPP steps
+    float4 av[2][4];
+    float ad[2];
+    auto fetch_row = [&](int i, int buf) {
+      const int nq = (i + 3) / 4;
+      const float* arow = Ar + i * kC + r * 16;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        if (q4 * 4 < nq) av[buf][q4] = *(const float4*)(arow + q4 * 4);
+      ad[buf] = Ar[i * kC + (col & 3) * 16 + (col >> 2)];
+    };
+    fetch_row(1, 1);
 #pragma unroll
     for (int i = 1; i < kC; ++i) {
-      constexpr int kMaxQ = 16;
       const int nq = (i + 3) / 4;  // q < nq covers every m < i of residue r
-      const float* arow = Ar + i * kC + r * 16;
+      const int b = i & 1;
+      if (i + 1 < kC) fetch_row(i + 1, b ^ 1);
       float part = 0.f;
 #pragma unroll
-      for (int q4 = 0; q4 < kMaxQ / 4; ++q4) {
+      for (int q4 = 0; q4 < 4; ++q4) {
         if (q4 * 4 >= nq) break;
-        const float4 av = *(const float4*)(arow + q4 * 4);
-        part += av.x * treg[q4 * 4];
-        if (q4 * 4 + 1 < nq) part += av.y * treg[q4 * 4 + 1];
-        if (q4 * 4 + 2 < nq) part += av.z * treg[q4 * 4 + 2];
-        if (q4 * 4 + 3 < nq) part += av.w * treg[q4 * 4 + 3];
+        const float4 a4 = av[b][q4];
+        part += a4.x * treg[q4 * 4];
+        if (q4 * 4 + 1 < nq) part += a4.y * treg[q4 * 4 + 1];
+        if (q4 * 4 + 2 < nq) part += a4.z * treg[q4 * 4 + 2];
+        if (q4 * 4 + 3 < nq) part += a4.w * treg[q4 * 4 + 3];
       }
       // sum over the 4 lanes of the column: DPP quad permutes (xor 1, xor 2)
       // instead of LDS-routed shuffles on this serial chain
@@ -236,7 +267,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
                                             0, __builtin_bit_cast(int, part), 0xB1, 0xF, 0xF, true));
       part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                                             0, __builtin_bit_cast(int, part), 0x4E, 0xF, 0xF, true));
-      const float val = Ar[i * kC + (col & 3) * 16 + (col >> 2)] + part;
+      const float val = ad[b] + part;
       if (r == (i & 3)) treg[i >> 2] = val;
     }
 #pragma unroll
