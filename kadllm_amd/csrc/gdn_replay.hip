@@ -146,9 +146,17 @@ __global__ __launch_bounds__(256) void gdn_replay_kernel(
         const int vrow = v0 + mt * 16 + col;
         const int kc = ks * 32 + quad * 8;
         float x[8];
+        if (state_dtype == KAD_DTYPE_F32) {
+          // the common case without the per-element dtype branches, so that
+          // all 64 loads go out back to back
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          x[i] = load_as_float(state, sbase + (int64_t)(kc + i) * VD + vrow, state_dtype);
+          for (int i = 0; i < 8; ++i)
+            x[i] = ((const float*)state)[sbase + (int64_t)(kc + i) * VD + vrow];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            x[i] = load_as_float(state, sbase + (int64_t)(kc + i) * VD + vrow, state_dtype);
+        }
         split8(x, a_hi[mt][ks], a_lo[mt][ks]);
       }
     }
