@@ -111,8 +111,11 @@ struct Raw4<float> {
   }
 };
 
+// one-token suffixes fit three workgroups per CU (150 registers), whose
+// extra waves hide the per-group load latency (5% faster than two)
 template <int KD, int VD, typename TIN, int kTMax>
-__global__ __launch_bounds__(256) void gdn_replay_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kTMax == 1 ? 3 : 1, 8)))
+void gdn_replay_kernel(
     const TIN* __restrict__ q, const TIN* __restrict__ k, const TIN* __restrict__ v,
     int64_t ld_qk, int64_t ld_v, const void* __restrict__ gdecay, int gate_dtype,
     const void* __restrict__ beta, int beta_dtype, int64_t ld_gate,
