@@ -108,7 +108,8 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
  * direct-to-LDS loads and a 16-byte store epilogue, which needs 16-byte
  * aligned C (and R) with ldc, ldr and the output width multiples of 8;
  * 18 = 16 persistent, one workgroup per CU walking the tiles; 19 = 16's
- * design on 128x128 tiles with 4 waves, two workgroups per CU).  Every
+ * design on 128x128 tiles with 4 waves, two workgroups per CU; 20 = 16 with
+ * a third LDS slot for the operand that streams from beyond the L2).  Every
  * configuration accumulates K in the same order, so all give bit-identical
  * results; other numbers are rejected (KAD_ERR_UNSUPPORTED). */
 int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,

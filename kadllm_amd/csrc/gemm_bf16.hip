@@ -467,6 +467,152 @@ int launch_x16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, 
   return kad_launch_status("gemm_x16_kernel");
 }
 
+// 256 x 256 tiles as gemm_x16_kernel, but the operand that streams from
+// beyond the L2 gets three LDS slots of 64-deep K and the other two (160 KB):
+// the streamed operand's tile kt + 3 goes out when tile kt's slot frees, so
+// its loads have two tiles of time to land instead of one.  Which operand
+// streams follows the tile order: A (the activations) for M-major orders,
+// where an XCD keeps its W panels in L2 across rounds and fetches new A
+// panels each round; W for N-major ones.  The prefill's long-K projections
+// (K = 3,584), whose loads wait 600-800 cycles per tile at the barrier with
+// two slots, run 10% faster; at K = 1,024 the per-tile prologue (one
+// workgroup per CU: nothing overlaps it) eats the gain.
+template <int EPI, class TX, bool STREAM_A>
+__global__ __launch_bounds__(64 * TX::NW) void gemm_s3_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group) {
+  constexpr int BM = TX::BM, BN = TX::BN;
+  constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
+  constexpr int AG = TX::AG, WGW = TX::WGW;
+  constexpr int SA = STREAM_A ? 3 : 2, SW = STREAM_A ? 2 : 3;
+  constexpr int kASlot = BM * kBK, kWSlot = BN * kBK;
+  constexpr int kStages = SA * kASlot + SW * kWSlot;
+  constexpr int kSmem = kStages > NW * TX::EpiWave ? kStages : NW * TX::EpiWave;
+  constexpr int n3 = STREAM_A ? AG : WGW;   // loads of the 3-slot operand per wave per tile
+  constexpr int n2 = STREAM_A ? WGW : AG;
+  constexpr int kLoads = AG + WGW;
+  constexpr int NM = NI * NJ, NR = NI + NJ;
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[kSmem];
+  bf16_t* a_lds = smem;
+  bf16_t* w_lds = smem + SA * kASlot;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int m0, n0;
+  tile_origin(M, N, BM, BN, n_major, group, m0, n0);
+
+  const int d_row = lane >> 3;
+  const int d_kc = ((lane & 7) ^ ((wave & 1) * 4 + (lane >> 4))) * 8;
+  const bf16_t* a_base = A + (int64_t)m0 * lda;
+  const bf16_t* b_base = Wt + (int64_t)n0 * ldw;
+  int a_off[AG], b_off[WGW];
+#pragma unroll
+  for (int i = 0; i < AG; ++i) {
+    const int r = (wave + NW * i) * 8 + d_row;
+    a_off[i] = (int)((int64_t)(min(m0 + r, M - 1) - m0) * lda) + d_kc;
+  }
+#pragma unroll
+  for (int i = 0; i < WGW; ++i) {
+    const int r = (wave + NW * i) * 8 + d_row;
+    b_off[i] = (int)((int64_t)(min(n0 + r, N - 1) - n0) * ldw) + d_kc;
+  }
+  const int KT = K / kBK;
+  auto issue_a = [&](int t) {
+    const int k0 = min(t, KT - 1) * kBK;
+    bf16_t* base = a_lds + (t % SA) * kASlot + wave * 8 * kBK;
+#pragma unroll
+    for (int i = 0; i < AG; ++i) dma16(a_base + (a_off[i] + k0), base + i * NW * 8 * kBK);
+  };
+  auto issue_w = [&](int t) {
+    const int k0 = min(t, KT - 1) * kBK;
+    bf16_t* base = w_lds + (t % SW) * kWSlot + wave * 8 * kBK;
+#pragma unroll
+    for (int i = 0; i < WGW; ++i) dma16(b_base + (b_off[i] + k0), base + i * NW * 8 * kBK);
+  };
+  // the 2-slot operand's loads go out before the 3-slot one's, so that
+  // vmcnt(n3) at a barrier leaves only the newest 3-slot loads in flight
+  auto issue2 = [&](int t) { if (STREAM_A) issue_w(t); else issue_a(t); };
+  auto issue3 = [&](int t) { if (STREAM_A) issue_a(t); else issue_w(t); };
+
+  const int f_row = lane & 15, f_sw = (lane & 15) >> 1, f_q = lane >> 4;
+  const int fa_row = (wm * NI * 16 + f_row) * kBK;
+  const int fw_row = (wn * NJ * 16 + f_row) * kBK;
+  bf16x8 fa[2][NI], fw[2][NJ];
+  auto load_frags = [&](int t, int step, int buf) {
+    const int ch = ((step * 4 + f_q) ^ f_sw) * 8;
+    const bf16_t* ab = a_lds + (t % SA) * kASlot + ch;
+    const bf16_t* wb = w_lds + (t % SW) * kWSlot + ch;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) fw[buf][j] = as_bf16x8(*(const u32x4*)(wb + fw_row + j * 16 * kBK));
+#pragma unroll
+    for (int i = 0; i < NI; ++i) fa[buf][i] = as_bf16x8(*(const u32x4*)(ab + fa_row + i * 16 * kBK));
+  };
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{};
+  auto mfma_rows = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x32(fw[buf][j], fa[buf][i], acc[i][j]);
+  };
+
+  issue2(0);
+  issue3(0);
+  issue2(1);
+  issue3(1);
+  issue3(2);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(n2 + 2 * n3));   // tile 0 landed
+  ring_barrier();
+  load_frags(0, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(kt, 1, 1);
+    mfma_rows(0);
+    interleave_x16<NM, NR, 0>();
+    // tile kt + 1 landed (the 3-slot operand's tile kt + 2 may still be in
+    // flight); every wave is done reading tile kt's slots
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(n3));
+    ring_barrier();
+    __builtin_amdgcn_s_setprio(1);
+    load_frags(kt + 1, 0, 0);
+    issue2(kt + 2);
+    issue3(kt + 3);
+    mfma_rows(1);
+    interleave_x16<NM, NR, kLoads>();
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 16) / 2 : n0 + wn * NJ * 16;
+  epilogue_x16<EPI, NI, NJ>(acc, smem + wave * TX::EpiWave, lane, m0 + wm * NI * 16, col0, C,
+                            ldc, R, ldr, M, N);
+}
+
+template <int EPI, class TX>
+int launch_s3(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+              const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t nblocks = kad_cdiv(M, TX::BM) * kad_cdiv(N, TX::BN);
+  if (nblocks > 0x7fffffff) KAD_UNSUPPORTED("gemm grid too large");
+  if ((int64_t)TX::BM * (lda > ldw ? lda : ldw) + K >= 0x7fffffff)
+    KAD_UNSUPPORTED("gemm rows too long for 32-bit tile offsets");
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  if (n_major)
+    hipLaunchKernelGGL((gemm_s3_kernel<EPI, TX, false>), dim3((unsigned)nblocks), dim3(64 * TX::NW),
+                       0, s, (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                       (const bf16_t*)R, ldr, M, N, K, n_major, 8);
+  else
+    hipLaunchKernelGGL((gemm_s3_kernel<EPI, TX, true>), dim3((unsigned)nblocks), dim3(64 * TX::NW),
+                       0, s, (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                       (const bf16_t*)R, ldr, M, N, K, n_major, 8);
+  return kad_launch_status("gemm_s3_kernel");
+}
+
 // Persistent form of the 16x16x32 kernel: one workgroup per CU walks the
 // tiles v = blockIdx.x, + gridDim.x, ... (the same grouped, XCD-aware order).
 // The K slices of successive tiles form one stream through the two LDS
@@ -723,14 +869,16 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled): the
 // forms the automatic choice uses; the numbers are part of the C ABI
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_128x32 = 11,
-       CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19 };
+       CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19,
+       CFG_256x256_S3 = 20 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
     // the 8-wave 256x256 kernel on 16x16x32 MFMAs when its tiles still fill
-    // every CU (and the output suits 16-byte stores), persistent except for
+    // every CU (and the output suits 16-byte stores): with a third LDS slot
+    // for the streamed operand for K >= 3072, else persistent except for
     // the SwiGLU epilogue, where both forms measured the same; then the
     // 128x128 form, two workgroups per CU, when its tiles fill two rounds
     // (N = 1,024 at M = 8,192: 5-7% faster than 8-wave 256x128 tiles, and
@@ -746,6 +894,8 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       cfg = CFG_128x32;
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
+    else if (tiles256 >= 256 && K >= 3072)
+      cfg = CFG_256x256_S3;
     else if (tiles256 >= 256)
       cfg = EPI == KAD_EPI_SWIGLU ? CFG_256x256_X16 : CFG_256x256_X16P;
     else if (vec && tiles128 >= 512)
@@ -765,11 +915,14 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_256x256_X16:
     case CFG_256x256_X16P:
     case CFG_128x128_X16:
+    case CFG_256x256_S3:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
                         cfg);
       if (cfg == CFG_256x256_X16)
         return launch_x16<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_256x256_S3)
+        return launch_s3<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_128x128_X16)
         return launch_x16<EPI, TileX16<128, 128, 2, 2>>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K,
                                                         s);

@@ -101,7 +101,7 @@ def test_gemm_tile_configurations_agree(device, epi):
     x = torch.randn(M, n_out, generator=g).bfloat16()
     ad, wd = a.to(device), w.to(device)
     outs = {}
-    cfgs = [c for c in (1, 2, 5, 11, 16, 18, 19) if not (c == 11 and epi == layers.EPI_SWIGLU)]
+    cfgs = [c for c in (1, 2, 5, 11, 16, 18, 19, 20) if not (c == 11 and epi == layers.EPI_SWIGLU)]
     for cfg in cfgs:
         c = torch.zeros(M, n_out + 16, dtype=torch.bfloat16, device=device)  # ldc > width
         cv = c[:, :n_out]
@@ -142,7 +142,7 @@ def test_gemm_short_k_pipelines_agree(device, K):
     a = torch.randn(M, K, generator=g).bfloat16().to(device)
     w = (torch.randn(N, K, generator=g) * 0.05).bfloat16().to(device)
     outs = {}
-    for cfg in (1, 2, 5, 16, 18, 19):
+    for cfg in (1, 2, 5, 16, 18, 19, 20):
         c = torch.zeros(M, N, dtype=torch.bfloat16, device=device)
         _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), N, None, 0,
                   M, N, K, layers.EPI_STORE, cfg, _lib.stream_of(a))
@@ -157,9 +157,11 @@ def test_gemm_short_k_pipelines_agree(device, K):
 @pytest.mark.parametrize("epi", [layers.EPI_STORE, layers.EPI_RESIDUAL, layers.EPI_SWIGLU])
 def test_gemm_persistent_tiles_agree(device, K, epi):
     """The persistent kernel (config 18) against the one-tile-per-workgroup
-    forms (16, 19) with more tiles than CUs, ragged last tiles in
+    forms (16, 19, 20) with more tiles than CUs, ragged last tiles in
     both dimensions, and tiles of one or three K slices, so that the load
-    stream crosses tile boundaries at both stage parities."""
+    stream crosses tile boundaries at both stage parities; config 20 with the
+    activations as its three-slot operand (M > N; the other order is covered
+    by the tests above)."""
     from kadllm_amd import _lib
     M, N = 256 * 17 + 40, 256 * 16 + 64
     g = torch.Generator().manual_seed(90 + K + epi)
@@ -168,7 +170,7 @@ def test_gemm_persistent_tiles_agree(device, K, epi):
     n_out = N // 2 if epi == layers.EPI_SWIGLU else N
     x = torch.randn(M, n_out, generator=g).bfloat16().to(device)
     outs = {}
-    for cfg in (16, 18, 19):
+    for cfg in (16, 18, 19, 20):
         c = x.clone() if epi == layers.EPI_RESIDUAL else torch.zeros(M, n_out, dtype=torch.bfloat16,
                                                                      device=device)
         _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), n_out,
@@ -179,6 +181,7 @@ def test_gemm_persistent_tiles_agree(device, K, epi):
         outs[cfg] = c.cpu()
     assert torch.equal(outs[18], outs[16]), f"persistent 256x256 differs at K={K}"
     assert torch.equal(outs[16], outs[19]), f"128x128 tiles differ at K={K}"
+    assert torch.equal(outs[16], outs[20]), f"three-slot 256x256 differs at K={K}"
 
 
 def test_gemm_pipelined_tile_rejects_unaligned_output(device):
@@ -191,7 +194,7 @@ def test_gemm_pipelined_tile_rejects_unaligned_output(device):
                   0, 256, 256, 64, layers.EPI_STORE, 16, _lib.stream_of(a))
 
 
-@pytest.mark.parametrize("cfg", [3, 7, 17, 20, -1])
+@pytest.mark.parametrize("cfg", [3, 7, 17, 21, -1])
 def test_gemm_rejects_unknown_tile_configuration(device, cfg):
     from kadllm_amd import _lib
     a = torch.zeros(256, 64, dtype=torch.bfloat16, device=device)
