@@ -902,6 +902,33 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       cfg = CFG_128x128_X16;
     else
       cfg = CFG_128x128;
+    // A last round of 256 x 256 workgroups that would leave more than a
+    // quarter of the CUs idle, in a launch of few rounds (the decode SwiGLU
+    // projection at M = 8,192: 3.5 rounds): the columns past the last whole
+    // round go to 128 x 128 tiles, two workgroups per CU, in a second launch
+    // (114.8 -> 111.9 us there).  Every configuration accumulates K in the
+    // same order, so the split does not change a bit of the result.  The
+    // persistent kernel gains nothing from it (its workgroups take the
+    // leftover tiles in turn: the decode QKV projection at 2.5 rounds ran
+    // 79.2 us either way, the vocabulary head 0.6% slower split).
+    if (cfg == CFG_256x256_X16) {
+      const int64_t mt = kad_cdiv(M, 256), nt = kad_cdiv(N, 256);
+      const int64_t cus = device_cu_count();
+      const int64_t rem = tiles256 % cus;
+      if (rem != 0 && rem * 4 < cus * 3 && tiles256 < 8 * cus) {
+        int64_t n1 = nt - 1;
+        while (n1 > 0 && (mt * n1) % cus != 0) --n1;
+        if (n1 > 0) {
+          const int N1 = (int)(n1 * 256);
+          const int64_t c_off = EPI == KAD_EPI_SWIGLU ? N1 / 2 : N1;
+          const int rc = pick<EPI>(cfg, A, lda, W, ldw, C, ldc, R, ldr, M, N1, K, s);
+          if (rc) return rc;
+          return pick<EPI>(CFG_128x128_X16, A, lda, (const bf16_t*)W + (int64_t)N1 * ldw, ldw,
+                           (bf16_t*)C + c_off, ldc, R ? (const bf16_t*)R + N1 : nullptr, ldr, M,
+                           N - N1, K, s);
+        }
+      }
+    }
   }
   switch (cfg) {
     case CFG_32x256: return launch<32, 256, 1, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);

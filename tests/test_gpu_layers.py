@@ -132,6 +132,38 @@ def test_gemm_tile_configurations_agree(device, epi):
         _bf16_ulp_close(outs[16], ref, "gemm tiles swiglu", min_exact=0.9)
 
 
+@pytest.mark.parametrize("N,epi", [(7168, layers.EPI_SWIGLU), (5120, layers.EPI_STORE),
+                                   (5120, layers.EPI_RESIDUAL)])
+def test_gemm_last_round_column_split_is_bitwise(device, N, epi):
+    """At M = 8,192 the 256 x 256 tiles of the SwiGLU projection (N = 7,168)
+    fill 3.5 rounds of the chip's CUs: the automatic choice runs the columns
+    past the last whole round as 128 x 128 tiles in a second launch.  The
+    result equals the unsplit 256 x 256 kernel's bit for bit (and so does the
+    automatic choice for N = 5,120, left whole)."""
+    from kadllm_amd import _lib
+    M, K = 8192, 1024
+    gen = torch.Generator(device=device).manual_seed(N + epi)
+    a = torch.randn(M, K, generator=gen, device=device).bfloat16()
+    w = (torch.randn(N, K, generator=gen, device=device) * 0.05).bfloat16()
+    n_out = N // 2 if epi == layers.EPI_SWIGLU else N
+    x = torch.randn(M, n_out, generator=gen, device=device).bfloat16()
+    outs = []
+    for cfg in (0, 16):
+        c = x.clone() if epi == layers.EPI_RESIDUAL else torch.zeros(M, n_out, dtype=torch.bfloat16,
+                                                                      device=device)
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), n_out,
+                  _lib.ptr(c) if epi == layers.EPI_RESIDUAL else None,
+                  n_out if epi == layers.EPI_RESIDUAL else 0, M, N, K, epi, cfg,
+                  _lib.stream_of(a))
+        outs.append(c)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    rows = torch.tensor([0, 4097, 8191], device=device)
+    prod = (a[rows].float() @ w.float().T).bfloat16()
+    if epi == layers.EPI_STORE:
+        _bf16_ulp_close(outs[0][rows], prod, "split gemm store")
+
+
 @pytest.mark.parametrize("K", [64, 128, 192])
 def test_gemm_short_k_pipelines_agree(device, K):
     """The 16x16x32 configurations at K of one to three 64-deep tiles, where
