@@ -222,56 +222,72 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   }
   __syncthreads();
 
-  // ---- forward substitution T'[i][j] = A[i][j] + sum_{m<i} A[i][m] T'[m][j]
-  // (A strictly lower).  Columns are independent: wave w owns columns
-  // 16w..16w+15 with 4 lanes per column; lane r of column j keeps rows
-  // m = 4q + r (q < 16) of the column in registers.  Rows not yet computed are
-  // zero, so each row needs no masking; no barriers are involved.
+  // ---- T' = (I - A)^-1 - I (A strictly lower) by 16 x 16 blocks, T = I + T'.
+  // 1. Wave w inverts diagonal block w by forward substitution,
+  //    T'[i][j] = A[i][j] + sum_{m<i} A[i][m] T'[m][j] within the block: lane
+  //    (column j = 16w + lane/4, residue r = lane%4) keeps rows 16w + 4q + r
+  //    in registers; rows not yet computed are zero and A is zero on and above
+  //    the diagonal, so no term needs a mask.  It also clears the blocks to the
+  //    right of its diagonal block.
+  // 2. Wave j then walks block column j downwards on fp32 MFMAs:
+  //    (I - A_ii) T_ij = sum_{m<i} A_im T_mj gives T'_ij = T_ij = P + T'_ii P
+  //    with P = sum_{m=j}^{i-1} A_im T_mj.  A wave reads only the diagonal
+  //    blocks and its own column's blocks, in the order it wrote them, so the
+  //    walk needs no barrier.
   {
     const int col = wave * 16 + (lane >> 2), r = lane & 3;
-    float treg[16];
+    float treg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int qq = 0; qq < 16; ++qq) treg[qq] = 0.f;
-    // row i's A values (this lane's residue part and the column's own entry)
-    // are read while row i - 1 is being computed: the chain then waits only
-    // on its own arithmetic and the two DPP steps
-    float4 av[2][4];
-    float ad[2];
-    auto fetch_row = [&](int i, int buf) {
-      const int nq = (i + 3) / 4;
-      const float* arow = Ar + i * kC + r * 16;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        if (q4 * 4 < nq) av[buf][q4] = *(const float4*)(arow + q4 * 4);
-      ad[buf] = Ar[i * kC + (col & 3) * 16 + (col >> 2)];
-    };
-    fetch_row(1, 1);
-#pragma unroll
-    for (int i = 1; i < kC; ++i) {
-      const int nq = (i + 3) / 4;  // q < nq covers every m < i of residue r
-      const int b = i & 1;
-      if (i + 1 < kC) fetch_row(i + 1, b ^ 1);
-      float part = 0.f;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        if (q4 * 4 >= nq) break;
-        const float4 a4 = av[b][q4];
-        part += a4.x * treg[q4 * 4];
-        if (q4 * 4 + 1 < nq) part += a4.y * treg[q4 * 4 + 1];
-        if (q4 * 4 + 2 < nq) part += a4.z * treg[q4 * 4 + 2];
-        if (q4 * 4 + 3 < nq) part += a4.w * treg[q4 * 4 + 3];
-      }
+    for (int li = 1; li < 16; ++li) {
+      const int i = wave * 16 + li;
+      const float4 a4 = *(const float4*)(Ar + i * kC + r * 16 + wave * 4);
+      float part = a4.x * treg[0];
+      part += a4.y * treg[1];
+      part += a4.z * treg[2];
+      part += a4.w * treg[3];
       // sum over the 4 lanes of the column: DPP quad permutes (xor 1, xor 2)
-      // instead of LDS-routed shuffles on this serial chain
       part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                                             0, __builtin_bit_cast(int, part), 0xB1, 0xF, 0xF, true));
       part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                                             0, __builtin_bit_cast(int, part), 0x4E, 0xF, 0xF, true));
-      const float val = ad[b] + part;
-      if (r == (i & 3)) treg[i >> 2] = val;
+      const float val = Ar[i * kC + (col & 3) * 16 + (col >> 2)] + part;
+      if (r == (li & 3)) treg[li >> 2] = val;
     }
 #pragma unroll
-    for (int qq = 0; qq < 16; ++qq) Tm[qq * 4 + r][col] = treg[qq];
+    for (int qq = 0; qq < 4; ++qq) Tm[wave * 16 + qq * 4 + r][col] = treg[qq];
+    for (int jb = wave + 1; jb < 4; ++jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Tm[wave * 16 + (lane >> 4) * 4 + e][jb * 16 + (lane & 15)] = 0.f;
+  }
+  __syncthreads();
+  if (wave < 3) {
+    // v_mfma_f32_16x16x4_f32: lane l holds A[l%16][l/16] and B[l/16][l%16];
+    // accumulator element e of lane l is C[(l/16)*4 + e][l%16]
+    const int jb = wave, rr = lane & 15, kq = lane >> 4;
+    for (int ib = jb + 1; ib < 4; ++ib) {
+      f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int mb = jb; mb < ib; ++mb) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int kk = st * 4 + kq;
+          const float av = Ar[(ib * 16 + rr) * kC + (kk & 3) * 16 + mb * 4 + (kk >> 2)];
+          const float bv = Tm[mb * 16 + kk][jb * 16 + rr] + (mb == jb && kk == rr ? 1.f : 0.f);
+          P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
+        }
+      }
+      // P goes through block (ib, jb) of Tm to become the B operand
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Tm[ib * 16 + kq * 4 + e][jb * 16 + rr] = P[e];
+      f32x4 acc = P;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int kk = st * 4 + kq;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Tm[ib * 16 + rr][ib * 16 + kk],
+                                                   Tm[ib * 16 + kk][jb * 16 + rr], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Tm[ib * 16 + kq * 4 + e][jb * 16 + rr] = acc[e];
+    }
   }
   __syncthreads();
 
