@@ -111,7 +111,8 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
  * design on 128x128 tiles with 4 waves, two workgroups per CU; 20 = 16 with
  * a third LDS slot for the operand that streams from beyond the L2).  Every
  * configuration accumulates K in the same order, so all give bit-identical
- * results; other numbers are rejected (KAD_ERR_UNSUPPORTED). */
+ * results (the automatic choice may also split the columns of one call
+ * between two of them); other numbers are rejected (KAD_ERR_UNSUPPORTED). */
 int kad_gemm_bf16_tiled(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
                         int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                         int epilogue, int tile_config, kad_stream_t stream);
