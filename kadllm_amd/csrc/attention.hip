@@ -117,7 +117,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn2_kernel(AttnArgs a) {
   const int qgrp = wave / DS;            // query group of 64 rows
   const int dbase = (wave % DS) * DT;    // this wave's first d tile
   const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int qb_blk = lid % a.nqblk;
+  // causal: the blocks of a (request, KV head) go out longest first (the
+  // last query rows see the most keys), so that the short ones fill the tail
+  const int qb_blk = CAUSAL ? a.nqblk - 1 - lid % a.nqblk : lid % a.nqblk;
   const int bk = lid / a.nqblk;
   const int kh = bk % a.HK, b = bk / a.HK;
   const int G = a.H / a.HK;
@@ -615,7 +617,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hi = lane >> 5, col = lane & 31;
   const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int qb_blk = lid % a.nqblk;
+  // causal: the blocks of a (request, KV head) go out longest first (the
+  // last query rows see the most keys), so that the short ones fill the tail
+  const int qb_blk = CAUSAL ? a.nqblk - 1 - lid % a.nqblk : lid % a.nqblk;
   const int bk = lid / a.nqblk;
   const int kh = bk % a.HK, b = bk / a.HK;
   const int G = a.H / a.HK;
