@@ -103,7 +103,7 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
                   kad_stream_t stream);
 /* Same with an explicit tile configuration, the forms the automatic choice
  * picks from (0 = automatic choice as kad_gemm_bf16; 1 = 32x256 with 4 waves;
- * 2 = 128x128 with 4 waves; 5 = 256x256 with 8 waves; 11 = 128x32 with 4
+ * 2 = 128x128 with 4 waves; 5 = 256x256 with 8 waves; 11 = 64x32 with 2
  * waves, no SwiGLU epilogue; 16 = 256x256 with 8 waves on 16x16x32 MFMAs,
  * direct-to-LDS loads and a 16-byte store epilogue, which needs 16-byte
  * aligned C (and R) with ldc, ldr and the output width multiples of 8;

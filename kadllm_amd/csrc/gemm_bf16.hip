@@ -868,7 +868,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled): the
 // forms the automatic choice uses; the numbers are part of the C ABI
-enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_128x32 = 11,
+enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_64x32 = 11,
        CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19,
        CFG_256x256_S3 = 20 };
 
@@ -882,7 +882,7 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     // the SwiGLU epilogue, where both forms measured the same; then the
     // 128x128 form, two workgroups per CU, when its tiles fill two rounds
     // (N = 1,024 at M = 8,192: 5-7% faster than 8-wave 256x128 tiles, and
-    // 14% slower than 256x256 where those fill the chip); 128x32 for outputs
+    // 14% slower than 256x256 where those fill the chip); 64x32 for outputs
     // of at most 32 columns (the GDN gate projection); the register-staged
     // 128x128 kernel otherwise (all measured on the decode/prefill shapes)
     const int64_t tiles256 = kad_cdiv(M, 256) * kad_cdiv(N, 256);
@@ -891,7 +891,7 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     if (M <= 64)
       cfg = CFG_32x256;
     else if (N <= 32)
-      cfg = CFG_128x32;
+      cfg = CFG_64x32;
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
     else if (tiles256 >= 256 && K >= 3072)
@@ -933,9 +933,11 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
   switch (cfg) {
     case CFG_32x256: return launch<32, 256, 1, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_128x128: return launch<128, 128, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-    case CFG_128x32:
+    case CFG_64x32:
+      // two waves of 32x32: twice the workgroups of 128x32 tiles for this
+      // read-bound shape (12.1 against 14.0 us at M = 32,768, N = 32)
       if (EPI == KAD_EPI_SWIGLU) KAD_UNSUPPORTED("tile configuration 11 has no SwiGLU epilogue");
-      return launch<128, 32, 4, 1, EPI == KAD_EPI_SWIGLU ? KAD_EPI_STORE : EPI>(
+      return launch<64, 32, 2, 1, EPI == KAD_EPI_SWIGLU ? KAD_EPI_STORE : EPI>(
           A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_256x256_8W:
       return launch<256, 256, 2, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
