@@ -104,7 +104,7 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
 /* Same with an explicit tile configuration, the forms the automatic choice
  * picks from (0 = automatic choice as kad_gemm_bf16; 1 = 32x256 with 4 waves;
  * 2 = 128x128 with 4 waves; 5 = 256x256 with 8 waves; 11 = 64x32 with 2
- * waves, no SwiGLU epilogue; 16 = 256x256 with 8 waves on 16x16x32 MFMAs,
+ * waves, no SwiGLU epilogue; 12 = 32x64 with 2 waves, no SwiGLU epilogue; 16 = 256x256 with 8 waves on 16x16x32 MFMAs,
  * direct-to-LDS loads and a 16-byte store epilogue, which needs 16-byte
  * aligned C (and R) with ldc, ldr and the output width multiples of 8;
  * 18 = 16 persistent, one workgroup per CU walking the tiles; 19 = 16's

@@ -869,6 +869,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled): the
 // forms the automatic choice uses; the numbers are part of the C ABI
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_64x32 = 11,
+       CFG_32x64 = 12,
        CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19,
        CFG_256x256_S3 = 20 };
 
@@ -889,7 +890,7 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     const int64_t tiles128 = kad_cdiv(M, 128) * kad_cdiv(N, 128);
     const bool vec = vector_epilogue_ok(C, ldc, R, ldr, N, EPI);
     if (M <= 64)
-      cfg = CFG_32x256;
+      cfg = N <= 2048 && EPI != KAD_EPI_SWIGLU ? CFG_32x64 : CFG_32x256;
     else if (N <= 32)
       cfg = CFG_64x32;
     else if (tiles256 >= 256 && !vec)
@@ -932,6 +933,13 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
   }
   switch (cfg) {
     case CFG_32x256: return launch<32, 256, 1, 4, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_32x64:
+      // a few rows against a narrow weight (the pruned last prefill layer's
+      // output and down projections, M = 32, N = 1,024): four times the
+      // workgroups of 32x256 tiles (13.2 against 25.8 us at K = 2,048)
+      if (EPI == KAD_EPI_SWIGLU) KAD_UNSUPPORTED("tile configuration 12 has no SwiGLU epilogue");
+      return launch<32, 64, 1, 2, EPI == KAD_EPI_SWIGLU ? KAD_EPI_STORE : EPI>(
+          A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_128x128: return launch<128, 128, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_64x32:
       // two waves of 32x32: twice the workgroups of 128x32 tiles for this
