@@ -678,6 +678,26 @@ __global__ __launch_bounds__(kRowThreads) void row_select_float_kernel(
   }
 }
 
+// hist[bin] += 1 for the active lanes.  The merge's keys are cumulative
+// log-probabilities of one request, so its first radix rounds put nearly
+// every key in one or two bins, where one atomic per lane serialises on a
+// single LDS address: the lanes of the (up to) two most common bins of the
+// wave instruction add their count with one atomic each, the rest one by one.
+__device__ __forceinline__ void hist_add_grouped(int* hist, bool active, int bin) {
+  const int lane = threadIdx.x & 63;
+  uint64_t pending = __ballot(active);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    if (pending == 0) break;
+    const int leader = __ffsll((unsigned long long)pending) - 1;
+    const int lb = __shfl(bin, leader, 64);
+    const uint64_t same = __ballot(active && bin == lb) & pending;
+    if (lane == leader) atomicAdd(&hist[lb], (int)__popcll(same));
+    pending &= ~same;
+  }
+  if ((pending >> lane) & 1ull) atomicAdd(&hist[bin], 1);
+}
+
 __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
     const float* __restrict__ cand_key, const int* __restrict__ cand_idx, int ncand, int W,
     int V, float* __restrict__ scores, int64_t* __restrict__ parents,
@@ -713,7 +733,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
     for (int i = tid; i < 256; i += kMergeThreads) hist[i] = 0;
     __syncthreads();
     for_each([&](uint32_t u, int) {
-      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
+      hist_add_grouped(hist, (u & pmask) == prefix, (int)((u >> shift) & 255));
     });
     __syncthreads();
     if (tid < 64) {
