@@ -227,6 +227,19 @@ def test_gemm_pipelined_tile_rejects_unaligned_output(device):
                   0, 256, 256, 64, layers.EPI_STORE, 16, _lib.stream_of(a))
 
 
+@pytest.mark.parametrize("cfg", [11, 12])
+def test_gemm_skinny_tiles_reject_swiglu(device, cfg):
+    """The 64x32 and 32x64 register-staged tiles carry no SwiGLU epilogue (a
+    wave's 32 columns cannot hold a [gate 32 | up 32] block) and say so."""
+    from kadllm_amd import _lib
+    a = torch.zeros(64, 64, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(128, 64, dtype=torch.bfloat16, device=device)
+    c = torch.zeros(64, 64, dtype=torch.bfloat16, device=device)
+    with pytest.raises(_lib.KadLibraryError, match="has no SwiGLU epilogue"):
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), 64, _lib.ptr(w), 64, _lib.ptr(c), 64, None,
+                  0, 64, 128, 64, layers.EPI_SWIGLU, cfg, _lib.stream_of(a))
+
+
 @pytest.mark.parametrize("cfg", [3, 7, 17, 21, -1])
 def test_gemm_rejects_unknown_tile_configuration(device, cfg):
     from kadllm_amd import _lib
