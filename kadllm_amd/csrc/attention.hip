@@ -34,7 +34,7 @@ namespace {
 
 constexpr int kThreads = 256;
 // suffix keys folded per beam row (decode): 4, or 8 for longer suffixes
-constexpr int kSuffixFold = 4, kSuffixFoldLong = 8;
+constexpr int kSuffixFold = 4, kSuffixFoldLong = 8, kSuffixFoldShort = 2;
 
 struct AttnArgs {
   const bf16_t* q; int64_t sq_n, sq_t, sq_h;
@@ -1069,8 +1069,8 @@ int launch_attn3(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
 }
 
 // rows: query rows per (request, KV head); bh: number of (request, KV head)
-// (the fold of up to 8 suffix keys is its own instantiation: a row's
-// arithmetic is the same in both, the keys past Tk scoring -inf)
+// (the folds of up to 2, 4 and 8 suffix keys are instantiations of their
+// own: a row's arithmetic is the same in each, the keys past Tk scoring -inf)
 template <bool CAUSAL, int NSUF>
 int dispatch_d(int D, const AttnArgs& a, int64_t rows, int64_t bh, hipStream_t s) {
   if (D == 256) return launch_attn3<CAUSAL, NSUF>(a, rows, bh, s);
@@ -1082,6 +1082,10 @@ int dispatch_d(int D, const AttnArgs& a, int64_t rows, int64_t bh, hipStream_t s
 template <bool CAUSAL>
 int dispatch(int D, const AttnArgs& a, int64_t rows, int64_t bh, hipStream_t s) {
   if (!CAUSAL && a.Tk > kSuffixFold) return dispatch_d<CAUSAL, kSuffixFoldLong>(D, a, rows, bh, s);
+  // one or two suffix keys (the first two search levels): a fold of two, which
+  // skips the dot products and V loads of the keys a row cannot have (decode
+  // attention 145 -> 139 us at one or two keys)
+  if (!CAUSAL && a.Tk <= kSuffixFoldShort) return dispatch_d<CAUSAL, kSuffixFoldShort>(D, a, rows, bh, s);
   return dispatch_d<CAUSAL, kSuffixFold>(D, a, rows, bh, s);
 }
 
