@@ -226,7 +226,7 @@ __device__ int wave_rank_bin(const int* hist, int r, int* above) {
 //     column) emits the row's top K, unordered: the merge stage orders them.
 // If fewer than K or more than CAP entries qualify, the exact histogram path
 // runs instead, so the result never depends on the sample.
-template <int CAP>
+template <int CAP, bool MASKED>
 __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
     const bf16_t* __restrict__ logits, int64_t ld, const uint8_t* __restrict__ mask,
     int64_t ld_mask, const float* __restrict__ parent, int Wp, int V, int K,
@@ -241,7 +241,9 @@ __global__ __launch_bounds__(kRowThreads) void row_select_kernel(
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const bf16_t* x = logits + row * ld;
-  const uint8_t* mk = mask ? mask + row * ld_mask : nullptr;
+  // a separate instantiation for unmasked rows drops the mask tests from the
+  // per-logit loop, which is VALU-bound
+  const uint8_t* mk = MASKED ? mask + row * ld_mask : nullptr;
   const bool vec = (ld % 8) == 0 && (((uintptr_t)logits) % 16) == 0 &&
                    (!mask || ((ld_mask % 8) == 0 && (((uintptr_t)mask) % 8) == 0));
   auto key_of = [&](uint16_t bits, int c) -> uint32_t {
@@ -885,14 +887,19 @@ int launch_row_select(const void* logits, int logits_dtype, int64_t ld, const vo
   const int nlines = (V + kLine - 1) / kLine;
   const int line_stride = nlines > kTargetLines ? nlines / kTargetLines : 1;
   const int rank = (int)kad_cdiv(2 * (int64_t)K + 256, line_stride);
-  if (2 * (int64_t)K + 256 <= kCandCapSmall / 2)
-    hipLaunchKernelGGL(row_select_kernel<kCandCapSmall>, dim3(rows), dim3(kRowThreads), 0, s,
-                       (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores,
-                       Wp, V, K, cand_key, cand_idx, line_stride, rank);
-  else
-    hipLaunchKernelGGL(row_select_kernel<kCandCapLarge>, dim3(rows), dim3(kRowThreads), 0, s,
-                       (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores,
-                       Wp, V, K, cand_key, cand_idx, line_stride, rank);
+#define KAD_ROW_SELECT(CAP, MASKED)                                                        \
+  hipLaunchKernelGGL((row_select_kernel<CAP, MASKED>), dim3(rows), dim3(kRowThreads), 0, s,  \
+                     (const bf16_t*)logits, ld, (const uint8_t*)mask, ld_mask, parent_scores,  \
+                     Wp, V, K, cand_key, cand_idx, line_stride, rank)
+  const bool small = 2 * (int64_t)K + 256 <= kCandCapSmall / 2;
+  if (mask) {
+    if (small) KAD_ROW_SELECT(kCandCapSmall, true);
+    else KAD_ROW_SELECT(kCandCapLarge, true);
+  } else {
+    if (small) KAD_ROW_SELECT(kCandCapSmall, false);
+    else KAD_ROW_SELECT(kCandCapLarge, false);
+  }
+#undef KAD_ROW_SELECT
   return kad_launch_status("row_select_kernel");
 }
 
