@@ -90,11 +90,11 @@ __device__ __forceinline__ void hf_l2_apply(u32x4& r, float rs) {
 }
 
 // ---------------------------------------------------------------------------
-template <int K>
+template <int K, bool HF>
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t ld_qk,
     const void* __restrict__ g, int gdt, const void* __restrict__ beta, int bdt, int64_t ld_gate,
-    uint8_t* __restrict__ ws, int T, int H, int HV, int nchunks, float scale, int hf_norm) {
+    uint8_t* __restrict__ ws, int T, int H, int HV, int nchunks, float scale) {
   constexpr int LD = K + 8;
   constexpr int CPR = K / 8;       // 16-byte slices per k row
   constexpr int RPI = 64 / CPR;    // rows per wave instruction
@@ -153,10 +153,10 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
         kr[it] = u32x4{0, 0, 0, 0};
         qr[it] = u32x4{0, 0, 0, 0};
       }
-      const float kss = row_sumsq<CPR>(kr[it], hf_norm);
-      const float qss = row_sumsq<CPR>(qr[it], hf_norm);
+      const float kss = row_sumsq<CPR>(kr[it], HF);
+      const float qss = row_sumsq<CPR>(qr[it], HF);
       float km = 1.f, kr_s = 1.f, qr_s = 1.f, qm = scale;
-      if (hf_norm) {
+      if constexpr (HF) {
         kr_s = hf_l2_rs(kss);
         qr_s = hf_l2_rs(qss);
         hf_l2_apply(kr[it], kr_s);
@@ -351,13 +351,12 @@ __device__ __forceinline__ bf16x8 kt_frag(const bf16_t* kb, int kt, int s, int l
   return as_bf16x8(u32x4{lo[0], lo[1], up[0], up[1]});
 }
 
-template <int K, int V>
+template <int K, int V, bool HF>
 __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t ld_qk,
     const bf16_t* __restrict__ v, int64_t ld_v, const uint8_t* __restrict__ ws,
     const void* __restrict__ state0, int sdt, int beams_per_state, bf16_t* __restrict__ out,
-    int64_t ld_out, float* __restrict__ final_state, int T, int H, int HV, int nchunks,
-    int hf_norm) {
+    int64_t ld_out, float* __restrict__ final_state, int T, int H, int HV, int nchunks) {
   constexpr int KT = K / 32;      // 32-row k tiles of S
   constexpr int KS = K / 16;      // k16 steps over K
   constexpr int LDK = K + 8;      // bf16 [64][K] rows (16-byte padding)
@@ -444,7 +443,7 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     for (int u = 0; u < kRowU; ++u) {
       const int e = tid + u * NTH;
       const int i = e / CPR, ch = e % CPR;
-      if (hf_norm) {
+      if constexpr (HF) {
         hf_l2_apply(rk[u], krs_u[u]);
         hf_l2_apply(rq[u], qrs_u[u]);
       }
@@ -651,16 +650,23 @@ int launch_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, int
                  void* ws, int N, int T, int H, int HV, float scale, int hf_norm, hipStream_t s) {
   const int nchunks = (T + kC - 1) / kC;
   const int64_t nrec = (int64_t)N * HV * nchunks;
-  hipLaunchKernelGGL((gdn_chunk_prep<K>), dim3((unsigned)nrec), dim3(kPrepThreads), 0, s,
-                     (const bf16_t*)q, (const bf16_t*)k, ld_qk, g, gdt, beta, bdt, ld_gate,
-                     (uint8_t*)ws, T, H, HV, nchunks, scale, hf_norm);
-  int rc = kad_launch_status("gdn_chunk_prep");
-  if (rc) return rc;
-  hipLaunchKernelGGL((gdn_chunk_scan<K, V>), dim3((unsigned)((int64_t)N * HV)), dim3(V * 2), 0, s,
-                     (const bf16_t*)q, (const bf16_t*)k, ld_qk, (const bf16_t*)v, ld_v,
-                     (const uint8_t*)ws, state0, sdt, bps, (bf16_t*)out, ld_out, fin, T, H, HV,
-                     nchunks, hf_norm);
-  return kad_launch_status("gdn_chunk_scan");
+  // transformers' bf16 l2norm rounding (hf_norm) or the operator's fp32
+  // scales: an instantiation each, so the VALU-bound loops carry no test
+#define KAD_CHUNK(HFV)                                                                         \
+  hipLaunchKernelGGL((gdn_chunk_prep<K, HFV>), dim3((unsigned)nrec), dim3(kPrepThreads), 0, s, \
+                     (const bf16_t*)q, (const bf16_t*)k, ld_qk, g, gdt, beta, bdt, ld_gate,    \
+                     (uint8_t*)ws, T, H, HV, nchunks, scale);                                  \
+  if (const int rc = kad_launch_status("gdn_chunk_prep")) return rc;                           \
+  hipLaunchKernelGGL((gdn_chunk_scan<K, V, HFV>), dim3((unsigned)((int64_t)N * HV)),          \
+                     dim3(V * 2), 0, s, (const bf16_t*)q, (const bf16_t*)k, ld_qk,             \
+                     (const bf16_t*)v, ld_v, (const uint8_t*)ws, state0, sdt, bps,             \
+                     (bf16_t*)out, ld_out, fin, T, H, HV, nchunks);                            \
+  return kad_launch_status("gdn_chunk_scan")
+  if (hf_norm) {
+    KAD_CHUNK(true);
+  }
+  KAD_CHUNK(false);
+#undef KAD_CHUNK
 }
 
 int64_t chunk_ws_bytes(int N, int T, int HV) {
