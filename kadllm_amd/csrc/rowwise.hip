@@ -39,21 +39,30 @@ __device__ __forceinline__ float group_sum(float v, int lanes) {
 }
 
 // Rows of D elements; `lanes` lanes per row, each handling D/(8*lanes) chunks.
+// LANES, CHUNKS > 0: the common shape fixed at compile time, the row's chunks
+// held in registers between the two passes (0: the runtime form, which reads
+// them again).
+template <int LANES, int CHUNKS>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16_t* __restrict__ x, int64_t ldx,
                                                       const bf16_t* __restrict__ w,
                                                       bf16_t* __restrict__ y, int64_t ldy,
-                                                      int64_t rows, int D, int lanes, float eps,
-                                                      float w_offset) {
+                                                      int64_t rows, int D, int lanes_rt,
+                                                      float eps, float w_offset) {
+  constexpr bool kFixed = LANES > 0;
+  const int lanes = kFixed ? LANES : lanes_rt;
   const int rows_per_block = 256 / lanes;
   const int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / lanes;
   const int li = threadIdx.x % lanes;
-  const int chunks = D / (8 * lanes);
+  const int chunks = kFixed ? CHUNKS : D / (8 * lanes);
   const bool live = row < rows;
   const bf16_t* xr = x + (live ? row : 0) * ldx;
+  u32x4 xs[kFixed ? CHUNKS : 1];
   float ss = 0.f;
   for (int c = 0; c < chunks; ++c) {
+    const u32x4 raw = *(const u32x4*)(xr + (c * lanes + li) * 8);
+    if constexpr (kFixed) xs[c] = raw;
     float f[8];
-    unpack8(*(const u32x4*)(xr + (c * lanes + li) * 8), f);
+    unpack8(raw, f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
   }
@@ -63,7 +72,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16_t* __restrict__
   for (int c = 0; c < chunks; ++c) {
     const int off = (c * lanes + li) * 8;
     float f[8], wv[8];
-    unpack8(*(const u32x4*)(xr + off), f);
+    if constexpr (kFixed)
+      unpack8(xs[c], f);
+    else
+      unpack8(*(const u32x4*)(xr + off), f);
     unpack8(*(const u32x4*)(w + off), wv);
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = (f[i] * r) * (w_offset + wv[i]);
@@ -73,24 +85,30 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16_t* __restrict__
 
 // groups of D elements: x row stride ldx between tokens, `heads` groups per
 // token at stride D; z likewise with ldz; y contiguous [rows, heads*D] (ldy)
+template <int LANES, int CHUNKS>
 __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ z, int64_t ldz,
     const bf16_t* __restrict__ w, bf16_t* __restrict__ y, int64_t ldy, int64_t groups, int heads,
-    int D, int lanes, float eps) {
+    int D, int lanes_rt, float eps) {
+  constexpr bool kFixed = LANES > 0;
+  const int lanes = kFixed ? LANES : lanes_rt;
   const int per_block = 256 / lanes;
   const int64_t gidx = (int64_t)blockIdx.x * per_block + threadIdx.x / lanes;
   const int li = threadIdx.x % lanes;
-  const int chunks = D / (8 * lanes);
+  const int chunks = kFixed ? CHUNKS : D / (8 * lanes);
   const bool live = gidx < groups;
   const int64_t g = live ? gidx : 0;
   const int64_t tok = g / heads;
   const int hh = (int)(g % heads);
   const bf16_t* xr = x + tok * ldx + (int64_t)hh * D;
   const bf16_t* zr = z + tok * ldz + (int64_t)hh * D;
+  u32x4 xs[kFixed ? CHUNKS : 1];
   float ss = 0.f;
   for (int c = 0; c < chunks; ++c) {
+    const u32x4 raw = *(const u32x4*)(xr + (c * lanes + li) * 8);
+    if constexpr (kFixed) xs[c] = raw;
     float f[8];
-    unpack8(*(const u32x4*)(xr + (c * lanes + li) * 8), f);
+    unpack8(raw, f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
   }
@@ -100,7 +118,10 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(
   for (int c = 0; c < chunks; ++c) {
     const int off = (c * lanes + li) * 8;
     float f[8], wv[8], zv[8];
-    unpack8(*(const u32x4*)(xr + off), f);
+    if constexpr (kFixed)
+      unpack8(xs[c], f);
+    else
+      unpack8(*(const u32x4*)(xr + off), f);
     unpack8(*(const u32x4*)(w + off), wv);
     unpack8(*(const u32x4*)(zr + off), zv);
 #pragma unroll
@@ -310,9 +331,15 @@ extern "C" int kad_rmsnorm(const void* x, int64_t ldx, const void* w, float w_of
               "16-byte aligned rows required");
   const int lanes = lanes_for(D);
   const int64_t per_block = 256 / lanes;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)kad_cdiv(rows, per_block)), dim3(256), 0,
-                     (hipStream_t)stream, (const bf16_t*)x, ldx, (const bf16_t*)w, (bf16_t*)y, ldy,
-                     rows, D, lanes, eps, w_offset);
+  const dim3 grid((unsigned)kad_cdiv(rows, per_block));
+  if (lanes == 64 && D == 1024)   // the model's hidden size
+    hipLaunchKernelGGL((rmsnorm_kernel<64, 2>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)x, ldx, (const bf16_t*)w, (bf16_t*)y, ldy, rows, D, lanes,
+                       eps, w_offset);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 0>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)x, ldx, (const bf16_t*)w, (bf16_t*)y, ldy, rows, D, lanes,
+                       eps, w_offset);
   return kad_launch_status("rmsnorm_kernel");
 }
 
@@ -326,9 +353,15 @@ extern "C" int kad_rmsnorm_gated(const void* x, int64_t ldx, const void* z, int6
               "16-byte aligned rows required");
   const int lanes = lanes_for(D);
   const int64_t groups = rows * heads, per_block = 256 / lanes;
-  hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3((unsigned)kad_cdiv(groups, per_block)), dim3(256),
-                     0, (hipStream_t)stream, (const bf16_t*)x, ldx, (const bf16_t*)z, ldz,
-                     (const bf16_t*)w, (bf16_t*)y, ldy, groups, heads, D, lanes, eps);
+  const dim3 grid((unsigned)kad_cdiv(groups, per_block));
+  if (lanes == 16 && D == 128)   // the GDN value head
+    hipLaunchKernelGGL((rmsnorm_gated_kernel<16, 1>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)x, ldx, (const bf16_t*)z, ldz, (const bf16_t*)w, (bf16_t*)y,
+                       ldy, groups, heads, D, lanes, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_gated_kernel<0, 0>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)x, ldx, (const bf16_t*)z, ldz, (const bf16_t*)w, (bf16_t*)y,
+                       ldy, groups, heads, D, lanes, eps);
   return kad_launch_status("rmsnorm_gated_kernel");
 }
 
