@@ -205,11 +205,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 // rotary cos/sin are computed once per token (lane l evaluates frequency
 // l % (rot/2)) and reused by every head; the rotate-half partner (dim d +- rot/2, P = rot/16 lanes
 // away) comes from a lane exchange.  Needs rot/16 a power of two (or rot 0).
+// DT, ROTT > 0: the model's head (d 256, rotary 64, normed) fixed at compile
+// time, so the lane arithmetic, shuffles and loops are constants; 0: runtime
+template <int DT, int ROTT>
 __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
     const bf16_t* __restrict__ src, int64_t ld_src, int64_t src_head_stride, int heads,
     const bf16_t* __restrict__ w, bf16_t* __restrict__ dst, int64_t period, int64_t s_b,
-    int64_t s_t, int64_t s_h, int64_t rows, int D, int rot, const float* __restrict__ inv_freq,
-    int64_t pos0, int64_t pos_period, float eps, int do_norm) {
+    int64_t s_t, int64_t s_h, int64_t rows, int D_rt, int rot_rt,
+    const float* __restrict__ inv_freq, int64_t pos0, int64_t pos_period, float eps,
+    int do_norm_rt) {
+  constexpr bool kFixed = DT > 0;
+  const int D = kFixed ? DT : D_rt;
+  const int rot = kFixed ? ROTT : rot_rt;
+  const bool do_norm = kFixed ? true : do_norm_rt != 0;
   const int64_t tok = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
   const int lane = threadIdx.x & 63;
   if (tok >= rows) return;
@@ -393,10 +401,17 @@ extern "C" int kad_qk_norm_rope(const void* src, int64_t ld_src, int64_t src_hea
                    ld_src % 8 == 0 && src_head_stride % 8 == 0 && s_b % 8 == 0 && s_t % 8 == 0 &&
                    s_h % 8 == 0;
   if (vec) {
-    hipLaunchKernelGGL(qk_norm_rope_vec_kernel, dim3((unsigned)kad_cdiv(rows, 4)), dim3(256), 0,
-                       (hipStream_t)stream, (const bf16_t*)src, ld_src, src_head_stride, heads,
-                       (const bf16_t*)w, (bf16_t*)dst, period, s_b, s_t, s_h, rows, D, rot,
-                       inv_freq, pos0, pos_period, eps, do_norm);
+    const dim3 grid((unsigned)kad_cdiv(rows, 4));
+    if (D == 256 && rot == 64 && do_norm)   // Qwen3.5's attention heads
+      hipLaunchKernelGGL((qk_norm_rope_vec_kernel<256, 64>), grid, dim3(256), 0,
+                         (hipStream_t)stream, (const bf16_t*)src, ld_src, src_head_stride, heads,
+                         (const bf16_t*)w, (bf16_t*)dst, period, s_b, s_t, s_h, rows, D, rot,
+                         inv_freq, pos0, pos_period, eps, do_norm);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_vec_kernel<0, 0>), grid, dim3(256), 0,
+                         (hipStream_t)stream, (const bf16_t*)src, ld_src, src_head_stride, heads,
+                         (const bf16_t*)w, (bf16_t*)dst, period, s_b, s_t, s_h, rows, D, rot,
+                         inv_freq, pos0, pos_period, eps, do_norm);
     return kad_launch_status("qk_norm_rope_vec_kernel");
   }
   const int64_t waves = rows * heads;
