@@ -78,11 +78,15 @@ __global__ __launch_bounds__(256) void conv_suffix_scalar(
 // computed so that every thread keeps one 16-byte load in flight.
 constexpr int kConvBeams = 8;
 
+// TT > 0: the suffix length fixed at compile time (the search's one- to
+// four-token suffixes), so the (beam, token) of each step needs no division
+template <int TT>
 __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
     const bf16_t* __restrict__ x, int64_t sx_n, int64_t sx_t, const bf16_t* __restrict__ state,
     int64_t ss_b, int64_t ss_c, int64_t ss_t, int history, const bf16_t* __restrict__ w,
-    bf16_t* __restrict__ out, int64_t so_n, int64_t so_t, int W, int C, int T_, int nbg,
+    bf16_t* __restrict__ out, int64_t so_n, int64_t so_t, int W, int C, int T_rt, int nbg,
     int silu) {
+  const int T_ = TT > 0 ? TT : T_rt;
   const int c8 = blockIdx.y * 256 + threadIdx.x;
   if (c8 >= C / 8) return;
   const int c0 = c8 * 8;
@@ -313,10 +317,20 @@ extern "C" int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c,
   if (vec) {
     const int nbg = (int)kad_cdiv(W, kConvBeams);
     KAD_REQUIRE((int64_t)B * nbg < 2147483647, "too many beams for the grid");
-    hipLaunchKernelGGL(conv_suffix_vec_bf16, dim3((unsigned)(B * nbg), (unsigned)kad_cdiv(C / 8, 256)),
-                       dim3(256), 0, s, (const bf16_t*)x, sx_n, sx_t, (const bf16_t*)state, ss_b,
-                       ss_c, ss_t, history, (const bf16_t*)weight, (bf16_t*)out, so_n, so_t, W, C,
-                       T, nbg, activation_silu);
+    const dim3 grid((unsigned)(B * nbg), (unsigned)kad_cdiv(C / 8, 256));
+#define KAD_CONV_VEC(TTV)                                                                    \
+  hipLaunchKernelGGL((conv_suffix_vec_bf16<TTV>), grid, dim3(256), 0, s, (const bf16_t*)x,   \
+                     sx_n, sx_t, (const bf16_t*)state, ss_b, ss_c, ss_t, history,             \
+                     (const bf16_t*)weight, (bf16_t*)out, so_n, so_t, W, C, T, nbg,           \
+                     activation_silu)
+    switch (T) {
+      case 1: KAD_CONV_VEC(1); break;
+      case 2: KAD_CONV_VEC(2); break;
+      case 3: KAD_CONV_VEC(3); break;
+      case 4: KAD_CONV_VEC(4); break;
+      default: KAD_CONV_VEC(0); break;
+    }
+#undef KAD_CONV_VEC
     return kad_launch_status("conv_suffix_vec_bf16");
   }
   if (dtype == KAD_DTYPE_BF16)
