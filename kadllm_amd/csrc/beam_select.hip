@@ -857,17 +857,20 @@ __global__ __launch_bounds__(256) void history_kernel(const int64_t* __restrict_
 // dst rows (n, t), t < rows_copy, of beam n = b * W + w  <-  src rows
 // (b * Wp + parents[n], t): a beam's cached per-token rows follow its parent.
 // 16 bytes per thread; rows are row_bytes long (a multiple of 16).
+// IDX: the index type of the flat chunk count (32-bit divisions whenever
+// it fits, the 64-bit ones costing several times the copy's own work)
+template <typename IDX>
 __global__ __launch_bounds__(256) void gather_beam_rows_kernel(
     const uint8_t* __restrict__ src, int64_t ld_src, int src_rows_per_beam,
     uint8_t* __restrict__ dst, int64_t ld_dst, int dst_rows_per_beam, int rows_copy,
     const int64_t* __restrict__ parents, int W, int Wp, int64_t nbeams, int chunks_per_row) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t per_beam = (int64_t)rows_copy * chunks_per_row;
-  if (idx >= nbeams * per_beam) return;
-  const int64_t n = idx / per_beam;
+  const IDX idx = (IDX)blockIdx.x * 256 + threadIdx.x;
+  const IDX per_beam = (IDX)rows_copy * chunks_per_row;
+  if (idx >= (IDX)nbeams * per_beam) return;
+  const IDX n = idx / per_beam;
   const int rest = (int)(idx - n * per_beam);
   const int t = rest / chunks_per_row, c = rest - t * chunks_per_row;
-  const int64_t b = n / W;
+  const int64_t b = n / (IDX)W;
   const int64_t pn = parents[n];
   const int64_t sn = b * Wp + (pn < 0 ? 0 : (pn >= Wp ? Wp - 1 : pn));  // stay in bounds
   const u32x4 v = *(const u32x4*)(src + (sn * src_rows_per_beam + t) * ld_src + c * 16);
@@ -1053,9 +1056,15 @@ extern "C" int kad_gather_beam_rows(const void* src, int64_t ld_src_bytes, int s
   const int64_t nbeams = (int64_t)B * W;
   const int cpr = (int)(row_bytes / 16);
   const int64_t total = nbeams * rows_copy * cpr;
-  hipLaunchKernelGGL(gather_beam_rows_kernel, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
-                     (hipStream_t)stream, (const uint8_t*)src, ld_src_bytes, src_rows_per_beam,
-                     (uint8_t*)dst, ld_dst_bytes, dst_rows_per_beam, rows_copy, parents, W, Wp,
-                     nbeams, cpr);
+  if (total + 256 < ((int64_t)1 << 31))
+    hipLaunchKernelGGL(gather_beam_rows_kernel<uint32_t>, dim3((unsigned)kad_cdiv(total, 256)),
+                       dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, ld_src_bytes,
+                       src_rows_per_beam, (uint8_t*)dst, ld_dst_bytes, dst_rows_per_beam,
+                       rows_copy, parents, W, Wp, nbeams, cpr);
+  else
+    hipLaunchKernelGGL(gather_beam_rows_kernel<int64_t>, dim3((unsigned)kad_cdiv(total, 256)),
+                       dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, ld_src_bytes,
+                       src_rows_per_beam, (uint8_t*)dst, ld_dst_bytes, dst_rows_per_beam,
+                       rows_copy, parents, W, Wp, nbeams, cpr);
   return kad_launch_status("gather_beam_rows_kernel");
 }
