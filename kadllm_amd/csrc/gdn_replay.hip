@@ -120,7 +120,11 @@ void gdn_replay_kernel(
     int64_t ld_qk, int64_t ld_v, const void* __restrict__ gdecay, int gate_dtype,
     const void* __restrict__ beta, int beta_dtype, int64_t ld_gate,
     const void* __restrict__ state, int state_dtype, TIN* __restrict__ out, int64_t ld_out,
-    int W, int T, int H, int HV, float scale, int beams_per_block, int nbb) {
+    int W, int T_rt, int H, int HV, float scale, int beams_per_block, int nbb) {
+  // each suffix length has its own instantiation (launched only with
+  // T == kTMax), so the per-token tests and the row arithmetic see a constant
+  constexpr int T = kTMax;
+  (void)T_rt;
   constexpr int KSTEPS = KD / 32;
   constexpr int VROWS = VD / 4;
   constexpr int MT = VROWS / 16;
