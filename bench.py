@@ -63,7 +63,7 @@ T975 = {1: 12.706, 2: 4.303, 3: 3.182, 4: 2.776, 5: 2.571, 6: 2.447, 7: 2.365, 9
 # for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the number of
 # GEMM calls (346; a call that splits its last round launches two kernels).
 # Re-measured with the commands in profiles/hbm_traffic_and_busy_b32_p1024_w256.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 382.2e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 379.2e6
 
 
 def validate_output(tokens, batch, width, depth):
