@@ -289,7 +289,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
   }
 }
 
-// copy [rows, heads, D] head rows into a strided destination (prefill V cache)
+// copy [rows, heads, D] head rows into a strided destination (prefill V
+// cache); IDX: 32-bit index arithmetic whenever the chunk count fits
+template <typename IDX>
 __global__ __launch_bounds__(256) void scatter_heads_kernel(const bf16_t* __restrict__ src,
                                                             int64_t ld_src, int heads, int D,
                                                             bf16_t* __restrict__ dst,
@@ -297,14 +299,15 @@ __global__ __launch_bounds__(256) void scatter_heads_kernel(const bf16_t* __rest
                                                             int64_t s_t, int64_t s_h,
                                                             int64_t rows) {
   const int chunks = D / 8;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= rows * heads * chunks) return;
-  const int c = (int)(idx % chunks);
-  const int64_t gh = idx / chunks;
-  const int hh = (int)(gh % heads);
-  const int64_t tok = gh / heads;
-  const u32x4 v = *(const u32x4*)(src + tok * ld_src + (int64_t)hh * D + c * 8);
-  *(u32x4*)(dst + (tok / period) * s_b + (tok % period) * s_t + hh * s_h + c * 8) = v;
+  const IDX idx = (IDX)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (IDX)rows * heads * chunks) return;
+  const int c = (int)(idx % (IDX)chunks);
+  const IDX gh = idx / (IDX)chunks;
+  const int hh = (int)(gh % (IDX)heads);
+  const IDX tok = gh / (IDX)heads;
+  const int64_t tb = (int64_t)(tok / (IDX)period), tt = (int64_t)(tok % (IDX)period);
+  const u32x4 v = *(const u32x4*)(src + (int64_t)tok * ld_src + (int64_t)hh * D + c * 8);
+  *(u32x4*)(dst + tb * s_b + tt * s_t + hh * s_h + c * 8) = v;
 }
 
 __global__ __launch_bounds__(256) void embedding_kernel(const int64_t* __restrict__ ids,
@@ -431,9 +434,14 @@ extern "C" int kad_scatter_heads(const void* src, int64_t ld_src, int heads, int
                   s_t % 8 == 0 && s_h % 8 == 0,
               "16-byte aligned rows required");
   const int64_t total = rows * heads * (D / 8);
-  hipLaunchKernelGGL(scatter_heads_kernel, dim3((unsigned)kad_cdiv(total, 256)), dim3(256), 0,
-                     (hipStream_t)stream, (const bf16_t*)src, ld_src, heads, D, (bf16_t*)dst,
-                     period, s_b, s_t, s_h, rows);
+  if (total + 256 < ((int64_t)1 << 31) && period < ((int64_t)1 << 31))
+    hipLaunchKernelGGL(scatter_heads_kernel<uint32_t>, dim3((unsigned)kad_cdiv(total, 256)),
+                       dim3(256), 0, (hipStream_t)stream, (const bf16_t*)src, ld_src, heads, D,
+                       (bf16_t*)dst, period, s_b, s_t, s_h, rows);
+  else
+    hipLaunchKernelGGL(scatter_heads_kernel<int64_t>, dim3((unsigned)kad_cdiv(total, 256)),
+                       dim3(256), 0, (hipStream_t)stream, (const bf16_t*)src, ld_src, heads, D,
+                       (bf16_t*)dst, period, s_b, s_t, s_h, rows);
   return kad_launch_status("scatter_heads_kernel");
 }
 
