@@ -32,6 +32,9 @@ Other modes:
   --workload conditional_sid  two-level SID search (configuration 5)
   --workload hbm_copy    a 1 GiB device copy: measured streaming bandwidth and
                          the calibration of rocprofv3's FETCH/WRITE_SIZE
+  --workload hbm_probe   the library's streaming probe over 4 GiB (copy, read,
+                         write), which the default run also measures and
+                         reports every HBM-bound kernel against
   --depth 7 --batch 4    the reference's 7-token runs (README.md:125)
 """
 
@@ -64,6 +67,33 @@ T975 = {1: 12.706, 2: 4.303, 3: 3.182, 4: 2.776, 5: 2.571, 6: 2.447, 7: 2.365, 9
 # GEMM calls (346; a call that splits its last round launches two kernels).
 # Re-measured with the commands in profiles/hbm_traffic_and_busy_b32_p1024_w256.md.
 GEMM_TRAFFIC_BYTES_PER_LAUNCH = 379.2e6
+
+
+def repeat_stability(outputs, first):
+    """Whether any timed call's tokens differ from the last warm-up call's, and
+    each call's mean per-request overlap of the beam sets with it
+    (benchmarks/grbeam.py:331-340)."""
+    differ = any(out != first for out in outputs)
+    overlap = [round(statistics.mean(
+        len({tuple(x) for x in left} & {tuple(x) for x in right}) / len(right)
+        for left, right in zip(out, first)), 6) for out in outputs]
+    return {"repeat_tokens_differ": differ, "repeat_beam_set_overlap": overlap}
+
+
+def provenance(cfg, sd, ids):
+    """SHA-256 of the model configuration, of the weights (in state-dict key
+    order, raw bytes) and of the prompt ids (benchmarks/grbeam.py:24-29,159-160)."""
+    import dataclasses
+    import hashlib
+
+    conf = json.dumps(dataclasses.asdict(cfg), sort_keys=True, default=str).encode()
+    w = hashlib.sha256()
+    for k in sorted(sd):
+        w.update(k.encode())
+        w.update(sd[k].detach().contiguous().cpu().view(torch.uint8).numpy().tobytes())
+    p = hashlib.sha256(ids.cpu().contiguous().numpy().tobytes())
+    return {"config_sha256": hashlib.sha256(conf).hexdigest(), "weights_sha256": w.hexdigest(),
+            "prompt_ids_sha256": p.hexdigest()}
 
 
 def validate_output(tokens, batch, width, depth):
@@ -298,9 +328,11 @@ def grbeam(a):
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(a.steps)]
+    first = None
     with DeviceMemorySampler() as mem:
         for _ in range(a.warmup):
-            validate_output(run(), a.batch, a.beam, a.depth)
+            first = run()
+            validate_output(first, a.batch, a.beam, a.depth)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
         # The tokens' host copy (.tolist(), inside the timed region as in the
@@ -326,6 +358,7 @@ def grbeam(a):
     gpu_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
     for out in outputs:
         validate_output(out, a.batch, a.beam, a.depth)
+    stability = repeat_stability(outputs, first if first is not None else outputs[0])
     memory = {"device_peak_gib": round(mem.peak / 2**30, 2),
               "torch_peak_allocated_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
               "torch_peak_reserved_gib": round(torch.cuda.max_memory_reserved() / 2**30, 2)}
@@ -351,6 +384,11 @@ def grbeam(a):
                         "algorithmic_bytes_per_launch": g["bytes_per_launch"],
                         "launches_per_step": g["launches_per_step"],
                         "gemm_ms_per_step": g["ms_per_step"]}
+
+    probe = None
+    if not a.no_probe:
+        probe = hbm_probe_rates(4 << 30, 10)
+        add_probe_fractions(kernels, probe)
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -386,12 +424,17 @@ def grbeam(a):
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "hbm_probe": probe,
         "memory": memory,
+        **stability,
+        "provenance": provenance(cfg, sd, ids) if not a.no_provenance else None,
         "step_ms": [round(1000 * t, 2) for t in times],
         "step_gpu_ms": [round(t, 2) for t in gpu_ms],
         "step_enqueue_ms": [round(1000 * t, 2) for t in enqueue[:a.steps]],
     }
     print(json.dumps(line), flush=True)
+    if stability["repeat_tokens_differ"]:
+        raise SystemExit("the timed searches did not all return the warm-up's tokens")
     return line
 
 
@@ -402,7 +445,7 @@ def reference_protocol(a):
     child = [sys.executable, os.path.abspath(__file__), "--steps", str(a.steps),
              "--warmup", str(a.warmup), "--batch", str(a.batch), "--prefix", str(a.prefix),
              "--beam", str(a.beam), "--depth", str(a.depth), "--prompts", a.prompts,
-             "--no-cpu-baseline", "--profile-steps", "0"]
+             "--no-cpu-baseline", "--profile-steps", "0", "--no-provenance", "--no-probe"]
     means, peaks, lines = [], [], []
     for p in range(a.processes):
         res = subprocess.run(child, capture_output=True, text=True, timeout=900)
@@ -707,6 +750,58 @@ def ops_gemm(a):
               "hipblaslt_tflops": round(total["flops"] / total["lib_s"] / 1e12, 1)})
 
 
+# kernel classes whose algorithmic bytes are almost all reads (reported
+# against the read probe); the others against the copy probe
+READ_DOMINATED = {"row_select", "merge_select"}
+
+
+def hbm_probe_rates(size=4 << 30, iters=10):
+    """GB/s of the library's streaming probe (kad_hbm_probe) over `size`
+    bytes: copy (read + write, counting both), read only, write only."""
+    from kadllm_amd import _lib
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(size, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    stream = _lib.stream_of(src)
+    rates = {}
+    for mode, name, factor in ((0, "copy", 2), (1, "read", 1), (2, "write", 1)):
+        def launch():
+            _lib.call("kad_hbm_probe", _lib.ptr(src), _lib.ptr(dst), size, mode, stream)
+        launch()
+        sec = _time_calls(launch, iters)
+        rates[name + "_GB/s"] = round(factor * size / sec / 1e9, 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    rates["bytes"] = size
+    return rates
+
+
+def add_probe_fractions(kernels, probe):
+    """Each HBM-bound kernel class's GB/s as a fraction of the probe's (read
+    probe for read-dominated classes, copy probe otherwise)."""
+    for label, e in (kernels or {}).items():
+        if e.get("GB/s") is None:
+            continue
+        ref = probe["read_GB/s"] if label in READ_DOMINATED else probe["copy_GB/s"]
+        e["probe_frac"] = round(e["GB/s"] / ref, 4)
+        e["probe"] = "read" if label in READ_DOMINATED else "copy"
+
+
+def hbm_probe(a):
+    """The library's own streaming kernel over 4 GiB (no profiler): the
+    bandwidth this board gives a plain copy, read and write."""
+    rates = hbm_probe_rates(4 << 30, a.op_iters)
+    gbs = rates["copy_GB/s"]
+    _op_line("HBM streaming probe 4 GiB: achieved GB/s (copy, read + write)", gbs, "GB/s",
+             {"workload": "hbm_probe 4 GiB, 16-byte lanes, 8 workgroups per CU"},
+             {"kernel": "hbm_probe_kernel", "bound": "hbm", "achieved": gbs,
+              "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+              "traffic": None, "algorithmic_bytes_per_launch": 2 * rates["bytes"]}, None,
+             {"iters": a.op_iters, "ms": round(2 * rates["bytes"] / gbs / 1e6, 4),
+              "probe": rates})
+
+
 def hbm_copy(a):
     """A 1 GiB device-to-device copy (torch's copy kernel), repeated: the
     bandwidth a plain streaming kernel reaches on this board, and the known
@@ -788,6 +883,10 @@ def main():
     ap.add_argument("--depth", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=2)
+    ap.add_argument("--no-probe", action="store_true",
+                    help="skip the 4 GiB HBM streaming probe after the timed steps")
+    ap.add_argument("--no-provenance", action="store_true",
+                    help="skip the SHA-256 of the configuration, weights and prompts")
     ap.add_argument("--no-gc-freeze", action="store_true",
                     help="leave the start-up heap to Python's full garbage collections")
     ap.add_argument("--profile-steps", type=int, default=2,
@@ -800,7 +899,7 @@ def main():
     ap.add_argument("--op-iters", type=int, default=50)
     ap.add_argument("--workload",
                     choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention", "ops_gemm",
-                             "hbm_copy"),
+                             "hbm_copy", "hbm_probe"),
                     default="grbeam")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -811,7 +910,7 @@ def main():
         return reference_protocol(a)
     return {"grbeam": grbeam, "conditional_sid": conditional_sid, "ops_gdn": ops_gdn,
             "ops_attention": ops_attention, "ops_gemm": ops_gemm,
-            "hbm_copy": hbm_copy}[a.workload](a)
+            "hbm_copy": hbm_copy, "hbm_probe": hbm_probe}[a.workload](a)
 
 
 if __name__ == "__main__":

@@ -362,6 +362,16 @@ int kad_embedding_f32(const int64_t* ids, const float* table, float* out, int64_
                       int64_t vocab, kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
+ * HBM streaming probe (no reference counterpart): the bandwidth a plain
+ * streaming kernel reaches on this device, for reporting the HBM-bound
+ * kernels against it beside the datasheet peak.  mode 0 copies `bytes` from
+ * src to dst (read + write), 1 reads src (dst receives at most a few
+ * sentinel words), 2 writes dst.  bytes a multiple of 16, buffers 16-byte
+ * aligned; src may be NULL for mode 2.
+ */
+int kad_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
  * MFMA lane-layout self-test (no reference counterpart): C[16x16] = A[16x32]
  * B[32x16] (bf16 in, fp32 out, all row-major) computed by one wave with the
  * operand layout the kernels above assume for v_mfma_f32_16x16x32_bf16, and

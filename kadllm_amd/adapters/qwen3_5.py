@@ -113,12 +113,36 @@ class Qwen35GRBeamAdapter:
         if tokens.device != self.device:
             raise ValueError("tokens and model must share a device")
 
+    def _range_probe(self, tokens):
+        """Start the check that every token id lies in the embedding table:
+        the ids' (min, max) go to pinned host memory behind an event, so the
+        call's own kernels are enqueued before the host waits for the result
+        (the embedding kernel clamps ids, so nothing reads outside the table
+        meanwhile).  _raise_out_of_range finishes the check."""
+        lo_hi = torch.stack(torch.aminmax(tokens))
+        host = torch.empty(2, dtype=lo_hi.dtype, pin_memory=True)
+        host.copy_(lo_hi, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        return host, done
+
+    def _raise_out_of_range(self, probe):
+        """IndexError with torch's nn.Embedding message for any id outside
+        [0, vocab_size)."""
+        host, done = probe
+        done.synchronize()
+        lo, hi = host.tolist()
+        if lo < 0 or hi >= self.config.vocab_size:
+            raise IndexError("index out of range in self")
+
     @torch.no_grad()
     def prefill(self, input_ids):
         self._check(input_ids)
         if input_ids.ndim != 2 or min(input_ids.shape) < 1:
             raise ValueError("input_ids must be nonempty unpadded [B,L]")
+        probe = self._range_probe(input_ids)
         logits, layers = self._runner.prefill(input_ids)
+        self._raise_out_of_range(probe)
         state = Qwen35Prefix(input_ids.shape[1], input_ids.shape[0], self._owner, layers)
         return PrefillResult(logits, state)
 
@@ -129,7 +153,10 @@ class Qwen35GRBeamAdapter:
             raise ValueError("prefix belongs to a different adapter")
         if history.ndim != 3 or min(history.shape) < 1 or history.shape[0] != state.batch:
             raise ValueError("history must be nonempty [B,W,T] matching the prefix")
-        return self._runner.decode(history, state.layers, state.length)
+        probe = self._range_probe(history)
+        logits = self._runner.decode(history, state.layers, state.length)
+        self._raise_out_of_range(probe)
+        return logits
 
     @classmethod
     def from_pretrained(cls, path, device="cuda", **kwargs):
@@ -184,7 +211,10 @@ class Qwen35GRBeamAdapter:
         if cache is not None and (parents.shape != history.shape[:2] or parents.device != history.device):
             raise ValueError("parents must be [B, W] on the history's device")
         tokens = history[:, :, -1].contiguous()
-        return self._runner.decode_step(tokens, parents, state.layers, state.length, cache)
+        probe = self._range_probe(tokens)
+        out = self._runner.decode_step(tokens, parents, state.layers, state.length, cache)
+        self._raise_out_of_range(probe)
+        return out
 
 
 def native_model(cfg, state_dict):

@@ -874,7 +874,8 @@ __global__ __launch_bounds__(256) void gather_beam_rows_kernel(
   const int64_t pn = parents[n];
   const int64_t sn = b * Wp + (pn < 0 ? 0 : (pn >= Wp ? Wp - 1 : pn));  // stay in bounds
   const u32x4 v = *(const u32x4*)(src + (sn * src_rows_per_beam + t) * ld_src + c * 16);
-  *(u32x4*)(dst + (n * dst_rows_per_beam + t) * ld_dst + c * 16) = v;
+  // row offsets in 64 bits: only the flat chunk count is bounded by IDX
+  *(u32x4*)(dst + ((int64_t)n * dst_rows_per_beam + t) * ld_dst + c * 16) = v;
 }
 
 int launch_row_select(const void* logits, int logits_dtype, int64_t ld, const void* mask,

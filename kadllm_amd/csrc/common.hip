@@ -70,3 +70,63 @@ extern "C" int kad_selftest_mfma32(const void* a, const void* b, float* c, kad_s
                      (const bf16_t*)b, c);
   return kad_launch_status("selftest32");
 }
+
+// ---------------------------------------------------------------------------
+// HBM streaming probe: the bandwidth a plain streaming kernel reaches on this
+// device, which the HBM-bound kernels are reported against beside the 8 TB/s
+// datasheet figure.  mode 0 copies src to dst (read + write), 1 reads src (a
+// lane writes only when its running XOR equals `magic`, which keeps the loads
+// live), 2 writes dst.  16 bytes per lane per access, kProbeUnroll accesses in
+// flight per lane, grid-stride over the buffer; every index is below n16.
+constexpr int kProbeUnroll = 4;
+
+__global__ __launch_bounds__(256) void hbm_probe_kernel(const u32x4* __restrict__ src,
+                                                        u32x4* __restrict__ dst, int64_t n16,
+                                                        int mode, uint32_t magic) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const u32x4 fill = {magic, magic ^ 1u, magic ^ 2u, magic ^ 3u};
+  int64_t i = gid;
+  for (; i + (kProbeUnroll - 1) * stride < n16; i += kProbeUnroll * stride) {
+    if (mode == 2) {
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) dst[i + u * stride] = fill;
+      continue;
+    }
+    u32x4 v[kProbeUnroll];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+    if (mode == 0) {
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) dst[i + u * stride] = v[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u];
+    }
+  }
+  for (; i < n16; i += stride) {
+    if (mode == 2) dst[i] = fill;
+    else if (mode == 0) dst[i] = src[i];
+    else acc ^= src[i];
+  }
+  if (mode == 1 && acc[0] == magic && acc[1] == magic && gid < n16) dst[gid] = acc;
+}
+
+extern "C" int kad_hbm_probe(const void* src, void* dst, int64_t bytes, int mode,
+                             kad_stream_t stream) {
+  KAD_REQUIRE(mode >= 0 && mode <= 2, "probe mode must be 0 (copy), 1 (read) or 2 (write)");
+  KAD_REQUIRE(bytes > 0 && bytes % 16 == 0, "probe size must be a positive multiple of 16");
+  KAD_REQUIRE(dst && (mode == 2 || src), "null pointer argument");
+  KAD_REQUIRE(((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0,
+              "probe buffers must be 16-byte aligned");
+  const int64_t n16 = bytes / 16;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t want = (int64_t)cus * 8;  // 8 workgroups of 256 lanes per CU
+  const int64_t blocks = want < kad_cdiv(n16, 256) ? want : kad_cdiv(n16, 256);
+  hipLaunchKernelGGL(hbm_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const u32x4*)src, (u32x4*)dst, n16, mode, 0x9e3779b9u);
+  return kad_launch_status("hbm_probe_kernel");
+}

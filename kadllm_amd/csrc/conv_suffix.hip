@@ -5,14 +5,16 @@
 // prefix taps (state[b, c, history-3 ..]) and the weights are read by every
 // beam of the request and stay in L2.  Rounding follows the reference torch
 // path: the convolution result is rounded to the tensor dtype, then SiLU is
-// applied and rounded again (for fp32 both roundings are exact).  The decode
-// kernels take SiLU with the hardware reciprocal (silu_fast: they are
-// VALU-bound); the prefill kernel keeps the IEEE divide.
+// applied and rounded again (for fp32 both roundings are exact).  The bf16
+// decode kernels take SiLU with the hardware reciprocal (silu_fast: they are
+// VALU-bound and the result is rounded to bf16); fp16 and fp32 tensors and the
+// prefill kernel keep the IEEE exp and divide.
 //
-// Two paths: a vectorised one when channels are contiguous in x and out
+// Three paths: a vectorised one when channels are contiguous in x and out
 // (8 channels per thread, 16-byte accesses; the [rows, T, C] layout produced by
-// the projection GEMM), and a scalar one for any other strides (the
-// reference's [BW, C, T] layout).
+// the projection GEMM), a vectorised one for the reference's contiguous
+// [BW, C, T] layout (8 channels x T tokens per thread), and a scalar one for
+// any other strides, widths and dtypes.
 
 #include "kad_common.h"
 
@@ -20,6 +22,14 @@ namespace {
 
 template <typename T>
 __device__ __forceinline__ float ld(const T* p) { return Elem<T>::to_f(*p); }
+
+// SiLU in the dtype's precision: the hardware reciprocal for bf16 outputs, the
+// IEEE exp and divide (torch's silu) for fp16 and fp32
+template <typename T>
+__device__ __forceinline__ float silu_for(float x) {
+  if constexpr (Elem<T>::code == KAD_DTYPE_BF16) return silu_fast(x);
+  else return x / (1.0f + expf(-x));
+}
 
 template <typename T>
 __global__ __launch_bounds__(256) void conv_suffix_scalar(
@@ -45,7 +55,7 @@ __global__ __launch_bounds__(256) void conv_suffix_scalar(
         acc += ld(w + (int64_t)c * width + i) * xv;
       }
       float y = round_to_dtype(acc, Elem<T>::code);
-      if (silu) y = silu_fast(y);
+      if (silu) y = silu_for<T>(y);
       out[n * so_n + (int64_t)c * so_c + (int64_t)t * so_t] = Elem<T>::from_f(y);
     }
     return;
@@ -66,7 +76,7 @@ __global__ __launch_bounds__(256) void conv_suffix_scalar(
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc += wt[i] * win[i];
     float y = round_to_dtype(acc, Elem<T>::code);
-    if (silu) y = silu_fast(y);
+    if (silu) y = silu_for<T>(y);
     out[n * so_n + (int64_t)c * so_c + (int64_t)t * so_t] = Elem<T>::from_f(y);
   }
 }
@@ -176,6 +186,87 @@ __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
   }
 }
 
+
+// The reference's contiguous [BW, C, T] layout (each beam's block of C * T
+// elements is one contiguous run, tokens fastest): 8 channels x TT tokens per
+// thread are TT consecutive 16-byte words, so a beam streams through with
+// vector loads and stores exactly as the token-major kernel does.  Same grid
+// and arithmetic as conv_suffix_vec_bf16 (kConvBeams beams of one request per
+// thread, the next beam's words loaded before the current one is computed).
+template <int TT>
+__global__ __launch_bounds__(256) void conv_suffix_ct_bf16(
+    const bf16_t* __restrict__ x, int64_t sx_n, const bf16_t* __restrict__ state, int64_t ss_b,
+    int64_t ss_c, int64_t ss_t, int history, const bf16_t* __restrict__ w,
+    bf16_t* __restrict__ out, int64_t so_n, int W, int C, int nbg, int silu) {
+  const int c8 = blockIdx.y * 256 + threadIdx.x;
+  if (c8 >= C / 8) return;
+  const int c0 = c8 * 8;
+  const int b = blockIdx.x / nbg;
+  const int j0 = (blockIdx.x % nbg) * kConvBeams;
+  const int nj = min(W - j0, kConvBeams);
+  float wt[8][4];
+  {
+    const u32x4* wp = (const u32x4*)(w + (int64_t)c0 * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4 r = wp[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int flat = j * 8 + e * 2;
+        wt[flat / 4][flat % 4] = __uint_as_float(r[e] << 16);
+        wt[(flat + 1) / 4][(flat + 1) % 4] = __uint_as_float(r[e] & 0xffff0000u);
+      }
+    }
+  }
+  float tap[8][3];
+  const bf16_t* sb = state + (int64_t)b * ss_b;
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      tap[ch][i] = bf2f(sb[(int64_t)(c0 + ch) * ss_c + (int64_t)(history - 3 + i) * ss_t]);
+
+  const int64_t n0 = (int64_t)b * W + j0;
+  const int64_t off = (int64_t)c0 * TT;  // this thread's 8 * TT elements in a beam's block
+  u32x4 next[TT];
+#pragma unroll
+  for (int k = 0; k < TT; ++k) next[k] = ((const u32x4*)(x + n0 * sx_n + off))[k];
+  for (int j = 0; j < nj; ++j) {
+    u32x4 cur[TT];
+#pragma unroll
+    for (int k = 0; k < TT; ++k) cur[k] = next[k];
+    if (j + 1 < nj) {
+#pragma unroll
+      for (int k = 0; k < TT; ++k) next[k] = ((const u32x4*)(x + (n0 + j + 1) * sx_n + off))[k];
+    }
+    u32x4 o[TT];
+#pragma unroll
+    for (int k = 0; k < TT; ++k) o[k] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) {
+      float w0 = tap[ch][0], w1 = tap[ch][1], w2 = tap[ch][2];
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const int e = ch * TT + t;  // element index within the thread's run
+        const uint32_t word = cur[e / 8][(e % 8) / 2];
+        const float xv = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+        float acc = 0.f;
+        acc += wt[ch][0] * w0;
+        acc += wt[ch][1] * w1;
+        acc += wt[ch][2] * w2;
+        acc += wt[ch][3] * xv;
+        w0 = w1;
+        w1 = w2;
+        w2 = xv;
+        float y = round_bf(acc);
+        if (silu) y = silu_fast(y);
+        o[e / 8][(e % 8) / 2] |= (uint32_t)f2bf(y) << (16 * (e & 1));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < TT; ++k) ((u32x4*)(out + (n0 + j) * so_n + off))[k] = o[k];
+  }
+}
 
 // Prefill: causal width-4 conv + SiLU over whole prompts with zero history
 // (transformers causal_conv1d_fn, modeling_qwen3_5.py:220-239), and the conv
@@ -332,6 +423,28 @@ extern "C" int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c,
     }
 #undef KAD_CONV_VEC
     return kad_launch_status("conv_suffix_vec_bf16");
+  }
+  // [BW, C, T] with each beam's C * T block contiguous (the reference's layout)
+  const bool ct = dtype == KAD_DTYPE_BF16 && width == 4 && bias == nullptr && T <= 4 &&
+                  sx_t == 1 && sx_c == T && so_t == 1 && so_c == T && C % 8 == 0 &&
+                  sx_n % 8 == 0 && so_n % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
+                  ((uintptr_t)out % 16) == 0 && ((uintptr_t)weight % 16) == 0;
+  if (ct) {
+    const int nbg = (int)kad_cdiv(W, kConvBeams);
+    KAD_REQUIRE((int64_t)B * nbg < 2147483647, "too many beams for the grid");
+    const dim3 grid((unsigned)(B * nbg), (unsigned)kad_cdiv(C / 8, 256));
+#define KAD_CONV_CT(TTV)                                                                     \
+  hipLaunchKernelGGL((conv_suffix_ct_bf16<TTV>), grid, dim3(256), 0, s, (const bf16_t*)x,    \
+                     sx_n, (const bf16_t*)state, ss_b, ss_c, ss_t, history,                   \
+                     (const bf16_t*)weight, (bf16_t*)out, so_n, W, C, nbg, activation_silu)
+    switch (T) {
+      case 1: KAD_CONV_CT(1); break;
+      case 2: KAD_CONV_CT(2); break;
+      case 3: KAD_CONV_CT(3); break;
+      default: KAD_CONV_CT(4); break;
+    }
+#undef KAD_CONV_CT
+    return kad_launch_status("conv_suffix_ct_bf16");
   }
   if (dtype == KAD_DTYPE_BF16)
     return launch_scalar<bf16_t>(x, sx_n, sx_c, sx_t, state, ss_b, ss_c, ss_t, history, weight,

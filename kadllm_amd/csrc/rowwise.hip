@@ -320,7 +320,9 @@ __global__ __launch_bounds__(256) void embedding_kernel(const int64_t* __restric
   const int64_t r = idx / chunks;
   const int c = (int)(idx % chunks);
   int64_t id = ids[r];
-  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // ids are validated on the host
+  // clamped so that the table read stays in bounds whatever the caller passes;
+  // the model adapters reject out-of-range ids on the host before launching
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
   *(u32x4*)(out + r * D + c * 8) = *(const u32x4*)(table + id * D + c * 8);
 }
 

@@ -22,7 +22,7 @@ def _on(device, *ts):
 
 @pytest.mark.parametrize("dtype,B,W,T,H,HV,K,V", [
     (torch.float32, 2, 3, 7, 2, 2, 8, 8),
-    (torch.float32, 1, 4, 6, 1, 2, 128, 128),
+    (torch.float32, 1, 4, 9, 1, 2, 128, 128),   # past the factored replay's 8 tokens
     (torch.bfloat16, 2, 2, 5, 2, 4, 32, 48),
     (torch.float16, 2, 3, 3, 2, 2, 64, 64),
     (torch.float32, 1, 2, 2, 1, 1, 256, 70),
@@ -69,7 +69,8 @@ def _attn_inputs(B, W, T, H, HK, L, D, dtype, seed, Tk=None):
 @pytest.mark.parametrize("dtype,B,W,T,H,HK,L,D", [
     (torch.float32, 2, 1, 5, 2, 2, 0, 8),       # a whole prompt, no prefix
     (torch.float32, 2, 3, 3, 4, 2, 17, 48),
-    (torch.bfloat16, 1, 4, 6, 8, 2, 40, 256),   # suffix longer than the MFMA kernel's 4
+    (torch.bfloat16, 1, 4, 10, 8, 2, 40, 256),  # suffix longer than the MFMA kernel's 8
+    (torch.float32, 1, 2, 3, 4, 2, 20, 256),    # fp32 at head dim 256
     (torch.float16, 2, 2, 2, 4, 4, 33, 64),
     (torch.bfloat16, 2, 2, 3, 2, 1, 9, 96),     # head dim outside 64/128/256
 ])

@@ -342,6 +342,8 @@ def _attn_inputs(B, W, T, H, HK, L, D, seed):
 @pytest.mark.parametrize("B,W,T,H,HK,L,D", [
     (2, 256, 1, 8, 2, 1024, 256), (2, 256, 3, 8, 2, 1024, 256),   # config-3 shape, 2 requests
     (2, 5, 2, 4, 1, 70, 64), (3, 3, 4, 4, 2, 5, 128), (1, 2, 3, 2, 2, 0, 64),
+    (2, 3, 7, 4, 1, 45, 64),    # head dim 64 with 5-8 suffix keys (the 8-key fold)
+    (1, 4, 6, 4, 2, 33, 128),   # head dim 128 with the 8-key fold
 ])
 def test_prefix_attention_matches_oracle(device, B, W, T, H, HK, L, D):
     q, pk, pv, sk, sv = _attn_inputs(B, W, T, H, HK, L, D, seed=L + T)

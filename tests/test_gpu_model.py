@@ -80,7 +80,7 @@ def test_tiny_prefill_matches_oracle(device, tiny):
             assert_logits_close(b, rb, f"layer {i} V", rel=1e-2)
 
 
-@pytest.mark.parametrize("T", [1, 2, 3, 5, 6])
+@pytest.mark.parametrize("T", [1, 2, 3, 5, 6, 8, 10])
 def test_tiny_decode_matches_oracle(device, tiny, T):
     cfg, oracle, adapter = tiny
     g = torch.Generator().manual_seed(T)
@@ -167,6 +167,38 @@ def test_08b_shape_prefill_and_decode(device):
     assert_bf16_parity(res.logits, ref_logits, truth_logits, "0.8B prefill logits")
     assert_bf16_parity(logits, oracle.decode(hist, ref_state), truth.decode(hist, truth_state),
                        "0.8B decode logits")
+
+
+def test_08b_shape_decode_long_suffix(device):
+    """The 0.8B shape with 10-token suffixes, past the specialised kernels'
+    8: every GDN layer runs the per-token recurrence (key/value dims 128) and
+    every attention layer the general kernel (head dim 256), against the oracle;
+    the incremental decode of the same histories agrees within bf16 noise."""
+    cfg = qwen35_08b_config()
+    sd = random_state_dict(cfg, seed=8, dtype=torch.bfloat16, device=device)
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, sd))
+    oracle = Qwen35Oracle(cfg, {k: v.cpu() for k, v in sd.items()})
+    truth = Qwen35Oracle(cfg, {k: v.cpu().float() for k, v in sd.items()})
+    g = torch.Generator().manual_seed(10)
+    ids = torch.randint(0, cfg.vocab_size, (2, 36), generator=g)
+    hist = torch.randint(0, cfg.vocab_size, (2, 3, 10), generator=g)
+    res = adapter.prefill(ids.to(device))
+    logits = adapter.decode(hist.to(device), res.state)
+    torch.cuda.synchronize()
+    _, ref_state = oracle.prefill(ids)
+    _, t_state = truth.prefill(ids)
+    ref, exact = oracle.decode(hist, ref_state), truth.decode(hist, t_state)
+    assert_bf16_parity(logits, ref, exact, "0.8B decode T=10")
+    # the same histories built level by level with the cached suffixes: past
+    # 8 tokens both paths run the general kernels, whose bf16 results round
+    # differently, so each is held to the fp32 truth
+    dev_hist = hist.to(device)
+    lg, cache = adapter.decode_incremental(dev_hist[:, :, :1], None, res.state, None)
+    parents = torch.arange(3, device=device).expand(2, 3).contiguous()
+    for t in range(2, 11):
+        lg, cache = adapter.decode_incremental(dev_hist[:, :, :t], parents, res.state, cache)
+    torch.cuda.synchronize()
+    assert_bf16_parity(lg, ref, exact, "0.8B incremental decode T=10")
 
 
 def _incremental_matches_stateless(adapter, state, B, widths, V, device, seed):
@@ -412,3 +444,27 @@ def test_sid_only_head_search(device, tiny):
     with pytest.raises(ValueError):
         Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}),
                             head_tokens=[cfg.vocab_size])
+
+
+def test_out_of_range_token_ids_raise(device, tiny):
+    """Token ids outside the vocabulary raise IndexError in prefill, decode and
+    the incremental decode, as torch's embedding does, before any kernel runs."""
+    cfg, _, adapter = tiny
+    V = cfg.vocab_size
+    ids = torch.randint(0, V, (2, 20), generator=torch.Generator().manual_seed(3)).to(device)
+    bad = ids.clone()
+    bad[1, 7] = V
+    with pytest.raises(IndexError, match="index out of range"):
+        adapter.prefill(bad)
+    bad[1, 7] = -1
+    with pytest.raises(IndexError, match="index out of range"):
+        adapter.prefill(bad)
+    res = adapter.prefill(ids)
+    hist = torch.randint(0, V, (2, 3, 2), generator=torch.Generator().manual_seed(4)).to(device)
+    hist[0, 2, 1] = V + 5
+    with pytest.raises(IndexError, match="index out of range"):
+        adapter.decode(hist, res.state)
+    with pytest.raises(IndexError, match="index out of range"):
+        adapter.decode_incremental(hist[:, :, 1:], None, res.state, None)
+    hist[0, 2, 1] = V - 1   # the largest valid id is accepted
+    assert adapter.decode(hist, res.state).shape == (2, 3, V)

@@ -200,6 +200,24 @@ def test_conv_beam_groups_and_state_history(device, T, history):
     assert (a == e).float().mean().item() > 0.99
 
 
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+@pytest.mark.parametrize("history", [3, 4, 6])
+def test_conv_reference_layout_equals_token_major(device, T, history):
+    """The contiguous [BW, C, T] layout (the reference's, with its own vector
+    kernel) gives the token-major kernel's bits, beam counts straddling the
+    beam groups and prefix states of 3, 4 and 6 taps."""
+    B, W, C = 3, 13, 6144 // 8
+    x, st, w = conv_inputs(B, W, C, T, seed=history * 7 + T, history=history)
+    xd, sd, wd = x.to(device), st.to(device), w.to(device)
+    ref_layout = ops.causal_conv1d(xd, sd, wd, beam_width=W)
+    tm = ops.causal_conv1d(xd.transpose(1, 2).contiguous().transpose(1, 2), sd, wd, beam_width=W)
+    torch.cuda.synchronize()
+    assert ref_layout.is_contiguous() and torch.equal(ref_layout, tm)
+    e = ops_ref.causal_conv1d(x, st, w, beam_width=W).float()
+    a = ref_layout.cpu().float()
+    assert ((a - e).abs() <= (e.abs() * 2 ** -7).clamp_min(1e-30)).all()
+
+
 def test_conv_golden_fixture(device):
     f = load_npz("ops_bf16.npz")
     x, st, w = (bf16_from_bits(f[n]) for n in ("conv_x", "conv_state", "conv_w"))
