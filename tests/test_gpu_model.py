@@ -11,6 +11,7 @@ checked level by level with teacher forcing: the GPU's selection must equal
 the oracle's selection applied to the GPU's own logits (exact).
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -468,3 +469,102 @@ def test_out_of_range_token_ids_raise(device, tiny):
         adapter.decode_incremental(hist[:, :, 1:], None, res.state, None)
     hist[0, 2, 1] = V - 1   # the largest valid id is accepted
     assert adapter.decode(hist, res.state).shape == (2, 3, V)
+
+
+def _parents_of(history, prev):
+    """Parent index of each beam of ``history`` [B, W, t] in ``prev`` [B, Wp, t-1]
+    (the previous level's distinct beams) and its new token."""
+    B, W, t = history.shape
+    parents = torch.empty(B, W, dtype=torch.int64)
+    for b in range(B):
+        index = {tuple(s): i for i, s in enumerate(prev[b].tolist())}
+        for w in range(W):
+            parents[b, w] = index[tuple(history[b, w, :-1].tolist())]
+    return parents, history[:, :, -1]
+
+
+def test_reference_bf16_run_replayed_through_hip(device):
+    """The reference's own bf16 search on the tiny model
+    (tests/golden/grbeam_tiny_bf16.npz: the transformers bf16 prefill and the
+    reference's bf16 decode, batch 1, prefix 128, widths [8, 8, 8]) replayed
+    through the HIP adapter with the fixture's inputs at every level: the
+    prefill and both decode levels' logits and every prefix tensor within rel
+    1e-2 of the reference's, or (for tensors that compound several layers'
+    bf16 rounding) no more than 10% farther from the fp32 evaluation of the
+    same weights than the reference's own bf16 result is; at each level whose
+    rank-W / W+1 key gap in the
+    reference's own keys exceeds twice the measured largest logit error, the
+    selected (parent, token) set equals the reference's; and where every level
+    qualifies, grbeam_search returns the reference's tokens."""
+    from _fixtures import bf16_from_bits, load_npz
+    from kadllm_amd.grbeam import select_level
+
+    f = load_npz("grbeam_tiny_bf16.npz")
+
+    def t(name):
+        a = f[name]
+        return bf16_from_bits(a) if a.dtype == np.uint16 else torch.from_numpy(a)
+
+    cfg = tiny_hybrid_config()
+    sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16)   # the fixture's weights
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}))
+    ids = t("input_ids")
+    widths = [int(w) for w in f["widths"]]
+    pre = adapter.prefill(ids.to(device))
+    torch.cuda.synchronize()
+    truth = Qwen35Oracle(cfg, {k: v.float() for k, v in sd.items()})
+    _, t_state = truth.prefill(ids)
+    for i, (a, b) in enumerate(pre.state.layers):
+        for j, (name, got) in enumerate((("a", a), ("b", b))):
+            ref = t(f"prefix{i}_{name}")
+            assert got.shape == ref.shape, (i, name, got.shape, ref.shape)
+            r = rel_l2(got, ref)
+            e_gpu, e_ref = rel_l2(got, t_state.layers[i][j]), rel_l2(ref, t_state.layers[i][j])
+            print(f"prefix {i} {name}: rel L2 to the reference {r:.2e}; to fp32 truth: "
+                  f"GPU {e_gpu:.2e}, reference {e_ref:.2e}", flush=True)
+            assert r <= 1e-2 or e_gpu <= 1.1 * e_ref, f"prefix {i} {name}: rel L2 {r:.2e}"
+    hist = [torch.empty(1, 1, 0, dtype=torch.int64), t("decode1_history"),
+            t("decode2_history"), t("tokens")]
+    ref_logits = [t("prefill_logits")[:, None], t("decode1_logits"), t("decode2_logits")]
+    gpu_logits = [pre.logits[:, None]] + [adapter.decode(hist[s].to(device), pre.state)
+                                          for s in (1, 2)]
+    torch.cuda.synchronize()
+    s_ref = torch.zeros(1, 1, dtype=torch.float64)
+    s_gpu = torch.zeros(1, 1, device=device)
+    all_levels = True
+    exact = [truth.prefill(ids)[0][:, None]] + [truth.decode(hist[s], t_state) for s in (1, 2)]
+    for step, W in enumerate(widths):
+        g, r = gpu_logits[step], ref_logits[step]
+        e = rel_l2(g, r)
+        e_gpu, e_ref = rel_l2(g, exact[step]), rel_l2(r, exact[step])
+        assert e <= 1e-2 or e_gpu <= 1.1 * e_ref, f"level {step}: logits rel L2 {e:.2e}"
+        err = (g.float().cpu() - r.float()).abs().max().item()
+        keys = (r.double().log_softmax(-1) + s_ref[..., None]).reshape(1, -1)
+        top = torch.topk(keys, W + 1).values[0]
+        gap = (top[W - 1] - top[W]).item()
+        parents, tokens = _parents_of(hist[step + 1], hist[step])
+        scores, p, tk, _ = select_level(g, s_gpu, W)
+        torch.cuda.synchronize()
+        decided = gap > 2 * err
+        print(f"level {step}: logits rel L2 {e:.2e} (to fp32 truth: GPU {e_gpu:.2e}, reference "
+              f"{e_ref:.2e}), max abs err {err:.3e}, rank-W/W+1 gap "
+              f"{gap:.3e} -> {'compared' if decided else 'inside tolerance'}", flush=True)
+        if decided:
+            got = set(zip(p.cpu()[0].tolist(), tk.cpu()[0].tolist()))
+            want = set(zip(parents[0].tolist(), tokens[0].tolist()))
+            assert got == want, f"level {step}: selection differs from the reference's"
+        all_levels &= decided
+        # follow the reference's path: its beams (in its order) and scores
+        flat = parents * r.shape[-1] + tokens
+        s_ref = keys.gather(1, flat)
+        order = [list(zip(p.cpu()[0].tolist(), tk.cpu()[0].tolist())).index(pt)
+                 if decided else 0 for pt in zip(parents[0].tolist(), tokens[0].tolist())]
+        s_gpu = scores[:, order] if decided else s_ref.float().to(device)
+    if all_levels:
+        result = grbeam_search(adapter, ids.to(device), widths)
+        torch.cuda.synchronize()
+        got = dict(zip(map(tuple, result.tokens.cpu()[0].tolist()), result.scores.cpu()[0].tolist()))
+        want = dict(zip(map(tuple, t("tokens")[0].tolist()), t("scores")[0].tolist()))
+        assert got.keys() == want.keys(), "search returns other beams than the reference's"
+        for seq, sc in want.items():
+            assert abs(got[seq] - sc) <= 3 * 2 * err + 1e-4, (seq, got[seq], sc)
