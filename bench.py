@@ -30,6 +30,9 @@ Other modes:
   --workload ops_gemm    every GEMM shape of the headline search alone, beside
                          torch.matmul (hipBLASLt) on the same operands
   --workload conditional_sid  two-level SID search (configuration 5)
+  --workload sid_study   the setting of the reference's two-level SID study
+                         (4,096-token SID head, beam 256, prefill + one suffix
+                         decode, P512/1024 x B8/32; README.md:139-148)
   --workload hbm_copy    a 1 GiB device copy: measured streaming bandwidth and
                          the calibration of rocprofv3's FETCH/WRITE_SIZE
   --workload hbm_probe   the library's streaming probe over 4 GiB (copy, read,
@@ -871,6 +874,77 @@ def conditional_sid(a):
         "step_ms": [round(1000 * t, 2) for t in times]}), flush=True)
 
 
+# the reference's two-level conditional-SID study (README.md:139-148, RTX 4090,
+# grouped prefix reuse): batch latency in ms by (prefix, batch)
+SID_STUDY_4090_MS = {(512, 8): 89.2, (512, 32): 420.3, (1024, 8): 158.8, (1024, 32): 720.1}
+
+
+def sid_study(a):
+    """The setting of the reference's two-level conditional-SID study
+    (README.md:139-148): a SID-only head of 4,096 token ids (each level picks
+    from those 4,096 codes), beam 256, the first level from the prefill and the
+    second from one suffix decode, at prefix 512 / 1024 x batch 8 / 32.  One
+    step is one grbeam_search call with the tokens copied to the host, as in the
+    headline protocol.  Latency is reported beside the reference's published
+    RTX 4090 latencies (grouped column) as context: another GPU, and the
+    reference's head and scoring details beyond this are unpublished."""
+    from kadllm_amd import grbeam_search
+    from kadllm_amd.adapters import Qwen35GRBeamAdapter, native_model
+    from kadllm_amd.config import qwen35_08b_config
+    from kadllm_amd.weights import random_state_dict
+
+    dev = torch.device("cuda:0")
+    cfg = qwen35_08b_config()
+    sd = random_state_dict(cfg, seed=0, dtype=torch.bfloat16, device=dev)
+    n_sid, beam = 4096, 256
+    sid = torch.randperm(cfg.vocab_size, generator=torch.Generator().manual_seed(0))[:n_sid]
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, sd), head_tokens=sid)
+    rows = []
+    for P in (512, 1024):
+        for B in (8, 32):
+            ids = torch.randint(0, cfg.vocab_size, (B, P),
+                                generator=torch.Generator().manual_seed(P + B)).to(dev)
+
+            def run():
+                return grbeam_search(adapter, ids, [beam, beam]).tokens.tolist()
+
+            for _ in range(a.warmup):
+                validate_output(run(), B, beam, 2)
+            torch.cuda.synchronize()
+            if not a.no_gc_freeze:   # as in the headline run
+                gc.collect()
+                gc.freeze()
+            times = []
+            for _ in range(a.steps):
+                t0 = time.perf_counter()
+                out = run()
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                validate_output(out, B, beam, 2)
+            mean = statistics.mean(times)
+            ci = (T975.get(len(times) - 1, 1.96) * statistics.stdev(times) / math.sqrt(len(times))
+                  if len(times) > 1 else None)
+            ref = SID_STUDY_4090_MS[(P, B)]
+            rows.append({"prefix": P, "batch": B, "latency_ms": round(1000 * mean, 3),
+                         "ci95_ms": round(1000 * ci, 3) if ci is not None else None,
+                         "requests_per_s": round(B / mean, 2),
+                         "reference_4090_grouped_ms": ref,
+                         "reference_4090_over_this": round(ref / (1000 * mean), 2)})
+            print(f"sid study P{P} B{B}: {1000 * mean:.2f} ms per batch "
+                  f"(RTX 4090 grouped: {ref} ms)", file=sys.stderr, flush=True)
+    main_row = rows[-1]
+    print(json.dumps({
+        "metric": "batch latency, two-level conditional-SID study setting (P1024 B32 row)",
+        "value": main_row["latency_ms"], "unit": "ms", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": main_row["latency_ms"], "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform-random prompt ids, seeded 4096-id "
+                "SID-only head)",
+        "config": {"workload": "sid_study qwen3.5-0.8B-shaped SID head 4096, beam 256, "
+                               "prefill + one suffix decode, P512/1024 x B8/32"},
+        "roofline": None, "cpu_baseline": None, "rows": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -899,7 +973,7 @@ def main():
     ap.add_argument("--op-iters", type=int, default=50)
     ap.add_argument("--workload",
                     choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention", "ops_gemm",
-                             "hbm_copy", "hbm_probe"),
+                             "hbm_copy", "hbm_probe", "sid_study"),
                     default="grbeam")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -910,7 +984,7 @@ def main():
         return reference_protocol(a)
     return {"grbeam": grbeam, "conditional_sid": conditional_sid, "ops_gdn": ops_gdn,
             "ops_attention": ops_attention, "ops_gemm": ops_gemm,
-            "hbm_copy": hbm_copy, "hbm_probe": hbm_probe}[a.workload](a)
+            "hbm_copy": hbm_copy, "hbm_probe": hbm_probe, "sid_study": sid_study}[a.workload](a)
 
 
 if __name__ == "__main__":
