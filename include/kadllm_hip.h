@@ -109,7 +109,10 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
  * aligned C (and R) with ldc, ldr and the output width multiples of 8;
  * 18 = 16 persistent, one workgroup per CU walking the tiles; 19 = 16's
  * design on 128x128 tiles with 4 waves, two workgroups per CU; 20 = 16 with
- * a third LDS slot for the operand that streams from beyond the L2).  Every
+ * a third LDS slot for the operand that streams from beyond the L2; 22 =
+ * 256x256 persistent with its 8 waves in two groups that alternate between
+ * MFMA phases and load phases across workgroup barriers, M and N multiples
+ * of 256, 16-byte store epilogue as 16).  Every
  * configuration accumulates K in the same order, so all give bit-identical
  * results (the automatic choice may also split the columns of one call
  * between two of them); other numbers are rejected (KAD_ERR_UNSUPPORTED). */

@@ -216,6 +216,18 @@ __device__ __forceinline__ void dma16(const bf16_t* g, bf16_t* lds_block) {
   __builtin_amdgcn_global_load_lds((global_void_t*)g, (lds_void_t*)lds_block, 16, 0, 0);
 }
 
+// The same 16 bytes per lane through a buffer resource: a per-lane 32-bit
+// byte offset (voff) plus a wave-uniform one (soff) from the resource's base,
+// so that no per-lane 64-bit address is formed.  Raw buffer, no format
+// conversion (third dword 0x00020000); an offset past num_records reads 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                          bf16_t* lds_block) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_block, 16, voff, soff, 0, 0);
+}
+
 // workgroup barrier without __syncthreads' wait for every outstanding load;
 // the empty asm statements keep LDS accesses on their side of it
 __device__ __forceinline__ void ring_barrier() {
@@ -825,6 +837,250 @@ int device_cu_count() {
   return cached[dev];
 }
 
+// 256 x 256 tiles, 8 waves in two groups that alternate roles ("ping-pong"),
+// persistent.  Waves w and w + 4 share a SIMD; group 0 (waves 0-3) owns
+// output rows 0-127 of a tile, group 1 rows 128-255, each wave a 128 x 64
+// sub-tile.  Between two workgroup barriers one group issues only MFMAs
+// (all 64 of a 64-deep K slice, from fragments already in registers) while
+// the other does memory work: the LDS fragment reads of its next slice and
+// its part of the global->LDS loads.  So each SIMD's matrix unit is fed by
+// one wave at a time and no load stalls an MFMA wave's issue.
+//
+// Phases (each ends at a barrier): 2g: group 0 reads slice g, group 1
+// computes slice g - 1; 2g + 1: group 0 computes slice g, group 1 reads
+// slice g.  A stage (g % 2) may be reloaded only once every wave that reads
+// the rows is done with them, which the barriers order (a wave waits for
+// its own LDS reads before the barrier that ends its read phase).
+//
+// One workgroup per CU walks the tiles v = blockIdx.x, + gridDim.x, ... (the
+// grouped, XCD-aware order); the K slices of its tiles form one stream
+// through the two stages, and a group's epilogue for a tile runs in its read
+// phase of the next tile's first slice (through a small LDS region of its
+// own, as in gemm_x16p_kernel) while the other group's MFMAs run.  Tiles
+// must be whole (M, N multiples of 256).  Every K slice accumulates in the
+// order of the other configurations, so results are bit-identical to them.
+// An instrumented copy (shader-clock timers at each barrier) puts a slice at
+// 3,100-3,700 cycles against 2,048 of MFMA work: the read phases (24
+// fragment reads per wave, 85 B/clk per CU, where an LDS microbenchmark of
+// the same pattern reads 253) set the pace.
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_ppp_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group, int ntiles) {
+  using TX = Tile256;
+  constexpr int BM = TX::BM, BN = TX::BN;
+  constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
+  constexpr int kStage = TX::Stage, AG = TX::AG, WGW = TX::WGW;
+  constexpr int kLoads = AG + WGW;
+  constexpr int kEpiChunk = 16 * ((EPI == KAD_EPI_SWIGLU ? NJ * 8 : NJ * 16) + 8);
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[2 * kStage + NW * kEpiChunk];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int swave = __builtin_amdgcn_readfirstlane(wave);
+  const int grp = swave / WN;
+  const int wm = grp, wn = swave % WN;
+  const int KT = K / kBK;
+  const int my_tiles = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  if (my_tiles <= 0) return;
+  const int total = my_tiles * KT;   // slices in this workgroup's stream
+  auto origin = [&](int r, int& m0, int& n0) {
+    const int v = (int)blockIdx.x + r * (int)gridDim.x;
+    tile_origin_of(xcd_logical_id(v, ntiles), M, N, BM, BN, n_major, group, m0, n0);
+  };
+
+  // Loads.  Group 1 reads only A rows 128-255, so the A rows 0-127 of a
+  // stage are free once group 0 has read them: group 1 loads those (row
+  // groups w + 4i of 8 rows, w = its wave index in the group) during its own
+  // read phase, two slices ahead.  Group 0 loads A rows 128-255 and every W
+  // row (row groups 16 + w + 4i and w + 4i) during its read phase, one slice
+  // ahead, once both groups have read the stage.  So no load is issued in an
+  // MFMA phase.  A row group's swizzle phase is its parity, which is that of
+  // w for all of a wave's groups.  Load cursor (per wave, uniform): every
+  // wave issues its part of slices 0, 1, 2, ... in order; past the last slice
+  // it re-fetches that one (uniform wait counts).
+  constexpr int kL1 = 4, kL0 = 12;   // loads per slice of a group-1 / group-0 wave
+  const int gw = swave & 3;
+  const int l_row = lane >> 3;
+  const int l_kc = ((lane & 7) ^ ((gw & 1) * 4 + (lane >> 4))) * 8;
+  const uint32_t a_lane = (uint32_t)(l_row * (int)lda + l_kc) * 2u;
+  const uint32_t b_lane = (uint32_t)(l_row * (int)ldw + l_kc) * 2u;
+  int ld_g = 0, ld_k = 0, ld_r = 0;
+  __amdgpu_buffer_rsrc_t ld_a, ld_b;
+  auto set_tile = [&](int r) {
+    int m0, n0;
+    origin(r, m0, n0);
+    ld_a = buffer_rsrc(A + (int64_t)m0 * lda);
+    ld_b = buffer_rsrc(Wt + (int64_t)n0 * ldw);
+  };
+  set_tile(0);
+  const uint32_t a_rg = (uint32_t)(8 * lda * 2), b_rg = (uint32_t)(8 * ldw * 2);  // bytes per row group
+  auto issue_loads = [&]() {
+    const uint32_t k0 = (uint32_t)ld_k * kBK * 2;
+    bf16_t* base = smem + (ld_g & 1) * kStage;
+    if (grp == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rg = gw + 4 * i;
+        dma16_buf(ld_a, a_lane, (uint32_t)rg * a_rg + k0, base + rg * 8 * kBK);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rg = 16 + gw + 4 * i;
+        dma16_buf(ld_a, a_lane, (uint32_t)rg * a_rg + k0, base + rg * 8 * kBK);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int rg = gw + 4 * i;
+        dma16_buf(ld_b, b_lane, (uint32_t)rg * b_rg + k0, base + BM * kBK + rg * 8 * kBK);
+      }
+    }
+  };
+  // the stage alternates with every issue; the slice stays at the stream's
+  // last one once reached
+  auto advance = [&]() {
+    ++ld_g;
+    if (ld_r * KT + ld_k + 1 < total) {
+      if (++ld_k == KT) {
+        ld_k = 0;
+        set_tile(++ld_r);
+      }
+    }
+  };
+  auto issue = [&]() {
+    issue_loads();
+    advance();
+  };
+
+  const int f_row = lane & 15, f_sw = (lane & 15) >> 1, f_q = lane >> 4;
+  const int fa_row = (wm * NI * 16 + f_row) * kBK;
+  const int fw_row = BM * kBK + (wn * NJ * 16 + f_row) * kBK;
+  bf16x8 fa[2][NI], fw[2][NJ];
+  auto read_slice = [&](int g) {
+#pragma unroll
+    for (int step = 0; step < 2; ++step) {
+      const bf16_t* base = smem + (g & 1) * kStage + (((step * 4 + f_q) ^ f_sw) * 8);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        fw[step][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 16 * kBK));
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        fa[step][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 16 * kBK));
+    }
+  };
+  f32x4 acc[NI][NJ];
+  auto zero = [&]() {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{};
+  };
+  auto compute = [&]() {
+#pragma unroll
+    for (int step = 0; step < 2; ++step)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x32(fw[step][j], fa[step][i], acc[i][j]);
+  };
+  bf16_t* ep = smem + 2 * kStage + swave * kEpiChunk;
+  auto epilogue = [&](int r) {
+    int m0, n0;
+    origin(r, m0, n0);
+    const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 16) / 2 : n0 + wn * NJ * 16;
+    epilogue_x16_chunked<EPI, NI, NJ>(acc, ep, lane, m0 + wm * NI * 16, col0, C, ldc, R, ldr, M,
+                                      N);
+  };
+
+  zero();
+  issue();
+  issue();
+  if (grp == 0)
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kL0));   // own part of slice 0 landed
+  else
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kL1));
+  ring_barrier();
+  if (grp == 0) {
+    for (int g = 0; g < total; ++g) {
+      __builtin_amdgcn_sched_barrier(0);
+      // phase 2g: the previous tile's epilogue when g starts a tile, the
+      // fragments of slice g, this wave's part of slice g + 1 (its stage was
+      // last read in phase 2g - 1)
+      const int kt = g % KT;
+      if (kt == 0 && g > 0) {
+        epilogue(g / KT - 1);
+        zero();
+      }
+      read_slice(g);
+      if (g >= 1) issue();
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(63));   // this wave's LDS accesses done
+      __builtin_amdgcn_sched_barrier(0);
+      ring_barrier();
+      // phase 2g + 1: compute slice g, then wait for this wave's part of
+      // slice g + 1
+      compute();
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+      ring_barrier();
+    }
+  } else {
+    // phase 2g: compute slice g - 1; phase 2g + 1: the previous tile's
+    // epilogue when g starts a tile, the fragments of slice g, this wave's
+    // part of slice g + 2 (A rows that only group 0 reads, and it has), and
+    // the wait for its part of slice g + 1
+    auto read_phase = [&](int g) {
+      const int kt = g % KT;
+      if (kt == 0 && g > 0) {
+        // the epilogue's stores are not ordered with the loads that the
+        // counted wait below expects: drain the loads first
+        __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+        epilogue(g / KT - 1);
+        zero();
+      }
+      issue();
+      read_slice(g);
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kL1));
+      __builtin_amdgcn_sched_barrier(0);
+      ring_barrier();
+    };
+    ring_barrier();
+    read_phase(0);
+    for (int g = 1; g < total; ++g) {
+      __builtin_amdgcn_sched_barrier(0);
+      compute();
+      __builtin_amdgcn_sched_barrier(0);
+      ring_barrier();
+      read_phase(g);
+    }
+    compute();
+  }
+  epilogue(my_tiles - 1);
+  // no LDS write may land after the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+template <int EPI>
+int launch_ppp(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t ntiles = kad_cdiv(M, 256) * kad_cdiv(N, 256);
+  if (ntiles > 0x7fffffff / 2 || ntiles * (K / kBK) > 0x7fffffff)
+    KAD_UNSUPPORTED("gemm grid too large");
+  if ((int64_t)256 * (lda > ldw ? lda : ldw) + K >= 0x7fffffff)
+    KAD_UNSUPPORTED("gemm rows too long for 32-bit tile offsets");
+  if (M % 256 || N % 256) KAD_UNSUPPORTED("tile configuration 22 needs M and N multiples of 256");
+  int grid = device_cu_count();
+  grid -= grid % 8;
+  if (grid <= 0) grid = 8;
+  if (ntiles < grid) grid = (int)ntiles;
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  hipLaunchKernelGGL((gemm_ppp_kernel<EPI>), dim3((unsigned)grid), dim3(512), 0, s,
+                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N, K, n_major, 8, (int)ntiles);
+  return kad_launch_status("gemm_ppp_kernel");
+}
+
 template <int EPI, int BN>
 int launch_x16p(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
                 const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
@@ -871,7 +1127,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_64x32 = 11,
        CFG_32x64 = 12,
        CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19,
-       CFG_256x256_S3 = 20 };
+       CFG_256x256_S3 = 20, CFG_256x256_PPP = 22 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
@@ -895,6 +1151,12 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       cfg = CFG_64x32;
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
+    else if (M % 256 == 0 && N % 256 == 0 && K <= 2048 && tiles256 > 4 * device_cu_count())
+      // the persistent ping-pong kernel where its tiles give each CU more
+      // than four: the prefill input, QKV and SwiGLU projections (M =
+      // 32,768) 4-14% and the vocabulary head 3% faster than configuration
+      // 18 / 16, the same on four rounds, slower on fewer or at K = 3,584
+      cfg = CFG_256x256_PPP;
     else if (tiles256 >= 256 && K >= 3072)
       cfg = CFG_256x256_S3;
     else if (tiles256 >= 256)
@@ -953,6 +1215,7 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_256x256_X16P:
     case CFG_128x128_X16:
     case CFG_256x256_S3:
+    case CFG_256x256_PPP:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
                         cfg);
@@ -960,6 +1223,8 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
         return launch_x16<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_256x256_S3)
         return launch_s3<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_256x256_PPP)
+        return launch_ppp<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_128x128_X16)
         return launch_x16<EPI, TileX16<128, 128, 2, 2>>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K,
                                                         s);
