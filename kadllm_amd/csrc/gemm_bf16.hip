@@ -1081,171 +1081,6 @@ int launch_ppp(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, 
   return kad_launch_status("gemm_ppp_kernel");
 }
 
-// 256 x 256 tiles with 4 waves, one per SIMD, each owning a 128 x 128
-// sub-tile (256 accumulators, in AGPRs: one wave per SIMD may hold 512
-// registers), persistent as gemm_x16p_kernel.  Per 64-deep slice a wave
-// reads 32 KB of fragments from LDS where the 8-wave tile's waves read 24 KB
-// for half the outputs, so the CU's LDS reads per slice fall from 192 to 128
-// KB.  Two 32-deep steps per slice: the MFMAs of step 0 run with the
-// fragment reads of step 1, and those of step 1 with the next slice's step-0
-// reads and this wave's loads of the slice after next; one barrier per
-// slice, between the steps, orders both (every wave is done reading the
-// stage the loads go to, and every wave's loads of the next slice landed).
-template <int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_w4p_kernel(
-    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
-    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
-    int group, int ntiles) {
-  using TX = TileX16<256, 256, 2, 2>;
-  constexpr int BM = TX::BM, BN = TX::BN;
-  constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
-  constexpr int kStage = TX::Stage;
-  constexpr int kLoads = (BM + BN) / 8 / NW;   // row groups (1 KB loads) per wave per slice
-  constexpr int NM = NI * NJ, NR = NI + NJ;
-  constexpr int kEpiChunk = 16 * ((EPI == KAD_EPI_SWIGLU ? NJ * 8 : NJ * 16) + 8);
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[2 * kStage + NW * kEpiChunk];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int swave = __builtin_amdgcn_readfirstlane(wave);
-  const int wm = swave / WN, wn = swave % WN;
-  const int KT = K / kBK;
-  const int my_tiles = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
-  if (my_tiles <= 0) return;
-  const int total = my_tiles * KT;
-  auto origin = [&](int r, int& m0, int& n0) {
-    const int v = (int)blockIdx.x + r * (int)gridDim.x;
-    tile_origin_of(xcd_logical_id(v, ntiles), M, N, BM, BN, n_major, group, m0, n0);
-  };
-
-  // loads: wave w takes A and W row groups w + 4i (8 rows each), whose
-  // swizzle phase (the group's parity) is that of w
-  const int l_row = lane >> 3;
-  const int l_kc = ((lane & 7) ^ ((swave & 1) * 4 + (lane >> 4))) * 8;
-  const uint32_t a_lane = (uint32_t)(l_row * (int)lda + l_kc) * 2u;
-  const uint32_t b_lane = (uint32_t)(l_row * (int)ldw + l_kc) * 2u;
-  const uint32_t a_rg = (uint32_t)(8 * lda * 2), b_rg = (uint32_t)(8 * ldw * 2);
-  int ld_g = 0, ld_k = 0, ld_r = 0;
-  __amdgpu_buffer_rsrc_t ld_a, ld_b;
-  auto set_tile = [&](int r) {
-    int m0, n0;
-    origin(r, m0, n0);
-    ld_a = buffer_rsrc(A + (int64_t)m0 * lda);
-    ld_b = buffer_rsrc(Wt + (int64_t)n0 * ldw);
-  };
-  set_tile(0);
-  auto issue_loads = [&]() {
-    const uint32_t k0 = (uint32_t)ld_k * kBK * 2;
-    bf16_t* base = smem + (ld_g & 1) * kStage;
-#pragma unroll
-    for (int i = 0; i < BM / 8 / NW; ++i) {
-      const int rg = swave + NW * i;
-      dma16_buf(ld_a, a_lane, (uint32_t)rg * a_rg + k0, base + rg * 8 * kBK);
-    }
-#pragma unroll
-    for (int i = 0; i < BN / 8 / NW; ++i) {
-      const int rg = swave + NW * i;
-      dma16_buf(ld_b, b_lane, (uint32_t)rg * b_rg + k0, base + BM * kBK + rg * 8 * kBK);
-    }
-  };
-  // the stage alternates with every issue; the slice stays at the stream's
-  // last one once reached (the loads then re-fetch it: uniform wait counts)
-  auto advance = [&]() {
-    ++ld_g;
-    if (ld_r * KT + ld_k + 1 < total) {
-      if (++ld_k == KT) {
-        ld_k = 0;
-        set_tile(++ld_r);
-      }
-    }
-  };
-
-  const int f_row = lane & 15, f_sw = (lane & 15) >> 1, f_q = lane >> 4;
-  const int fa_row = (wm * NI * 16 + f_row) * kBK;
-  const int fw_row = BM * kBK + (wn * NJ * 16 + f_row) * kBK;
-  bf16x8 fa[2][NI], fw[2][NJ];
-  auto load_frags = [&](int g, int step, int buf) {
-    const bf16_t* base = smem + (g & 1) * kStage + (((step * 4 + f_q) ^ f_sw) * 8);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      fw[buf][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 16 * kBK));
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      fa[buf][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 16 * kBK));
-  };
-  f32x4 acc[NI][NJ];
-  auto zero = [&]() {
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{};
-  };
-  auto mfma_step = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x32(fw[buf][j], fa[buf][i], acc[i][j]);
-  };
-  bf16_t* ep = smem + 2 * kStage + swave * kEpiChunk;
-
-  issue_loads();
-  advance();
-  issue_loads();
-  advance();
-  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kLoads));   // own rows of slice 0 landed
-  ring_barrier();
-  load_frags(0, 0, 0);
-  for (int r = 0; r < my_tiles; ++r) {
-    zero();
-    for (int kt = 0; kt < KT; ++kt) {
-      __builtin_amdgcn_sched_barrier(0);
-      const int g = r * KT + kt;
-      // step 0 of slice g, with the reads of its step 1
-      load_frags(g, 1, 1);
-      mfma_step(0);
-      interleave_x16<NM, NR, 0>();
-      // this wave's rows of slice g + 1 landed and its reads of stage g
-      // done; past the barrier every wave's are
-      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
-      ring_barrier();
-      // step 1, with the reads of slice g + 1's step 0 and the loads of
-      // slice g + 2 into stage g % 2
-      load_frags(g + 1, 0, 0);
-      issue_loads();
-      mfma_step(1);
-      interleave_x16<NM, NR, kLoads>();
-      advance();
-    }
-    int m0, n0;
-    origin(r, m0, n0);
-    const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 16) / 2 : n0 + wn * NJ * 16;
-    epilogue_x16_chunked<EPI, NI, NJ>(acc, ep, lane, m0 + wm * NI * 16, col0, C, ldc, R, ldr, M,
-                                      N);
-  }
-  // no LDS write may land after the workgroup ends
-  __builtin_amdgcn_s_waitcnt(0);
-}
-
-template <int EPI>
-int launch_w4p(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
-  const int64_t ntiles = kad_cdiv(M, 256) * kad_cdiv(N, 256);
-  if (ntiles > 0x7fffffff / 2 || ntiles * (K / kBK) > 0x7fffffff)
-    KAD_UNSUPPORTED("gemm grid too large");
-  if ((int64_t)256 * (lda > ldw ? lda : ldw) + K >= 0x7fffffff)
-    KAD_UNSUPPORTED("gemm rows too long for 32-bit tile offsets");
-  if (M % 256 || N % 256) KAD_UNSUPPORTED("tile configuration 23 needs M and N multiples of 256");
-  int grid = device_cu_count();
-  grid -= grid % 8;
-  if (grid <= 0) grid = 8;
-  if (ntiles < grid) grid = (int)ntiles;
-  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
-  hipLaunchKernelGGL((gemm_w4p_kernel<EPI>), dim3((unsigned)grid), dim3(256), 0, s,
-                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
-                     (const bf16_t*)R, ldr, M, N, K, n_major, 8, (int)ntiles);
-  return kad_launch_status("gemm_w4p_kernel");
-}
-
 template <int EPI, int BN>
 int launch_x16p(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
                 const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
@@ -1292,16 +1127,19 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_64x32 = 11,
        CFG_32x64 = 12,
        CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19,
-       CFG_256x256_S3 = 20, CFG_256x256_PPP = 22, CFG_256x256_W4P = 23 };
+       CFG_256x256_S3 = 20, CFG_256x256_PPP = 22 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
          const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
   if (cfg == CFG_AUTO) {
-    // the 8-wave 256x256 kernel on 16x16x32 MFMAs when its tiles still fill
-    // every CU (and the output suits 16-byte stores): with a third LDS slot
-    // for the streamed operand for K >= 3072, else persistent except for
-    // the SwiGLU epilogue, where both forms measured the same; then the
+    // the 8-wave 256x256 kernels on 16x16x32 MFMAs when their tiles still
+    // fill every CU (and the output suits 16-byte stores): the ping-pong
+    // kernel for plain products of at least four whole tiles per CU, a third
+    // LDS slot for the streamed operand for K >= 3072 (residual outputs
+    // from K = 2048: the prefill mixer output projection 2% faster), else
+    // persistent except for the SwiGLU epilogue, where both forms measured
+    // the same; then the
     // 128x128 form, two workgroups per CU, when its tiles fill two rounds
     // (N = 1,024 at M = 8,192: 5-7% faster than 8-wave 256x128 tiles, and
     // 14% slower than 256x256 where those fill the chip); 64x32 for outputs
@@ -1316,15 +1154,13 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       cfg = CFG_64x32;
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
-    else if (M % 256 == 0 && N % 256 == 0 && K <= 2048 && tiles256 > 4 * device_cu_count())
-      // whole tiles, more than four per CU: the 4-wave kernel (128 x 128 per
-      // wave) for the prefill input, QKV and SwiGLU projections (M = 32,768,
-      // N <= 8,192: 4-7% faster than the ping-pong kernel, 7-12% faster than
-      // configuration 18 / 16), the ping-pong kernel for the vocabulary head
-      // (3% faster than the 4-wave one and configuration 18); both are
-      // slower than 18 / 20 on four rounds or fewer, or at K = 3,584
-      cfg = N <= 16384 ? CFG_256x256_W4P : CFG_256x256_PPP;
-    else if (tiles256 >= 256 && K >= 3072)
+    else if (EPI == KAD_EPI_STORE && M % 256 == 0 && N % 256 == 0 && K <= 2048 &&
+             tiles256 >= 4 * device_cu_count())
+      // plain products of whole tiles, at least four per CU: the ping-pong
+      // kernel (the GDN input projections 1-6%, the vocabulary head 3%
+      // faster than configuration 18, interleaved A/B medians on one box)
+      cfg = CFG_256x256_PPP;
+    else if (tiles256 >= 256 && (K >= 3072 || (EPI == KAD_EPI_RESIDUAL && K >= 2048)))
       cfg = CFG_256x256_S3;
     else if (tiles256 >= 256)
       cfg = EPI == KAD_EPI_SWIGLU ? CFG_256x256_X16 : CFG_256x256_X16P;
@@ -1383,7 +1219,6 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_128x128_X16:
     case CFG_256x256_S3:
     case CFG_256x256_PPP:
-    case CFG_256x256_W4P:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
                         cfg);
@@ -1391,8 +1226,6 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
         return launch_x16<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_256x256_S3)
         return launch_s3<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
-      if (cfg == CFG_256x256_W4P)
-        return launch_w4p<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_256x256_PPP)
         return launch_ppp<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_128x128_X16)
