@@ -12,8 +12,9 @@ the native HIP kernels (kadllm_amd.qwen35.Qwen35Runner).  The backend
 arguments keep their reference names and validation; every accepted value
 runs the single HIP implementation.  The prefix is request-sized and is never
 written by decode.  Models must be on one ROCm device, in bf16 (the packed
-bf16 kernels, with the transformers bf16 rounding points) or fp32 (fp32
-kernels throughout, kadllm_amd.qwen35_f32).
+bf16 kernels, with the transformers bf16 rounding points), fp32 (fp32
+kernels throughout, kadllm_amd.qwen35_f32) or fp16 (the fp32 kernels on
+weights widened once; fp32 logits and prefix).
 """
 
 from dataclasses import dataclass
@@ -24,7 +25,7 @@ from ..config import Qwen35Config
 from ..grbeam import PrefillResult
 from ..ops import _gdn_launch
 from ..qwen35 import LMHead, Qwen35Runner, Qwen35TextModel
-from ..qwen35_f32 import Qwen35RunnerF32
+from ..qwen35_f32 import Qwen35RunnerF16, Qwen35RunnerF32
 
 
 @dataclass(frozen=True)
@@ -84,8 +85,11 @@ class Qwen35GRBeamAdapter:
             runner = Qwen35Runner
         elif dtypes == {torch.float32}:
             runner = Qwen35RunnerF32
+        elif dtypes == {torch.float16}:
+            runner = Qwen35RunnerF16
         else:
-            raise TypeError("the HIP GRBeam path runs bf16 or fp32 models; convert with .to()")
+            raise TypeError("the HIP GRBeam path runs bf16, fp16 or fp32 models with one dtype; "
+                            "convert with .to()")
         if device.type != "cuda":
             raise RuntimeError("the HIP GRBeam path needs the model on a ROCm device")
         self.layer_types = tuple(cfg.layer_types)
@@ -98,8 +102,9 @@ class Qwen35GRBeamAdapter:
         self._runner = runner(self.config, text_model.state_dict(),
                               lm_head_weight=lm_head.weight, device=device,
                               head_tokens=head_tokens)
-        if runner is Qwen35RunnerF32:
-            # fp32 models replay the whole suffix at every level, as the reference does
+        if runner in (Qwen35RunnerF32, Qwen35RunnerF16):
+            # fp32 and fp16 models replay the whole suffix at every level, as
+            # the reference does
             self.decode_incremental = None
         # logits column -> token id for a SID-only head (None: the full vocabulary)
         self.vocab_ids = self._runner.head_ids

@@ -250,3 +250,13 @@ class Qwen35RunnerF32:
         _lib.call("kad_embedding_f32", _lib.ptr(ids), _lib.ptr(self.embed), _lib.ptr(out),
                   ids.numel(), D, self.embed.shape[0], _lib.stream_of(out))
         return out
+
+
+class Qwen35RunnerF16(Qwen35RunnerF32):
+    """fp16 models (the reference adapter wraps a model in any float dtype,
+    src/kadllm/adapters/qwen3_5.py:40-104) on the fp32 kernels above: the
+    weights are widened once, at construction, and every step runs in fp32,
+    which carries the fp16 model's arithmetic more accurately than fp16
+    rounding would.  Logits and the prefix are fp32, as for an fp32 model."""
+
+    source_dtype = torch.float16

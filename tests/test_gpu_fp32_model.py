@@ -129,3 +129,52 @@ def test_fp32_decode_matches_oracle_deeper(device):
     torch.testing.assert_close(pre.logits.cpu(), ref_logits, atol=1e-4, rtol=1e-4)
     torch.testing.assert_close(logits.cpu(), oracle.decode(hist, state), atol=1e-4, rtol=1e-4)
     assert np.isfinite(logits.cpu().numpy()).all()
+
+
+def test_fp16_model_on_the_fp32_kernels(device):
+    """An fp16 model (the reference adapter wraps any float dtype,
+    src/kadllm/adapters/qwen3_5.py:40-104) runs on the fp32 kernels with its
+    weights widened once: prefill and a 3-token decode no farther from the
+    fp32 evaluation of the same fp16 weights than the oracle's own fp16
+    arithmetic is, and the search equal to the oracle's selection on the GPU's
+    own logits, level by level."""
+    from oracle import grbeam_ref
+    cfg = tiny_hybrid_config()
+    sd = random_state_dict(cfg, seed=5, dtype=torch.float16)
+    adapter = Qwen35GRBeamAdapter(*native_model(cfg, {k: v.to(device) for k, v in sd.items()}))
+    assert adapter.decode_incremental is None
+    half = Qwen35Oracle(cfg, sd)
+    truth = Qwen35Oracle(cfg, {k: v.float() for k, v in sd.items()})
+    g = torch.Generator().manual_seed(6)
+    ids = torch.randint(0, cfg.vocab_size, (2, 70), generator=g)
+    hist = torch.randint(0, cfg.vocab_size, (2, 5, 3), generator=g)
+    res = adapter.prefill(ids.to(device))
+    logits = adapter.decode(hist.to(device), res.state)
+    torch.cuda.synchronize()
+    h_logits, h_state = half.prefill(ids)
+    t_logits, t_state = truth.prefill(ids)
+
+    def rel(a, e):
+        return ((a.float().cpu() - e.float()).norm() / e.float().norm()).item()
+
+    for name, got, ref, exact in (("prefill", res.logits, h_logits, t_logits),
+                                  ("decode", logits, half.decode(hist, h_state),
+                                   truth.decode(hist, t_state))):
+        e_gpu, e_ref = rel(got, exact), rel(ref, exact)
+        print(f"fp16 model {name}: rel L2 to fp32 evaluation {e_gpu:.2e} (fp16 oracle {e_ref:.2e})",
+              flush=True)
+        assert e_gpu <= e_ref, f"fp16 {name}: GPU {e_gpu:.2e} vs fp16 oracle {e_ref:.2e}"
+    widths = [6, 5, 4]
+    result = grbeam_search(adapter, ids.to(device), widths)
+    torch.cuda.synchronize()
+    scores = torch.zeros(2, 1)
+    history = torch.empty(2, 1, 0, dtype=torch.int64)
+    lg = res.logits.cpu()[:, None]
+    for step, w in enumerate(widths):
+        if step:
+            lg = adapter.decode(history.to(device), res.state).cpu()
+        scores, parents, tokens = grbeam_ref.level_select(lg, scores, w)
+        history = torch.cat((history.gather(1, parents[..., None].expand(2, w, step)),
+                             tokens[..., None]), -1)
+    assert torch.equal(history, result.tokens.cpu())
+    assert torch.allclose(result.scores.cpu(), scores, atol=1e-4)
