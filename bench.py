@@ -69,7 +69,7 @@ T975 = {1: 12.706, 2: 4.303, 3: 3.182, 4: 2.776, 5: 2.571, 6: 2.447, 7: 2.365, 9
 # for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the number of
 # GEMM calls (346; a call that splits its last round launches two kernels).
 # Re-measured with the commands in profiles/hbm_traffic_and_busy_b32_p1024_w256.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 379.2e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 378.8e6
 
 
 def repeat_stability(outputs, first):
@@ -687,47 +687,85 @@ GEMM_SHAPES = (
 
 
 def ops_gemm(a):
-    """The bf16 GEMM shapes of the headline search, one at a time, through
-    kad_gemm_bf16 (automatic tile choice, fused epilogue) and, beside it, the
-    same product through torch's F.linear (hipBLASLt, no epilogue), both timed
-    with events over --op-iters back-to-back calls.  Inputs ~ N(0,1), weights
-    ~ N(0, 0.05^2); each result is checked against F.linear on 64 rows."""
+    """The bf16 GEMM shapes of the headline search, one at a time: kad_gemm_bf16
+    (automatic tile choice, fused epilogue), each tile configuration named by
+    --gemm-configs through kad_gemm_bf16_tiled, and the same product through
+    torch.matmul (hipBLASLt, no epilogue).  Inputs ~ N(0,1), weights ~ N(0,
+    0.05^2); the automatic choice is checked against F.linear on 64 rows and
+    every configuration against it bit for bit.  Timing: each form warmed,
+    then 7 interleaved rounds (the order rotating per round) of --op-iters / 7
+    back-to-back calls with HIP events, and each form's median; forms timed one
+    after another show an order bias (the first form measured runs slowest)."""
     from torch.nn import functional as F
 
-    from kadllm_amd import layers
+    from kadllm_amd import _lib, layers
 
+    cfgs = [int(c) for c in a.gemm_configs.split(",") if c.strip()] if a.gemm_configs else []
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(0)
-    total = {"ours_s": 0.0, "lib_s": 0.0, "flops": 0.0}
+    rounds = 7
+    per = max(a.op_iters // rounds, 3)
+    total = {"auto": 0.0, "lib": 0.0, "flops": 0.0}
+    total.update({c: 0.0 for c in cfgs})
     for name, M, N, K, epi, count in GEMM_SHAPES:
         x = torch.randn(M, K, generator=g, device=dev).bfloat16()
         w = (torch.randn(N, K, generator=g, device=dev) * 0.05).bfloat16()
         n_out = N // 2 if epi == layers.EPI_SWIGLU else N
-        out = torch.randn(M, n_out, generator=g, device=dev).bfloat16()
-        res0 = out[:64].clone()
-        if epi == layers.EPI_RESIDUAL:
-            call = lambda: layers.gemm(x, w, out=out, epilogue=epi, residual=out)  # noqa: E731
-        else:
-            call = lambda: layers.gemm(x, w, out=out, epilogue=epi)  # noqa: E731
-        call()
+        res = torch.randn(M, n_out, generator=g, device=dev).bfloat16()
+        stream = _lib.stream_of(x)
+
+        def form(cfg):
+            out = res.clone()
+            r = out if epi == layers.EPI_RESIDUAL else None
+
+            def call():
+                _lib.call("kad_gemm_bf16_tiled", _lib.ptr(x), K, _lib.ptr(w), K, _lib.ptr(out),
+                          n_out, _lib.ptr(r), n_out if r is not None else 0, M, N, K, epi, cfg,
+                          stream)
+            return out, call
+
+        out, auto = form(0)
+        auto()
         torch.cuda.synchronize()
+        first = out.clone()
         prod = F.linear(x[:64], w).float()
         if epi == layers.EPI_SWIGLU:
             gu = prod.bfloat16().float().view(64, N // 64, 2, 32)
             expect = (F.silu(gu[:, :, 0]).bfloat16().float() * gu[:, :, 1]).reshape(64, n_out)
         elif epi == layers.EPI_RESIDUAL:
-            expect = res0.float() + prod.bfloat16().float()
+            expect = res[:64].float() + prod.bfloat16().float()
         else:
             expect = prod
-        _rel_check(out[:64].float(), expect, name, rtol=2e-2, atol_frac=1e-2)
-        sec = _time_calls(call, a.op_iters)
-        lib = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        lib_sec = _time_calls(lambda: torch.matmul(x, w.t(), out=lib), a.op_iters)
+        _rel_check(first[:64].float(), expect, name, rtol=2e-2, atol_frac=1e-2)
+        calls = {"auto": auto}
+        for c in cfgs:
+            o, f = form(c)
+            try:
+                f()
+            except _lib.KadLibraryError:
+                continue                      # the configuration does not take this shape
+            torch.cuda.synchronize()
+            if not torch.equal(o, first):
+                raise SystemExit(f"{name}: tile configuration {c} differs from the automatic choice")
+            calls[c] = f
+        lib_out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        calls["lib"] = lambda: torch.matmul(x, w.t(), out=lib_out)
+        for f in calls.values():
+            for _ in range(3):
+                f()
+        samples = {k: [] for k in calls}
+        keys = list(calls)
+        for rd in range(rounds):
+            for k in keys[rd % len(keys):] + keys[:rd % len(keys)]:
+                samples[k].append(_time_calls(calls[k], per))
+        med = {k: statistics.median(v) for k, v in samples.items()}
         flops = 2.0 * M * N * K
         nbytes = 2 * (M * K + N * K + M * n_out * (2 if epi == layers.EPI_RESIDUAL else 1))
+        sec, lib_sec = med["auto"], med["lib"]
         tfs, lib_tfs = flops / sec / 1e12, flops / lib_sec / 1e12
-        total["ours_s"] += count * sec
-        total["lib_s"] += count * lib_sec
+        for k in med:
+            if k in total:
+                total[k] += count * med[k]
         total["flops"] += count * flops
         _op_line(f"bf16 GEMM {name}: achieved TFLOP/s", round(tfs, 1), "TFLOP/s",
                  {"workload": f"gemm M{M} N{N} K{K} epilogue {epi}"},
@@ -735,22 +773,25 @@ def ops_gemm(a):
                   "achieved": round(tfs, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                   "frac": round(tfs / PEAK_BF16_TFLOPS, 4), "traffic": None,
                   "algorithmic_flops_per_launch": flops, "algorithmic_bytes_per_launch": nbytes},
-                 None, {"iters": a.op_iters, "ms": round(sec * 1e3, 4),
+                 None, {"iters": rounds * per, "ms": round(sec * 1e3, 4),
                         "us_per_call": round(sec * 1e6, 2), "dispatches_per_search": count,
                         "hipblaslt_us_per_call": round(lib_sec * 1e6, 2),
                         "hipblaslt_tflops": round(lib_tfs, 1),
-                        "vs_hipblaslt": round(lib_sec / sec, 3)})
-        del x, w, out, lib
+                        "vs_hipblaslt": round(lib_sec / sec, 3),
+                        "tile_config_us": {str(k): round(v * 1e6, 2) for k, v in med.items()
+                                           if k not in ("auto", "lib")}})
+        del x, w, res, lib_out, calls
         torch.cuda.empty_cache()
-    tfs = total["flops"] / total["ours_s"] / 1e12
+    tfs = total["flops"] / total["auto"] / 1e12
     _op_line("bf16 GEMMs of one headline search, dispatch-weighted: achieved TFLOP/s",
              round(tfs, 1), "TFLOP/s", {"workload": "gemm shapes of grbeam B32 P1024 W256 3 tokens"},
              {"kernel": "gemm (automatic tile choice)", "bound": "mfma", "achieved": round(tfs, 1),
               "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tfs / PEAK_BF16_TFLOPS, 4),
               "traffic": None}, None,
-             {"iters": a.op_iters, "ms": round(total["ours_s"] * 1e3, 3),
-              "hipblaslt_ms": round(total["lib_s"] * 1e3, 3),
-              "hipblaslt_tflops": round(total["flops"] / total["lib_s"] / 1e12, 1)})
+             {"iters": rounds * per, "ms": round(total["auto"] * 1e3, 3),
+              "hipblaslt_ms": round(total["lib"] * 1e3, 3),
+              "hipblaslt_tflops": round(total["flops"] / total["lib"] / 1e12, 1),
+              "tile_config_ms": {str(c): round(total[c] * 1e3, 3) for c in cfgs}})
 
 
 # kernel classes whose algorithmic bytes are almost all reads (reported
@@ -971,6 +1012,9 @@ def main():
     ap.add_argument("--protocol", choices=("single", "reference"), default="single")
     ap.add_argument("--processes", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=50)
+    ap.add_argument("--gemm-configs", default="",
+                    help="ops_gemm: tile configurations to time beside the automatic choice, "
+                         "e.g. 16,18,20,22")
     ap.add_argument("--workload",
                     choices=("grbeam", "conditional_sid", "ops_gdn", "ops_attention", "ops_gemm",
                              "hbm_copy", "hbm_probe", "sid_study"),
