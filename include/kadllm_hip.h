@@ -222,6 +222,15 @@ int kad_attention_prefill(const void* q, int64_t sq_b, int64_t sq_l, int64_t sq_
  *                        candidates, sorted by (key desc, index asc): scores
  *                        [B, W] fp32, parents = index / V, tokens = index % V
  *                        (int64), valid = isfinite(score) (uint8).  W <= 16384.
+ * kad_beam_merge_select_wide  the same selection for any W (the reference's
+ *                        topk has no width cap, src/kadllm/grbeam.py:95):
+ *                        the radix rounds histogrammed by many workgroups
+ *                        per request, the winners sorted in caller workspace
+ *                        of kad_beam_merge_select_wide_workspace_bytes(B, W)
+ *                        bytes (16-byte aligned).  Keys are ordered by their
+ *                        order-preserving bit pattern, so -0 ranks below +0,
+ *                        where kad_beam_merge_select's sort treats them as a
+ *                        tie; otherwise the results are identical.
  * kad_beam_history       out[b, w, :] = [history[b, parents[b, w], :step], tokens[b, w]]
  *                        (history [B, Wp, step] int64, out [B, W, step + 1]).
  */
@@ -231,6 +240,11 @@ int kad_beam_row_select(const void* logits, int logits_dtype, int64_t ld, const 
 int kad_beam_merge_select(const float* cand_key, const int* cand_idx, int B, int ncand, int W,
                           int V, float* scores, int64_t* parents, int64_t* tokens, void* valid,
                           kad_stream_t stream);
+int kad_beam_merge_select_wide_workspace_bytes(int B, int W, int64_t* bytes);
+int kad_beam_merge_select_wide(const float* cand_key, const int* cand_idx, int B, int ncand,
+                               int W, int V, float* scores, int64_t* parents, int64_t* tokens,
+                               void* valid, void* workspace, int64_t workspace_bytes,
+                               kad_stream_t stream);
 /* Allocation-free selection: kad_beam_row_select then kad_beam_merge_select
  * (same arguments, same results bit for bit) with the candidates kept in a
  * 32 MiB device array inside the library instead of caller workspace, so the

@@ -46,6 +46,8 @@ SIGNATURES = {
     "kad_gdn_recurrent": "ppplli" "pipil" "pii" "plp" "iiiiiif" "s",
     "kad_attention_general": "plll" "pplll" "plll" "plll" "pp" "lll" "plll" "iiiiiiiii" "f" "s",
     "kad_beam_merge_select": "ppiiiipppps",
+    "kad_beam_merge_select_wide_workspace_bytes": "iip",
+    "kad_beam_merge_select_wide": "ppiiiippppp" "l" "s",
     "kad_beam_history": "piipppiis",
     "kad_gather_beam_rows": "pli" "pli" "i" "l" "p" "iii" "s",
     "kad_gdn_chunk_workspace_bytes": "iiiip",

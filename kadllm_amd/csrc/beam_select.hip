@@ -18,12 +18,16 @@
 // Stage 2, kad_beam_merge_select (one workgroup per request): an 8-bit radix
 // select over the request's Wp*K candidate keys finds the W-th key, a second
 // radix select over flat indices resolves ties (lower flat index first), and
-// the W winners are bitonic-sorted by (key desc, index asc).
+// the W winners are bitonic-sorted by (key desc, index asc) in LDS, for W up
+// to 16384.  kad_beam_merge_select_wide serves wider levels (the reference's
+// topk has no width cap): the same radix rounds, histogrammed by many
+// workgroups per request, and the winners sorted in caller workspace.
 //
 // Stage 3, kad_beam_history: new_history[b, w] = [history[b, parent], token].
 
 #include "kad_common.h"
 
+#include <algorithm>
 #include <mutex>
 
 // Scratch of kad_beam_select_noalloc (32 MiB per GPU; see scratch_address).
@@ -836,6 +840,219 @@ __global__ __launch_bounds__(kMergeThreads) void merge_select_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide levels (W > kMaxW): the same selection as merge_select_kernel -- the
+// W-th largest order key by four 8-bit radix rounds, the ties at it taken
+// lowest flat index first by up to four rounds over the indices -- but each
+// round's histogram is built by many workgroups per request (global atomics
+// into a per-request 256-bin histogram), and the winners are sorted in
+// global memory.  Winners are 64-bit words (~order key << 32 | index), so an
+// ascending sort orders them by (key desc, index asc); P = the next power of
+// two >= W words per request, the tail padded with all-ones words.
+//
+// Workspace: [B][P] u64 sort words, then [B][256] int histograms, then
+// [B][kWideState] int per-request selection state.
+constexpr int kWideState = 8;
+enum { WS_PREFIX, WS_PMASK, WS_NEED, WS_TIES, WS_IPREFIX, WS_IMASK, WS_INEED, WS_COUNT };
+constexpr int kWideThreads = 256;
+constexpr int kWideItems = 16;        // candidates per thread per histogram block
+constexpr int kSortLocal = 8192;      // sort words per workgroup in LDS (64 KB)
+constexpr int kSortThreads = 1024;
+
+__global__ __launch_bounds__(kWideThreads) void wide_init_kernel(uint64_t* __restrict__ words,
+                                                                 int* __restrict__ hist,
+                                                                 int* __restrict__ state, int B,
+                                                                 int W, int P) {
+  const int b = blockIdx.y;
+  for (int i = W + blockIdx.x * kWideThreads + threadIdx.x; i < P; i += gridDim.x * kWideThreads)
+    words[(int64_t)b * P + i] = ~0ull;
+  if (blockIdx.x == 0) {
+    hist[b * 256 + threadIdx.x] = 0;
+    if (threadIdx.x < kWideState) {
+      int v = 0;
+      if (threadIdx.x == WS_NEED || threadIdx.x == WS_INEED) v = W;
+      state[b * kWideState + threadIdx.x] = v;
+    }
+  }
+}
+
+// one histogram round over a block of kWideThreads * kWideItems candidates of
+// request blockIdx.y: IDX false: bins of (key >> shift) among the keys
+// matching the prefix so far; IDX true: bins of (index >> shift) among the
+// keys equal to the W-th key whose indices match the index prefix so far.
+template <bool IDX>
+__global__ __launch_bounds__(kWideThreads) void wide_hist_kernel(
+    const float* __restrict__ cand_key, const int* __restrict__ cand_idx, int ncand,
+    int* __restrict__ hist, const int* __restrict__ state, int shift) {
+  __shared__ int h[256];
+  const int b = blockIdx.y;
+  const int* st = state + b * kWideState;
+  const uint32_t prefix = (uint32_t)st[WS_PREFIX], pmask = (uint32_t)st[WS_PMASK];
+  if (IDX && st[WS_NEED] == st[WS_TIES]) return;  // every tie is taken: no index rounds
+  const uint32_t iprefix = (uint32_t)st[WS_IPREFIX], imask = (uint32_t)st[WS_IMASK];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const float* keys = cand_key + (int64_t)b * ncand;
+  const int* idxs = cand_idx + (int64_t)b * ncand;
+  const int64_t i0 = (int64_t)blockIdx.x * kWideThreads * kWideItems + threadIdx.x;
+  float kv[kWideItems];
+#pragma unroll
+  for (int q = 0; q < kWideItems; ++q) {
+    const int64_t i = i0 + q * kWideThreads;
+    kv[q] = i < ncand ? keys[i] : 0.f;
+  }
+#pragma unroll
+  for (int q = 0; q < kWideItems; ++q) {
+    const int64_t i = i0 + q * kWideThreads;
+    const uint32_t u = order32(kv[q]);
+    if (!IDX) {
+      hist_add_grouped(h, i < ncand && (u & pmask) == prefix, (int)((u >> shift) & 255));
+    } else if (i < ncand && u == prefix) {
+      const uint32_t x = (uint32_t)idxs[i];
+      if ((x & imask) == iprefix) atomicAdd(&h[(x >> shift) & 255], 1);
+    }
+  }
+  __syncthreads();
+  const int c = h[threadIdx.x];
+  if (c) atomicAdd(&hist[b * 256 + threadIdx.x], c);
+}
+
+// one wave per request: the bin of this round (as in merge_select_kernel),
+// the state update, and the histogram cleared for the next round
+template <bool IDX>
+__global__ __launch_bounds__(64) void wide_pick_kernel(int* __restrict__ hist,
+                                                       int* __restrict__ state, int shift) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  int* st = state + b * kWideState;
+  int* hb = hist + b * 256;
+  if (IDX && st[WS_NEED] == st[WS_TIES]) return;
+  int d = 0, acc = 0;
+  const int need = IDX ? st[WS_INEED] : st[WS_NEED];
+  const bool found = IDX ? pick_bin<false>(hb, need, lane, d, acc)
+                         : pick_bin<true>(hb, need, lane, d, acc);
+  const int ties = found ? hb[d] : 0;
+  __syncthreads();  // every lane has read the histogram
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hb[lane * 4 + i] = 0;
+  if (found) {
+    if (!IDX) {
+      st[WS_PREFIX] = (int)((uint32_t)st[WS_PREFIX] | ((uint32_t)d << shift));
+      st[WS_PMASK] = (int)((uint32_t)st[WS_PMASK] | (255u << shift));
+      st[WS_NEED] = need - acc;
+      st[WS_TIES] = ties;  // after the last round: the candidates equal to the key
+      st[WS_INEED] = need - acc;  // the index rounds start from the ties still needed
+    } else {
+      st[WS_IPREFIX] = (int)((uint32_t)st[WS_IPREFIX] | ((uint32_t)d << shift));
+      st[WS_IMASK] = (int)((uint32_t)st[WS_IMASK] | (255u << shift));
+      st[WS_INEED] = need - acc;
+    }
+  }
+}
+
+// the W winners of each request as sort words, one slot each (wave-aggregated
+// slot counter); words [W, P) were padded by wide_init_kernel
+__global__ __launch_bounds__(kWideThreads) void wide_gather_kernel(
+    const float* __restrict__ cand_key, const int* __restrict__ cand_idx, int ncand,
+    int* __restrict__ state, uint64_t* __restrict__ words, int W, int P) {
+  const int b = blockIdx.y;
+  int* st = state + b * kWideState;
+  const uint32_t kth = (uint32_t)st[WS_PREFIX];
+  const bool all_ties = st[WS_NEED] == st[WS_TIES];
+  const uint32_t idx_cut = all_ties ? 0xffffffffu : (uint32_t)st[WS_IPREFIX];
+  const float* keys = cand_key + (int64_t)b * ncand;
+  const int* idxs = cand_idx + (int64_t)b * ncand;
+  const int lane = threadIdx.x & 63;
+  const int64_t i0 = (int64_t)blockIdx.x * kWideThreads * kWideItems + threadIdx.x;
+#pragma unroll 4
+  for (int q = 0; q < kWideItems; ++q) {
+    const int64_t i = i0 + q * kWideThreads;
+    uint32_t u = 0, x = 0;
+    bool take = false;
+    if (i < ncand) {
+      u = order32(keys[i]);
+      if (u >= kth) {
+        x = (uint32_t)idxs[i];
+        take = u > kth || x <= idx_cut;
+      }
+    }
+    const uint64_t m = __ballot(take);
+    if (!m) continue;
+    const int leader = __ffsll((unsigned long long)m) - 1;
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&st[WS_COUNT], (int)__popcll(m));
+    base = __shfl(base, leader, 64);
+    if (take) {
+      const int slot = base + (int)__popcll(m & ((1ull << lane) - 1));
+      if (slot < W) words[(int64_t)b * P + slot] = ((uint64_t)(~u) << 32) | x;
+    }
+  }
+}
+
+// bitonic stages on LDS chunks of `chunk` words: sizes size_lo..size_hi, for
+// each the strides below min(size, chunk); a pair's direction follows its
+// position inside the request's P words (ascending where (pos & size) == 0)
+__global__ __launch_bounds__(kSortThreads) void bitonic_local_kernel(uint64_t* __restrict__ words,
+                                                                     int P, int chunk,
+                                                                     int size_lo, int size_hi) {
+  __shared__ uint64_t t[kSortLocal];
+  const int64_t base = (int64_t)blockIdx.x * chunk;
+  const int pos0 = (int)(base & (P - 1));
+  for (int i = threadIdx.x; i < chunk; i += kSortThreads) t[i] = words[base + i];
+  __syncthreads();
+  for (int size = size_lo; size <= size_hi; size <<= 1) {
+    for (int stride = min(size, chunk) >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < chunk / 2; i += kSortThreads) {
+        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
+        const int hi = lo | stride;
+        const bool asc = ((pos0 + lo) & size) == 0;
+        const uint64_t a = t[lo], c = t[hi];
+        if ((a > c) == asc) {
+          t[lo] = c;
+          t[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < chunk; i += kSortThreads) words[base + i] = t[i];
+}
+
+// one bitonic stage (size, stride >= the LDS chunk) over all requests' words
+__global__ __launch_bounds__(256) void bitonic_global_kernel(uint64_t* __restrict__ words, int P,
+                                                             int size, int stride,
+                                                             int64_t npairs) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= npairs) return;
+  const int64_t lo = ((i & ~(int64_t)(stride - 1)) << 1) | (i & (stride - 1));
+  const int64_t hi = lo | stride;
+  const bool asc = ((lo & (P - 1)) & size) == 0;
+  const uint64_t a = words[lo], c = words[hi];
+  if ((a > c) == asc) {
+    words[lo] = c;
+    words[hi] = a;
+  }
+}
+
+__global__ __launch_bounds__(256) void wide_emit_kernel(const uint64_t* __restrict__ words, int P,
+                                                        int B, int W, int V,
+                                                        float* __restrict__ scores,
+                                                        int64_t* __restrict__ parents,
+                                                        int64_t* __restrict__ tokens,
+                                                        uint8_t* __restrict__ valid) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (int64_t)B * W) return;
+  const int64_t b = n / W, j = n % W;
+  const uint64_t w = words[b * P + j];
+  const uint32_t u = ~(uint32_t)(w >> 32);
+  // inverse of order32
+  const float key = __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+  const int id = (int)(uint32_t)w;
+  scores[n] = key;
+  parents[n] = id / V;
+  tokens[n] = id % V;
+  valid[n] = (key == key) && (key != INFINITY) && (key != -INFINITY);
+}
+
 __global__ __launch_bounds__(256) void history_kernel(const int64_t* __restrict__ hist, int Wp,
                                                       int step, const int64_t* __restrict__ parents,
                                                       const int64_t* __restrict__ tokens,
@@ -928,6 +1145,61 @@ int launch_merge(const float* cand_key, const int* cand_idx, int B, int ncand, i
   return kad_launch_status("merge_select_kernel");
 }
 
+int64_t wide_words(int W) {
+  int64_t P = 1;
+  while (P < W) P <<= 1;
+  return P;
+}
+
+int64_t wide_ws_bytes(int B, int W) {
+  return (int64_t)B * wide_words(W) * 8 + (int64_t)B * 256 * 4 + (int64_t)B * kWideState * 4;
+}
+
+int launch_merge_wide(const float* cand_key, const int* cand_idx, int B, int ncand, int W, int V,
+                      float* scores, int64_t* parents, int64_t* tokens, void* valid, void* ws,
+                      hipStream_t s) {
+  const int64_t P = wide_words(W);
+  uint64_t* words = (uint64_t*)ws;
+  int* hist = (int*)(words + (int64_t)B * P);
+  int* state = hist + (int64_t)B * 256;
+  const int64_t init_blocks = std::min<int64_t>(std::max<int64_t>((P - W + kWideThreads - 1) /
+                                                                      kWideThreads, 1), 4096);
+  hipLaunchKernelGGL(wide_init_kernel, dim3((unsigned)init_blocks, (unsigned)B), dim3(kWideThreads),
+                     0, s, words, hist, state, B, W, (int)P);
+  if (const int rc = kad_launch_status("wide_init_kernel")) return rc;
+  const int64_t per_block = (int64_t)kWideThreads * kWideItems;
+  const dim3 grid((unsigned)((ncand + per_block - 1) / per_block), (unsigned)B);
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hipLaunchKernelGGL((wide_hist_kernel<false>), grid, dim3(kWideThreads), 0, s, cand_key,
+                       cand_idx, ncand, hist, state, shift);
+    hipLaunchKernelGGL((wide_pick_kernel<false>), dim3(B), dim3(64), 0, s, hist, state, shift);
+  }
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hipLaunchKernelGGL((wide_hist_kernel<true>), grid, dim3(kWideThreads), 0, s, cand_key,
+                       cand_idx, ncand, hist, state, shift);
+    hipLaunchKernelGGL((wide_pick_kernel<true>), dim3(B), dim3(64), 0, s, hist, state, shift);
+  }
+  if (const int rc = kad_launch_status("wide_hist_kernel")) return rc;
+  hipLaunchKernelGGL(wide_gather_kernel, grid, dim3(kWideThreads), 0, s, cand_key, cand_idx,
+                     ncand, state, words, W, (int)P);
+  if (const int rc = kad_launch_status("wide_gather_kernel")) return rc;
+  const int chunk = (int)std::min<int64_t>(P, kSortLocal);
+  const int64_t total = (int64_t)B * P;
+  hipLaunchKernelGGL(bitonic_local_kernel, dim3((unsigned)(total / chunk)), dim3(kSortThreads), 0,
+                     s, words, (int)P, chunk, 2, chunk);
+  for (int64_t size = 2 * (int64_t)chunk; size <= P; size <<= 1) {
+    for (int64_t stride = size / 2; stride >= chunk; stride >>= 1)
+      hipLaunchKernelGGL(bitonic_global_kernel, dim3((unsigned)((total / 2 + 255) / 256)),
+                         dim3(256), 0, s, words, (int)P, (int)size, (int)stride, total / 2);
+    hipLaunchKernelGGL(bitonic_local_kernel, dim3((unsigned)(total / chunk)), dim3(kSortThreads),
+                       0, s, words, (int)P, chunk, (int)size, (int)size);
+  }
+  if (const int rc = kad_launch_status("bitonic_kernels")) return rc;
+  hipLaunchKernelGGL(wide_emit_kernel, dim3((unsigned)(((int64_t)B * W + 255) / 256)), dim3(256),
+                     0, s, words, (int)P, B, W, V, scores, parents, tokens, (uint8_t*)valid);
+  return kad_launch_status("wide_emit_kernel");
+}
+
 int check_logits_dtype(int dtype) {
   KAD_REQUIRE(dtype == KAD_DTYPE_BF16 || dtype == KAD_DTYPE_F16 || dtype == KAD_DTYPE_F32,
               "unknown logits dtype code %d", dtype);
@@ -991,9 +1263,36 @@ extern "C" int kad_beam_merge_select(const float* cand_key, const int* cand_idx,
                                      int64_t* tokens, void* valid, kad_stream_t stream) {
   KAD_REQUIRE(cand_key && cand_idx && scores && parents && tokens && valid, "null pointer argument");
   KAD_REQUIRE(B > 0 && W > 0 && ncand >= W && V > 0, "bad dimensions (need ncand >= W)");
-  if (W > kMaxW) KAD_UNSUPPORTED("beam width %d exceeds %d", W, kMaxW);
+  if (W > kMaxW)
+    KAD_UNSUPPORTED("beam width %d exceeds %d; kad_beam_merge_select_wide sorts wider levels", W,
+                    kMaxW);
   return launch_merge(cand_key, cand_idx, B, ncand, W, V, scores, parents, tokens, valid,
                       (hipStream_t)stream);
+}
+
+extern "C" int kad_beam_merge_select_wide_workspace_bytes(int B, int W, int64_t* bytes) {
+  KAD_REQUIRE(bytes, "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0, "bad dimensions");
+  *bytes = wide_ws_bytes(B, W);
+  return KAD_OK;
+}
+
+extern "C" int kad_beam_merge_select_wide(const float* cand_key, const int* cand_idx, int B,
+                                          int ncand, int W, int V, float* scores,
+                                          int64_t* parents, int64_t* tokens, void* valid,
+                                          void* workspace, int64_t workspace_bytes,
+                                          kad_stream_t stream) {
+  KAD_REQUIRE(cand_key && cand_idx && scores && parents && tokens && valid && workspace,
+              "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0 && ncand >= W && V > 0, "bad dimensions (need ncand >= W)");
+  KAD_REQUIRE(B <= 65535, "at most 65535 requests per call");
+  KAD_REQUIRE(wide_words(W) <= (1ll << 30), "beam width %d too large", W);
+  const int64_t need = wide_ws_bytes(B, W);
+  KAD_REQUIRE(workspace_bytes >= need, "workspace of %lld bytes is smaller than %lld",
+              (long long)workspace_bytes, (long long)need);
+  KAD_REQUIRE(((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
+  return launch_merge_wide(cand_key, cand_idx, B, ncand, W, V, scores, parents, tokens, valid,
+                           workspace, (hipStream_t)stream);
 }
 
 extern "C" int kad_beam_select_noalloc(const void* logits, int logits_dtype, int64_t ld,

@@ -9,6 +9,7 @@ temporaries).  Ties are broken by the lower flat index (parent * V + token);
 the reference's torch.topk leaves tie order unspecified (grbeam.py:95).
 """
 
+import ctypes
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 from typing import Any, Protocol
@@ -48,13 +49,9 @@ class GRBeamResult:
 Constraint = Callable[[torch.Tensor, torch.Tensor], torch.Tensor]
 
 
-# Widest level the merge kernel sorts in LDS (kad_beam_merge_select).
-MAX_WIDTH = 16384
-
-
-def _check_widths(widths):
-    if any(w > MAX_WIDTH for w in widths):
-        raise ValueError(f"beam widths above {MAX_WIDTH} are not supported by the HIP selection")
+# Widest level the merge kernel sorts in LDS (kad_beam_merge_select); wider
+# levels take kad_beam_merge_select_wide, which sorts in workspace.
+MAX_LDS_WIDTH = 16384
 
 
 def select_level(logits, scores, width, mask=None):
@@ -70,8 +67,6 @@ def select_level(logits, scores, width, mask=None):
     B, Wp, V = logits.shape
     if logits.dtype not in _lib.DTYPE_CODES:
         raise RuntimeError("HIP beam selection takes bf16, fp16 or fp32 logits")
-    if width > MAX_WIDTH:
-        raise ValueError(f"beam width {width} exceeds the HIP selection limit {MAX_WIDTH}")
     if not logits.is_cuda:
         raise RuntimeError("HIP beam selection needs logits on a ROCm device")
     if logits.stride(2) != 1 or logits.stride(0) != Wp * logits.stride(1):
@@ -101,9 +96,28 @@ def select_level(logits, scores, width, mask=None):
     parents = torch.empty(B, width, dtype=torch.int64, device=dev)
     tokens = torch.empty(B, width, dtype=torch.int64, device=dev)
     valid = torch.empty(B, width, dtype=torch.bool, device=dev)
-    _lib.call("kad_beam_merge_select", _lib.ptr(cand_key), _lib.ptr(cand_idx), B, Wp * K, width,
-              V, _lib.ptr(new_scores), _lib.ptr(parents), _lib.ptr(tokens), _lib.ptr(valid), stream)
+    merge(cand_key, cand_idx, B, Wp * K, width, V, new_scores, parents, tokens, valid, stream)
     return new_scores, parents, tokens, valid
+
+
+def merge(cand_key, cand_idx, B, ncand, width, V, scores, parents, tokens, valid, stream,
+          wide=None):
+    """The request-level stage of the selection: the LDS-sorting kernel up to
+    MAX_LDS_WIDTH beams, the workspace-sorting one beyond (``wide`` forces
+    either)."""
+    if wide is None:
+        wide = width > MAX_LDS_WIDTH
+    if not wide:
+        _lib.call("kad_beam_merge_select", _lib.ptr(cand_key), _lib.ptr(cand_idx), B, ncand,
+                  width, V, _lib.ptr(scores), _lib.ptr(parents), _lib.ptr(tokens),
+                  _lib.ptr(valid), stream)
+        return
+    nbytes = ctypes.c_int64()
+    _lib.call("kad_beam_merge_select_wide_workspace_bytes", B, width, ctypes.byref(nbytes))
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=cand_key.device)
+    _lib.call("kad_beam_merge_select_wide", _lib.ptr(cand_key), _lib.ptr(cand_idx), B, ncand,
+              width, V, _lib.ptr(scores), _lib.ptr(parents), _lib.ptr(tokens), _lib.ptr(valid),
+              _lib.ptr(ws), nbytes.value, stream)
 
 
 def select_level_grouped(logits, scores, groups, width, mask=None):
@@ -180,7 +194,6 @@ def grbeam_search(
         not isinstance(w, int) or isinstance(w, bool) or w < 1 for w in widths
     ):
         raise ValueError("widths must contain positive integers")
-    _check_widths(widths)
     prefill = adapter.prefill(input_ids)
     B = input_ids.shape[0]
     if prefill.logits.ndim != 2 or prefill.logits.shape[0] != B:
@@ -246,7 +259,6 @@ def conditional_search(
             raise ValueError("widths must contain positive integers")
     if input_ids.ndim != 2 or min(input_ids.shape) < 1:
         raise ValueError("input_ids must be nonempty [B, prompt_length]")
-    _check_widths(list(coarse_widths) + list(fine_widths))
     prefill = adapter.prefill(input_ids)
     B = input_ids.shape[0]
     V = prefill.logits.shape[-1]

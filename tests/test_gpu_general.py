@@ -162,6 +162,68 @@ def test_select_beams_above_1024(device, B, Wp, V, width):
     assert bool(valid.all())
 
 
+@pytest.mark.parametrize("B,Wp,V,width", [(1, 3, 12000, 20000), (2, 40, 2048, 40000)])
+def test_select_beams_above_lds_limit(device, B, Wp, V, width):
+    """Widths past the LDS-sorting merge (16,384) take the workspace-sorting
+    one; judged gap-aware against fp64 keys as the narrower widths are."""
+    g = torch.Generator().manual_seed(width + Wp)
+    logits = torch.randn(B, Wp, V, generator=g).bfloat16()
+    scores = torch.randn(B, Wp, generator=g)
+    s, p, t, valid = select_level(*_on(device, logits, scores), width)
+    keys = logits.double().log_softmax(-1) + scores.double()[..., None]
+    assert_selection_gap_aware(s, p, t, keys, width, delta=2e-5, name=f"W={width}")
+    assert bool(valid.all())
+
+
+def test_select_wide_exact_ties_and_mask(device):
+    """One row per request with a handful of distinct logit values, so the
+    20,000th pick falls inside a class of equal keys: ties go to the lower
+    column, exactly as the oracle orders them; masked entries score -inf and
+    rank last."""
+    g = torch.Generator().manual_seed(5)
+    B, Wp, V, width = 2, 1, 60000, 20000
+    logits = (torch.randint(-4, 5, (B, Wp, V), generator=g).float() / 2).bfloat16()
+    scores = torch.zeros(B, Wp)
+    mask = torch.rand(B, Wp, V, generator=g) > 0.5
+    for m in (None, mask):
+        es, ep, et = grbeam_ref.level_select(logits, scores, width, m)
+        s, p, t, valid = select_level(*_on(device, logits, scores), width,
+                                      None if m is None else m.to(device))
+        assert torch.equal(p.cpu(), ep) and torch.equal(t.cpu(), et)
+        fin = torch.isfinite(es)
+        assert torch.equal(valid.cpu(), fin)
+        torch.testing.assert_close(s.cpu()[fin], es[fin], atol=1e-5, rtol=0)
+
+
+@pytest.mark.parametrize("B,Wp,V,width", [(3, 5, 1000, 7), (2, 8, 4096, 3000),
+                                          (2, 16, 2048, 16384)])
+def test_wide_merge_equals_lds_merge(device, B, Wp, V, width):
+    """The two request-level kernels on the same row candidates (logits with
+    many exact ties) give the same picks, scores and order, bit for bit."""
+    from kadllm_amd import _lib
+    from kadllm_amd.grbeam import merge
+
+    g = torch.Generator().manual_seed(width)
+    logits = (torch.randint(-20, 21, (B, Wp, V), generator=g).float() / 4).bfloat16().to(device)
+    parent = torch.randint(-3, 1, (B, Wp), generator=g).float().to(device)
+    K = min(width, V)
+    cand_key = torch.empty(B * Wp, K, dtype=torch.float32, device=device)
+    cand_idx = torch.empty(B * Wp, K, dtype=torch.int32, device=device)
+    stream = _lib.stream_of(logits)
+    _lib.call("kad_beam_row_select", _lib.ptr(logits), 0, V, None, V, _lib.ptr(parent),
+              B * Wp, Wp, V, K, _lib.ptr(cand_key), _lib.ptr(cand_idx), stream)
+    outs = []
+    for wide in (False, True):
+        o = (torch.empty(B, width, device=device), torch.empty(B, width, dtype=torch.int64,
+                                                                device=device),
+             torch.empty(B, width, dtype=torch.int64, device=device),
+             torch.empty(B, width, dtype=torch.bool, device=device))
+        merge(cand_key, cand_idx, B, Wp * K, width, V, *o, stream, wide=wide)
+        outs.append([x.cpu() for x in o])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 def test_reference_hybrid_lm_readme_example(device):
     """README.md:254-266: ReferenceHybridLM(vocab_size=32), prompts [2, 5],
     widths [2, 3, 4] gives tokens [2, 4, 3]."""

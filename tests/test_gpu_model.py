@@ -485,6 +485,40 @@ def _parents_of(history, prev):
     return parents, history[:, :, -1]
 
 
+def test_tiny_grbeam_wide_level(device, tiny):
+    """A level wider than the LDS-sorting merge (20,000 beams per request, on
+    the workspace-sorting one), decoded and selected from again: widths
+    [64, 20000, 4].  Level 0 equals the oracle's selection on the GPU's
+    prefill logits; levels 1 and 2 are judged gap-aware against fp64 keys of
+    the GPU's own logits (thousands of cross-row near-ties at the 20,000th
+    key are ordered by fp32 rounding)."""
+    from conftest import assert_selection_gap_aware
+
+    cfg, oracle, adapter = tiny
+    g = torch.Generator().manual_seed(23)
+    ids = torch.randint(0, cfg.vocab_size, (2, 48), generator=g)
+    two = grbeam_search(adapter, ids.to(device), [64, 20000])
+    three = grbeam_search(adapter, ids.to(device), [64, 20000, 4])
+    torch.cuda.synchronize()
+    assert two.tokens.shape == (2, 20000, 2) and bool(two.valid.all())
+    assert three.tokens.shape == (2, 4, 3) and bool(three.valid.all())
+    h1 = two.tokens.cpu()
+    for b in range(2):
+        assert len({tuple(x) for x in h1[b].tolist()}) == 20000, "beams must be distinct"
+    pre = adapter.prefill(ids.to(device))
+    s0, p0, t0 = grbeam_ref.level_select(pre.logits.cpu()[:, None], torch.zeros(2, 1), 64)
+    h0 = t0[..., None]
+    logits1 = adapter.decode(h0.to(device), pre.state).cpu()
+    keys1 = logits1.double().log_softmax(-1) + s0.double()[..., None]
+    p1, t1 = _parents_of(h1, h0)   # every level-1 beam extends a level-0 beam
+    assert_selection_gap_aware(two.scores.cpu(), p1, t1, keys1, 20000, delta=2e-5,
+                               name="level 1")
+    logits2 = adapter.decode(h1.to(device), pre.state).cpu()
+    keys2 = logits2.double().log_softmax(-1) + two.scores.cpu().double()[..., None]
+    p2, t2 = _parents_of(three.tokens.cpu(), h1)
+    assert_selection_gap_aware(three.scores.cpu(), p2, t2, keys2, 4, delta=2e-5, name="level 2")
+
+
 def test_reference_bf16_run_replayed_through_hip(device):
     """The reference's own bf16 search on the tiny model
     (tests/golden/grbeam_tiny_bf16.npz: the transformers bf16 prefill and the

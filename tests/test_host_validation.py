@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from kadllm_amd import conditional_search, grbeam_search
-from kadllm_amd.grbeam import MAX_WIDTH, PrefillResult
+from kadllm_amd.grbeam import MAX_LDS_WIDTH, PrefillResult
 from kadllm_amd.qwen35 import reject_biases
 
 
@@ -23,14 +23,17 @@ class _MetaAdapter:
         raise AssertionError("decode must not be reached")
 
 
-def test_width_above_limit_raises_before_prefill():
-    a = _MetaAdapter()
+def test_width_beyond_candidate_slots_raises_before_selection():
+    """Widths have no cap of their own (the reference's topk has none); a level
+    wider than its candidate slots raises the reference's ValueError
+    (src/kadllm/grbeam.py:85-86) before any selection kernel."""
+    a = _MetaAdapter(V=16)
     ids = torch.zeros(1, 3, dtype=torch.int64)
-    with pytest.raises(ValueError, match="not supported by the HIP selection"):
-        grbeam_search(a, ids, [4, MAX_WIDTH + 1])
-    with pytest.raises(ValueError, match="not supported by the HIP selection"):
-        conditional_search(a, ids, [4], [MAX_WIDTH + 1])
-    assert a.prefills == 0
+    with pytest.raises(ValueError, match="exceeds the number of candidate slots"):
+        grbeam_search(a, ids, [MAX_LDS_WIDTH + 1])
+    with pytest.raises(ValueError, match="exceeds the number of candidate slots"):
+        conditional_search(a, ids, [17], [2])
+    assert a.prefills == 2
 
 
 def test_constraint_mask_on_another_device_raises():
