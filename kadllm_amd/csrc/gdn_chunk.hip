@@ -17,18 +17,20 @@
 //
 // Two kernels.  gdn_chunk_prep runs every (sequence, head, chunk) in
 // parallel and does the part that needs no state: the q and k row scales,
-// the k Gram matrix on bf16 MFMA, the decay masks and the triangular solve.  It writes T' as bf16 hi/lo planes (x = hi + lo to 2^-16),
-// already in the scan's MFMA fragment order, and per-token scalars: 17 KB per
-// chunk.  gdn_chunk_scan walks the chunks of one (sequence, head) in order
-// with 4 waves, wave w owning value columns [32w, 32w+32) of the fp32 state
-// S [K, V]; two workgroups share a CU so one's loads overlap the other's
-// MFMAs.  It reads q, k and v itself and scales q and k with the prep's row
-// scales (k to the prep's bits), so In never goes through memory: the In^T
-// tiles come out of the
-// MFMA with tokens j in the accumulator order, which is the K order of the
-// In v_new product.  S lives in accumulator registers (rows k, columns v) and
-// the same registers, split hi/lo, are the B operand of k S and q S; the S
-// update reads k^T straight from the row-major k tile with transposing LDS
+// the k Gram matrix and the q k^T tiles on bf16 MFMA, the decay masks, the
+// triangular solve, and In.  It writes T' and In as bf16 hi/lo planes
+// (x = hi + lo to 2^-16), already in the scan's MFMA fragment order (the
+// In^T tiles come out of the MFMA with tokens j in the accumulator order,
+// which is the K order of the In v_new product), and per-token scalars:
+// 26 KB per chunk.  gdn_chunk_scan walks the chunks of one (sequence, head)
+// in order with 4 waves, wave w owning value columns [32w, 32w+32) of the
+// fp32 state S [K, V]; two workgroups share a CU so one's loads overlap the
+// other's MFMAs.  It reads q, k and v itself and scales q and k with the
+// prep's row scales (k to the prep's bits).  Forming In in the prep instead
+// of in every wave of the scan took 42% of the VALU instructions out of the
+// scan's serial chain.  S lives in accumulator registers (rows k, columns v)
+// and the same registers, split hi/lo, are the B operand of k S and q S; the
+// S update reads k^T straight from the row-major k tile with transposing LDS
 // reads.  All products run on v_mfma_f32_32x32x16_bf16 with fp32
 // accumulation; fp32 operands take 2-3 hi/lo passes.
 
@@ -40,22 +42,45 @@ constexpr int kC = 64;
 constexpr int kPrepThreads = 256;
 
 // per-token scalars of a chunk record
-// (EG e^G, BT beta, KM k multiplier, WU state-update weight, G2 G log2(e),
-// KRS / QRS the bf16 l2norm row scales of k / q (1 in fp32 mode), QM the q
-// multiplier incl. scale)
-enum { S_EG = 0, S_BT, S_KM, S_WU, S_G2, S_KRS, S_QRS, S_QM, kScal };
+// (EG e^G, BT beta, ZK = beta e^G kmul (kmul the k multiplier), WU the
+// state-update weight kmul e^{G_last - G}, KRS / QRS the bf16 l2norm row
+// scales of k / q (1 in fp32 mode), EQ = e^G qmul (qmul the q multiplier
+// incl. scale))
+enum { S_EG = 0, S_BT, S_ZK, S_WU, S_KRS, S_QRS, S_EQ, kScal };
 constexpr float kLog2e = 1.4426950408889634f;
 
-// workspace record of one (sequence, head, chunk), in bytes: T' hi/lo as the
-// scan's A fragments ([it 2][s 4][plane 2][lane 64][8] bf16: lane L of
-// fragment (it, s) holds T'[it*32 + L%32][s*16 + (t/4)*8 + (L/32)*4 + t%4],
-// t < 8), then fp32 [kScal][64]
+// workspace record of one (sequence, head, chunk), in bytes: T' and then In
+// (both strictly / non-strictly lower triangular 64 x 64) as hi/lo bf16 A
+// fragments of the scan's 32x32x16 MFMAs, then fp32 [kScal][64].  Fragment
+// (it, s), s < 2 (it + 1) (the others lie above the diagonal), is stored at
+// index frag_index(it, s) as [plane 2][lane 64][8]: lane L holds
+// X[it*32 + L%32][s*16 + (t/4)*8 + (L/32)*4 + t%4], t < 8.
 struct ChunkRec {
-  static constexpr int tf_elems = 2 * 4 * 2 * 64 * 8;
+  static constexpr int frags = 6;
+  static constexpr int frag_elems = frags * 2 * 64 * 8;
+  static constexpr int tf_elems = 2 * frag_elems;   // T' then In
   static constexpr size_t tf = 0;
+  static constexpr size_t in = tf + frag_elems * 2;
   static constexpr size_t scal = tf + tf_elems * 2;
   static constexpr size_t bytes = scal + kScal * kC * 4;
 };
+__device__ __forceinline__ int frag_index(int it, int s) { return it == 0 ? s : 2 + s; }
+
+// B fragments (hi, lo) of an fp32 accumulator tile for K step s: the 8
+// accumulator entries (s%2)*8 .. +7 of 32-row tile s/2
+__device__ __forceinline__ void acc_frags(const f32x16& t, int half, bf16x8& hi, bf16x8& lo) {
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = t[half * 8 + i];
+  split8(x, hi, lo);
+}
+
+// x of the lane the DPP control selects (every lane valid)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, true));
+}
 
 // sum of squares of a row whose CPR 16-byte slices sit in CPR consecutive
 // lanes (aligned groups); hf: the squares rounded to bf16 as transformers'
@@ -67,11 +92,23 @@ __device__ __forceinline__ float row_sumsq(const u32x4& r, bool hf) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float lo = __uint_as_float(r[e] << 16), hi = __uint_as_float(r[e] & 0xffff0000u);
-    ss += hf ? round_bf(lo * lo) : lo * lo;
-    ss += hf ? round_bf(hi * hi) : hi * hi;
+    if (hf) {
+      // both squares rounded by one packed conversion
+      const uint32_t sq = pack_bf16x2(lo * lo, hi * hi);
+      ss += __uint_as_float(sq << 16);
+      ss += __uint_as_float(sq & 0xffff0000u);
+    } else {
+      ss += lo * lo;
+      ss += hi * hi;
+    }
   }
-#pragma unroll
-  for (int o = CPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  // the row's sum on DPP lane permutes within its 16- or 8-lane row (xor 1,
+  // xor 2, half-row mirror, row mirror): no LDS round trips
+  static_assert(CPR == 8 || CPR == 16, "rows span 8 or 16 lanes");
+  ss += dpp_f32<0xB1>(ss);   // quad_perm [1, 0, 3, 2]
+  ss += dpp_f32<0x4E>(ss);   // quad_perm [2, 3, 0, 1]
+  ss += dpp_f32<0x141>(ss);  // row_half_mirror
+  if constexpr (CPR == 16) ss += dpp_f32<0x140>(ss);  // row_mirror
   return ss;
 }
 
@@ -82,11 +119,8 @@ __device__ __forceinline__ float hf_l2_rs(float ss) {
 }
 __device__ __forceinline__ void hf_l2_apply(u32x4& r, float rs) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float lo = round_bf(__uint_as_float(r[e] << 16) * rs);
-    const float hi = round_bf(__uint_as_float(r[e] & 0xffff0000u) * rs);
-    r[e] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-  }
+  for (int e = 0; e < 4; ++e)
+    r[e] = pack_bf16x2(__uint_as_float(r[e] << 16) * rs, __uint_as_float(r[e] & 0xffff0000u) * rs);
 }
 
 // ---------------------------------------------------------------------------
@@ -98,16 +132,17 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   constexpr int LD = K + 8;
   constexpr int CPR = K / 8;       // 16-byte slices per k row
   constexpr int RPI = 64 / CPR;    // rows per wave instruction
-  // the bf16 k rows (Gram phase) and, later, A in residue-major order plus
-  // the T' tile share one LDS region
-  constexpr size_t kRows = kC * LD * sizeof(bf16_t);
+  // the bf16 k and q rows (Gram phase) and, later, A in residue-major order
+  // plus the T' tile share one LDS region
+  constexpr size_t kRows = 2 * kC * LD * sizeof(bf16_t);
   constexpr size_t kMats = (kC * kC + kC * (kC + 1)) * sizeof(float);
   __shared__ __attribute__((aligned(16))) unsigned char region[kRows > kMats ? kRows : kMats];
   bf16_t* kb = (bf16_t*)region;
+  bf16_t* qb = kb + kC * LD;
   float* Ar = (float*)region;                         // Ar[i*64 + (j%4)*16 + j/4] = A[i][j]
   float(*Tm)[kC + 1] = (float(*)[kC + 1])(Ar + kC * kC);
   __shared__ __attribute__((aligned(16))) float Gs[kC];
-  __shared__ float bt[kC], kmul[kC], krs[kC], qrs[kC], qmul[kC];
+  __shared__ float bt[kC], kmul[kC], krs[kC], qrs[kC], qmul[kC], g2s[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x % nchunks;
@@ -160,11 +195,13 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
         kr_s = hf_l2_rs(kss);
         qr_s = hf_l2_rs(qss);
         hf_l2_apply(kr[it], kr_s);
+        hf_l2_apply(qr[it], qr_s);
       } else {
         km = 1.0f / sqrtf(kss + 1e-6f);
         qm = scale / sqrtf(qss + 1e-6f);
       }
       *(u32x4*)(kb + i * LD + ch * 8) = kr[it];
+      *(u32x4*)(qb + i * LD + ch * 8) = qr[it];
       if (ch == 0) {
         kmul[i] = km;
         krs[i] = kr_s;
@@ -187,38 +224,67 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   __syncthreads();
   if (tid < kC) {
     float* sc = (float*)(rec + ChunkRec::scal);
-    sc[S_EG * kC + tid] = expf(Gs[tid]);
+    const float eg = expf(Gs[tid]);
+    sc[S_EG * kC + tid] = eg;
     sc[S_BT * kC + tid] = bt[tid];
-    sc[S_KM * kC + tid] = kmul[tid];
+    sc[S_ZK * kC + tid] = bt[tid] * (eg * kmul[tid]);
     sc[S_WU * kC + tid] = kmul[tid] * expf(Gs[kC - 1] - Gs[tid]);
-    sc[S_G2 * kC + tid] = Gs[tid] * kLog2e;
     sc[S_KRS * kC + tid] = krs[tid];
     sc[S_QRS * kC + tid] = qrs[tid];
-    sc[S_QM * kC + tid] = qmul[tid];
+    sc[S_EQ * kC + tid] = eg * qmul[tid];
+    g2s[tid] = Gs[tid] * kLog2e;
   }
 
-  // ---- k k^T: the three 32x32 tiles on or below the diagonal, waves 0..2
-  // (tile (0,1) lies above it: A is zero there)
+  // ---- k k^T and (q k^T)^T: the three 32x32 tiles on or below the diagonal,
+  // waves 0..2 (tile (0,1) lies above it: A and In are zero there).  The
+  // In^T tile has the k tokens j as rows: its accumulator order is the K
+  // order of the scan's In v_new product.
   const int ti = wave == 0 ? 0 : 1, tj = wave == 2 ? 1 : 0;
-  f32x16 gram = f32x16{};
+  f32x16 gram = f32x16{}, inT = f32x16{};
   if (wave < 3) {
     const int fr = lane & 31, fk = (lane >> 5) * 8;
 #pragma unroll
     for (int s = 0; s < K / 16; ++s) {
       const bf16x8 a = as_bf16x8(*(const u32x4*)(kb + (ti * 32 + fr) * LD + s * 16 + fk));
       const bf16x8 b = as_bf16x8(*(const u32x4*)(kb + (tj * 32 + fr) * LD + s * 16 + fk));
+      const bf16x8 bq = as_bf16x8(*(const u32x4*)(qb + (ti * 32 + fr) * LD + s * 16 + fk));
       gram = mfma32x32x16(a, b, gram);
+      inT = mfma32x32x16(b, bq, inT);
     }
   }
   __syncthreads();  // rows no longer needed: the region becomes A / T'
+  // In_ij = (q^_i . k^_j) qmul_i kmul_j e^{G_i - G_j} for j <= i, as hi/lo
+  // A fragments (it = ti, s = tj * 2 + half) straight from the accumulators
+  if (wave < 3) {
+    const int irow = ti * 32 + (lane & 31);
+    const float qmi = qmul[irow], gi = g2s[irow];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = tj * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
+      inT[e] = j <= irow ? (inT[e] * qmi * kmul[j]) * __builtin_amdgcn_exp2f(gi - g2s[j]) : 0.f;
+    }
+    bf16_t* inf = (bf16_t*)(rec + ChunkRec::in);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      bf16x8 ih, il;
+      acc_frags(inT, half, ih, il);
+      const int f = frag_index(ti, tj * 2 + half);
+      *(bf16x8*)(inf + ((f * 2 + 0) * 64 + lane) * 8) = ih;
+      *(bf16x8*)(inf + ((f * 2 + 1) * 64 + lane) * 8) = il;
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     // wave 3 clears tile (0,1)
     const int ri = wave == 3 ? 0 : ti, rj = wave == 3 ? 1 : tj;
     const int i = ri * 32 + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
     const int j = rj * 32 + (lane & 31);
+    // the decay e^{G_i - G_j} as 2^(G_i log2 e - G_j log2 e) on the hardware
+    // exp2, as for In (a few ulp from expf of the difference)
     Ar[i * kC + (j & 3) * 16 + (j >> 2)] =
-        wave < 3 && j < i ? -bt[i] * (gram[e] * kmul[i] * kmul[j]) * expf(Gs[i] - Gs[j]) : 0.f;
+        wave < 3 && j < i
+            ? -bt[i] * (gram[e] * kmul[i] * kmul[j]) * __builtin_amdgcn_exp2f(g2s[i] - g2s[j])
+            : 0.f;
   }
   __syncthreads();
 
@@ -291,21 +357,23 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep(
   }
   __syncthreads();
 
-  // ---- T' hi/lo in fragment order: 512 (it, s, lane) fragments, 2 per thread
+  // ---- T' hi/lo in fragment order: 384 (fragment, lane) pairs
   {
     bf16_t* tf = (bf16_t*)(rec + ChunkRec::tf);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int f = tid + u * kPrepThreads;
-      const int it = f >> 8, s = (f >> 6) & 3, L = f & 63;
+      const int fl_ = tid + u * kPrepThreads;
+      if (fl_ >= ChunkRec::frags * 64) break;
+      const int f = fl_ >> 6, L = fl_ & 63;
+      const int it = f < 2 ? 0 : 1, s = f < 2 ? f : f - 2;
       const int i = it * 32 + (L & 31), jb = s * 16 + (L >> 5) * 4;
       float x[8];
 #pragma unroll
       for (int t = 0; t < 8; ++t) x[t] = Tm[i][jb + (t / 4) * 8 + t % 4];
       bf16x8 fh, fl;
       split8(x, fh, fl);
-      *(bf16x8*)(tf + (((it * 4 + s) * 2 + 0) * 64 + L) * 8) = fh;
-      *(bf16x8*)(tf + (((it * 4 + s) * 2 + 1) * 64 + L) * 8) = fl;
+      *(bf16x8*)(tf + ((f * 2 + 0) * 64 + L) * 8) = fh;
+      *(bf16x8*)(tf + ((f * 2 + 1) * 64 + L) * 8) = fl;
     }
   }
 }
@@ -318,15 +386,6 @@ __device__ __forceinline__ bf16x8 perm_frag(const bf16_t* rowp, int base, int hi
   const u32x2 b = *(const u32x2*)(rowp + base + 8 + hi * 4);
   const u32x4 v = {a[0], a[1], b[0], b[1]};
   return as_bf16x8(v);
-}
-
-// B fragments (hi, lo) of an fp32 accumulator tile for K step s: the 8
-// accumulator entries (s%2)*8 .. +7 of 32-row tile s/2
-__device__ __forceinline__ void acc_frags(const f32x16& t, int half, bf16x8& hi, bf16x8& lo) {
-  float x[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = t[half * 8 + i];
-  split8(x, hi, lo);
 }
 
 typedef short tr_v4s_t __attribute__((ext_vector_type(4)));
@@ -505,7 +564,7 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
       // within the two-workgroups-per-CU budget
       __builtin_amdgcn_sched_barrier(0);
     }
-    // ---- Z_j = beta_j (v_j - e^{G_j} kmul_j (k S)_j)
+    // ---- Z_j = beta_j (v_j - e^{G_j} kmul_j (k S)_j) = beta_j v_j - ZK_j (k S)_j
     f32x16 Z[2];
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
@@ -513,7 +572,7 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
       for (int e = 0; e < 16; ++e) {
         const int j = jt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
         const float vj = bf2f(vb[j * LDV + vcol]);
-        Z[jt][e] = sc[S_BT][j] * (vj - sc[S_EG][j] * (sc[S_KM][j] * KSa[jt][e]));
+        Z[jt][e] = fmaf(-sc[S_ZK][j], KSa[jt][e], sc[S_BT][j] * vj);
       }
     }
     // ---- v_new = Z + T' Z (T' strictly lower: rows 0..31 see tokens 0..31)
@@ -526,8 +585,9 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
       f32x16 acc = Z[it];
 #pragma unroll
       for (int s = 0; s < 2 * (it + 1); ++s) {
-        const bf16x8 ah = *(const bf16x8*)(tf + (((it * 4 + s) * 2 + 0) * 64 + lane) * 8);
-        const bf16x8 al = *(const bf16x8*)(tf + (((it * 4 + s) * 2 + 1) * 64 + lane) * 8);
+        const int f = frag_index(it, s);
+        const bf16x8 ah = *(const bf16x8*)(tf + ((f * 2 + 0) * 64 + lane) * 8);
+        const bf16x8 al = *(const bf16x8*)(tf + ((f * 2 + 1) * 64 + lane) * 8);
         acc = mfma32x32x16(ah, zh[s], acc);
         acc = mfma32x32x16(ah, zl[s], acc);
         acc = mfma32x32x16(al, zh[s], acc);
@@ -540,45 +600,25 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     bf16x8 vh[4], vl[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc_frags(VN[s / 2], s % 2, vh[s], vl[s]);
-    // ---- o_i = e^{G_i} qmul_i (q S)_i + sum_{j<=i} In_ij v_new_j.  In^T tiles
-    // (tokens j as rows) come from k rows x q rows; their accumulator order
-    // is the K order of the In v_new product.
+    // ---- o_i = e^{G_i} qmul_i (q S)_i + sum_{j<=i} In_ij v_new_j, In from
+    // the prep's fragments
+    const bf16_t* inb = tf + ChunkRec::frag_elems;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       f32x16& o = QSa[it];
-      const int irow = it * 32 + col;  // this lane's query token in the In^T tiles
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int i = it * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
-        o[e] *= sc[S_EG][i] * sc[S_QM][i];
+        o[e] *= sc[S_EQ][i];
       }
 #pragma unroll
-      for (int jt = 0; jt <= it; ++jt) {
-        f32x16 inT = f32x16{};
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const bf16x8 a = as_bf16x8(*(const u32x4*)(kb + (jt * 32 + col) * LDK + s * 16 + hi * 8));
-          const bf16x8 b = as_bf16x8(*(const u32x4*)(qb + irow * LDK + s * 16 + hi * 8));
-          inT = mfma32x32x16(a, b, inT);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        const float qmi = sc[S_QM][irow], gi = sc[S_G2][irow];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int j = jt * 32 + (e / 4) * 8 + hi * 4 + (e % 4);
-          inT[e] = j <= irow ? (inT[e] * qmi * sc[S_KM][j]) *
-                                   __builtin_amdgcn_exp2f(gi - sc[S_G2][j])
-                             : 0.f;
-        }
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          bf16x8 ih, il;
-          acc_frags(inT, half, ih, il);
-          const int s = jt * 2 + half;
-          o = mfma32x32x16(ih, vh[s], o);
-          o = mfma32x32x16(ih, vl[s], o);
-          o = mfma32x32x16(il, vh[s], o);
-        }
+      for (int s = 0; s < 2 * (it + 1); ++s) {
+        const int f = frag_index(it, s);
+        const bf16x8 ih = *(const bf16x8*)(inb + ((f * 2 + 0) * 64 + lane) * 8);
+        const bf16x8 il = *(const bf16x8*)(inb + ((f * 2 + 1) * 64 + lane) * 8);
+        o = mfma32x32x16(ih, vh[s], o);
+        o = mfma32x32x16(ih, vl[s], o);
+        o = mfma32x32x16(il, vh[s], o);
       }
     }
     // ---- output: o goes through LDS (the v tile, which every wave has

@@ -100,14 +100,29 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// split 8 floats into bf16 hi/lo parts: x ~= hi + lo with |x-hi-lo| <= 2^-16 |x|
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+
+// two floats to a packed bf16 pair, each rounded to nearest even: one
+// v_cvt_pk_bf16_f32 for both (a scalar conversion spends one per element)
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_v){a, b}, bf16x2_v));
+}
+
+// split 8 floats into bf16 hi/lo parts: x ~= hi + lo with |x-hi-lo| <= 2^-16 |x|;
+// the same bits as rounding each element on its own, with a packed
+// conversion per pair and the pair's hi parts widened by shift / mask
 __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __bf16 h = (__bf16)x[i];
-    hi[i] = h;
-    lo[i] = (__bf16)(x[i] - (float)h);
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t hp = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    h[i] = hp;
+    l[i] = pack_bf16x2(x[2 * i] - __uint_as_float(hp << 16),
+                       x[2 * i + 1] - __uint_as_float(hp & 0xffff0000u));
   }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
 }
 
 // wave-level reductions (wave64)
