@@ -115,7 +115,16 @@ __device__ __forceinline__ float row_sumsq(const u32x4& r, bool hf) {
 // transformers l2norm in bf16: x * rsqrt(sum(x*x) + eps), each op rounded;
 // hf_l2_rs gives the row scale, hf_l2_apply the scaled slice
 __device__ __forceinline__ float hf_l2_rs(float ss) {
-  return round_bf(1.0f / sqrtf(round_bf(round_bf(ss) + 1e-6f)));
+  const float y = round_bf(round_bf(ss) + 1e-6f);
+  // torch's rsqrt here is 1 / sqrt(y), each step rounded in fp32, then
+  // rounded to bf16.  The hardware reciprocal square root lies within 2 ulp
+  // of that, so its bf16 rounding is the same unless it sits within a few
+  // ulp of a rounding midpoint (low 16 bits near 0x8000: about 1 row in
+  // 4,000), where the two-step form is evaluated instead
+  const float r = __builtin_amdgcn_rsqf(y);
+  const int mid = (int)(__float_as_uint(r) & 0xffffu) - 0x8000;
+  if (mid >= -8 && mid <= 8) return round_bf(1.0f / sqrtf(y));
+  return round_bf(r);
 }
 __device__ __forceinline__ void hf_l2_apply(u32x4& r, float rs) {
 #pragma unroll

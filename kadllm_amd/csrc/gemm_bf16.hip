@@ -1138,8 +1138,10 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     // kernel for plain products of at least four whole tiles per CU, a third
     // LDS slot for the streamed operand for K >= 3072 (residual outputs
     // from K = 2048: the prefill mixer output projection 2% faster), else
-    // persistent except for the SwiGLU epilogue, where both forms measured
-    // the same; then the
+    // persistent, except for the SwiGLU epilogue in launches of fewer than
+    // eight rounds, where one workgroup per tile with a split last round is
+    // faster (decode SwiGLU 111.9 against 114.8 us; at M = 32,768 the
+    // persistent form is 2% faster, interleaved medians); then the
     // 128x128 form, two workgroups per CU, when its tiles fill two rounds
     // (N = 1,024 at M = 8,192: 5-7% faster than 8-wave 256x128 tiles, and
     // 14% slower than 256x256 where those fill the chip); 64x32 for outputs
@@ -1163,7 +1165,8 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     else if (tiles256 >= 256 && (K >= 3072 || (EPI == KAD_EPI_RESIDUAL && K >= 2048)))
       cfg = CFG_256x256_S3;
     else if (tiles256 >= 256)
-      cfg = EPI == KAD_EPI_SWIGLU ? CFG_256x256_X16 : CFG_256x256_X16P;
+      cfg = EPI == KAD_EPI_SWIGLU && tiles256 < 8 * device_cu_count() ? CFG_256x256_X16
+                                                                        : CFG_256x256_X16P;
     else if (vec && tiles128 >= 512)
       cfg = CFG_128x128_X16;
     else
