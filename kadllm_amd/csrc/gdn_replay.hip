@@ -293,18 +293,12 @@ void gdn_replay_kernel(
     // full 128-element dot products: sum the 4 lanes (quad 0..3) of each beam
 #pragma unroll
     for (int t = 0; t < kTMax; ++t) {
-      qq[t] += __shfl_xor(qq[t], 16, 64);
-      qq[t] += __shfl_xor(qq[t], 32, 64);
-      kk[t] += __shfl_xor(kk[t], 16, 64);
-      kk[t] += __shfl_xor(kk[t], 32, 64);
+      qq[t] = add_xor32(add_xor16(qq[t]));
+      kk[t] = add_xor32(add_xor16(kk[t]));
 #pragma unroll
       for (int j = 0; j <= t; ++j) {
-        kqx[j][t] += __shfl_xor(kqx[j][t], 16, 64);
-        kqx[j][t] += __shfl_xor(kqx[j][t], 32, 64);
-        if (j < t) {
-          kkx[j][t] += __shfl_xor(kkx[j][t], 16, 64);
-          kkx[j][t] += __shfl_xor(kkx[j][t], 32, 64);
-        }
+        kqx[j][t] = add_xor32(add_xor16(kqx[j][t]));
+        if (j < t) kkx[j][t] = add_xor32(add_xor16(kkx[j][t]));
       }
     }
 
@@ -352,6 +346,251 @@ void gdn_replay_kernel(
   }
 }
 
+// The same replay for the decode shapes (bf16, K = V = 128, up to 4 suffix
+// tokens, 16-beam groups that are all full), with each group's q, k and v
+// rows staged in LDS instead of loaded by every wave: one set of DMA loads
+// (global_load_lds, 16 bytes per lane) per workgroup fills a stage, issued
+// NS - 1 groups ahead of its use, so the groups' load latency overlaps the
+// products of the groups before (an instrumented copy of the register-load
+// kernel spent about 5,000 of 7,000 cycles per one-token group waiting for
+// its loads).  Rows are 256 bytes with their 16-byte chunks XOR-swizzled by
+// the beam index, so a fragment read of 16 beams touches 16 distinct bank
+// groups.  The arithmetic is the register kernel's, operation for operation,
+// so the outputs are bit-identical.
+typedef __attribute__((address_space(1))) void replay_global_t;
+typedef __attribute__((address_space(3))) void replay_lds_t;
+
+template <int T, int NS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 1 ? 3 : (T == 4 ? 1 : 2), 8)))
+void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                           const bf16_t* __restrict__ v, int64_t ld_qk, int64_t ld_v,
+                           const void* __restrict__ gdecay, int gate_dtype,
+                           const void* __restrict__ beta, int beta_dtype, int64_t ld_gate,
+                           const void* __restrict__ state, int state_dtype,
+                           bf16_t* __restrict__ out, int64_t ld_out, int W, int H, int HV,
+                           float scale, int beams_per_block, int nbb) {
+  constexpr int KD = 128, VD = 128;
+  constexpr int KSTEPS = KD / 32;
+  constexpr int VROWS = VD / 4;
+  constexpr int MT = VROWS / 16;
+  constexpr int ROWS = 16 * T;               // (beam, token) rows of a group
+  constexpr int BLK = ROWS * 256;            // bytes of one q, k or v block
+  constexpr int STAGE = 3 * BLK + 512;      // + the gates: 64 fp32 decays, 64 beta words
+  __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int bb = lid % nbb;
+  const int rh = lid / nbb;
+  const int hv = rh % HV;
+  const int b = rh / HV;
+  const int h = hv / (HV / H);
+  const int v0 = wave * VROWS;
+  const int col = lane & 15;   // beam within the 16-beam group (MFMA N index)
+  const int quad = lane >> 4;  // 0..3
+
+  const int n_begin = bb * beams_per_block;
+  const int n_end = min(W, n_begin + beams_per_block);
+  const int ngroups = (n_end - n_begin) / 16;
+
+  // DMA of group gi into stage s: wave w moves 1 KB pieces w*T .. w*T+T-1 of
+  // each block; lane L of piece I fills row 4I + L/16, swizzled chunk L%16
+  auto dma_group = [&](int gi, int s) {
+    const int64_t row0 = ((int64_t)b * W + n_begin + gi * 16) * T;
+    uint8_t* sb = stage_buf + s * STAGE;
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int j = 0; j < T; ++j) {
+      const int I = w * T + j;
+      const int r = 4 * I + (lane >> 4);
+      const int c = (lane & 15) ^ ((r / T) & 15);
+      const int64_t qrow = (row0 + r) * ld_qk + (int64_t)h * KD + c * 8;
+      const int64_t vrow = (row0 + r) * ld_v + (int64_t)hv * VD + c * 8;
+      __builtin_amdgcn_global_load_lds((replay_global_t*)(q + qrow),
+                                       (replay_lds_t*)(sb + I * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((replay_global_t*)(k + qrow),
+                                       (replay_lds_t*)(sb + BLK + I * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((replay_global_t*)(v + vrow),
+                                       (replay_lds_t*)(sb + 2 * BLK + I * 1024), 16, 0, 0);
+    }
+    // the group's gates, lane r = (beam, token) row: wave 0 the fp32 log
+    // decays, wave 1 the 4-byte words holding the bf16 betas (rows have an
+    // even stride, so a beta's half of its word is hv % 2)
+    if (w < 2 && lane < ROWS) {
+      const int64_t gix = (row0 + lane) * ld_gate + hv;
+      const void* src = w == 0 ? (const void*)((const float*)gdecay + gix)
+                               : (const void*)((const uint32_t*)beta + (gix >> 1));
+      __builtin_amdgcn_global_load_lds((replay_global_t*)src,
+                                       (replay_lds_t*)(sb + 3 * BLK + w * 256), 4, 0, 0);
+    }
+  };
+  // the first NS - 1 groups' loads go out before the state's, so they land
+  // meanwhile
+#pragma unroll
+  for (int d = 0; d < NS - 1; ++d)
+    if (d < ngroups) dma_group(d, d);
+
+  // ---- S0^T fragments, hi/lo bf16, held in registers for the whole kernel
+  bf16x8 a_hi[MT][KSTEPS], a_lo[MT][KSTEPS];
+  {
+    const int64_t sbase = ((int64_t)b * HV + hv) * KD * VD;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int vrow = v0 + mt * 16 + col;
+        const int kc = ks * 32 + quad * 8;
+        float x[8];
+        if (state_dtype == KAD_DTYPE_F32) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            x[i] = ((const float*)state)[sbase + (int64_t)(kc + i) * VD + vrow];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            x[i] = load_as_float(state, sbase + (int64_t)(kc + i) * VD + vrow, state_dtype);
+        }
+        split8(x, a_hi[mt][ks], a_lo[mt][ks]);
+      }
+    }
+  }
+
+  // One group.  At its start, group gi's loads (all DMA into LDS, issued
+  // NS - 1 groups earlier) must have landed.  The only loads issued after
+  // them are the groups' in between: with NS = 3, group gi + 1's (at least 3T
+  // per lane), which may stay outstanding; with NS = 2, none.  Loads complete
+  // in issue order, so at most 3T outstanding operations leaves every older
+  // load complete, whatever the output stores in between have done.
+  auto group = [&](int gi) {
+    if (NS == 3 && gi + 1 < ngroups)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * T) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // every wave's part of the stage is in, and every wave is done with the
+    // stage the next DMA refills; a plain s_barrier, which (unlike
+    // __syncthreads) leaves the prefetches in flight
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int s = gi % NS;
+    if (gi + NS - 1 < ngroups) dma_group(gi + NS - 1, (gi + NS - 1) % NS);
+
+    const uint8_t* sq = stage_buf + s * STAGE;
+    const uint8_t* sk = sq + BLK;
+    const uint8_t* sv = sq + 2 * BLK;
+    const int g0 = n_begin + gi * 16;
+    const int64_t n = (int64_t)b * W + g0 + col;
+
+    f32x4 acc_q[T][MT], acc_k[T][MT];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc_q[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc_k[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    float qq[T], kk[T], kkx[T][T], kqx[T][T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      qq[t] = 0.f;
+      kk[t] = 0.f;
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        kkx[j][t] = 0.f;
+        kqx[j][t] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      bf16x8 fq[T], fk[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int r = col * T + t;
+        const int off = r * 256 + (((ks * 4 + quad) ^ (col & 15)) * 16);
+        fq[t] = *(const bf16x8*)(sq + off);
+        fk[t] = *(const bf16x8*)(sk + off);
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        qq[t] = dot8_bf16(fq[t], fq[t], qq[t]);
+        kk[t] = dot8_bf16(fk[t], fk[t], kk[t]);
+#pragma unroll
+        for (int j = 0; j <= t; ++j) {
+          kqx[j][t] = dot8_bf16(fk[j], fq[t], kqx[j][t]);
+          if (j < t) kkx[j][t] = dot8_bf16(fk[j], fk[t], kkx[j][t]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc_k[t][mt] = mfma16x16x32(a_hi[mt][ks], fk[t], acc_k[t][mt]);
+          acc_k[t][mt] = mfma16x16x32(a_lo[mt][ks], fk[t], acc_k[t][mt]);
+          acc_q[t][mt] = mfma16x16x32(a_hi[mt][ks], fq[t], acc_q[t][mt]);
+          acc_q[t][mt] = mfma16x16x32(a_lo[mt][ks], fq[t], acc_q[t][mt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      qq[t] = add_xor32(add_xor16(qq[t]));
+      kk[t] = add_xor32(add_xor16(kk[t]));
+#pragma unroll
+      for (int j = 0; j <= t; ++j) {
+        kqx[j][t] = add_xor32(add_xor16(kqx[j][t]));
+        if (j < t) kkx[j][t] = add_xor32(add_xor16(kkx[j][t]));
+      }
+    }
+
+    float rk[T], rq[T], et[T], btf[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      rk[t] = 1.0f / sqrtf(kk[t] + 1e-6f);
+      rq[t] = scale / sqrtf(qq[t] + 1e-6f);
+      const uint8_t* sg = stage_buf + s * STAGE + 3 * BLK;
+      et[t] = expf(((const float*)sg)[col * T + t]);
+      const uint32_t bw = ((const uint32_t*)(sg + 256))[col * T + t];
+      btf[t] = __uint_as_float((hv & 1) ? (bw & 0xffff0000u) : (bw << 16));
+    }
+
+    float u[T][MT][4];
+    float c[T];
+    float gam = 1.f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      gam *= et[t];
+#pragma unroll
+      for (int j = 0; j < t; ++j) c[j] *= et[t];
+      const int r = col * T + t;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int e = v0 + mt * 16 + quad * 4;
+        const u32x2 raw =
+            *(const u32x2*)(sv + r * 256 + (((e >> 3) ^ (col & 15)) * 16) + (e & 7) * 2);
+        float vt[4], ov[4];
+        vt[0] = __uint_as_float(raw[0] << 16);
+        vt[1] = __uint_as_float(raw[0] & 0xffff0000u);
+        vt[2] = __uint_as_float(raw[1] << 16);
+        vt[3] = __uint_as_float(raw[1] & 0xffff0000u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float recall = gam * (acc_k[t][mt][i] * rk[t]);
+#pragma unroll
+          for (int j = 0; j < t; ++j) recall += c[j] * (kkx[j][t] * rk[j] * rk[t]) * u[j][mt][i];
+          const float ut = btf[t] * (vt[i] - recall);
+          u[t][mt][i] = ut;
+          float o = gam * (acc_q[t][mt][i] * rq[t]);
+#pragma unroll
+          for (int j = 0; j < t; ++j) o += c[j] * (kqx[j][t] * rk[j] * rq[t]) * u[j][mt][i];
+          o += (kqx[t][t] * rk[t] * rq[t]) * ut;
+          ov[i] = o;
+        }
+        store4<bf16_t>(out + (n * T + t) * ld_out + (int64_t)hv * VD + e, ov);
+      }
+      c[t] = 1.f;
+    }
+  };
+  for (int gi = 0; gi < ngroups; ++gi) group(gi);
+}
+
 template <int KD, int VD, typename TIN>
 int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
                   const void* g, int gdt, const void* beta, int bdt, int64_t ld_gate,
@@ -359,11 +598,37 @@ int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, in
                   int T, int H, int HV, float scale, hipStream_t stream) {
   int bpb = W >= 256 ? 128 : ((W + 15) / 16) * 16;
   if (bpb > 128) bpb = 128;
+  // the staged kernel takes a request's beams in one workgroup up to 256, so
+  // the state prologue is paid once per (request, head): two-token suffixes
+  // at 256 beams 7% faster than two workgroups of 128
+  if (KD == 128 && VD == 128 && sizeof(TIN) == 2 && T <= 4 && W % 16 == 0 && W <= 256) bpb = W;
   const int nbb = (int)kad_cdiv(W, bpb);
   const int64_t nblocks = (int64_t)B * HV * nbb;
   if (nblocks > 0x7fffffff) {
     kad_set_error("gdn replay grid too large");
     return KAD_ERR_UNSUPPORTED;
+  }
+  // the LDS-staged kernel for the decode shapes (all groups full, 16-byte rows)
+  if constexpr (KD == 128 && VD == 128 && sizeof(TIN) == 2) {
+    const bool staged = T <= 4 && W % 16 == 0 && bpb % 16 == 0 && gdt == KAD_DTYPE_F32 &&
+                        bdt == KAD_DTYPE_BF16 && ld_gate % 2 == 0 &&
+                        ((uintptr_t)beta % 4) == 0 && ((uintptr_t)g % 4) == 0 && ld_qk % 8 == 0 &&
+                        ld_v % 8 == 0 && ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 == 0;
+    if (staged) {
+#define KAD_REPLAY_LDS(TT, NS)                                                                \
+  if (T == TT) {                                                                              \
+    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, NS>), dim3((unsigned)nblocks), dim3(256), 0, \
+                       stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ld_qk,   \
+                       ld_v, g, gdt, beta, bdt, ld_gate, state, sdt, (bf16_t*)out, ld_out, W, \
+                       H, HV, scale, bpb, nbb);                                               \
+    return kad_launch_status("gdn_replay_lds_kernel");                                        \
+  }
+      KAD_REPLAY_LDS(1, 3)
+      KAD_REPLAY_LDS(2, 3)
+      KAD_REPLAY_LDS(3, 2)
+      KAD_REPLAY_LDS(4, 2)
+#undef KAD_REPLAY_LDS
+    }
   }
   // one instantiation per suffix length: the per-token arrays then hold only
   // T entries, which keeps the register count (and so the occupancy) down

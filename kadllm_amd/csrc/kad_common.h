@@ -125,6 +125,26 @@ __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
   lo = __builtin_bit_cast(bf16x8, l);
 }
 
+// x combined with x of lane ^ 16 or lane ^ 32 by the gfx950 row / half-wave
+// swaps (v_permlane16_swap, v_permlane32_swap: VALU, no LDS round trip).  The
+// swap of x with itself leaves x and its partner in the two results, so
+// their sum (or max) equals x + shfl_xor(x, 16 or 32) bit for bit.
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // wave-level reductions (wave64)
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

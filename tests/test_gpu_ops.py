@@ -66,6 +66,25 @@ def test_gdn_replay_bf16_matches_oracle(device, case):
     assert_close_rel(out.cpu(), expected, rtol=1e-2, atol_frac=2e-3, name=f"gdn {case}")
 
 
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+@pytest.mark.parametrize("W", [16, 48, 256, 512])
+def test_gdn_replay_lds_staged_equals_register_kernel(device, T, W):
+    """The decode shapes (bf16, K = V = 128, fp32 decay, bf16 beta, beams in
+    whole groups of 16) run the LDS-staged replay; the same values with an
+    fp32 beta take the register-load kernel, whose arithmetic the staged one
+    repeats, so the two agree bit for bit (W = 512: four workgroups of 128
+    beams per request; 48: three groups, so the 3-stage ring wraps)."""
+    B, H, HV, K, V = 2, 4, 8, 128, 128
+    q, k, v, g, beta, S = gdn_inputs(B, W, T, H, HV, K, V, seed=T * 1000 + W)
+    qd, kd, vd, gd, bd, Sd = _to(device, q, k, v, g, beta, S)
+    staged = ops.gated_delta(qd, kd, vd, gd, bd, Sd, beam_width=W)
+    plain = ops.gated_delta(qd, kd, vd, gd, bd.float(), Sd, beam_width=W)
+    torch.cuda.synchronize()
+    assert torch.equal(staged, plain)
+    expected = ops_ref.gated_delta(q, k, v, g, beta, S, beam_width=W)
+    assert_close_rel(staged.cpu(), expected, rtol=1e-2, atol_frac=2e-3, name=f"staged T={T} W={W}")
+
+
 @pytest.mark.parametrize("case", [(2, 7, 3, 2, 4, 64, 64), (1, 16, 4, 4, 4, 128, 128),
                                   (1, 9, 8, 2, 2, 128, 128)])
 def test_gdn_replay_fp32_matches_oracle(device, case):
