@@ -112,7 +112,9 @@ int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
  * a third LDS slot for the operand that streams from beyond the L2; 22 =
  * 256x256 persistent with its 8 waves in two groups that alternate between
  * MFMA phases and load phases across workgroup barriers, M and N multiples
- * of 256, 16-byte store epilogue as 16).  Every
+ * of 256, 16-byte store epilogue as 16; 24 = 256x256 persistent with 4
+ * waves of 128x128, M and N multiples of 256, epilogues from the
+ * accumulators, aligned outputs as 16).  Every
  * configuration accumulates K in the same order, so all give bit-identical
  * results (the automatic choice may also split the columns of one call
  * between two of them); other numbers are rejected (KAD_ERR_UNSUPPORTED). */

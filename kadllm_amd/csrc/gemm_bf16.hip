@@ -1081,6 +1081,400 @@ int launch_ppp(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, 
   return kad_launch_status("gemm_ppp_kernel");
 }
 
+// issue order of a first step that stores the previous tile, NB rows of 8
+// blocks: per MFMA the staging of its block (4 accumulator reads, 2 packed
+// conversions, one 8-byte LDS write), after each row its 4 staged 16-byte
+// reads and stores; the first NR MFMAs each followed by one fragment read,
+// the NV global loads spread over the others
+template <int NB, int NR, int NV>
+__device__ __forceinline__ void interleave_store_step() {
+  constexpr int NM = NB * 8;
+#pragma unroll
+  for (int t = 0; t < NM; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (t < NR) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    } else if constexpr (NV > 0) {
+      constexpr int kSlots = NM > NR ? NM - NR : 1;
+      const int c = ((t - NR + 1) * NV) / kSlots - ((t - NR) * NV) / kSlots;
+#pragma unroll
+      for (int q = 0; q < c; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    if (t % 8 == 7) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x040, 4, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// 256 x 256 tiles with 4 waves, one per SIMD, each owning a 128 x 128
+// sub-tile: 256 fp32 accumulators per lane, which the compiler keeps in
+// AGPRs (a wave alone on its SIMD may hold 512 registers).  Per 64-deep
+// slice a wave reads 32 KB of fragments from LDS, so the CU reads 128 KB per
+// slice where the 8-wave tiles read 192 KB, and no second wave competes for
+// the SIMD's issue slots.  Persistent (one workgroup per CU walks the
+// grouped, XCD-aware tile order); the K slices of successive tiles form one
+// load stream through two 64-deep LDS stages, as in gemm_x16p_kernel.  Two
+// 32-deep steps per slice: the MFMAs of step 0 run with the fragment reads of
+// step 1, those of step 1 with the next slice's step-0 reads and this wave's
+// loads of the slice after next; one barrier per slice, between the steps.
+//
+// Epilogue: straight from the accumulators to global memory, each lane's 4
+// consecutive columns of a 16 x 16 block as one 8-byte buffer store (the L2
+// merges a row's pieces before they reach HBM).  For plain stores it runs
+// inside the first MFMA step of the next tile: each block is converted and
+// stored just before the step's MFMA that restarts it from zero, so the
+// matrix unit never waits for an epilogue.  The residual and SwiGLU
+// epilogues run after the tile's last slice, while the loads of the next
+// tile's first two slices land.  Tiles must be whole (M, N multiples of 256).
+// Every K slice accumulates in the order of the other configurations, so
+// results are bit-identical to them.
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_w4e_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
+    int group, int ntiles) {
+  using TX = TileX16<256, 256, 2, 2>;
+  constexpr int BM = TX::BM, BN = TX::BN;
+  constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
+  constexpr int kStage = TX::Stage;
+  constexpr int kLoads = (BM + BN) / 8 / NW;   // 1 KB row-group loads per wave per slice
+  constexpr int NM = NI * NJ, NR = NI + NJ;
+  // plain-store and residual epilogues stage a 16-row block of the wave's
+  // sub-tile through LDS (rows of 128 columns + 8 padding, so that both the
+  // 8-byte writes of the accumulator layout and the 16-byte row reads are
+  // free of bank conflicts): every store then writes 4 whole 256-byte rows
+  constexpr int kStgLd = NJ * 16 + 8;
+  constexpr int kStg = EPI == KAD_EPI_SWIGLU ? 0 : 16 * kStgLd;
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[2 * kStage + NW * kStg];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int swave = __builtin_amdgcn_readfirstlane(wave);
+  const int wm = swave / WN, wn = swave % WN;
+  const int KT = K / kBK;
+  const int my_tiles = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  if (my_tiles <= 0) return;
+  const int total = my_tiles * KT;
+  auto origin = [&](int r, int& m0, int& n0) {
+    const int v = (int)blockIdx.x + r * (int)gridDim.x;
+    tile_origin_of(xcd_logical_id(v, ntiles), M, N, BM, BN, n_major, group, m0, n0);
+  };
+
+  // loads: wave w takes A and W row groups w + 4i (8 rows each), whose
+  // swizzle phase (the group's parity) is that of w
+  const int l_row = lane >> 3;
+  const int l_kc = ((lane & 7) ^ ((swave & 1) * 4 + (lane >> 4))) * 8;
+  const uint32_t a_lane = (uint32_t)(l_row * (int)lda + l_kc) * 2u;
+  const uint32_t b_lane = (uint32_t)(l_row * (int)ldw + l_kc) * 2u;
+  const uint32_t a_rg = (uint32_t)(8 * lda * 2), b_rg = (uint32_t)(8 * ldw * 2);
+  int ld_g = 0, ld_k = 0, ld_r = 0;
+  __amdgpu_buffer_rsrc_t ld_a, ld_b;
+  auto set_tile = [&](int r) {
+    int m0, n0;
+    origin(r, m0, n0);
+    ld_a = buffer_rsrc(A + (int64_t)m0 * lda);
+    ld_b = buffer_rsrc(Wt + (int64_t)n0 * ldw);
+  };
+  set_tile(0);
+  // a slice's loads in two halves: its A rows, then its W rows
+  auto issue_a = [&]() {
+    const uint32_t k0 = (uint32_t)ld_k * kBK * 2;
+    bf16_t* base = smem + (ld_g & 1) * kStage;
+#pragma unroll
+    for (int i = 0; i < BM / 8 / NW; ++i) {
+      const int rg = swave + NW * i;
+      dma16_buf(ld_a, a_lane, (uint32_t)rg * a_rg + k0, base + rg * 8 * kBK);
+    }
+  };
+  auto issue_b = [&]() {
+    const uint32_t k0 = (uint32_t)ld_k * kBK * 2;
+    bf16_t* base = smem + (ld_g & 1) * kStage;
+#pragma unroll
+    for (int i = 0; i < BN / 8 / NW; ++i) {
+      const int rg = swave + NW * i;
+      dma16_buf(ld_b, b_lane, (uint32_t)rg * b_rg + k0, base + BM * kBK + rg * 8 * kBK);
+    }
+  };
+  constexpr int kHalf = BM / 8 / NW;   // loads per half slice per wave
+  static_assert(BN / 8 / NW == kHalf, "both halves issue the same number of loads");
+  // the stage alternates with every issue; the slice stays at the stream's
+  // last one once reached (the loads then re-fetch it: uniform wait counts)
+  auto advance = [&]() {
+    ++ld_g;
+    if (ld_r * KT + ld_k + 1 < total) {
+      if (++ld_k == KT) {
+        ld_k = 0;
+        set_tile(++ld_r);
+      }
+    }
+  };
+
+  const int f_row = lane & 15, f_sw = (lane & 15) >> 1, f_q = lane >> 4;
+  const int fa_row = (wm * NI * 16 + f_row) * kBK;
+  const int fw_row = BM * kBK + (wn * NJ * 16 + f_row) * kBK;
+  bf16x8 fa[2][NI], fw[2][NJ];
+  auto load_frags = [&](int g, int step, int buf) {
+    const bf16_t* base = smem + (g & 1) * kStage + (((step * 4 + f_q) ^ f_sw) * 8);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      fw[buf][j] = as_bf16x8(*(const u32x4*)(base + fw_row + j * 16 * kBK));
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      fa[buf][i] = as_bf16x8(*(const u32x4*)(base + fa_row + i * 16 * kBK));
+  };
+  f32x4 acc[NI][NJ];
+  auto mfma_rows = [&](int buf, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x32(fw[buf][j], fa[buf][i], acc[i][j]);
+  };
+  auto mfma_first_rows = [&](int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x32(fw[0][j], fa[0][i], f32x4{});
+  };
+
+  // output addressing: a buffer resource at the wave's sub-tile origin per
+  // tile.  The epilogue works on pairs of 16 x 16 blocks (32 columns): two
+  // lane-row swaps (permlane32, permlane16) turn each lane's 4 + 4 columns
+  // into 8 consecutive ones, so lane l stores 16 bytes at row l % 16, columns
+  // 8 (l / 16) .. + 7 of the pair, and each row receives 64 contiguous bytes
+  // per store instruction (32 with the accumulator layout as it is).
+  const uint32_t c_lane = ((uint32_t)(lane & 15) * (uint32_t)ldc + (uint32_t)(lane >> 4) * 8u) * 2u;
+  const uint32_t c_row16 = (uint32_t)(16 * ldc * 2);
+  auto out_rsrc = [&](int r) {
+    int m0, n0;
+    origin(r, m0, n0);
+    const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 16) / 2 : n0 + wn * NJ * 16;
+    return buffer_rsrc(C + (int64_t)(m0 + wm * NI * 16) * ldc + col0);
+  };
+  // x: a lane's 4 packed columns of the left block (2 words), y: of the
+  // right one; returns the lane's 8 consecutive columns of the pair
+  auto pair_swap = [&](uint32_t x0, uint32_t x1, uint32_t y0, uint32_t y1) {
+    const auto a = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], a[1], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(b[0], b[1], false, false);
+    return u32x4{c[0], d[0], c[1], d[1]};
+  };
+  // staged stores: block (i, j) goes into the wave's LDS block at row
+  // lane % 16, columns j * 16 + 4 (lane / 16); lane l then reads 16 bytes of
+  // row l / 16 + 4k, columns 8 (l % 16) .. + 7, and stores them
+  bf16_t* stg = smem + 2 * kStage + swave * kStg;
+  const int stg_w = (lane & 15) * kStgLd + (lane >> 4) * 4;
+  const int stg_r = (lane >> 4) * kStgLd + (lane & 15) * 8;
+  const uint32_t s_lane = ((uint32_t)(lane >> 4) * (uint32_t)ldc + (uint32_t)(lane & 15) * 8u) * 2u;
+  const uint32_t c_row4 = (uint32_t)(4 * ldc * 2);
+  auto stage_block = [&](int i, int j) {
+    const f32x4& x = acc[i][j];
+    *(u32x2*)(stg + stg_w + j * 16) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+  };
+  auto store_staged = [&](__amdgpu_buffer_rsrc_t rc, int i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 v = *(const u32x4*)(stg + stg_r + q * 4 * kStgLd);
+      __builtin_amdgcn_raw_buffer_store_b128(v, rc, s_lane, (uint32_t)i * c_row16 + q * c_row4, 0);
+    }
+  };
+  // plain-store epilogue of tile r - 1 fused into tile r's first step (a
+  // wave's LDS accesses complete in order, so block i + 1's writes never
+  // overtake block i's reads)
+  auto mfma_first_store = [&](__amdgpu_buffer_rsrc_t rc, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        stage_block(i, j);
+        acc[i][j] = mfma16x16x32(fw[0][j], fa[0][i], f32x4{});
+      }
+      store_staged(rc, i);
+    }
+  };
+  auto epilogue = [&](int r) {
+    const __amdgpu_buffer_rsrc_t rc = out_rsrc(r);
+    if constexpr (EPI == KAD_EPI_STORE) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) stage_block(i, j);
+        store_staged(rc, i);
+      }
+    } else if constexpr (EPI == KAD_EPI_SWIGLU) {
+      // blocks 4g, 4g + 1 gate and 4g + 2, 4g + 3 up of each 64-column
+      // group: output blocks 2g, 2g + 1 form the pair
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int g = 0; g < NJ / 4; ++g) {
+          uint32_t w[4];
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              uint32_t two = 0;
+#pragma unroll
+              for (int q = 0; q < 2; ++q) {
+                const float gv = round_bf(acc[i][4 * g + b][h * 2 + q]);
+                const float uv = round_bf(acc[i][4 * g + b + 2][h * 2 + q]);
+                two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
+              }
+              w[b * 2 + h] = two;
+            }
+          const u32x4 v = pair_swap(w[0], w[1], w[2], w[3]);
+          __builtin_amdgcn_raw_buffer_store_b128(v, rc, c_lane, (uint32_t)i * c_row16 + g * 64, 0);
+        }
+    } else {
+      int m0, n0;
+      origin(r, m0, n0);
+      const __amdgpu_buffer_rsrc_t rr =
+          buffer_rsrc(R + (int64_t)(m0 + wm * NI * 16) * ldr + n0 + wn * NJ * 16);
+      const uint32_t r_lane = ((uint32_t)(lane >> 4) * (uint32_t)ldr + (uint32_t)(lane & 15) * 8u) * 2u;
+      const uint32_t r_row4 = (uint32_t)(4 * ldr * 2), r_row16 = (uint32_t)(16 * ldr * 2);
+      // C = bf16(R + bf16(acc)): the residual rows of half the sub-tile in
+      // flight (16-byte pieces of whole rows, as the staged stores)
+#pragma unroll
+      for (int ih = 0; ih < NI; ih += NI / 2) {
+        u32x4 rv[NI / 2][4];
+#pragma unroll
+        for (int i = 0; i < NI / 2; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            rv[i][q] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           rr, r_lane, (uint32_t)(ih + i) * r_row16 + q * r_row4, 0));
+#pragma unroll
+        for (int i = 0; i < NI / 2; ++i) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) stage_block(ih + i, j);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            u32x4 v = *(const u32x4*)(stg + stg_r + q * 4 * kStgLd);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+              const float lo = __uint_as_float(rv[i][q][h] << 16) + __uint_as_float(v[h] << 16);
+              const float hi = __uint_as_float(rv[i][q][h] & 0xffff0000u) +
+                               __uint_as_float(v[h] & 0xffff0000u);
+              v[h] = pack_bf16x2(lo, hi);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(v, rc, s_lane,
+                                                   (uint32_t)(ih + i) * c_row16 + q * c_row4, 0);
+          }
+        }
+      }
+    }
+  };
+
+  // Slice g, with two barriers: step 0's first two rows of MFMAs carry the
+  // reads of step 1's fragments; once every wave's reads are done (barrier
+  // 1) stage g % 2 is free, and the A rows of slice g + 2 go into it during
+  // the rest of step 0; barrier 2 (after this wave's loads of slice g + 1
+  // landed) makes slice g + 1 visible, and step 1 carries the reads of its
+  // step-0 fragments and the W rows of slice g + 2.  So each slice's loads
+  // issue over one and three quarter steps instead of one.
+  constexpr int kRowsA = 2;   // MFMA rows before barrier 1
+  auto mid_barrier1 = [&]() {
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(63));   // own fragment reads done
+    ring_barrier();
+  };
+  auto mid_barrier2 = [&]() {
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kHalf));   // own slice g + 1 landed
+    ring_barrier();
+  };
+  auto step1 = [&](int g) {
+    load_frags(g + 1, 0, 0);
+    issue_b();
+    mfma_rows(1, 0, NI);
+    interleave_x16<NM, NR, kHalf>();
+    advance();
+  };
+
+  issue_a();
+  issue_b();
+  advance();
+  issue_a();
+  issue_b();
+  advance();
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * kHalf));   // own rows of slice 0 landed
+  ring_barrier();
+  load_frags(0, 0, 0);
+  // the first tile's fused epilogue stores go to a resource of no records
+  // (buffer stores past num_records are dropped), so every tile runs the
+  // same branch-free code and the accumulators keep their registers
+  __amdgpu_buffer_rsrc_t rc_prev = __builtin_amdgcn_make_buffer_rsrc(C, 0, 0, 0x00020000);
+  // the loads of slice 2 (A half) are issued in slice 0's step 0: the stream
+  // runs one half slice ahead of the slice count below
+  for (int r = 0; r < my_tiles; ++r) {
+    __builtin_amdgcn_sched_barrier(0);
+    // slice 0: step 0 restarts the accumulators (storing the previous tile
+    // for plain stores)
+    const int g0 = r * KT;
+    load_frags(g0, 1, 1);
+    if constexpr (EPI == KAD_EPI_STORE) {
+      mfma_first_store(rc_prev, 0, kRowsA);
+      interleave_store_step<kRowsA, NR, 0>();
+      mid_barrier1();
+      issue_a();
+      mfma_first_store(rc_prev, kRowsA, NI);
+      interleave_store_step<NI - kRowsA, 0, kHalf>();
+      rc_prev = out_rsrc(r);
+    } else {
+      mfma_first_rows(0, kRowsA);
+      interleave_x16<kRowsA * NJ, NR, 0>();
+      mid_barrier1();
+      issue_a();
+      mfma_first_rows(kRowsA, NI);
+      interleave_x16<(NI - kRowsA) * NJ, 0, kHalf>();
+    }
+    mid_barrier2();
+    step1(g0);
+    for (int kt = 1; kt < KT; ++kt) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int g = g0 + kt;
+      load_frags(g, 1, 1);
+      mfma_rows(0, 0, kRowsA);
+      interleave_x16<kRowsA * NJ, NR, 0>();
+      mid_barrier1();
+      issue_a();
+      mfma_rows(0, kRowsA, NI);
+      interleave_x16<(NI - kRowsA) * NJ, 0, kHalf>();
+      mid_barrier2();
+      step1(g);
+    }
+    if constexpr (EPI != KAD_EPI_STORE) epilogue(r);
+  }
+  if constexpr (EPI == KAD_EPI_STORE) epilogue(my_tiles - 1);
+  // no LDS write may land after the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+template <int EPI>
+int launch_w4e(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  const int64_t ntiles = kad_cdiv(M, 256) * kad_cdiv(N, 256);
+  if (ntiles > 0x7fffffff / 2 || ntiles * (K / kBK) > 0x7fffffff)
+    KAD_UNSUPPORTED("gemm grid too large");
+  if ((int64_t)256 * (lda > ldw ? lda : ldw) + K >= 0x7fffffff)
+    KAD_UNSUPPORTED("gemm rows too long for 32-bit tile offsets");
+  if ((int64_t)256 * (ldc > ldr ? ldc : ldr) >= 0x7fffffff)
+    KAD_UNSUPPORTED("gemm output rows too long for 32-bit tile offsets");
+  if (M % 256 || N % 256) KAD_UNSUPPORTED("tile configuration 24 needs M and N multiples of 256");
+  int grid = device_cu_count();
+  grid -= grid % 8;
+  if (grid <= 0) grid = 8;
+  if (ntiles < grid) grid = (int)ntiles;
+  const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
+  hipLaunchKernelGGL((gemm_w4e_kernel<EPI>), dim3((unsigned)grid), dim3(256), 0, s,
+                     (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N, K, n_major, 8, (int)ntiles);
+  return kad_launch_status("gemm_w4e_kernel");
+}
+
 template <int EPI, int BN>
 int launch_x16p(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
                 const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
@@ -1127,7 +1521,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_64x32 = 11,
        CFG_32x64 = 12,
        CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19,
-       CFG_256x256_S3 = 20, CFG_256x256_PPP = 22 };
+       CFG_256x256_S3 = 20, CFG_256x256_PPP = 22, CFG_256x256_W4E = 24 };
 
 template <int EPI>
 int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
@@ -1162,6 +1556,14 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       // kernel (the GDN input projections 1-6%, the vocabulary head 3%
       // faster than configuration 18, interleaved A/B medians on one box)
       cfg = CFG_256x256_PPP;
+    else if (EPI != KAD_EPI_STORE && M % 256 == 0 && N % 256 == 0 &&
+             (EPI == KAD_EPI_RESIDUAL ? K >= 2048 && tiles256 >= 2 * device_cu_count()
+                                      : tiles256 >= 8 * device_cu_count()))
+      // the 4-wave kernel for whole-tile residual outputs from K = 2,048 (the
+      // prefill mixer output and down projections 14% and 13% faster than
+      // configuration 20) and SwiGLU launches of eight rounds or more (the
+      // prefill gate/up projection 2% faster than configuration 18)
+      cfg = CFG_256x256_W4E;
     else if (tiles256 >= 256 && (K >= 3072 || (EPI == KAD_EPI_RESIDUAL && K >= 2048)))
       cfg = CFG_256x256_S3;
     else if (tiles256 >= 256)
@@ -1222,6 +1624,7 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     case CFG_128x128_X16:
     case CFG_256x256_S3:
     case CFG_256x256_PPP:
+    case CFG_256x256_W4E:
       if (!vector_epilogue_ok(C, ldc, R, ldr, N, EPI))
         KAD_UNSUPPORTED("tile configuration %d needs 16-byte aligned outputs in 8-column units",
                         cfg);
@@ -1229,6 +1632,8 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
         return launch_x16<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_256x256_S3)
         return launch_s3<EPI, Tile256>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+      if (cfg == CFG_256x256_W4E)
+        return launch_w4e<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_256x256_PPP)
         return launch_ppp<EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
       if (cfg == CFG_128x128_X16)

@@ -220,11 +220,12 @@ def test_gemm_persistent_tiles_agree(device, K, epi):
 @pytest.mark.parametrize("K", [64, 192, 1024])
 @pytest.mark.parametrize("epi", [layers.EPI_STORE, layers.EPI_RESIDUAL, layers.EPI_SWIGLU])
 def test_gemm_ping_pong_tiles_agree(device, K, epi):
-    """The persistent ping-pong kernel (config 22) against config 16, bit for
-    bit: 40 x 16 whole tiles (two or three per CU, so that epilogues run
-    inside the next tile's first read phase) and tiles of one, three and 16 K
-    slices, so that the load stream crosses tile boundaries at both stage
-    parities."""
+    """The persistent ping-pong kernel (config 22) and the persistent 4-wave
+    kernel (config 24) against config 16, bit for bit: 40 x 16 whole tiles
+    (two or three per CU, so that epilogues run inside the next tile's first
+    read phase, and a plain store's inside its first MFMA step) and tiles of
+    one, three and 16 K slices, so that the load stream crosses tile
+    boundaries at both stage parities."""
     from kadllm_amd import _lib
     M, N = 256 * 40, 256 * 16
     g = torch.Generator().manual_seed(190 + K + epi)
@@ -233,7 +234,7 @@ def test_gemm_ping_pong_tiles_agree(device, K, epi):
     n_out = N // 2 if epi == layers.EPI_SWIGLU else N
     x = torch.randn(M, n_out, generator=g).bfloat16().to(device)
     outs = {}
-    for cfg in (16, 22):
+    for cfg in (16, 22, 24):
         c = x.clone() if epi == layers.EPI_RESIDUAL else torch.zeros(M, n_out, dtype=torch.bfloat16,
                                                                      device=device)
         _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), n_out,
@@ -243,9 +244,36 @@ def test_gemm_ping_pong_tiles_agree(device, K, epi):
         torch.cuda.synchronize()
         outs[cfg] = c.cpu()
     assert torch.equal(outs[22], outs[16]), f"ping-pong 256x256 differs at K={K}"
+    assert torch.equal(outs[24], outs[16]), f"4-wave 256x256 differs at K={K}"
 
 
-@pytest.mark.parametrize("cfg", [22])
+@pytest.mark.parametrize("epi", [layers.EPI_STORE, layers.EPI_RESIDUAL, layers.EPI_SWIGLU])
+def test_gemm_four_wave_tiles_padded_rows(device, epi):
+    """Config 24 with row strides above the widths (lda, ldw, ldc and ldr
+    padded), one tile per CU or fewer (the first tile's fused store goes to a
+    resource of no records), against config 16."""
+    from kadllm_amd import _lib
+    M, N, K = 256 * 8, 256 * 12, 320
+    lda, ldw = K + 64, K + 32
+    g = torch.Generator().manual_seed(290 + epi)
+    a = torch.randn(M, lda, generator=g).bfloat16().to(device)
+    w = (torch.randn(N, ldw, generator=g) * 0.05).bfloat16().to(device)
+    n_out = N // 2 if epi == layers.EPI_SWIGLU else N
+    ldc = n_out + 24
+    x = torch.randn(M, ldc, generator=g).bfloat16().to(device)
+    outs = {}
+    for cfg in (16, 24):
+        c = x.clone()
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), lda, _lib.ptr(w), ldw, _lib.ptr(c), ldc,
+                  _lib.ptr(c) if epi == layers.EPI_RESIDUAL else None,
+                  ldc if epi == layers.EPI_RESIDUAL else 0, M, N, K, epi, cfg, _lib.stream_of(a))
+        torch.cuda.synchronize()
+        outs[cfg] = c.cpu()
+    assert torch.equal(outs[24], outs[16]), "4-wave 256x256 differs with padded rows"
+    assert torch.equal(outs[24][:, n_out:], x[:, n_out:].cpu()), "wrote past the output width"
+
+
+@pytest.mark.parametrize("cfg", [22, 24])
 def test_gemm_whole_tile_kernels_reject_partial_tiles(device, cfg):
     from kadllm_amd import _lib
     a = torch.zeros(300, 64, dtype=torch.bfloat16, device=device)
