@@ -157,6 +157,11 @@ def kernel_work(name, a):
         N, T, H, HV, K, V = a[19:25]
         return "gdn_chunk", "hbm", N * T * (2 * H * K + 2 * HV * V) * 2 + N * HV * K * V * 4, \
             None
+    if name == "kad_gdn_chunk_gated":
+        # the chunk rule plus the gate rows it reads for the fused norm
+        N, T, H, HV, K, V = a[19:25]
+        return "gdn_chunk", "hbm", N * T * (2 * H * K + 3 * HV * V) * 2 + N * HV * K * V * 4, \
+            None
     if name == "kad_causal_conv_prefill":
         B, L, C = a[6], a[7], a[8]
         return "conv_prefill", "hbm", 2 * B * L * C * 2 + B * C * 4 * 2 + C * 8, None

@@ -298,6 +298,24 @@ int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, in
                   int beams_per_state, void* out, int64_t ld_out, float* final_state,
                   void* workspace, int64_t workspace_bytes, int N, int T, int H, int HV, int K,
                   int V, float scale, int transformers_l2norm, kad_stream_t stream);
+/* kad_gdn_chunk (transformers l2norm) with the layer's gated RMSNorm applied
+ * to each output row of a value head on its way out: out = bf16(bf16(w *
+ * bf16(o r)) * silu(z)), r = 1 / sqrt(mean(o^2) + eps) per (token, value
+ * head), o the chunk rule's bf16 output, as kad_rmsnorm_gated computes it
+ * (the same bits as the two calls in a row).  z: [N*T rows, HV*V] bf16 row
+ * strided (the gate projection columns), ldz a multiple of 8, 16-byte
+ * aligned; norm_w: [V] bf16.  No counterpart in the reference as one call:
+ * it fuses the chunk rule and the Qwen3_5RMSNormGated that follows it in the
+ * prefill the reference runs through transformers
+ * (src/kadllm/adapters/qwen3_5.py:111), so the output rows make one pass
+ * through memory instead of three. */
+int kad_gdn_chunk_gated(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
+                        int qkv_dtype, const void* log_decay, int gate_dtype, const void* beta,
+                        int beta_dtype, int64_t ld_gate, const void* initial_state,
+                        int state_dtype, int beams_per_state, void* out, int64_t ld_out,
+                        float* final_state, void* workspace, int64_t workspace_bytes, int N,
+                        int T, int H, int HV, int K, int V, float scale, const void* z,
+                        int64_t ldz, const void* norm_w, float eps, kad_stream_t stream);
 
 /* Causal width-4 conv + SiLU over whole prompts with zero history, and the
  * conv state (last 4 pre-conv inputs, [B, C, 4], nullable) that decode reads.

@@ -52,6 +52,7 @@ SIGNATURES = {
     "kad_gather_beam_rows": "pli" "pli" "i" "l" "p" "iii" "s",
     "kad_gdn_chunk_workspace_bytes": "iiiip",
     "kad_gdn_chunk": "ppplli" "pipil" "pii" "plp" "pl" "iiiiii" "fi" "s",
+    "kad_gdn_chunk_gated": "ppplli" "pipil" "pii" "plp" "pl" "iiiiii" "f" "plpf" "s",
     "kad_causal_conv_prefill": "plpplpiiiis",
     "kad_gemm_f32": "plplplpl" "iiii" "s",
     "kad_rmsnorm_f32": "plpfpllifs",

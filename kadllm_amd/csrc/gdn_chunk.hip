@@ -419,12 +419,45 @@ __device__ __forceinline__ bf16x8 kt_frag(const bf16_t* kb, int kt, int s, int l
   return as_bf16x8(u32x4{lo[0], lo[1], up[0], up[1]});
 }
 
-template <int K, int V, bool HF>
+// Gated output (GATED): each output row of a value head passes through the
+// model's gated RMSNorm on its way out, with the arithmetic of
+// rmsnorm_gated_kernel: the row's 8-element pieces sit in CPV consecutive
+// lanes as there, the same per-lane sum and butterfly over the lanes, so the
+// result equals the chunk rule followed by kad_rmsnorm_gated bit for bit.
+struct GateArgs {
+  const bf16_t* z;     // [N*T rows, HV*V], row stride ldz
+  int64_t ldz;
+  const bf16_t* w;     // [V]
+  float eps;
+};
+
+// sum over the `lanes` consecutive lanes (a power of two) that share a row,
+// in the butterfly order of the row-wise kernels (partners lane ^ lanes/2,
+// then ^ lanes/4, ...).  For 16-lane rows the partners come by DPP row
+// rotations: a rotation by 8 is the xor-8 partner, and after each step the
+// lanes a rotation by 4, 2 or 1 reaches hold the xor partner's value, so the
+// sums are the same bits without LDS round trips.
+template <int LANES>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  if constexpr (LANES == 16) {
+    v += dpp_f32<0x128>(v);   // row_ror:8
+    v += dpp_f32<0x124>(v);   // row_ror:4
+    v += dpp_f32<0x122>(v);   // row_ror:2
+    v += dpp_f32<0x121>(v);   // row_ror:1
+  } else {
+#pragma unroll
+    for (int o = LANES / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  }
+  return v;
+}
+
+template <int K, int V, bool HF, bool GATED>
 __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t ld_qk,
     const bf16_t* __restrict__ v, int64_t ld_v, const uint8_t* __restrict__ ws,
     const void* __restrict__ state0, int sdt, int beams_per_state, bf16_t* __restrict__ out,
-    int64_t ld_out, float* __restrict__ final_state, int T, int H, int HV, int nchunks) {
+    int64_t ld_out, float* __restrict__ final_state, int T, int H, int HV, int nchunks,
+    GateArgs gate) {
   constexpr int KT = K / 32;      // 32-row k tiles of S
   constexpr int KS = K / 16;      // k16 steps over K
   constexpr int LDK = K + 8;      // bf16 [64][K] rows (16-byte padding)
@@ -462,7 +495,8 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
   // the chunk's global data pass through registers into LDS; all loads are
   // issued before the barrier, so their latency is paid once per chunk (and
   // the second workgroup on the CU computes meanwhile).  Prefetching the next
-  // chunk instead needs the registers of a second workgroup.
+  // chunk instead needs the registers of a second workgroup (issuing its
+  // loads before the output stage spills 32-128 registers).
   constexpr int kRowU = kC * CPR / NTH;               // q/k slices per thread
   constexpr int kVU = kC * V / 8 / NTH;               // v slices per thread
   constexpr int kTU = ChunkRec::tf_elems / 8 / NTH;   // T' slices per thread
@@ -533,6 +567,7 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     }
   };
 
+  constexpr int kOUG = kC * (V / 8) / NTH;   // output pieces per thread
   for (int c = 0; c < nchunks; ++c) {
     // lane-derived indices are recomputed from an opaque copy of the thread
     // id every chunk, so the compiler does not keep dozens of precomputed
@@ -545,6 +580,17 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
     const int nt = min(kC, T - t0);
     const int64_t row0 = (int64_t)n * T + t0;
     fetch(c, tid);
+    // the gate rows of this thread's output pieces, loaded with the chunk's
+    // inputs (their latency is not on the store path)
+    u32x4 zr[GATED ? kOUG : 1], wr = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (GATED) {
+#pragma unroll
+      for (int u = 0; u < kOUG; ++u) {
+        const int i = min((tid + u * NTH) / (V / 8), nt - 1);
+        zr[u] = *(const u32x4*)(gate.z + (row0 + i) * gate.ldz + (int64_t)hv * V + (tid % (V / 8)) * 8);
+      }
+      wr = *(const u32x4*)(gate.w + (tid % (V / 8)) * 8);
+    }
     __syncthreads();  // previous chunk done with LDS
     stash(tid);
     __syncthreads();
@@ -673,11 +719,47 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
       S[kt] = acc;
     }
     __syncthreads();
+    if constexpr (GATED) {
 #pragma unroll
-    for (int u = 0; u < kOU; ++u) {
-      const int i = (tid + u * NTH) / CPV;
-      const u32x4 ov = *(const u32x4*)(vb + i * LDV + och * 8);
-      if (i < nt) *(u32x4*)(out + (row0 + i) * ld_out + (int64_t)hv * V + och * 8) = ov;
+      for (int u = 0; u < kOU; ++u) {
+        const int i = (tid + u * NTH) / CPV;
+        const u32x4 ov = *(const u32x4*)(vb + i * LDV + och * 8);
+        float f[8], wv[8], zv[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f[2 * e] = __uint_as_float(ov[e] << 16);
+          f[2 * e + 1] = __uint_as_float(ov[e] & 0xffff0000u);
+          wv[2 * e] = __uint_as_float(wr[e] << 16);
+          wv[2 * e + 1] = __uint_as_float(wr[e] & 0xffff0000u);
+          zv[2 * e] = __uint_as_float(zr[u][e] << 16);
+          zv[2 * e + 1] = __uint_as_float(zr[u][e] & 0xffff0000u);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+        ss = lane_group_sum<CPV>(ss);
+        const float r = 1.0f / sqrtf(ss / (float)V + gate.eps);
+        u32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float pr[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float nrm = round_bf(f[2 * e + h] * r);
+            const float wn = round_bf(wv[2 * e + h] * nrm);
+            pr[h] = wn * silu_fast(zv[2 * e + h]);
+          }
+          y[e] = (uint32_t)f2bf(pr[0]) | ((uint32_t)f2bf(pr[1]) << 16);
+        }
+        if (i < nt) *(u32x4*)(out + (row0 + i) * ld_out + (int64_t)hv * V + och * 8) = y;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kOU; ++u) {
+        const int i = (tid + u * NTH) / CPV;
+        const u32x4 ov = *(const u32x4*)(vb + i * LDV + och * 8);
+        if (i < nt) *(u32x4*)(out + (row0 + i) * ld_out + (int64_t)hv * V + och * 8) = ov;
+      }
     }
   }
   if (final_state) {
@@ -696,25 +778,32 @@ template <int K, int V>
 int launch_chunk(const void* q, const void* k, const void* v, int64_t ld_qk, int64_t ld_v,
                  const void* g, int gdt, const void* beta, int bdt, int64_t ld_gate,
                  const void* state0, int sdt, int bps, void* out, int64_t ld_out, float* fin,
-                 void* ws, int N, int T, int H, int HV, float scale, int hf_norm, hipStream_t s) {
+                 void* ws, int N, int T, int H, int HV, float scale, int hf_norm,
+                 const GateArgs* gate, hipStream_t s) {
   const int nchunks = (T + kC - 1) / kC;
   const int64_t nrec = (int64_t)N * HV * nchunks;
+  const GateArgs ga = gate ? *gate : GateArgs{nullptr, 0, nullptr, 0.f};
   // transformers' bf16 l2norm rounding (hf_norm) or the operator's fp32
   // scales: an instantiation each, so the VALU-bound loops carry no test
-#define KAD_CHUNK(HFV)                                                                         \
+#define KAD_CHUNK(HFV, GV)                                                                     \
   hipLaunchKernelGGL((gdn_chunk_prep<K, HFV>), dim3((unsigned)nrec), dim3(kPrepThreads), 0, s, \
                      (const bf16_t*)q, (const bf16_t*)k, ld_qk, g, gdt, beta, bdt, ld_gate,    \
                      (uint8_t*)ws, T, H, HV, nchunks, scale);                                  \
   if (const int rc = kad_launch_status("gdn_chunk_prep")) return rc;                           \
-  hipLaunchKernelGGL((gdn_chunk_scan<K, V, HFV>), dim3((unsigned)((int64_t)N * HV)),          \
+  hipLaunchKernelGGL((gdn_chunk_scan<K, V, HFV, GV>), dim3((unsigned)((int64_t)N * HV)),      \
                      dim3(V * 2), 0, s, (const bf16_t*)q, (const bf16_t*)k, ld_qk,             \
                      (const bf16_t*)v, ld_v, (const uint8_t*)ws, state0, sdt, bps,             \
-                     (bf16_t*)out, ld_out, fin, T, H, HV, nchunks);                            \
+                     (bf16_t*)out, ld_out, fin, T, H, HV, nchunks, ga);                        \
   return kad_launch_status("gdn_chunk_scan")
-  if (hf_norm) {
-    KAD_CHUNK(true);
+  // the gated output only with the transformers normalisation (the model
+  // prefill, whose layer applies the norm)
+  if (gate) {
+    KAD_CHUNK(true, true);
   }
-  KAD_CHUNK(false);
+  if (hf_norm) {
+    KAD_CHUNK(true, false);
+  }
+  KAD_CHUNK(false, false);
 #undef KAD_CHUNK
 }
 
@@ -728,7 +817,7 @@ int chunk_common(const void* q, const void* k, const void* v, int64_t ld_qk, int
                  int beams_per_state, void* out, int64_t ld_out,
                  float* final_state, void* workspace, int64_t workspace_bytes, int N, int T,
                  int H, int HV, int K, int V, float scale, int transformers_l2norm,
-                 hipStream_t s) {
+                 const GateArgs* gate, hipStream_t s) {
   KAD_REQUIRE(q && k && v && log_decay && beta && out && workspace, "null pointer argument");
   KAD_REQUIRE(N > 0 && T > 0 && H > 0 && HV > 0 && HV % H == 0, "bad dimensions");
   KAD_REQUIRE(!initial_state || (beams_per_state > 0 && N % beams_per_state == 0),
@@ -747,12 +836,19 @@ int chunk_common(const void* q, const void* k, const void* v, int64_t ld_qk, int
   KAD_REQUIRE(workspace_bytes >= need, "workspace of %lld bytes is smaller than %lld",
               (long long)workspace_bytes, (long long)need);
   KAD_REQUIRE(((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
+  if (gate) {
+    KAD_REQUIRE(gate->z && gate->w, "null pointer argument");
+    KAD_REQUIRE(transformers_l2norm, "the gated output takes the transformers l2norm");
+    KAD_REQUIRE(gate->ldz >= (int64_t)HV * V && gate->ldz % 8 == 0 &&
+                    ((uintptr_t)gate->z % 16) == 0 && ((uintptr_t)gate->w % 16) == 0,
+                "z rows and the norm weight must be 16-byte aligned, ldz >= HV*V");
+  }
 #define KAD_CHUNK(KK, VV)                                                                      \
   if (K == KK && V == VV)                                                                      \
     return launch_chunk<KK, VV>(q, k, v, ld_qk, ld_v, log_decay, gate_dtype, beta, beta_dtype, \
                                 ld_gate, initial_state, state_dtype, beams_per_state, out,     \
                                 ld_out, final_state, workspace, N, T, H, HV, scale,            \
-                                transformers_l2norm, s);
+                                transformers_l2norm, gate, s);
   KAD_CHUNK(128, 128)
   KAD_CHUNK(64, 64)
   KAD_CHUNK(128, 64)
@@ -781,5 +877,21 @@ extern "C" int kad_gdn_chunk(const void* q, const void* k, const void* v, int64_
   return chunk_common(q, k, v, ld_qk, ld_v, qkv_dtype, log_decay, gate_dtype, beta, beta_dtype,
                       ld_gate, initial_state, state_dtype, beams_per_state, out, ld_out,
                       final_state, workspace, workspace_bytes, N, T, H, HV, K, V, scale,
-                      transformers_l2norm, (hipStream_t)stream);
+                      transformers_l2norm, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int kad_gdn_chunk_gated(const void* q, const void* k, const void* v, int64_t ld_qk,
+                                   int64_t ld_v, int qkv_dtype, const void* log_decay,
+                                   int gate_dtype, const void* beta, int beta_dtype,
+                                   int64_t ld_gate, const void* initial_state, int state_dtype,
+                                   int beams_per_state, void* out, int64_t ld_out,
+                                   float* final_state, void* workspace, int64_t workspace_bytes,
+                                   int N, int T, int H, int HV, int K, int V, float scale,
+                                   const void* z, int64_t ldz, const void* norm_w, float eps,
+                                   kad_stream_t stream) {
+  const GateArgs ga{(const bf16_t*)z, ldz, (const bf16_t*)norm_w, eps};
+  return chunk_common(q, k, v, ld_qk, ld_v, qkv_dtype, log_decay, gate_dtype, beta, beta_dtype,
+                      ld_gate, initial_state, state_dtype, beams_per_state, out, ld_out,
+                      final_state, workspace, workspace_bytes, N, T, H, HV, K, V, scale, 1, &ga,
+                      (hipStream_t)stream);
 }

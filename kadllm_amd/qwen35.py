@@ -299,16 +299,22 @@ class Qwen35Runner:
                 base = conv.data_ptr()
                 es = conv.element_size()
                 ws = _lib.gdn_chunk_workspace(B, L, HV, dk, dev)
-                _lib.call("kad_gdn_chunk", _lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
-                          _lib.ptr_at(base + 2 * self.kd * es), self.conv_dim, self.conv_dim, 0,
-                          _lib.ptr(g), 2, _lib.ptr(beta), 0, HV, None, 2, 1, _lib.ptr(o), self.vd,
-                          _lib.ptr(S), _lib.ptr(ws), ws.numel(), B, L, H_, HV, dk, dv,
-                          float(dk ** -0.5), 1, _lib.stream_of(x))
+                args = (_lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
+                        _lib.ptr_at(base + 2 * self.kd * es), self.conv_dim, self.conv_dim, 0,
+                        _lib.ptr(g), 2, _lib.ptr(beta), 0, HV, None, 2, 1, _lib.ptr(o), self.vd,
+                        _lib.ptr(S), _lib.ptr(ws), ws.numel(), B, L, H_, HV, dk, dv,
+                        float(dk ** -0.5))
                 if terminal:
+                    _lib.call("kad_gdn_chunk", *args, 1, _lib.stream_of(x))
                     self._gdn_finish(lyr, o.view(B, L, -1)[:, -1], proj.view(B, L, -1)[:, -1],
                                      x_last)
                 else:
-                    self._gdn_finish(lyr, o, proj, x)
+                    # the chunk rule with the gated RMSNorm on its output rows
+                    # (the same bits as kad_gdn_chunk then kad_rmsnorm_gated)
+                    z = proj[:, self.conv_dim:self.conv_dim + self.vd]
+                    _lib.call("kad_gdn_chunk_gated", *args, _lib.ptr(z), z.stride(0),
+                              _lib.ptr(lyr.norm_w), float(cfg.rms_norm_eps), _lib.stream_of(x))
+                    layers.gemm(o, lyr.w_out, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
                 snap.append((conv_state, S))
             elif terminal:
                 snap.append(self._attn_terminal(lyr, n, x_last, B, L))

@@ -6,7 +6,7 @@ from torch.nn import functional as F
 
 from _fixtures import gdn_inputs
 from conftest import assert_close_rel
-from kadllm_amd import _lib, ops
+from kadllm_amd import _lib, layers, ops
 from kadllm_amd.grbeam import extend_history, select_level
 from oracle import grbeam_ref, ops_ref
 
@@ -145,6 +145,37 @@ def test_prefill_chunk_matches_transformers_semantics(device, L):
     torch.cuda.synchronize()
     assert_close_rel(o.cpu(), eo, rtol=1e-2, atol_frac=3e-3, name="prefill o")
     assert_close_rel(s.cpu(), es, rtol=1e-3, atol_frac=1e-4, name="prefill state")
+
+
+@pytest.mark.parametrize("L,K", [(37, 128), (200, 128), (100, 64)])
+def test_prefill_chunk_gated_equals_chunk_then_norm(device, L, K):
+    """kad_gdn_chunk_gated against kad_gdn_chunk followed by kad_rmsnorm_gated,
+    bit for bit (output and final state), with a gate row stride wider than
+    the value heads and a partial last chunk."""
+    B, H = 2, 4
+    q, k, v, g, beta, _ = gdn_inputs(B, 1, L, H, H, K, K, seed=300 + L)
+    dev = [t.to(device).contiguous() for t in (q, k, v, g, beta)]
+    gen = torch.Generator().manual_seed(301 + L)
+    zpad = torch.randn(B * L, H * K + 40, generator=gen).bfloat16().to(device)
+    z = zpad[:, 8:8 + H * K]
+    w = (1.0 + 0.1 * torch.randn(K, generator=gen)).bfloat16().to(device)
+    eps = 1e-6
+    ws = _lib.gdn_chunk_workspace(B, L, H, K, device)
+    args = (_lib.ptr(dev[0]), _lib.ptr(dev[1]), _lib.ptr(dev[2]), H * K, H * K, 0,
+            _lib.ptr(dev[3]), 2, _lib.ptr(dev[4]), 0, H, None, 2, 1)
+    o = torch.empty(B * L, H * K, dtype=torch.bfloat16, device=device)
+    s1 = torch.empty(B, H, K, K, dtype=torch.float32, device=device)
+    _lib.call("kad_gdn_chunk", *args, _lib.ptr(o), H * K, _lib.ptr(s1), _lib.ptr(ws), ws.numel(),
+              B, L, H, H, K, K, float(K ** -0.5), 1, _lib.stream_of(o))
+    y1 = layers.rmsnorm_gated(o, z, w, eps, H)
+    y2 = torch.full((B * L, H * K), 7.0, dtype=torch.bfloat16, device=device)
+    s2 = torch.empty(B, H, K, K, dtype=torch.float32, device=device)
+    _lib.call("kad_gdn_chunk_gated", *args, _lib.ptr(y2), H * K, _lib.ptr(s2), _lib.ptr(ws),
+              ws.numel(), B, L, H, H, K, K, float(K ** -0.5), _lib.ptr(z), z.stride(0),
+              _lib.ptr(w), eps, _lib.stream_of(o))
+    torch.cuda.synchronize()
+    assert torch.equal(y2.cpu(), y1.cpu()), "gated chunk output differs from chunk + norm"
+    assert torch.equal(s2.cpu(), s1.cpu()), "gated chunk final state differs"
 
 
 @pytest.mark.parametrize("L", [1, 3, 50])
