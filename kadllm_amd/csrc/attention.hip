@@ -33,6 +33,15 @@
 namespace {
 
 constexpr int kThreads = 256;
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>)
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
 // suffix keys folded per beam row (decode): 4, or 8 for longer suffixes
 constexpr int kSuffixFold = 4, kSuffixFoldLong = 8, kSuffixFoldShort = 2;
 
@@ -581,6 +590,24 @@ struct Attn3 {
   static constexpr int lds = stage_bytes > epi_bytes ? stage_bytes : epi_bytes;  // bytes
 };
 
+// p with both halves read from the first active lane: a wave-uniform value
+// the compiler can see as one (a buffer resource it cannot prove uniform
+// turns every load into a loop over lanes)
+__device__ __forceinline__ const bf16_t* uniform_ptr(const bf16_t* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi32 = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const bf16_t*)(uintptr_t)(((uint64_t)hi32 << 32) | lo);
+}
+// 16 bytes per lane from base + voff into LDS through a buffer resource of
+// nbytes bytes (pieces past it read zeros); base and nbytes wave-uniform
+__device__ __forceinline__ void dma16_extent(const bf16_t* base, int nbytes, uint32_t voff,
+                                             bf16_t* lds) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), 0, nbytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (attn_lds_t*)lds, 16, voff, 0, 0, 0);
+}
+
 // max and sum of a value over lanes l and l ^ 32 (both lanes get the same bits)
 __device__ __forceinline__ float xor32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -600,6 +627,18 @@ __device__ __forceinline__ u32x2 tr_read(const bf16_t* p) {
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"((uint32_t)(uintptr_t)p) : "memory");
   return r;
 }
+// the same at a constant byte offset from p (the instruction's offset field,
+// so that a tile's reads share a few base addresses)
+template <int OFF>
+__device__ __forceinline__ u32x2 tr_read_at(const bf16_t* p) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+               : "=v"(r)
+               : "v"((uint32_t)(uintptr_t)p), "i"(OFF)
+               : "memory");
+  return r;
+}
 // lgkmcnt(N) (vmcnt and expcnt not waited), tied to the fragment registers so
 // that their uses stay after it
 template <int N>
@@ -607,7 +646,9 @@ __device__ __forceinline__ void tr_wait(u32x2& a, u32x2& b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
 
-template <bool CAUSAL, int NSUF>
+// MASKED: a prefix mask is given (decode); an instantiation of its own, so
+// that the unmasked key loop carries no mask loads or branches
+template <bool CAUSAL, int NSUF, bool MASKED>
 __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
   constexpr int D = 256, KS = D / 16, DT = D / 32, ROWS = Attn3::ROWS, CPR = Attn3::CPR;
   constexpr int LOADS = Attn3::LOADS;
@@ -661,51 +702,45 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
     kend = (int)(rlast / G) + 1;
   }
   const int ntiles = (kend + kKeys2 - 1) / kKeys2;
+  // leading tiles every row of the block sees whole (no prefix mask either)
+  int nfull = kend / kKeys2;
+  if (CAUSAL) nfull = min(nfull, (int)(((int64_t)qb_blk * ROWS / G + 1) / kKeys2));
+  if (MASKED) nfull = 0;
   const bf16_t* pkb = a.pk + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
   const bf16_t* pvb = a.pv + (int64_t)b * a.sp_b + (int64_t)kh * a.sp_h;
   const int d_row = lane / CPR, d_pc = lane % CPR;
-  int dk_off[LOADS], dv_off[LOADS];   // element offsets from the tile's first key
+  // byte offsets of this lane's 16-byte pieces from the tile's first key
+  uint32_t dk_off[LOADS], dv_off[LOADS];
 #pragma unroll
   for (int k = 0; k < LOADS; ++k) {
     const int r = (wave + 4 * k) * (64 / CPR) + d_row;
-    dk_off[k] = r * (int)a.sp_l + (d_pc ^ (r & 15)) * 8;
-    dv_off[k] = r * (int)a.sp_l + (d_pc ^ ((r & 3) * 4)) * 8;
+    dk_off[k] = (uint32_t)(r * (int)a.sp_l + (d_pc ^ (r & 15)) * 8) * 2u;
+    dv_off[k] = (uint32_t)(r * (int)a.sp_l + (d_pc ^ ((r & 3) * 4)) * 8) * 2u;
   }
-  // loads of one tile: K and V row sources from the tile's first key (rows
-  // past the prefix, in its last tile, repeat its last key) and the wave's
+  // loads of one tile through buffer resources based at the tile's first key
+  // whose extent ends at the prefix end: rows past the prefix (in its last
+  // tile) read zeros, which the key mask makes weightless; the wave's
   // destination in the tile's stage
   struct TileLoad {
     const bf16_t* kb;
     const bf16_t* vb;
+    int nrec;   // bytes from the tile's first key to the prefix end
     bf16_t* dst;
-    bool full;
-    int k0;
   };
   auto tile_load = [&](int tile) {
     TileLoad tl;
-    tl.k0 = tile * kKeys2;
-    tl.full = tl.k0 + kKeys2 <= a.L;
-    tl.kb = pkb + (int64_t)tl.k0 * a.sp_l;
-    tl.vb = pvb + (int64_t)tl.k0 * a.sp_l;
+    const int k0 = tile * kKeys2;
+    tl.kb = uniform_ptr(pkb + (int64_t)k0 * a.sp_l);
+    tl.vb = uniform_ptr(pvb + (int64_t)k0 * a.sp_l);
+    // (the launcher bounds L * sp_l * 2 below 2^31)
+    tl.nrec = __builtin_amdgcn_readfirstlane(max(a.L - k0, 0) * (int)a.sp_l * 2);
     tl.dst = smem + (tile % kStages3) * Attn3::stage + wave * 64 * 8;
     return tl;
   };
   auto issue_one = [&](const TileLoad& tl, int k) {
     bf16_t* kd = tl.dst + k * 4 * 64 * 8;
-    if (tl.full) {
-      __builtin_amdgcn_global_load_lds((attn_global_t*)(tl.kb + dk_off[k]), (attn_lds_t*)kd, 16, 0,
-                                       0);
-      __builtin_amdgcn_global_load_lds((attn_global_t*)(tl.vb + dv_off[k]),
-                                       (attn_lds_t*)(kd + Attn3::tile), 16, 0, 0);
-    } else {
-      const int r = (wave + 4 * k) * (64 / CPR) + d_row;
-      const int64_t key = min(tl.k0 + r, a.L - 1);
-      __builtin_amdgcn_global_load_lds(
-          (attn_global_t*)(pkb + key * a.sp_l + (d_pc ^ (r & 15)) * 8), (attn_lds_t*)kd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (attn_global_t*)(pvb + key * a.sp_l + (d_pc ^ ((r & 3) * 4)) * 8),
-          (attn_lds_t*)(kd + Attn3::tile), 16, 0, 0);
-    }
+    dma16_extent(tl.kb, tl.nrec, dk_off[k], kd);
+    dma16_extent(tl.vb, tl.nrec, dv_off[k], kd + Attn3::tile);
   };
   auto issue = [&](int tile) {
     const TileLoad tl = tile_load(tile);
@@ -803,8 +838,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
       // one key tile: st holds its scores; with kNext, the scores of tile + 1
       // go to st_next.  Straight-line code apart from the rare prefix mask
       // and the load issue, so that the accumulators keep their registers.
-      auto step = [&](const int tile, f32x16& st, f32x16& st_next, auto next_c) {
+      // kMaskC: the tile holds keys some row must not see (the prefix end,
+      // or a causal row's own position); tiles below nfull need no mask
+      auto step = [&](const int tile, f32x16& st, f32x16& st_next, auto next_c, auto mask_c) {
         constexpr bool kNext = decltype(next_c)::value;
+        constexpr bool kMaskC = decltype(mask_c)::value;
         // tile + 1 landed (tile + 2 may still be in flight); every wave has
         // finished iteration tile - 1, whose stage the loads of tile + 3 reuse
         if (tile + 2 < ntiles)
@@ -813,7 +851,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
           __builtin_amdgcn_s_waitcnt(0x0070);
         tile_barrier();
         const int k0 = tile * kKeys2;
-        if (!CAUSAL && a.mask) {
+        if constexpr (!CAUSAL && MASKED) {
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int kj = (j / 4) * 8 + (j % 4);
@@ -832,7 +870,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
 #pragma unroll
             for (int j = 4 * s; j < 4 * s + 4; ++j) {
               const int kj = (j / 4) * 8 + (j % 4);
-              st[j] = kj <= lim ? st[j] : -INFINITY;
+              if constexpr (kMaskC) st[j] = kj <= lim ? st[j] : -INFINITY;
               tmax = fmaxf(tmax, st[j]);
             }
           } else if (s == 4) {
@@ -881,56 +919,67 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
         // each fragment's two transpose reads go out three fragments ahead,
         // and the exponentials of keys 8-15 run under the first 8 MFMAs
         const bf16_t* vs = smem + (tile % kStages3) * Attn3::stage + Attn3::tile;
-        auto vaddr = [&](int f, int rd) {
-          const int ks2 = f / DT, dg = f % DT;
-          return vs + v_off[dg & 3] + (dg >> 2) * 128 + (16 * ks2 + 8 * rd) * D;
-        };
+        // fragment f, read rd: base vb[dg & 3] plus a constant byte offset
+        const bf16_t* vb[4] = {vs + v_off[0], vs + v_off[1], vs + v_off[2], vs + v_off[3]};
         constexpr int NF = 2 * DT, AHEAD = 3;
+        auto vread = [&](auto f_c, auto rd_c) {
+          constexpr int f = decltype(f_c)::value, rd = decltype(rd_c)::value;
+          constexpr int ks2 = f / DT, dg = f % DT;
+          return tr_read_at<((dg >> 2) * 128 + (16 * ks2 + 8 * rd) * D) * 2>(vb[dg & 3]);
+        };
         u32x2 vlo[AHEAD + 1], vup[AHEAD + 1];
-#pragma unroll
-        for (int f = 0; f < AHEAD; ++f) {
-          vlo[f] = tr_read(vaddr(f, 0));
-          vup[f] = tr_read(vaddr(f, 1));
-        }
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
+        static_for<AHEAD>([&](auto f_c) {
+          constexpr int f = decltype(f_c)::value;
+          vlo[f] = vread(f_c, std::integral_constant<int, 0>{});
+          vup[f] = vread(f_c, std::integral_constant<int, 1>{});
+        });
+        static_for<NF>([&](auto f_c) {
+          constexpr int f = decltype(f_c)::value;
           const int cur = f % (AHEAD + 1);
-          if (f + AHEAD < NF) {
+          if constexpr (f + AHEAD < NF) {
             const int nxt = (f + AHEAD) % (AHEAD + 1);
-            vlo[nxt] = tr_read(vaddr(f + AHEAD, 0));
-            vup[nxt] = tr_read(vaddr(f + AHEAD, 1));
+            vlo[nxt] = vread(std::integral_constant<int, f + AHEAD>{},
+                             std::integral_constant<int, 0>{});
+            vup[nxt] = vread(std::integral_constant<int, f + AHEAD>{},
+                             std::integral_constant<int, 1>{});
             tr_wait<2 * AHEAD>(vlo[cur], vup[cur]);
-          } else if (f + 2 == NF) {
+          } else if constexpr (f + 2 == NF) {
             tr_wait<2>(vlo[cur], vup[cur]);
-          } else if (f + 1 == NF) {
+          } else if constexpr (f + 1 == NF) {
             tr_wait<0>(vlo[cur], vup[cur]);
           } else {
             tr_wait<4>(vlo[cur], vup[cur]);
           }
           const bf16x8 vf = as_bf16x8(u32x4{vlo[cur][0], vlo[cur][1], vup[cur][0], vup[cur][1]});
           O[f % DT] = mfma32x32x16(vf, pf[f / DT], O[f % DT]);
-          if (f < 8) {
+          if constexpr (f < 8) {
             const float p = __builtin_amdgcn_exp2f(fmaf(st[8 + f], sl2, nm));
             psum += p;
             pf[1][f] = (__bf16)p;
           }
-          if (f == 8) l += xor32_sum(psum);
-          if (f % 4 == 2 && load3) issue_one(tl3, f / 4);
+          if constexpr (f == 8) l += xor32_sum(psum);
+          if constexpr (f % 4 == 2) {
+            if (load3) issue_one(tl3, f / 4);
+          }
           __builtin_amdgcn_sched_barrier(0);
-        }
+        });
       };
       using yes = std::integral_constant<bool, true>;
       using no = std::integral_constant<bool, false>;
       int tile = 0;
+      for (; tile + 2 < ntiles && tile + 2 <= nfull; tile += 2) {
+        step(tile, st0, st1, yes{}, no{});
+        step(tile + 1, st1, st0, yes{}, no{});
+      }
       for (; tile + 2 < ntiles; tile += 2) {
-        step(tile, st0, st1, yes{});
-        step(tile + 1, st1, st0, yes{});
+        step(tile, st0, st1, yes{}, yes{});
+        step(tile + 1, st1, st0, yes{}, yes{});
       }
       if (tile + 1 < ntiles) {
-        step(tile, st0, st1, yes{});
-        step(tile + 1, st1, st0, no{});
+        step(tile, st0, st1, yes{}, yes{});
+        step(tile + 1, st1, st0, no{}, yes{});
       } else {
-        step(tile, st0, st1, no{});
+        step(tile, st0, st1, no{}, yes{});
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -1046,26 +1095,37 @@ __global__ __launch_bounds__(kThreads, 1) void attn3_kernel(AttnArgs a) {
   }
 }
 
-template <bool CAUSAL, int NSUF>
-int launch_attn3(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
-  if ((int64_t)kKeys2 * a.sp_l >= 0x7fffffff)
-    KAD_UNSUPPORTED("attention: prefix key stride %lld too large", (long long)a.sp_l);
-  a.nqblk = (int)kad_cdiv(rows, Attn3::ROWS);
-  const int64_t nblocks = bh * a.nqblk;
-  KAD_REQUIRE(nblocks < 0x7fffffff, "grid too large");
+template <bool CAUSAL, int NSUF, bool MASKED>
+int launch_attn3_as(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   const size_t lds = Attn3::lds;
   static bool configured = false;
   if (!configured) {
-    if (hipFuncSetAttribute((const void*)attn3_kernel<CAUSAL, NSUF>,
+    if (hipFuncSetAttribute((const void*)attn3_kernel<CAUSAL, NSUF, MASKED>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
       kad_set_error("attention: cannot reserve %zu bytes of LDS", lds);
       return KAD_ERR_HIP;
     }
     configured = true;
   }
-  hipLaunchKernelGGL((attn3_kernel<CAUSAL, NSUF>), dim3((unsigned)nblocks), dim3(kThreads), lds, s,
-                     a);
+  hipLaunchKernelGGL((attn3_kernel<CAUSAL, NSUF, MASKED>), dim3((unsigned)nblocks),
+                     dim3(kThreads), lds, s, a);
   return kad_launch_status("attn3_kernel");
+}
+
+template <bool CAUSAL, int NSUF>
+int launch_attn3(AttnArgs a, int64_t rows, int64_t bh, hipStream_t s) {
+  if ((int64_t)kKeys2 * a.sp_l >= 0x7fffffff)
+    KAD_UNSUPPORTED("attention: prefix key stride %lld too large", (long long)a.sp_l);
+  if ((int64_t)a.L * a.sp_l * 2 >= 0x7fffffff)
+    KAD_UNSUPPORTED("attention: prefix of %lld bytes per head too long for 32-bit offsets",
+                    (long long)a.L * a.sp_l * 2);
+  a.nqblk = (int)kad_cdiv(rows, Attn3::ROWS);
+  const int64_t nblocks = bh * a.nqblk;
+  KAD_REQUIRE(nblocks < 0x7fffffff, "grid too large");
+  if constexpr (!CAUSAL) {
+    if (a.mask) return launch_attn3_as<CAUSAL, NSUF, true>(a, nblocks, s);
+  }
+  return launch_attn3_as<CAUSAL, NSUF, false>(a, nblocks, s);
 }
 
 // rows: query rows per (request, KV head); bh: number of (request, KV head)
