@@ -38,6 +38,18 @@ __device__ __forceinline__ float silu_rcp(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
+// SwiGLU of two adjacent outputs, bf16(bf16(silu(bf16(g))) * bf16(u)) for
+// (g0, u0) in the low half and (g1, u1) in the high half: each bf16
+// rounding of the pair is one packed conversion (the same bits as rounding
+// each value on its own, with half the conversions and their widenings)
+__device__ __forceinline__ uint32_t swiglu2(float g0, float g1, float u0, float u1) {
+  const uint32_t gp = pack_bf16x2(g0, g1), up = pack_bf16x2(u0, u1);
+  const float ua = __uint_as_float(up << 16), ub = __uint_as_float(up & 0xffff0000u);
+  const uint32_t sp =
+      pack_bf16x2(silu_rcp(__uint_as_float(gp << 16)), silu_rcp(__uint_as_float(gp & 0xffff0000u)));
+  return pack_bf16x2(__uint_as_float(sp << 16) * ua, __uint_as_float(sp & 0xffff0000u) * ub);
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
@@ -280,16 +292,9 @@ __device__ __forceinline__ void epilogue_x16(f32x4 (&acc)[NI][NJ], bf16_t* ep, i
         if ((j & 3) >= 2) continue;
         u32x2 packed;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          uint32_t two = 0;
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const float gv = round_bf(acc[i][j][h * 2 + q]);
-            const float uv = round_bf(acc[i][j + 2][h * 2 + q]);
-            two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
-          }
-          packed[h] = two;
-        }
+        for (int h = 0; h < 2; ++h)
+          packed[h] = swiglu2(acc[i][j][h * 2], acc[i][j][h * 2 + 1], acc[i][j + 2][h * 2],
+                              acc[i][j + 2][h * 2 + 1]);
         *(u32x2*)(ep + (i * 16 + e_row) * kLd + (j >> 2) * 32 + (j & 3) * 16 + e_col) = packed;
       }
     } else {
@@ -654,16 +659,9 @@ __device__ __forceinline__ void epilogue_x16_chunked(f32x4 (&acc)[NI][NJ], bf16_
         if ((j & 3) >= 2) continue;
         u32x2 packed;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          uint32_t two = 0;
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const float gv = round_bf(acc[i][j][h * 2 + q]);
-            const float uv = round_bf(acc[i][j + 2][h * 2 + q]);
-            two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
-          }
-          packed[h] = two;
-        }
+        for (int h = 0; h < 2; ++h)
+          packed[h] = swiglu2(acc[i][j][h * 2], acc[i][j][h * 2 + 1], acc[i][j + 2][h * 2],
+                              acc[i][j + 2][h * 2 + 1]);
         *(u32x2*)(ep + e_row * kLd + (j >> 2) * 32 + (j & 3) * 16 + e_col) = packed;
       } else {
         u32x2 packed;
@@ -1317,14 +1315,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4e_kernel(
           for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-              uint32_t two = 0;
-#pragma unroll
-              for (int q = 0; q < 2; ++q) {
-                const float gv = round_bf(acc[i][4 * g + b][h * 2 + q]);
-                const float uv = round_bf(acc[i][4 * g + b + 2][h * 2 + q]);
-                two |= (uint32_t)f2bf(round_bf(silu_rcp(gv)) * uv) << (16 * q);
-              }
-              w[b * 2 + h] = two;
+              const f32x4& gv = acc[i][4 * g + b];
+              const f32x4& uv = acc[i][4 * g + b + 2];
+              w[b * 2 + h] = swiglu2(gv[h * 2], gv[h * 2 + 1], uv[h * 2], uv[h * 2 + 1]);
             }
           const u32x4 v = pair_swap(w[0], w[1], w[2], w[3]);
           __builtin_amdgcn_raw_buffer_store_b128(v, rc, c_lane, (uint32_t)i * c_row16 + g * 64, 0);
