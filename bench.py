@@ -183,6 +183,8 @@ def kernel_work(name, a):
         return "rowwise", "hbm", 4 * a[3] * a[4], None
     if name == "kad_gdn_gates":
         return "rowwise", "hbm", 10 * a[8] * a[9], None
+    if name == "kad_cache_prefetch":
+        return "prefetch", "hbm", (a[1] // 16 + a[3] // 16) * 16, None
     return "other", "hbm", None, None
 
 
@@ -801,7 +803,7 @@ def ops_gemm(a):
 
 # kernel classes whose algorithmic bytes are almost all reads (reported
 # against the read probe); the others against the copy probe
-READ_DOMINATED = {"row_select", "merge_select"}
+READ_DOMINATED = {"row_select", "merge_select", "prefetch"}
 
 
 def hbm_probe_rates(size=4 << 30, iters=10):

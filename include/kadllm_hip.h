@@ -409,6 +409,19 @@ int kad_embedding_f32(const int64_t* ids, const float* table, float* out, int64_
 int kad_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
+ * Cache prefetch (no reference counterpart; the reference leaves weight
+ * traffic to its GEMM library): reads the whole 16-byte pieces of up to two
+ * ranges [p0, p0 + bytes0) and [p1, p1 + bytes1) with cache-allocating loads
+ * and discards them, so that the next kernels on the stream find those bytes
+ * in the last-level cache.  A range with 0 bytes may have a NULL pointer;
+ * ranges 16-byte aligned.  Writes nothing; results of later kernels do not
+ * depend on it.  The decode levels call it for the MLP and QKV weights ahead
+ * of their GEMMs.
+ */
+int kad_cache_prefetch(const void* p0, int64_t bytes0, const void* p1, int64_t bytes1,
+                       kad_stream_t stream);
+
+/* --------------------------------------------------------------------------
  * MFMA lane-layout self-test (no reference counterpart): C[16x16] = A[16x32]
  * B[32x16] (bf16 in, fp32 out, all row-major) computed by one wave with the
  * operand layout the kernels above assume for v_mfma_f32_16x16x32_bf16, and

@@ -61,6 +61,7 @@ SIGNATURES = {
     "kad_qk_norm_rope_f32": "plli" "pp" "lllll" "ii" "p" "ll" "f" "i" "s",
     "kad_embedding_f32": "ppplils",
     "kad_hbm_probe": "pplis",
+    "kad_cache_prefetch": "plpls",
     "kad_selftest_mfma_f32": "ppps",
     "kad_selftest_mfma16": "ppps",
     "kad_selftest_mfma32": "ppps",

@@ -130,3 +130,57 @@ extern "C" int kad_hbm_probe(const void* src, void* dst, int64_t bytes, int mode
                      (const u32x4*)src, (u32x4*)dst, n16, mode, 0x9e3779b9u);
   return kad_launch_status("hbm_probe_kernel");
 }
+
+// ---------------------------------------------------------------------------
+// Cache prefetch: reads up to two ranges with ordinary (cache-allocating)
+// loads and discards the data, so that the next kernels on the stream find
+// them in the 256 MB last-level cache instead of HBM.  A GEMM whose weight
+// arrives cold pays far more than the weight's bytes at HBM rate: its
+// workgroups miss on the same panels together and wait out HBM latency.  The
+// loads stay live through an empty asm statement that takes their XOR; the
+// kernel writes nothing.  The two ranges form one index space, and each lane
+// issues all its kPrefetchDepth loads before it uses one, so that a launch of
+// a few tens of megabytes takes one memory round trip per lane: indices past
+// the end are clamped to the last piece (re-read, not skipped: a guarded load
+// would make the compiler wait for each one in turn).  Every load's index is
+// below n0 + n1 and maps into its own range.
+constexpr int kPrefetchDepth = 8;
+
+__global__ __launch_bounds__(256) void cache_prefetch_kernel(const u32x4* __restrict__ p0,
+                                                             int64_t n0,
+                                                             const u32x4* __restrict__ p1,
+                                                             int64_t n1) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t n = n0 + n1;
+  uint32_t acc = 0u;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += kPrefetchDepth * stride) {
+    u32x4 v[kPrefetchDepth];
+#pragma unroll
+    for (int u = 0; u < kPrefetchDepth; ++u) {
+      const int64_t j = min(i + u * stride, n - 1);
+      v[u] = *(j < n0 ? p0 + j : p1 + (j - n0));
+    }
+#pragma unroll
+    for (int u = 0; u < kPrefetchDepth; ++u) acc ^= v[u][0];
+  }
+  asm volatile("" ::"v"(acc));
+}
+
+extern "C" int kad_cache_prefetch(const void* p0, int64_t bytes0, const void* p1, int64_t bytes1,
+                                  kad_stream_t stream) {
+  KAD_REQUIRE(bytes0 >= 0 && bytes1 >= 0, "prefetch sizes must not be negative");
+  KAD_REQUIRE((bytes0 == 0 || p0) && (bytes1 == 0 || p1), "null pointer argument");
+  KAD_REQUIRE(((uintptr_t)p0 % 16) == 0 && ((uintptr_t)p1 % 16) == 0,
+              "prefetch ranges must be 16-byte aligned");
+  const int64_t n0 = bytes0 / 16, n1 = bytes1 / 16;   // whole 16-byte pieces
+  if (n0 + n1 == 0) return KAD_OK;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t want = (int64_t)cus * 8;  // 8 workgroups of 256 lanes per CU
+  const int64_t need = kad_cdiv(n0 + n1, 256);
+  const int64_t blocks = want < need ? want : need;
+  hipLaunchKernelGGL(cache_prefetch_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, (const u32x4*)p0, n0, (const u32x4*)p1, n1);
+  return kad_launch_status("cache_prefetch_kernel");
+}

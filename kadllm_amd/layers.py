@@ -97,3 +97,11 @@ def embedding(ids, table, out=None):
     _lib.call("kad_embedding", _lib.ptr(ids), _lib.ptr(table), _lib.ptr(out), rows, D,
               table.shape[0], _lib.stream_of(table))
     return out
+
+
+def cache_prefetch(t0, t1=None):
+    """Read one or two (contiguous) tensors into the last-level cache ahead of
+    the kernels that use them; computes nothing."""
+    b1 = t1.numel() * t1.element_size() if t1 is not None else 0
+    _lib.call("kad_cache_prefetch", _lib.ptr(t0), t0.numel() * t0.element_size(),
+              _lib.ptr(t1) if t1 is not None else None, b1, _lib.stream_of(t0))

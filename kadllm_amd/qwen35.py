@@ -188,8 +188,10 @@ class Qwen35Runner:
                          ).to(self.device)
 
     # ------------------------------------------------------------------
-    def _mlp(self, lyr, x, rows):
+    def _mlp(self, lyr, x, rows, prefetch=False):
         cfg = self.cfg
+        if prefetch:
+            layers.cache_prefetch(lyr.w_gu, lyr.w_down)
         n2 = layers.rmsnorm(x, lyr.post_norm, cfg.rms_norm_eps)
         h = layers.gemm(n2, lyr.w_gu, epilogue=layers.EPI_SWIGLU)
         layers.gemm(h, lyr.w_down, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
@@ -475,8 +477,21 @@ class Qwen35Runner:
                       _lib.ptr(dst), ld_dst, T, T - 1, row_bytes, _lib.ptr(parents), B, W, Wp,
                       stream)
 
+        # Weights arrive cold from HBM at every level (a layer's ~40 MB are long
+        # gone from the 256 MB last-level cache by the next level), which costs
+        # the 8,192-row GEMMs far more than their bytes: measured alone, the
+        # SwiGLU projection took 128 against 110 us with only its weight cold,
+        # QKV 99 against 83, down 66 against 61.  Reading the MLP weights (22
+        # MB) before the post-mixer norm and an attention layer's QKV weight
+        # before its input norm takes a few microseconds and restores the warm
+        # times.  The prefill's 32,768-row GEMMs lose only 2-3 us cold, less
+        # than the prefetch costs, and a GEMM of few rows reads its weight
+        # once at HBM rate whether or not it was prefetched.
+        prefetch = 2048 <= BW <= 16384
         new_layers = []
         for li, (lyr, cached) in enumerate(zip(self.layers, prefix_layers)):
+            if prefetch and not isinstance(lyr, _GdnLayer):
+                layers.cache_prefetch(lyr.w_qkv)
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
                 cols = self.gdn_cols
@@ -523,7 +538,7 @@ class Qwen35Runner:
                 layers.gemm(att.view(BW, nh * hd), lyr.w_o, out=x, epilogue=layers.EPI_RESIDUAL,
                             residual=x)
                 new_layers.append((k_all, v_all))
-            self._mlp(lyr, x, BW)
+            self._mlp(lyr, x, BW, prefetch)
             if self.trace is not None:
                 self.trace("step", li, x.clone())
         hN = layers.rmsnorm(x, self.norm_w, cfg.rms_norm_eps)

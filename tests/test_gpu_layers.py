@@ -28,6 +28,23 @@ def _bf16_ulp_close(actual, expected, name, min_exact=0.95):
     assert exact >= min_exact, f"{name}: only {exact:.4f} bit-exact"
 
 
+def test_cache_prefetch_reads_and_writes_nothing(device):
+    """kad_cache_prefetch leaves its ranges as they were (odd tails included)
+    and checks its arguments."""
+    from kadllm_amd import _lib
+    a = torch.randn(1 << 20, device=device).bfloat16()
+    b = torch.randint(0, 255, (12345,), dtype=torch.uint8, device=device)
+    a0, b0 = a.clone(), b.clone()
+    layers.cache_prefetch(a, b)
+    layers.cache_prefetch(a)
+    torch.cuda.synchronize()
+    assert torch.equal(a, a0) and torch.equal(b, b0)
+    with pytest.raises(_lib.KadLibraryError, match="16-byte aligned"):
+        layers.cache_prefetch(b[1:])
+    with pytest.raises(_lib.KadLibraryError, match="null pointer"):
+        _lib.call("kad_cache_prefetch", None, 64, None, 0, _lib.stream_of(a))
+
+
 # --------------------------------------------------------------------------
 # GEMM
 

@@ -231,6 +231,16 @@ def test_incremental_decode_equals_stateless_tiny(device, tiny):
                                    cfg.vocab_size, device, 22)
 
 
+def test_incremental_decode_with_weight_prefetch_equals_stateless(device, tiny):
+    """Levels of 2 x 1024 beams, where decode_step reads the MLP and QKV weights
+    into the cache ahead of their GEMMs: still exactly the stateless logits."""
+    cfg, _, adapter = tiny
+    ids = torch.randint(0, cfg.vocab_size, (2, 40), generator=torch.Generator().manual_seed(31))
+    res = adapter.prefill(ids.to(device))
+    _incremental_matches_stateless(adapter, res.state, 2, [1024, 1024, 1024],
+                                   cfg.vocab_size, device, 32)
+
+
 def test_tiny_grbeam_depth7_teacher_forced(device, tiny):
     """A 7-token search (the depth of the reference's README.md:125 runs; the
     reference has no depth limit, src/kadllm/grbeam.py:75-77): every level's
