@@ -198,13 +198,16 @@ class Qwen35GRBeamAdapter:
                                         hf_config if hf_config is not None else self.config.to_hf())
 
     @torch.no_grad()
-    def decode_incremental(self, history, parents, state, cache=None):
+    def decode_incremental(self, history, parents, state, cache=None, *, keep_cache=True):
         """decode(history, state) for a level whose beams extend the previous
         level's beams by one token: history[b, w] = history_prev[b, parents[b, w]]
         followed by one new token.  ``cache`` is what the previous call returned
         (None for the first decode level).  Returns (logits, cache); the logits
         equal decode(history, state) while only the new token goes through the
-        projections.  grbeam_search uses it when the adapter offers it."""
+        projections.  With ``keep_cache=False`` (a search's last level) the
+        returned cache is None and each layer's per-token rows are released as
+        soon as the layer is done.  grbeam_search uses it when the adapter
+        offers it."""
         self._check(history)
         if not isinstance(state, Qwen35Prefix) or state.owner is not self._owner:
             raise ValueError("prefix belongs to a different adapter")
@@ -217,7 +220,8 @@ class Qwen35GRBeamAdapter:
             raise ValueError("parents must be [B, W] on the history's device")
         tokens = history[:, :, -1].contiguous()
         probe = self._range_probe(tokens)
-        out = self._runner.decode_step(tokens, parents, state.layers, state.length, cache)
+        out = self._runner.decode_step(tokens, parents, state.layers, state.length, cache,
+                                       keep_cache=keep_cache)
         self._raise_out_of_range(probe)
         return out
 

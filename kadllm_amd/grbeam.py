@@ -10,6 +10,7 @@ the reference's torch.topk leaves tie order unspecified (grbeam.py:95).
 """
 
 import ctypes
+import inspect
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 from typing import Any, Protocol
@@ -172,6 +173,23 @@ def _column_tokens(adapter, tokens):
     return ids.index_select(0, tokens.reshape(-1)).view(tokens.shape)
 
 
+def _incremental_decoder(adapter):
+    """The adapter's decode_incremental as f(history, parents, state, cache,
+    last), or None.  On a search's last level an adapter that takes
+    ``keep_cache`` is told not to keep its suffix cache, which nothing would
+    read (at B32 x W256 with 2-token suffixes it is ~5 GB of per-layer rows)."""
+    fn = getattr(adapter, "decode_incremental", None)
+    if fn is None:
+        return None
+    try:
+        takes = "keep_cache" in inspect.signature(fn).parameters
+    except (TypeError, ValueError):
+        takes = False
+    if takes:
+        return lambda h, p, s, c, last: fn(h, p, s, c, keep_cache=not last)
+    return lambda h, p, s, c, last: fn(h, p, s, c)
+
+
 @torch.no_grad()
 def grbeam_search(
     adapter: GRBeamAdapter,
@@ -208,12 +226,13 @@ def grbeam_search(
     logits = prefill.logits[:, None, :]
     # An adapter that can extend the previous level's suffixes (keeping their
     # per-token state) gets the parents; its logits equal decode(history).
-    incremental = getattr(adapter, "decode_incremental", None)
+    incremental = _incremental_decoder(adapter)
     cache = parents = None
     for step, width in enumerate(widths):
         if step:
             if incremental is not None:
-                logits, cache = incremental(history, parents, prefill.state, cache)
+                logits, cache = incremental(history, parents, prefill.state, cache,
+                                            step == len(widths) - 1)
             else:
                 logits = adapter.decode(history, prefill.state)
         if logits.shape != (*history.shape[:2], V):
@@ -266,14 +285,15 @@ def conditional_search(
     history = torch.empty(B, 1, 0, dtype=torch.int64, device=dev)
     scores = torch.zeros(B, 1, device=dev)
     logits = prefill.logits[:, None, :]
-    incremental = getattr(adapter, "decode_incremental", None)
+    incremental = _incremental_decoder(adapter)
     cache = parents = valid = None
     levels = [(w, None) for w in coarse_widths] + [(w, "fine") for w in fine_widths]
     groups = None
     for step, (width, kind) in enumerate(levels):
         if step:
             if incremental is not None:
-                logits, cache = incremental(history, parents, prefill.state, cache)
+                logits, cache = incremental(history, parents, prefill.state, cache,
+                                            step == len(levels) - 1)
             else:
                 logits = adapter.decode(history, prefill.state)
         if logits.shape != (*history.shape[:2], V):

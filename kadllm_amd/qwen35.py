@@ -438,14 +438,16 @@ class Qwen35Runner:
 
     # ------------------------------------------------------------------
     @torch.no_grad()
-    def decode_step(self, tokens, parents, prefix_layers, prefix_length, cache=None):
+    def decode_step(self, tokens, parents, prefix_layers, prefix_length, cache=None,
+                    keep_cache=True):
         """One search level that extends each parent beam's suffix by one token.
 
         tokens [B, W] int64 are the new tokens, parents [B, W] int64 the
         indices of the previous level's beams they extend (ignored for the
         first level, ``cache=None``, whose parent is the prefix itself), and
         ``cache`` the DecodeCache the previous level returned.  Returns
-        (logits [B, W, V] bf16, DecodeCache).
+        (logits [B, W, V] bf16, DecodeCache), the cache None with
+        ``keep_cache=False`` (nothing keeps the layers' per-token rows then).
 
         The logits equal ``decode(history)`` for history = the parents'
         suffixes followed by ``tokens``: every per-token quantity of the cached
@@ -512,7 +514,8 @@ class Qwen35Runner:
                 z_new = pv[:, T - 1, C:C + self.vd]
                 y = layers.rmsnorm_gated(o_new, z_new, lyr.norm_w, cfg.rms_norm_eps, HV)
                 layers.gemm(y, lyr.w_out, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
-                new_layers.append(proj)
+                if keep_cache:
+                    new_layers.append(proj)
             else:
                 proj = layers.gemm(n, lyr.w_qkv)
                 ld = proj.stride(0)
@@ -537,13 +540,14 @@ class Qwen35Runner:
                                               gate_strides=(ld, ld, 2 * hd))
                 layers.gemm(att.view(BW, nh * hd), lyr.w_o, out=x, epilogue=layers.EPI_RESIDUAL,
                             residual=x)
-                new_layers.append((k_all, v_all))
+                if keep_cache:
+                    new_layers.append((k_all, v_all))
             self._mlp(lyr, x, BW, prefetch)
             if self.trace is not None:
                 self.trace("step", li, x.clone())
         hN = layers.rmsnorm(x, self.norm_w, cfg.rms_norm_eps)
         logits = layers.gemm(hN, self.lm_head)
-        return logits.view(B, W, -1), DecodeCache(T, W, tuple(new_layers))
+        return logits.view(B, W, -1), (DecodeCache(T, W, tuple(new_layers)) if keep_cache else None)
 
 
 @dataclass

@@ -241,6 +241,22 @@ def test_incremental_decode_with_weight_prefetch_equals_stateless(device, tiny):
                                    cfg.vocab_size, device, 32)
 
 
+def test_last_level_without_cache(device, tiny):
+    """keep_cache=False (a search's last level): the same logits, no cache."""
+    cfg, _, adapter = tiny
+    g = torch.Generator().manual_seed(33)
+    ids = torch.randint(0, cfg.vocab_size, (2, 40), generator=g)
+    res = adapter.prefill(ids.to(device))
+    hist = torch.randint(0, cfg.vocab_size, (2, 6, 2), generator=g).to(device)
+    _, cache = adapter.decode_incremental(hist[:, :, :1], None, res.state, None)
+    parents = torch.arange(6, device=device).expand(2, 6).contiguous()
+    kept, cache2 = adapter.decode_incremental(hist, parents, res.state, cache)
+    last, none = adapter.decode_incremental(hist, parents, res.state, cache, keep_cache=False)
+    torch.cuda.synchronize()
+    assert cache2 is not None and none is None
+    assert torch.equal(kept, last)
+
+
 def test_tiny_grbeam_depth7_teacher_forced(device, tiny):
     """A 7-token search (the depth of the reference's README.md:125 runs; the
     reference has no depth limit, src/kadllm/grbeam.py:75-77): every level's

@@ -66,3 +66,29 @@ def test_checkpoint_biases_are_refused():
     with pytest.raises(ValueError, match="attention_bias"):
         reject_biases(Cfg(), {})
     reject_biases(object(), {"layers.0.input_layernorm.weight": torch.zeros(1)})
+
+
+def test_last_level_cache_hint_only_for_adapters_that_take_it():
+    """grbeam passes keep_cache=False on a search's last level, and only to a
+    decode_incremental that declares the keyword."""
+    from kadllm_amd.grbeam import _incremental_decoder
+
+    calls = []
+
+    class WithHint:
+        def decode_incremental(self, history, parents, state, cache=None, *, keep_cache=True):
+            calls.append(keep_cache)
+            return "logits", None
+
+    class WithoutHint:
+        def decode_incremental(self, history, parents, state, cache=None):
+            calls.append("plain")
+            return "logits", cache
+
+    f = _incremental_decoder(WithHint())
+    f(None, None, None, None, False)
+    f(None, None, None, None, True)
+    g = _incremental_decoder(WithoutHint())
+    g(None, None, None, None, True)
+    assert calls == [True, False, "plain"]
+    assert _incremental_decoder(object()) is None
