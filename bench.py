@@ -136,6 +136,13 @@ def kernel_work(name, a):
             + BW * T * HV * 6
         label = "gdn_replay" if name == "kad_gdn_suffix_replay" else "gdn_recurrent"
         return label, "hbm", nbytes, BW * HV * 2 * T * 2 * K * V
+    if name == "kad_gdn_suffix_replay_conv":
+        # pre-conv q|k|v rows in, replay output out (the conv output stays on chip)
+        B, W, T, H, HV, K, V = a[17:24]
+        BW, C = B * W, 2 * H * K + HV * V
+        nbytes = BW * T * (C + HV * V) * 2 + B * HV * K * V * _es(a[14]) + BW * T * HV * 6 \
+            + B * C * 3 * 2 + C * 4 * 2
+        return "gdn_replay", "hbm", nbytes, BW * HV * 2 * T * 2 * K * V + 8 * BW * C * T
     if name == "kad_causal_conv_suffix":
         B, W, C, T, dt = a[16], a[17], a[18], a[19], a[20]
         return "conv_suffix", "hbm", (2 * B * W * C * T + B * C * 3 + C * 4) * _es(dt), \

@@ -63,6 +63,25 @@ int kad_gdn_suffix_replay(const void* q, const void* k, const void* v, int64_t l
                           int64_t ld_gate, const void* state, int state_dtype, void* out,
                           int64_t ld_out, int B, int W, int T, int H, int HV, int K,
                           int V, float scale, kad_stream_t stream);
+/* kad_causal_conv_suffix (width 4, SiLU, no bias) followed by
+ * kad_gdn_suffix_replay, as one call whose conv output never reaches HBM:
+ * proj holds each (beam, token) row's pre-conv channels [q (H*K) | k (H*K) |
+ * v (HV*V)] at [(n*T+t)*ld_proj + c] (bf16, ld_proj a multiple of 8, 16-byte
+ * aligned); conv_state / history / conv_weight ([C, 4] bf16, 8-byte aligned)
+ * as in kad_causal_conv_suffix; the rest as in kad_gdn_suffix_replay.  The
+ * outputs are the two calls' bits.  Supported: K = V = 128, T in {1, 2},
+ * W % 16 == 0, fp32 log decays and bf16 betas (even ld_gate); anything else
+ * is KAD_ERR_UNSUPPORTED (the caller then makes the two calls).  No
+ * counterpart in the reference as one call: it fuses the decode's
+ * causal_conv1d and gated_delta calls (src/kadllm/adapters/qwen3_5.py:146-174),
+ * so the suffix rows make one pass through memory instead of three. */
+int kad_gdn_suffix_replay_conv(const void* proj, int64_t ld_proj, const void* conv_state,
+                               int64_t ss_b, int64_t ss_c, int64_t ss_t, int history,
+                               const void* conv_weight, const void* log_decay, int gate_dtype,
+                               const void* beta, int beta_dtype, int64_t ld_gate,
+                               const void* state, int state_dtype, void* out, int64_t ld_out,
+                               int B, int W, int T, int H, int HV, int K, int V, float scale,
+                               kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
  * Depthwise causal short convolution over [prefix taps || suffix].

@@ -28,6 +28,7 @@ _CTYPES = {"p": _P, "l": _L, "i": _I, "f": _F, "s": _P}
 # f float, s stream), in the order of include/kadllm_hip.h
 SIGNATURES = {
     "kad_gdn_suffix_replay": "ppplli" "pipil" "pi" "pl" "iiiiiii" "f" "s",
+    "kad_gdn_suffix_replay_conv": "pl" "plllip" "pipil" "pi" "pl" "iiiiiii" "f" "s",
     "kad_causal_conv_suffix": "plll" "pllli" "pip" "plll" "iiiiii" "s",
     "kad_gemm_bf16": "plplplpl" "iiii" "s",
     "kad_gemm_bf16_tiled": "plplplpl" "iiiii" "s",

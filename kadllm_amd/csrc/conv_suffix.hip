@@ -6,9 +6,9 @@
 // beam of the request and stay in L2.  Rounding follows the reference torch
 // path: the convolution result is rounded to the tensor dtype, then SiLU is
 // applied and rounded again (for fp32 both roundings are exact).  The bf16
-// decode kernels take SiLU with the hardware reciprocal (silu_fast: they are
-// VALU-bound and the result is rounded to bf16); fp16 and fp32 tensors and the
-// prefill kernel keep the IEEE exp and divide.
+// kernels (decode and prefill) take SiLU with the hardware reciprocal
+// (silu_fast: they are VALU-bound and the result is rounded to bf16); fp16 and
+// fp32 tensors keep the IEEE exp and divide.
 //
 // Three paths: a vectorised one when channels are contiguous in x and out
 // (8 channels per thread, 16-byte accesses; the [rows, T, C] layout produced by
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float xv[2] = {__uint_as_float(r[e] << 16), __uint_as_float(r[e] & 0xffff0000u)};
-      uint32_t packed = 0;
+      float acc[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int ch = e * 2 + hh;
@@ -171,13 +171,16 @@ __global__ __launch_bounds__(256) void conv_suffix_vec_bf16(
         win[ch][1] = win[ch][2];
         win[ch][2] = win[ch][3];
         win[ch][3] = xv[hh];
-        float acc = 0.f;
+        float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc += wt[ch][i] * win[ch][i];
-        float y = round_bf(acc);
-        if (silu) y = silu_fast(y);
-        packed |= (uint32_t)f2bf(y) << (16 * hh);
+        for (int i = 0; i < 4; ++i) s += wt[ch][i] * win[ch][i];
+        acc[hh] = s;
       }
+      // the pair's roundings as one packed conversion each (the same bits)
+      uint32_t packed = pack_bf16x2(acc[0], acc[1]);
+      if (silu)
+        packed = pack_bf16x2(silu_fast(__uint_as_float(packed << 16)),
+                             silu_fast(__uint_as_float(packed & 0xffff0000u)));
       o[e] = packed;
     }
     const int j = k / T_;
@@ -341,7 +344,7 @@ __global__ __launch_bounds__(256) void conv_prefill_bf16(
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float xv[2] = {__uint_as_float(r[e] << 16), __uint_as_float(r[e] & 0xffff0000u)};
-      uint32_t packed = 0;
+      float acc[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int ch = e * 2 + hh;
@@ -349,13 +352,18 @@ __global__ __launch_bounds__(256) void conv_prefill_bf16(
         win[ch][1] = win[ch][2];
         win[ch][2] = win[ch][3];
         win[ch][3] = xv[hh];
-        float acc = 0.f;
+        float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc += wt[ch][i] * win[ch][i];
-        float y = round_bf(acc);
-        if (silu) y = silu_f(y);
-        packed |= (uint32_t)f2bf(y) << (16 * hh);
+        for (int i = 0; i < 4; ++i) s += wt[ch][i] * win[ch][i];
+        acc[hh] = s;
       }
+      // the pair's bf16 roundings (the conv output, then the SiLU output) as
+      // one packed conversion each; SiLU with the hardware reciprocal, as in
+      // the decode conv kernels (within one bf16 ulp of torch's silu)
+      uint32_t packed = pack_bf16x2(acc[0], acc[1]);
+      if (silu)
+        packed = pack_bf16x2(silu_fast(__uint_as_float(packed << 16)),
+                             silu_fast(__uint_as_float(packed & 0xffff0000u)));
       o[e] = packed;
     }
     *(u32x4*)(out + ((int64_t)b * L + t) * ldo + c0) = o;

@@ -739,17 +739,16 @@ __global__ __launch_bounds__(V * 2, V == 128 ? 2 : 1) void gdn_chunk_scan(
         for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
         ss = lane_group_sum<CPV>(ss);
         const float r = 1.0f / sqrtf(ss / (float)V + gate.eps);
+        // each bf16 rounding of a pair as one packed conversion (the same
+        // bits as rounding the elements one by one)
         u32x4 y;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float pr[2];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float nrm = round_bf(f[2 * e + h] * r);
-            const float wn = round_bf(wv[2 * e + h] * nrm);
-            pr[h] = wn * silu_fast(zv[2 * e + h]);
-          }
-          y[e] = (uint32_t)f2bf(pr[0]) | ((uint32_t)f2bf(pr[1]) << 16);
+          const uint32_t nb = pack_bf16x2(f[2 * e] * r, f[2 * e + 1] * r);
+          const uint32_t wb = pack_bf16x2(wv[2 * e] * __uint_as_float(nb << 16),
+                                          wv[2 * e + 1] * __uint_as_float(nb & 0xffff0000u));
+          y[e] = pack_bf16x2(__uint_as_float(wb << 16) * silu_fast(zv[2 * e]),
+                             __uint_as_float(wb & 0xffff0000u) * silu_fast(zv[2 * e + 1]));
         }
         if (i < nt) *(u32x4*)(out + (row0 + i) * ld_out + (int64_t)hv * V + och * 8) = y;
       }

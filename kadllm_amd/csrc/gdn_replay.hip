@@ -360,7 +360,32 @@ void gdn_replay_kernel(
 typedef __attribute__((address_space(1))) void replay_global_t;
 typedef __attribute__((address_space(3))) void replay_lds_t;
 
-template <int T, int NS>
+// The fused form (CONV) takes q, k and v before the depthwise causal conv +
+// SiLU of the decode (the column ranges of the projection rows) and applies
+// the conv in LDS as each group's rows land, with the arithmetic of
+// conv_suffix_vec_bf16 operation for operation (so the outputs are those of
+// kad_causal_conv_suffix followed by the replay, bit for bit); the conv output
+// never goes to HBM.  The prefix taps enter as per-channel partial sums: for
+// token t the window is [x_{t-3} .. x_t] with x_{-3..-1} the prefix taps, and
+// c_t is the chain of the window's tap terms (w_0 x_{t-3} + ..., in the conv
+// kernel's order), which the suffix terms then continue.
+struct ConvArgs {
+  const bf16_t* state;     // prefix conv inputs [B, C, hist] (strides ss_b, ss_c, ss_t)
+  int64_t ss_b, ss_c, ss_t;
+  int hist;                // the taps are slots hist - 3 .. hist - 1
+  const bf16_t* w;         // [C, 4], C the conv channels (q | k | v)
+};
+// per 8-channel chunk of the conv table: w_3 (bf16 x 8), then for T = 2 w_2;
+// c_0 (fp32 x 8), then for T = 2 c_1
+template <int T>
+struct ConvTab {
+  static constexpr int chunks = 48;                    // q, k and v of one head, 8 channels each
+  static constexpr int w_bytes = 16 * T, c_bytes = 32 * T;
+  static constexpr int chunk_bytes = w_bytes + c_bytes;
+  static constexpr int bytes = chunks * chunk_bytes;
+};
+
+template <int T, int NS, bool CONV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 1 ? 3 : (T == 4 ? 1 : 2), 8)))
 void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                            const bf16_t* __restrict__ v, int64_t ld_qk, int64_t ld_v,
@@ -368,7 +393,7 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
                            const void* __restrict__ beta, int beta_dtype, int64_t ld_gate,
                            const void* __restrict__ state, int state_dtype,
                            bf16_t* __restrict__ out, int64_t ld_out, int W, int H, int HV,
-                           float scale, int beams_per_block, int nbb) {
+                           float scale, int beams_per_block, int nbb, ConvArgs cv) {
   constexpr int KD = 128, VD = 128;
   constexpr int KSTEPS = KD / 32;
   constexpr int VROWS = VD / 4;
@@ -376,7 +401,10 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
   constexpr int ROWS = 16 * T;               // (beam, token) rows of a group
   constexpr int BLK = ROWS * 256;            // bytes of one q, k or v block
   constexpr int STAGE = 3 * BLK + 512;      // + the gates: 64 fp32 decays, 64 beta words
-  __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE];
+  static_assert(!CONV || T <= 2, "the fused conv takes one- and two-token suffixes");
+  constexpr int TAB = CONV ? ConvTab<T>::bytes : 0;
+  __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE + TAB];
+  uint8_t* const tab = stage_buf + NS * STAGE;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -425,6 +453,29 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
                                        (replay_lds_t*)(sb + 3 * BLK + w * 256), 4, 0, 0);
     }
   };
+  // the conv table of this head's 384 channels (q, k, v), one channel per
+  // thread and round: its inputs are loaded here, ahead of the groups' DMA and
+  // the state, and the table is formed once the state is in registers
+  constexpr int kTabRounds = CONV ? (ConvTab<T>::chunks * 8 + 255) / 256 : 0;
+  uint2 tab_w[kTabRounds > 0 ? kTabRounds : 1];
+  float tab_tap[kTabRounds > 0 ? kTabRounds : 1][3];
+  auto tab_channel = [&](int ci) {
+    const int chunk = ci >> 3, e = ci & 7, blk = chunk >> 4, c8 = (chunk & 15) * 8 + e;
+    return blk == 0 ? h * KD + c8 : (blk == 1 ? (H + h) * KD + c8 : 2 * H * KD + hv * VD + c8);
+  };
+  if constexpr (CONV) {
+#pragma unroll
+    for (int j = 0; j < kTabRounds; ++j) {
+      const int ci = threadIdx.x + 256 * j;
+      if (ci < ConvTab<T>::chunks * 8) {
+        const int gc = tab_channel(ci);
+        tab_w[j] = *(const uint2*)(cv.w + (int64_t)gc * 4);
+        const bf16_t* sp = cv.state + (int64_t)b * cv.ss_b + (int64_t)gc * cv.ss_c;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) tab_tap[j][i] = bf2f(sp[(int64_t)(cv.hist - 3 + i) * cv.ss_t]);
+      }
+    }
+  }
   // the first NS - 1 groups' loads go out before the state's, so they land
   // meanwhile
 #pragma unroll
@@ -456,6 +507,32 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
     }
   }
 
+  if constexpr (CONV) {
+#pragma unroll
+    for (int j = 0; j < kTabRounds; ++j) {
+      const int ci = threadIdx.x + 256 * j;
+      if (ci < ConvTab<T>::chunks * 8) {
+        const int chunk = ci >> 3, e = ci & 7;
+        const uint2 wr = tab_w[j];
+        const float w4[4] = {__uint_as_float(wr.x << 16), __uint_as_float(wr.x & 0xffff0000u),
+                             __uint_as_float(wr.y << 16), __uint_as_float(wr.y & 0xffff0000u)};
+        uint8_t* tc = tab + chunk * ConvTab<T>::chunk_bytes;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          // c_t: the window's tap terms i < 3 - t, in the conv kernel's order
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 3 - t; ++i) acc += w4[i] * tab_tap[j][t + i];
+          ((float*)(tc + ConvTab<T>::w_bytes + t * 32))[e] = acc;
+          // w_3 for token 0's slot, w_2 for token 1's
+          ((bf16_t*)(tc + t * 16))[e] = t == 0 ? (bf16_t)(wr.y >> 16) : (bf16_t)(wr.y & 0xffffu);
+        }
+      }
+    }
+    // the table's stores complete before the first group's barrier
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+
   // One group.  At its start, group gi's loads (all DMA into LDS, issued
   // NS - 1 groups earlier) must have landed.  The only loads issued after
   // them are the groups' in between: with NS = 3, group gi + 1's (at least 3T
@@ -475,6 +552,52 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
     asm volatile("" ::: "memory");
     const int s = gi % NS;
     if (gi + NS - 1 < ngroups) dma_group(gi + NS - 1, (gi + NS - 1) % NS);
+
+    if constexpr (CONV) {
+      // conv + SiLU of the stage's q, k and v rows in place: 16 beams x 48
+      // chunks, three (beam, chunk) items per thread, each over the T tokens
+      uint8_t* st = stage_buf + s * STAGE;
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        const int item = threadIdx.x + 256 * u;
+        const int beam = item / ConvTab<T>::chunks, chunk = item % ConvTab<T>::chunks;
+        uint8_t* rp = st + (chunk >> 4) * BLK + beam * T * 256 + (((chunk & 15) ^ beam) * 16);
+        const uint8_t* tc = tab + chunk * ConvTab<T>::chunk_bytes;
+        u32x4 x[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) x[t] = *(const u32x4*)(rp + t * 256);
+        const u32x4 w3r = *(const u32x4*)tc;
+        u32x4 w2r = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (T == 2) w2r = *(const u32x4*)(tc + 16);
+        const float* ct = (const float*)(tc + ConvTab<T>::w_bytes);
+        u32x4 y[T];   // token 1 reads token 0's inputs: stores after every token
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+#pragma unroll
+          for (int pr = 0; pr < 4; ++pr) {
+            float a[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int e = 2 * pr + hh;
+              auto lo16 = [&](uint32_t wv) { return __uint_as_float(hh ? (wv & 0xffff0000u) : (wv << 16)); };
+              float acc = ct[t * 8 + e];
+              if (t == 1) acc += lo16(w2r[pr]) * lo16(x[0][pr]);
+              acc += lo16(w3r[pr]) * lo16(x[t][pr]);
+              a[hh] = acc;
+            }
+            const uint32_t pk = pack_bf16x2(a[0], a[1]);
+            y[t][pr] = pack_bf16x2(silu_fast(__uint_as_float(pk << 16)),
+                                   silu_fast(__uint_as_float(pk & 0xffff0000u)));
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) *(u32x4*)(rp + t * 256) = y[t];
+      }
+      // every wave's conv outputs in place before any fragment read
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
 
     const uint8_t* sq = stage_buf + s * STAGE;
     const uint8_t* sk = sq + BLK;
@@ -617,10 +740,10 @@ int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, in
     if (staged) {
 #define KAD_REPLAY_LDS(TT, NS)                                                                \
   if (T == TT) {                                                                              \
-    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, NS>), dim3((unsigned)nblocks), dim3(256), 0, \
-                       stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ld_qk,   \
-                       ld_v, g, gdt, beta, bdt, ld_gate, state, sdt, (bf16_t*)out, ld_out, W, \
-                       H, HV, scale, bpb, nbb);                                               \
+    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, NS, false>), dim3((unsigned)nblocks),       \
+                       dim3(256), 0, stream, (const bf16_t*)q, (const bf16_t*)k,              \
+                       (const bf16_t*)v, ld_qk, ld_v, g, gdt, beta, bdt, ld_gate, state, sdt, \
+                       (bf16_t*)out, ld_out, W, H, HV, scale, bpb, nbb, ConvArgs{});          \
     return kad_launch_status("gdn_replay_lds_kernel");                                        \
   }
       KAD_REPLAY_LDS(1, 3)
@@ -670,7 +793,68 @@ int dispatch_dims(int K, int V, const void* q, const void* k, const void* v, int
   KAD_UNSUPPORTED("gdn replay supports K, V in {64, 128}; got K=%d V=%d", K, V);
 }
 
+int launch_replay_conv(const bf16_t* proj, int64_t ld, const ConvArgs& cv, const void* g,
+                       const void* beta, int64_t ld_gate, const void* state, int sdt, void* out,
+                       int64_t ld_out, int B, int W, int T, int H, int HV, float scale,
+                       hipStream_t stream) {
+  const int bpb = W <= 256 ? W : 128;
+  const int nbb = (int)kad_cdiv(W, bpb);
+  const int64_t nblocks = (int64_t)B * HV * nbb;
+  KAD_REQUIRE(nblocks <= 0x7fffffff, "gdn replay grid too large");
+  const bf16_t* q = proj;
+  const bf16_t* k = proj + (int64_t)H * 128;
+  const bf16_t* v = proj + (int64_t)2 * H * 128;
+#define KAD_REPLAY_CONV(TT)                                                                    \
+  if (T == TT) {                                                                               \
+    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, 3, true>), dim3((unsigned)nblocks), dim3(256), \
+                       0, stream, q, k, v, ld, ld, g, KAD_DTYPE_F32, beta, KAD_DTYPE_BF16,     \
+                       ld_gate, state, sdt, (bf16_t*)out, ld_out, W, H, HV, scale, bpb, nbb,   \
+                       cv);                                                                    \
+    return kad_launch_status("gdn_replay_lds_kernel");                                         \
+  }
+  KAD_REPLAY_CONV(1)
+  KAD_REPLAY_CONV(2)
+#undef KAD_REPLAY_CONV
+  KAD_UNSUPPORTED("the fused conv replay takes 1 or 2 suffix tokens, got %d", T);
+}
+
 }  // namespace
+
+extern "C" int kad_gdn_suffix_replay_conv(
+    const void* proj, int64_t ld_proj, const void* conv_state, int64_t ss_b, int64_t ss_c,
+    int64_t ss_t, int history, const void* conv_weight, const void* log_decay, int gate_dtype,
+    const void* beta, int beta_dtype, int64_t ld_gate, const void* state, int state_dtype,
+    void* out, int64_t ld_out, int B, int W, int T, int H, int HV, int K, int V, float scale,
+    kad_stream_t stream) {
+  KAD_REQUIRE(proj && conv_state && conv_weight && log_decay && beta && state && out,
+              "null pointer argument");
+  KAD_REQUIRE(B > 0 && W > 0 && T > 0 && H > 0 && HV > 0 && K > 0 && V > 0,
+              "dimensions must be positive");
+  KAD_REQUIRE(HV % H == 0, "HV must be divisible by H");
+  KAD_REQUIRE(history >= 3, "the conv state needs at least 3 taps, got %d", history);
+  KAD_REQUIRE(ld_proj >= (int64_t)2 * H * K + (int64_t)HV * V && ld_out >= (int64_t)HV * V &&
+                  ld_gate >= HV,
+              "row strides smaller than a row");
+  KAD_REQUIRE(ld_out % 4 == 0 && ((uintptr_t)out % 8) == 0,
+              "out rows must be 8-byte aligned (ld_out a multiple of 4)");
+  for (int dt : {gate_dtype, beta_dtype, state_dtype})
+    KAD_REQUIRE(dt == KAD_DTYPE_BF16 || dt == KAD_DTYPE_F16 || dt == KAD_DTYPE_F32,
+                "unknown dtype code %d", dt);
+  if (!(K == 128 && V == 128 && (T == 1 || T == 2) && W % 16 == 0))
+    KAD_UNSUPPORTED("the fused conv replay takes K = V = 128, 1 or 2 suffix tokens and beam "
+                    "counts that are multiples of 16 (got K=%d V=%d T=%d W=%d)", K, V, T, W);
+  if (!(gate_dtype == KAD_DTYPE_F32 && beta_dtype == KAD_DTYPE_BF16 && ld_gate % 2 == 0 &&
+        ((uintptr_t)beta % 4) == 0 && ((uintptr_t)log_decay % 4) == 0))
+    KAD_UNSUPPORTED("the fused conv replay takes fp32 log decays and bf16 betas with an even "
+                    "row stride");
+  if (!(ld_proj % 8 == 0 && ((uintptr_t)proj % 16) == 0 && ((uintptr_t)conv_weight % 8) == 0))
+    KAD_UNSUPPORTED("the fused conv replay takes 16-byte aligned projection rows and an 8-byte "
+                    "aligned [C, 4] weight");
+  const ConvArgs cv{(const bf16_t*)conv_state, ss_b, ss_c, ss_t, history,
+                    (const bf16_t*)conv_weight};
+  return launch_replay_conv((const bf16_t*)proj, ld_proj, cv, log_decay, beta, ld_gate, state,
+                            state_dtype, out, ld_out, B, W, T, H, HV, scale, (hipStream_t)stream);
+}
 
 extern "C" int kad_gdn_suffix_replay(const void* q, const void* k, const void* v,
                                      int64_t ld_qk, int64_t ld_v, int qkv_dtype,

@@ -233,6 +233,32 @@ class Qwen35Runner:
             _lib.call("kad_gdn_recurrent", *args, W, _lib.ptr(o), self.vd, None, B * W, T, H_, HV,
                       dk, dv, float(dk ** -0.5), _lib.stream_of(conv))
 
+    def _gdn_conv_replay(self, lyr, proj, T, cs, g, beta, S, o, B, W):
+        """The conv of the projection rows' q | k | v channels followed by the
+        replay: one fused call (kad_gdn_suffix_replay_conv, the same bits) where
+        it takes the shape, else kad_causal_conv_suffix into a buffer and
+        _gdn_replay.  proj: [B*W*T, cols] rows, token-major within each beam."""
+        cfg = self.cfg
+        H_, HV = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+        dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+        C = self.conv_dim
+        ld = proj.stride(0)
+        stream = _lib.stream_of(proj)
+        if (T <= 2 and W % 16 == 0 and dk == 128 and dv == 128 and g.dtype == torch.float32
+                and beta.dtype == torch.bfloat16 and g.stride(0) % 2 == 0 and ld % 8 == 0
+                and proj.data_ptr() % 16 == 0 and lyr.conv_w.is_contiguous()
+                and lyr.conv_w.data_ptr() % 8 == 0):
+            _lib.call("kad_gdn_suffix_replay_conv", _lib.ptr(proj), ld, _lib.ptr(cs),
+                      *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), _lib.ptr(g), 2,
+                      _lib.ptr(beta), 0, g.stride(0), _lib.ptr(S), _lib.dtype_code(S.dtype),
+                      _lib.ptr(o), self.vd, B, W, T, H_, HV, dk, dv, float(dk ** -0.5), stream)
+            return
+        conv = torch.empty(proj.shape[0], C, dtype=torch.bfloat16, device=proj.device)
+        _lib.call("kad_causal_conv_suffix", _lib.ptr(proj), T * ld, 1, ld, _lib.ptr(cs),
+                  *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), 4, None,
+                  _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, stream)
+        self._gdn_replay(conv, g, beta, S, o, B, W, T)
+
     def _gdn_finish(self, lyr, o, proj, x):
         cfg = self.cfg
         z = proj[:, self.conv_dim:self.conv_dim + self.vd]
@@ -374,16 +400,9 @@ class Qwen35Runner:
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
                 proj = self._gdn_proj(lyr, n)
-                ld = proj.stride(0)
-                conv = torch.empty(R, C, dtype=torch.bfloat16, device=dev)
-                cs = cached[0]
-                _lib.call("kad_causal_conv_suffix", _lib.ptr(proj), T * ld, 1, ld, _lib.ptr(cs),
-                          *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), 4, None,
-                          _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, _lib.stream_of(x))
                 g, beta = self._gdn_gates(lyr, proj)
                 o = torch.empty(R, self.vd, dtype=torch.bfloat16, device=dev)
-                S = cached[1]
-                self._gdn_replay(conv, g, beta, S, o, B, W, T)
+                self._gdn_conv_replay(lyr, proj, T, cached[0], g, beta, cached[1], o, B, W)
                 if terminal:
                     self._gdn_finish(lyr, o.view(BW, T, -1)[:, -1], proj.view(BW, T, -1)[:, -1],
                                      x_last)
@@ -502,14 +521,9 @@ class Qwen35Runner:
                 if T > 1:
                     follow(cache.layers[li], proj, T - 1, cols * 2, cols * 2, cols * 2)
                 self._gdn_proj(lyr, n, out=pv[:, T - 1])
-                conv = torch.empty(BW * T, C, dtype=torch.bfloat16, device=dev)
-                cs = cached[0]
-                _lib.call("kad_causal_conv_suffix", _lib.ptr(proj), T * cols, 1, cols, _lib.ptr(cs),
-                          *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), 4, None,
-                          _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, stream)
                 g, beta = self._gdn_gates(lyr, proj)
                 o = torch.empty(BW * T, self.vd, dtype=torch.bfloat16, device=dev)
-                self._gdn_replay(conv, g, beta, cached[1], o, B, W, T)
+                self._gdn_conv_replay(lyr, proj, T, cached[0], g, beta, cached[1], o, B, W)
                 o_new = o.view(BW, T, self.vd)[:, T - 1]
                 z_new = pv[:, T - 1, C:C + self.vd]
                 y = layers.rmsnorm_gated(o_new, z_new, lyr.norm_w, cfg.rms_norm_eps, HV)

@@ -263,3 +263,76 @@ def test_conv_width_and_bias_variants(device):
             torch.cuda.synchronize()
             assert_close_rel(out.cpu(), expected, rtol=1e-5, atol_frac=1e-6,
                              name=f"conv width {width} act {act}")
+
+
+def _conv_replay_inputs(B, W, T, H, HV, hist, seed):
+    K = V = 128
+    C = 2 * H * K + HV * V
+    ld = C + 40                     # the projection row carries more columns (z, gates, pad)
+    g = torch.Generator().manual_seed(seed)
+    R = B * W * T
+    proj = (torch.randn(R, ld, generator=g) * 0.7).bfloat16()
+    cs = (torch.randn(B, hist + 2, C, generator=g) * 0.7).bfloat16().transpose(1, 2)  # strided
+    cw = (torch.rand(C, 4, generator=g) - 0.5).bfloat16()
+    logd = -torch.rand(R, HV, generator=g) * 0.3
+    beta = torch.rand(R, HV, generator=g).bfloat16()
+    S = torch.randn(B, HV, K, V, generator=g) * 0.05
+    return proj, cs, cw, logd, beta, S, C, ld
+
+
+@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("W,H,HV,hist", [(16, 2, 2, 4), (48, 4, 8, 4), (256, 2, 4, 6),
+                                         (512, 1, 2, 4)])
+def test_gdn_replay_conv_fused_equals_conv_then_replay(device, T, W, H, HV, hist):
+    """kad_gdn_suffix_replay_conv against kad_causal_conv_suffix followed by
+    kad_gdn_suffix_replay, bit for bit: projection rows wider than q | k | v,
+    a strided prefix conv state with more than 3 slots, GQA heads, beams in
+    one and in several workgroups per request (W = 512)."""
+    B, K = 2, 128
+    proj, cs, cw, logd, beta, S, C, ld = _conv_replay_inputs(B, W, T, H, HV, hist,
+                                                             seed=T * 100 + W + hist)
+    pd, csd, cwd, gd, bd, Sd = _to(device, proj, cs, cw, logd, beta, S)
+    csd = csd[:, :, 1:1 + hist]     # [B, C, hist] view with strides (C*(hist+2), 1, C)
+    R = B * W * T
+    stream = _lib.stream_of(pd)
+    conv = torch.empty(R, C, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_causal_conv_suffix", _lib.ptr(pd), T * ld, 1, ld, _lib.ptr(csd), *csd.stride(),
+              hist, _lib.ptr(cwd), 4, None, _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, stream)
+    o1 = torch.empty(R, HV * K, dtype=torch.bfloat16, device=device)
+    base, es = conv.data_ptr(), conv.element_size()
+    _lib.call("kad_gdn_suffix_replay", _lib.ptr(conv), _lib.ptr_at(base + H * K * es),
+              _lib.ptr_at(base + 2 * H * K * es), C, C, 0, _lib.ptr(gd), 2, _lib.ptr(bd), 0, HV,
+              _lib.ptr(Sd), 2, _lib.ptr(o1), HV * K, B, W, T, H, HV, K, K, K ** -0.5, stream)
+    o2 = torch.full((R, HV * K), 3.0, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_gdn_suffix_replay_conv", _lib.ptr(pd), ld, _lib.ptr(csd), *csd.stride(), hist,
+              _lib.ptr(cwd), _lib.ptr(gd), 2, _lib.ptr(bd), 0, HV, _lib.ptr(Sd), 2, _lib.ptr(o2),
+              HV * K, B, W, T, H, HV, K, K, K ** -0.5, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, o1), "fused conv replay differs from conv then replay"
+    # and the oracle on the conv output the HIP conv produced
+    q = conv[:, :H * K].cpu().reshape(B * W, T, H, K)
+    k = conv[:, H * K:2 * H * K].cpu().reshape(B * W, T, H, K)
+    v = conv[:, 2 * H * K:].cpu().reshape(B * W, T, HV, K)
+    expected = ops_ref.gated_delta(q, k, v, logd.reshape(B * W, T, HV),
+                                   beta.reshape(B * W, T, HV), S, beam_width=W)
+    assert_close_rel(o2.cpu().reshape(B * W, T, HV, K), expected, rtol=1e-2, atol_frac=2e-3,
+                     name=f"fused T={T} W={W}")
+
+
+def test_gdn_replay_conv_rejects_what_it_does_not_fuse(device):
+    """Shapes outside the fused form are refused (the model then makes the two
+    calls): three-token suffixes, beam counts off the 16-beam groups, K = 64."""
+    for T, W, K in [(3, 16, 128), (1, 24, 128), (1, 16, 64)]:
+        B, H, HV = 1, 2, 2
+        C = 2 * H * K + HV * K
+        proj = torch.zeros(B * W * T, C, dtype=torch.bfloat16, device=device)
+        cs = torch.zeros(B, C, 4, dtype=torch.bfloat16, device=device)
+        cw = torch.zeros(C, 4, dtype=torch.bfloat16, device=device)
+        gd = torch.zeros(B * W * T, HV, device=device)
+        bd = torch.zeros(B * W * T, HV, dtype=torch.bfloat16, device=device)
+        Sd = torch.zeros(B, HV, K, K, device=device)
+        o = torch.empty(B * W * T, HV * K, dtype=torch.bfloat16, device=device)
+        with pytest.raises(_lib.KadLibraryError, match="unsupported"):
+            _lib.call("kad_gdn_suffix_replay_conv", _lib.ptr(proj), C, _lib.ptr(cs), *cs.stride(),
+                      4, _lib.ptr(cw), _lib.ptr(gd), 2, _lib.ptr(bd), 0, HV, _lib.ptr(Sd), 2,
+                      _lib.ptr(o), HV * K, B, W, T, H, HV, K, K, K ** -0.5, _lib.stream_of(proj))
