@@ -136,12 +136,15 @@ def kernel_work(name, a):
             + BW * T * HV * 6
         label = "gdn_replay" if name == "kad_gdn_suffix_replay" else "gdn_recurrent"
         return label, "hbm", nbytes, BW * HV * 2 * T * 2 * K * V
-    if name == "kad_gdn_suffix_replay_conv":
-        # pre-conv q|k|v rows in, replay output out (the conv output stays on chip)
-        B, W, T, H, HV, K, V = a[17:24]
+    if name in ("kad_gdn_suffix_replay_conv", "kad_gdn_suffix_replay_conv_gated"):
+        # pre-conv q|k|v rows in, replay output out (the conv output stays on
+        # chip); gated: the gate rows of the normed tokens in, normed rows out
+        gated = name.endswith("_gated")
+        B, W, T, H, HV, K, V = a[22:29] if gated else a[17:24]
         BW, C = B * W, 2 * H * K + HV * V
-        nbytes = BW * T * (C + HV * V) * 2 + B * HV * K * V * _es(a[14]) + BW * T * HV * 6 \
-            + B * C * 3 * 2 + C * 4 * 2
+        t_out = (1 if a[19] else T) if gated else T
+        nbytes = BW * T * C * 2 + BW * t_out * HV * V * 2 * (2 if gated else 1) \
+            + B * HV * K * V * _es(a[14]) + BW * T * HV * 6 + B * C * 3 * 2 + C * 4 * 2
         return "gdn_replay", "hbm", nbytes, BW * HV * 2 * T * 2 * K * V + 8 * BW * C * T
     if name == "kad_causal_conv_suffix":
         B, W, C, T, dt = a[16], a[17], a[18], a[19], a[20]

@@ -82,6 +82,25 @@ int kad_gdn_suffix_replay_conv(const void* proj, int64_t ld_proj, const void* co
                                const void* state, int state_dtype, void* out, int64_t ld_out,
                                int B, int W, int T, int H, int HV, int K, int V, float scale,
                                kad_stream_t stream);
+/* kad_gdn_suffix_replay_conv with the layer's gated RMSNorm applied to each
+ * output row of a value head on its way out, as kad_rmsnorm_gated computes
+ * it (the same bits as the three calls in a row): out = bf16(bf16(w *
+ * bf16(o r)) * silu(z)), r = 1 / sqrt(mean(o^2) + eps).  z: gate rows, (n, t)
+ * at [(n*T+t)*ldz + hv*V + j] (bf16, ldz a multiple of 4, 8-byte aligned);
+ * norm_w: [V] bf16.  last_token_only: only token T-1 of each beam is normed
+ * and written, at out row n (the incremental decode reads no other);
+ * otherwise every token, at row n*T + t.  No counterpart in the reference as
+ * one call: it fuses the decode's causal_conv1d, gated_delta and
+ * Qwen3_5RMSNormGated (src/kadllm/adapters/qwen3_5.py:146-176). */
+int kad_gdn_suffix_replay_conv_gated(const void* proj, int64_t ld_proj, const void* conv_state,
+                                     int64_t ss_b, int64_t ss_c, int64_t ss_t, int history,
+                                     const void* conv_weight, const void* log_decay,
+                                     int gate_dtype, const void* beta, int beta_dtype,
+                                     int64_t ld_gate, const void* state, int state_dtype,
+                                     const void* z, int64_t ldz, const void* norm_w, float eps,
+                                     int last_token_only, void* out, int64_t ld_out, int B,
+                                     int W, int T, int H, int HV, int K, int V, float scale,
+                                     kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
  * Depthwise causal short convolution over [prefix taps || suffix].

@@ -385,7 +385,24 @@ struct ConvTab {
   static constexpr int bytes = chunks * chunk_bytes;
 };
 
-template <int T, int NS, bool CONV>
+// The gated form (GATED, with CONV) passes each output row of a value head
+// through the layer's gated RMSNorm on its way out, with the arithmetic of
+// rmsnorm_gated_kernel<16, 1>: the row's 8-element pieces summed as one fma
+// chain each (a piece spans two lanes here: the first four squares' chain is
+// handed on by a lane shuffle), the 16 piece sums combined in that kernel's
+// butterfly order through LDS, so y equals the replay followed by
+// kad_rmsnorm_gated bit for bit.  Only the tokens from t_first on are
+// normed and written (the last token only in the incremental decode, whose
+// earlier tokens' outputs nothing reads): out row n * (T - t_first) + t - t_first.
+struct GateOutArgs {
+  const bf16_t* z;     // gate rows: (n, t) at z + (n*T + t) * ldz + hv*V
+  int64_t ldz;
+  const bf16_t* w;     // norm weight [V]
+  float eps;
+  int t_first;
+};
+
+template <int T, int NS, bool CONV, bool GATED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 1 ? 3 : (T == 4 ? 1 : 2), 8)))
 void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                            const bf16_t* __restrict__ v, int64_t ld_qk, int64_t ld_v,
@@ -393,7 +410,8 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
                            const void* __restrict__ beta, int beta_dtype, int64_t ld_gate,
                            const void* __restrict__ state, int state_dtype,
                            bf16_t* __restrict__ out, int64_t ld_out, int W, int H, int HV,
-                           float scale, int beams_per_block, int nbb, ConvArgs cv) {
+                           float scale, int beams_per_block, int nbb, ConvArgs cv,
+                           GateOutArgs go) {
   constexpr int KD = 128, VD = 128;
   constexpr int KSTEPS = KD / 32;
   constexpr int VROWS = VD / 4;
@@ -402,9 +420,12 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
   constexpr int BLK = ROWS * 256;            // bytes of one q, k or v block
   constexpr int STAGE = 3 * BLK + 512;      // + the gates: 64 fp32 decays, 64 beta words
   static_assert(!CONV || T <= 2, "the fused conv takes one- and two-token suffixes");
+  static_assert(!GATED || CONV, "the gated output comes with the fused conv");
   constexpr int TAB = CONV ? ConvTab<T>::bytes : 0;
-  __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE + TAB];
+  constexpr int PSUM = GATED ? T * 16 * 16 * 4 : 0;   // [token][beam][piece] row-sum pieces
+  __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE + TAB + PSUM];
   uint8_t* const tab = stage_buf + NS * STAGE;
+  float* const psum = (float*)(stage_buf + NS * STAGE + TAB);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -532,6 +553,12 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
     // the table's stores complete before the first group's barrier
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
+  // the norm weights of this lane's 8 value rows (v0 + mt*16 + quad*4 .. +3)
+  u32x2 gw[GATED ? MT : 1];
+  if constexpr (GATED) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) gw[mt] = *(const u32x2*)(go.w + v0 + mt * 16 + quad * 4);
+  }
 
   // One group.  At its start, group gi's loads (all DMA into LDS, issued
   // NS - 1 groups earlier) must have landed.  The only loads issued after
@@ -551,6 +578,20 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const int s = gi % NS;
+    // the gate rows of the normed tokens, issued before the next DMA so that
+    // waiting for them does not wait for it
+    u32x2 zg[GATED ? T : 1][GATED ? MT : 1];
+    if constexpr (GATED) {
+      const int64_t nz = (int64_t)b * W + n_begin + gi * 16 + col;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        if (t >= go.t_first) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            zg[t][mt] = *(const u32x2*)(go.z + (nz * T + t) * go.ldz + (int64_t)hv * VD + v0 +
+                                        mt * 16 + quad * 4);
+        }
+    }
     if (gi + NS - 1 < ngroups) dma_group(gi + NS - 1, (gi + NS - 1) % NS);
 
     if constexpr (CONV) {
@@ -674,6 +715,64 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
       btf[t] = __uint_as_float((hv & 1) ? (bw & 0xffff0000u) : (bw << 16));
     }
 
+    float og[MT][4];   // a token's outputs, for the gated form
+    // gated RMSNorm of token t's rows and their store (see GateOutArgs)
+    auto gated_out = [&](int t, const float (&o)[MT][4], const u32x2 (&zt)[MT], int64_t nrow) {
+      float f[MT][4];
+      float* ps = psum + t * 256;   // one buffer per token: no barrier between tokens
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        // o rounded to bf16 as the unfused path stores it; this lane's four
+        // squares continue the chain of piece wave*4 + mt*2 + quad/2 that
+        // the lane 16 down began (odd quads), or begin it (even quads)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[mt][i] = round_bf(o[mt][i]);
+        float h = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h += f[mt][i] * f[mt][i];
+        float pc = __shfl_up(h, 16, 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pc += f[mt][i] * f[mt][i];
+        if (quad & 1) ps[col * 16 + wave * 4 + mt * 2 + (quad >> 1)] = pc;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // the 16 pieces in rmsnorm_gated_kernel's butterfly order (partners
+      // xor 8, then 4, 2, 1)
+      float p[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 v4 = *(const f32x4*)(ps + col * 16 + j * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[j * 4 + i] = v4[i];
+      }
+      float s1[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s1[i] = p[i] + p[i + 8];
+      float s2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s2[i] = s1[i] + s1[i + 4];
+      const float s3a = s2[0] + s2[2], s3b = s2[1] + s2[3];
+      const float ss = s3a + s3b;
+      const float r = 1.0f / sqrtf(ss / (float)VD + go.eps);
+      const int64_t orow = nrow * (T - go.t_first) + (t - go.t_first);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t wb = gw[mt][i >> 1], zb = zt[mt][i >> 1];
+          const float wv = __uint_as_float((i & 1) ? (wb & 0xffff0000u) : (wb << 16));
+          const float zv = __uint_as_float((i & 1) ? (zb & 0xffff0000u) : (zb << 16));
+          const float nrm = round_bf(f[mt][i] * r);
+          const float wn = round_bf(wv * nrm);
+          y[i] = wn * silu_fast(zv);
+        }
+        const u32x2 yv = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+        *(u32x2*)(out + orow * ld_out + (int64_t)hv * VD + v0 + mt * 16 + quad * 4) = yv;
+      }
+    };
     float u[T][MT][4];
     float c[T];
     float gam = 1.f;
@@ -706,7 +805,15 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
           o += (kqx[t][t] * rk[t] * rq[t]) * ut;
           ov[i] = o;
         }
-        store4<bf16_t>(out + (n * T + t) * ld_out + (int64_t)hv * VD + e, ov);
+        if constexpr (GATED) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) og[mt][i] = ov[i];
+        } else {
+          store4<bf16_t>(out + (n * T + t) * ld_out + (int64_t)hv * VD + e, ov);
+        }
+      }
+      if constexpr (GATED) {
+        if (t >= go.t_first) gated_out(t, og, zg[t], n);
       }
       c[t] = 1.f;
     }
@@ -743,7 +850,8 @@ int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, in
     hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, NS, false>), dim3((unsigned)nblocks),       \
                        dim3(256), 0, stream, (const bf16_t*)q, (const bf16_t*)k,              \
                        (const bf16_t*)v, ld_qk, ld_v, g, gdt, beta, bdt, ld_gate, state, sdt, \
-                       (bf16_t*)out, ld_out, W, H, HV, scale, bpb, nbb, ConvArgs{});          \
+                       (bf16_t*)out, ld_out, W, H, HV, scale, bpb, nbb, ConvArgs{},           \
+                       GateOutArgs{});                                                        \
     return kad_launch_status("gdn_replay_lds_kernel");                                        \
   }
       KAD_REPLAY_LDS(1, 3)
@@ -796,7 +904,7 @@ int dispatch_dims(int K, int V, const void* q, const void* k, const void* v, int
 int launch_replay_conv(const bf16_t* proj, int64_t ld, const ConvArgs& cv, const void* g,
                        const void* beta, int64_t ld_gate, const void* state, int sdt, void* out,
                        int64_t ld_out, int B, int W, int T, int H, int HV, float scale,
-                       hipStream_t stream) {
+                       const GateOutArgs* go, hipStream_t stream) {
   const int bpb = W <= 256 ? W : 128;
   const int nbb = (int)kad_cdiv(W, bpb);
   const int64_t nblocks = (int64_t)B * HV * nbb;
@@ -804,28 +912,31 @@ int launch_replay_conv(const bf16_t* proj, int64_t ld, const ConvArgs& cv, const
   const bf16_t* q = proj;
   const bf16_t* k = proj + (int64_t)H * 128;
   const bf16_t* v = proj + (int64_t)2 * H * 128;
-#define KAD_REPLAY_CONV(TT)                                                                    \
-  if (T == TT) {                                                                               \
-    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, 3, true>), dim3((unsigned)nblocks), dim3(256), \
-                       0, stream, q, k, v, ld, ld, g, KAD_DTYPE_F32, beta, KAD_DTYPE_BF16,     \
-                       ld_gate, state, sdt, (bf16_t*)out, ld_out, W, H, HV, scale, bpb, nbb,   \
-                       cv);                                                                    \
+#define KAD_REPLAY_CONV(TT, GV)                                                                \
+  if (T == TT && (go != nullptr) == GV) {                                                      \
+    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, 3, true, GV>), dim3((unsigned)nblocks),      \
+                       dim3(256), 0, stream, q, k, v, ld, ld, g, KAD_DTYPE_F32, beta,          \
+                       KAD_DTYPE_BF16, ld_gate, state, sdt, (bf16_t*)out, ld_out, W, H, HV,    \
+                       scale, bpb, nbb, cv, go ? *go : GateOutArgs{});                         \
     return kad_launch_status("gdn_replay_lds_kernel");                                         \
   }
-  KAD_REPLAY_CONV(1)
-  KAD_REPLAY_CONV(2)
+  KAD_REPLAY_CONV(1, false)
+  KAD_REPLAY_CONV(2, false)
+  KAD_REPLAY_CONV(1, true)
+  KAD_REPLAY_CONV(2, true)
 #undef KAD_REPLAY_CONV
   KAD_UNSUPPORTED("the fused conv replay takes 1 or 2 suffix tokens, got %d", T);
 }
 
 }  // namespace
 
-extern "C" int kad_gdn_suffix_replay_conv(
+namespace {
+int replay_conv_common(
     const void* proj, int64_t ld_proj, const void* conv_state, int64_t ss_b, int64_t ss_c,
     int64_t ss_t, int history, const void* conv_weight, const void* log_decay, int gate_dtype,
     const void* beta, int beta_dtype, int64_t ld_gate, const void* state, int state_dtype,
     void* out, int64_t ld_out, int B, int W, int T, int H, int HV, int K, int V, float scale,
-    kad_stream_t stream) {
+    const GateOutArgs* go, kad_stream_t stream) {
   KAD_REQUIRE(proj && conv_state && conv_weight && log_decay && beta && state && out,
               "null pointer argument");
   KAD_REQUIRE(B > 0 && W > 0 && T > 0 && H > 0 && HV > 0 && K > 0 && V > 0,
@@ -853,7 +964,38 @@ extern "C" int kad_gdn_suffix_replay_conv(
   const ConvArgs cv{(const bf16_t*)conv_state, ss_b, ss_c, ss_t, history,
                     (const bf16_t*)conv_weight};
   return launch_replay_conv((const bf16_t*)proj, ld_proj, cv, log_decay, beta, ld_gate, state,
-                            state_dtype, out, ld_out, B, W, T, H, HV, scale, (hipStream_t)stream);
+                            state_dtype, out, ld_out, B, W, T, H, HV, scale, go,
+                            (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int kad_gdn_suffix_replay_conv(
+    const void* proj, int64_t ld_proj, const void* conv_state, int64_t ss_b, int64_t ss_c,
+    int64_t ss_t, int history, const void* conv_weight, const void* log_decay, int gate_dtype,
+    const void* beta, int beta_dtype, int64_t ld_gate, const void* state, int state_dtype,
+    void* out, int64_t ld_out, int B, int W, int T, int H, int HV, int K, int V, float scale,
+    kad_stream_t stream) {
+  return replay_conv_common(proj, ld_proj, conv_state, ss_b, ss_c, ss_t, history, conv_weight,
+                            log_decay, gate_dtype, beta, beta_dtype, ld_gate, state, state_dtype,
+                            out, ld_out, B, W, T, H, HV, K, V, scale, nullptr, stream);
+}
+
+extern "C" int kad_gdn_suffix_replay_conv_gated(
+    const void* proj, int64_t ld_proj, const void* conv_state, int64_t ss_b, int64_t ss_c,
+    int64_t ss_t, int history, const void* conv_weight, const void* log_decay, int gate_dtype,
+    const void* beta, int beta_dtype, int64_t ld_gate, const void* state, int state_dtype,
+    const void* z, int64_t ldz, const void* norm_w, float eps, int last_token_only, void* out,
+    int64_t ld_out, int B, int W, int T, int H, int HV, int K, int V, float scale,
+    kad_stream_t stream) {
+  KAD_REQUIRE(z && norm_w, "null pointer argument");
+  KAD_REQUIRE(ldz % 4 == 0 && ((uintptr_t)z % 8) == 0 && ((uintptr_t)norm_w % 8) == 0,
+              "z rows and the norm weight must be 8-byte aligned (ldz a multiple of 4)");
+  KAD_REQUIRE(ldz >= (int64_t)HV * V, "ldz smaller than a row");
+  const GateOutArgs go{(const bf16_t*)z, ldz, (const bf16_t*)norm_w, eps,
+                       last_token_only ? T - 1 : 0};
+  return replay_conv_common(proj, ld_proj, conv_state, ss_b, ss_c, ss_t, history, conv_weight,
+                            log_decay, gate_dtype, beta, beta_dtype, ld_gate, state, state_dtype,
+                            out, ld_out, B, W, T, H, HV, K, V, scale, &go, stream);
 }
 
 extern "C" int kad_gdn_suffix_replay(const void* q, const void* k, const void* v,

@@ -233,31 +233,46 @@ class Qwen35Runner:
             _lib.call("kad_gdn_recurrent", *args, W, _lib.ptr(o), self.vd, None, B * W, T, H_, HV,
                       dk, dv, float(dk ** -0.5), _lib.stream_of(conv))
 
-    def _gdn_conv_replay(self, lyr, proj, T, cs, g, beta, S, o, B, W):
-        """The conv of the projection rows' q | k | v channels followed by the
-        replay: one fused call (kad_gdn_suffix_replay_conv, the same bits) where
-        it takes the shape, else kad_causal_conv_suffix into a buffer and
-        _gdn_replay.  proj: [B*W*T, cols] rows, token-major within each beam."""
+    def _gdn_mix(self, lyr, proj, T, cached, B, W, last_only):
+        """A GDN layer's suffix mixer up to out_proj: conv of the projection
+        rows' q | k | v channels, replay against the prefix state, gated
+        RMSNorm.  Returns the normed rows [B*W, vd] (each beam's last token,
+        last_only) or [B*W*T, vd].  One fused call
+        (kad_gdn_suffix_replay_conv_gated, the same bits) where it takes the
+        shape, else kad_causal_conv_suffix into a buffer, _gdn_replay and
+        kad_rmsnorm_gated.  proj: [B*W*T, cols] rows, token-major per beam."""
         cfg = self.cfg
         H_, HV = cfg.linear_num_key_heads, cfg.linear_num_value_heads
         dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
         C = self.conv_dim
+        BW = B * W
         ld = proj.stride(0)
+        dev = proj.device
         stream = _lib.stream_of(proj)
-        if (T <= 2 and W % 16 == 0 and dk == 128 and dv == 128 and g.dtype == torch.float32
-                and beta.dtype == torch.bfloat16 and g.stride(0) % 2 == 0 and ld % 8 == 0
-                and proj.data_ptr() % 16 == 0 and lyr.conv_w.is_contiguous()
-                and lyr.conv_w.data_ptr() % 8 == 0):
-            _lib.call("kad_gdn_suffix_replay_conv", _lib.ptr(proj), ld, _lib.ptr(cs),
+        cs, S = cached
+        g, beta = self._gdn_gates(lyr, proj)
+        z = proj[:, C:C + self.vd]
+        if (T <= 2 and W % 16 == 0 and dk == 128 and dv == 128 and g.stride(0) % 2 == 0
+                and ld % 8 == 0 and proj.data_ptr() % 16 == 0 and lyr.conv_w.is_contiguous()
+                and lyr.conv_w.data_ptr() % 8 == 0 and lyr.norm_w.data_ptr() % 8 == 0):
+            y = torch.empty(BW if last_only else BW * T, self.vd, dtype=torch.bfloat16,
+                            device=dev)
+            _lib.call("kad_gdn_suffix_replay_conv_gated", _lib.ptr(proj), ld, _lib.ptr(cs),
                       *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), _lib.ptr(g), 2,
                       _lib.ptr(beta), 0, g.stride(0), _lib.ptr(S), _lib.dtype_code(S.dtype),
-                      _lib.ptr(o), self.vd, B, W, T, H_, HV, dk, dv, float(dk ** -0.5), stream)
-            return
-        conv = torch.empty(proj.shape[0], C, dtype=torch.bfloat16, device=proj.device)
+                      _lib.ptr(z), ld, _lib.ptr(lyr.norm_w), cfg.rms_norm_eps,
+                      1 if last_only else 0, _lib.ptr(y), self.vd, B, W, T, H_, HV, dk, dv,
+                      float(dk ** -0.5), stream)
+            return y
+        conv = torch.empty(proj.shape[0], C, dtype=torch.bfloat16, device=dev)
         _lib.call("kad_causal_conv_suffix", _lib.ptr(proj), T * ld, 1, ld, _lib.ptr(cs),
                   *cs.stride(), cs.shape[-1], _lib.ptr(lyr.conv_w), 4, None,
                   _lib.ptr(conv), T * C, 1, C, B, W, C, T, 0, 1, stream)
+        o = torch.empty(BW * T, self.vd, dtype=torch.bfloat16, device=dev)
         self._gdn_replay(conv, g, beta, S, o, B, W, T)
+        if last_only:
+            o, z = o.view(BW, T, -1)[:, -1], proj.view(BW, T, -1)[:, -1, C:C + self.vd]
+        return layers.rmsnorm_gated(o, z, lyr.norm_w, cfg.rms_norm_eps, HV)
 
     def _gdn_finish(self, lyr, o, proj, x):
         cfg = self.cfg
@@ -400,14 +415,9 @@ class Qwen35Runner:
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
                 proj = self._gdn_proj(lyr, n)
-                g, beta = self._gdn_gates(lyr, proj)
-                o = torch.empty(R, self.vd, dtype=torch.bfloat16, device=dev)
-                self._gdn_conv_replay(lyr, proj, T, cached[0], g, beta, cached[1], o, B, W)
-                if terminal:
-                    self._gdn_finish(lyr, o.view(BW, T, -1)[:, -1], proj.view(BW, T, -1)[:, -1],
-                                     x_last)
-                else:
-                    self._gdn_finish(lyr, o, proj, x)
+                y = self._gdn_mix(lyr, proj, T, cached, B, W, last_only=terminal)
+                xo = x_last if terminal else x
+                layers.gemm(y, lyr.w_out, out=xo, epilogue=layers.EPI_RESIDUAL, residual=xo)
             elif terminal:
                 proj = layers.gemm(n, lyr.w_qkv)
                 ld = proj.stride(0)
@@ -521,12 +531,7 @@ class Qwen35Runner:
                 if T > 1:
                     follow(cache.layers[li], proj, T - 1, cols * 2, cols * 2, cols * 2)
                 self._gdn_proj(lyr, n, out=pv[:, T - 1])
-                g, beta = self._gdn_gates(lyr, proj)
-                o = torch.empty(BW * T, self.vd, dtype=torch.bfloat16, device=dev)
-                self._gdn_conv_replay(lyr, proj, T, cached[0], g, beta, cached[1], o, B, W)
-                o_new = o.view(BW, T, self.vd)[:, T - 1]
-                z_new = pv[:, T - 1, C:C + self.vd]
-                y = layers.rmsnorm_gated(o_new, z_new, lyr.norm_w, cfg.rms_norm_eps, HV)
+                y = self._gdn_mix(lyr, proj, T, cached, B, W, last_only=True)
                 layers.gemm(y, lyr.w_out, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
                 if keep_cache:
                     new_layers.append(proj)

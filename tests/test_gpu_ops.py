@@ -5,7 +5,7 @@ import torch
 
 from _fixtures import bf16_from_bits, conv_inputs, gdn_inputs, load_npz
 from conftest import assert_close_rel
-from kadllm_amd import _lib, ops
+from kadllm_amd import _lib, layers, ops
 from oracle import ops_ref
 
 pytestmark = pytest.mark.gpu
@@ -307,6 +307,24 @@ def test_gdn_replay_conv_fused_equals_conv_then_replay(device, T, W, H, HV, hist
     _lib.call("kad_gdn_suffix_replay_conv", _lib.ptr(pd), ld, _lib.ptr(csd), *csd.stride(), hist,
               _lib.ptr(cwd), _lib.ptr(gd), 2, _lib.ptr(bd), 0, HV, _lib.ptr(Sd), 2, _lib.ptr(o2),
               HV * K, B, W, T, H, HV, K, K, K ** -0.5, stream)
+    # the gated form against kad_rmsnorm_gated of the same outputs (gate rows:
+    # any row-strided bf16 columns, here the projection's from column 8), all
+    # tokens and the last token only
+    zc = pd[:, 8:8 + HV * K]
+    gen = torch.Generator().manual_seed(5 + T)
+    nw = (1.0 + 0.1 * torch.randn(K, generator=gen)).bfloat16().to(device)
+    eps = 1e-6
+    y_all = layers.rmsnorm_gated(o1, zc, nw, eps, HV)
+    y_last = layers.rmsnorm_gated(o1.view(B * W, T, -1)[:, -1], zc.view(B * W, T, -1)[:, -1],
+                                  nw, eps, HV)
+    for last, ref in ((0, y_all), (1, y_last)):
+        yg = torch.full_like(ref, 5.0)
+        _lib.call("kad_gdn_suffix_replay_conv_gated", _lib.ptr(pd), ld, _lib.ptr(csd),
+                  *csd.stride(), hist, _lib.ptr(cwd), _lib.ptr(gd), 2, _lib.ptr(bd), 0, HV,
+                  _lib.ptr(Sd), 2, _lib.ptr(zc), zc.stride(0), _lib.ptr(nw), eps, last,
+                  _lib.ptr(yg), HV * K, B, W, T, H, HV, K, K, K ** -0.5, stream)
+        torch.cuda.synchronize()
+        assert torch.equal(yg, ref), f"gated fused replay differs (last_token_only={last})"
     torch.cuda.synchronize()
     assert torch.equal(o2, o1), "fused conv replay differs from conv then replay"
     # and the oracle on the conv output the HIP conv produced
