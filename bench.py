@@ -136,6 +136,12 @@ def kernel_work(name, a):
             + BW * T * HV * 6
         label = "gdn_replay" if name == "kad_gdn_suffix_replay" else "gdn_recurrent"
         return label, "hbm", nbytes, BW * HV * 2 * T * 2 * K * V
+    if name == "kad_gemm_bf16_conv":
+        # the GDN input projection with the prefill conv in its epilogue: A, W
+        # and the output once (the conv's inputs stay on chip), the conv state
+        M, N, K, Cc, L = a[6], a[7], a[8], a[9], a[11]
+        return "gemm", "mfma", 2 * (M * K + N * K + M * N) + (M // L) * Cc * 4 * 2, \
+            2 * M * N * K
     if name in ("kad_gdn_suffix_replay_conv", "kad_gdn_suffix_replay_conv_gated"):
         # pre-conv q|k|v rows in, replay output out (the conv output stays on
         # chip); gated: the gate rows of the normed tokens in, normed rows out

@@ -139,6 +139,26 @@ int kad_causal_conv_suffix(const void* x, int64_t sx_n, int64_t sx_c, int64_t sx
 int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
                   const void* R, int64_t ldr, int M, int N, int K, int epilogue,
                   kad_stream_t stream);
+
+/* kad_gemm_bf16 (KAD_EPI_STORE) of the prefill's GDN input projection with
+ * the depthwise causal conv (width 4, SiLU, no bias, zero history) of its
+ * first conv_cols columns fused into the epilogue: C[:, :conv_cols] receives
+ * the conv outputs kad_causal_conv_prefill would compute from the projection,
+ * C[:, conv_cols:N] the plain product, conv_state ([M / seq_len, conv_cols, 4]
+ * bf16, nullable) the last 4 inputs of each sequence, all the same bits as
+ * the two calls.  Rows are seq_len-token sequences; workspace: at least
+ * kad_gemm_bf16_conv_workspace_bytes (16-byte aligned).  Supported: M, N,
+ * conv_cols multiples of 256 (conv_cols <= N), K % 64 == 0, seq_len % 128 ==
+ * 0; anything else is KAD_ERR_UNSUPPORTED.  No counterpart in the reference
+ * as one call: it fuses in_proj_qkv and the causal conv1d of the prefill the
+ * reference runs through transformers (src/kadllm/adapters/qwen3_5.py:111),
+ * so the conv's input never reaches HBM. */
+int kad_gemm_bf16_conv_workspace_bytes(int M, int conv_cols, int64_t* bytes);
+int kad_gemm_bf16_conv(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
+                       int64_t ldc, int M, int N, int K, int conv_cols, const void* conv_weight,
+                       int seq_len, void* conv_state, void* workspace, int64_t workspace_bytes,
+                       kad_stream_t stream);
+
 /* Same with an explicit tile configuration, the forms the automatic choice
  * picks from (0 = automatic choice as kad_gemm_bf16; 1 = 32x256 with 4 waves;
  * 2 = 128x128 with 4 waves; 5 = 256x256 with 8 waves; 11 = 64x32 with 2

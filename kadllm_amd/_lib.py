@@ -34,6 +34,8 @@ SIGNATURES = {
     "kad_causal_conv_suffix": "plll" "pllli" "pip" "plll" "iiiiii" "s",
     "kad_gemm_bf16": "plplplpl" "iiii" "s",
     "kad_gemm_bf16_tiled": "plplplpl" "iiiii" "s",
+    "kad_gemm_bf16_conv_workspace_bytes": "iip",
+    "kad_gemm_bf16_conv": "plplpl" "iiii" "pip" "pl" "s",
     "kad_rmsnorm": "plpfpllifs",
     "kad_rmsnorm_gated": "plplpplliifs",
     "kad_gdn_gates": "plplpppplis",

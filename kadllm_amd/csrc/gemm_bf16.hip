@@ -691,6 +691,177 @@ __device__ __forceinline__ void epilogue_x16_chunked(f32x4 (&acc)[NI][NJ], bf16_
   }
 }
 
+// Epilogue of the prefill's GDN input projection (kEpiConv): the columns
+// below ce.cols are the depthwise causal conv's inputs (q | k | v), and the
+// tile leaves them convolved (width 4, SiLU), with conv_prefill_bf16's
+// arithmetic operation for operation: each 16-row block is staged in the
+// wave's LDS region as bf16 (the projection's rounding), and row r of a
+// wave's 128-row sub-tile (which lies inside one sequence) takes its taps from
+// rows r-3 .. r-1 of the block or, across blocks, from a 3-row carry of the
+// previous block.  Rows 0-2 of a sub-tile need the rows before it: they and
+// rows 124-127 go raw to ce.side ([M/128][7][cols]: slots 0-2, then 3-6), and
+// conv_fixup_kernel finishes rows 0-2 and the decode's conv state.  Columns
+// from ce.cols on are stored plain.
+struct ConvEpi {
+  const bf16_t* w;   // [cols, 4] conv weights
+  bf16_t* side;      // [M / 128][7][cols] raw rows 0-2 and 124-127 of every sub-tile
+  int cols;
+};
+constexpr int kEpiConv = 3;   // internal epilogue code (not part of the C ABI)
+
+template <int NI, int NJ>
+__device__ __forceinline__ void epilogue_conv_chunked(f32x4 (&acc)[NI][NJ], bf16_t* ep,
+                                                      bf16_t* carry, int lane, int row0,
+                                                      int col0, bf16_t* C, int64_t ldc,
+                                                      const ConvEpi& ce) {
+  static_assert(NI * 16 == 128 && NJ * 16 == 64, "128 x 64 wave sub-tiles");
+  constexpr int kCols = NJ * 16, kLd = kCols + 8;
+  const int e_row = lane & 15, e_col = (lane >> 4) * 4;
+  // 4 channels per lane (few registers beside the accumulators): rows
+  // c_row + 4 k of a block, channels col0 + c_col .. + 3
+  const int c_row = lane >> 4, c_col = (lane & 15) * 4;
+  // this lane's 4 channels' taps, packed: word j of wpk[h] holds channel
+  // 2h + j/2, taps 2 (j%2) and 2 (j%2) + 1
+  u32x4 wpk[2];
+  {
+    const u32x4* wp = (const u32x4*)(ce.w + (int64_t)(col0 + c_col) * 4);
+    wpk[0] = wp[0];
+    wpk[1] = wp[1];
+  }
+  auto wtap = [&](int ch, int d) {
+    const int flat = ch * 4 + d;
+    const uint32_t word = wpk[flat / 8][(flat % 8) / 2];
+    return __uint_as_float((flat & 1) ? (word & 0xffff0000u) : (word << 16));
+  };
+  bf16_t* side = ce.side + (int64_t)(row0 / 128) * 7 * ce.cols + col0 + c_col;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      u32x2 packed;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        packed[h] = (uint32_t)f2bf(acc[i][j][h * 2]) | ((uint32_t)f2bf(acc[i][j][h * 2 + 1]) << 16);
+      *(u32x2*)(ep + e_row * kLd + j * 16 + e_col) = packed;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int r = c_row + rr * 4, lr = i * 16 + r;   // row in the block, in the sub-tile
+      auto row_at = [&](int src) {   // block row src (-3 .. 15; negative: the carry)
+        return src >= 0 ? *(const u32x2*)(ep + src * kLd + c_col)
+                        : *(const u32x2*)(carry + (src + 3) * kLd + c_col);
+      };
+      u32x2 xw[4];   // rows r-3 .. r
+#pragma unroll
+      for (int d = 0; d < 4; ++d) xw[d] = row_at(r - 3 + d);
+      if (i == 0 && r < 3) {
+        *(u32x2*)(side + (int64_t)r * ce.cols) = xw[3];
+        continue;
+      }
+      if (i == NI - 1 && r >= 12) *(u32x2*)(side + (int64_t)(3 + r - 12) * ce.cols) = xw[3];
+      u32x2 o;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float a[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int ch = e * 2 + hh;
+          float sacc = 0.f;
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            sacc += wtap(ch, d) *
+                    __uint_as_float(hh ? (xw[d][e] & 0xffff0000u) : (xw[d][e] << 16));
+          a[hh] = sacc;
+        }
+        const uint32_t pk = pack_bf16x2(a[0], a[1]);
+        o[e] = pack_bf16x2(silu_fast(__uint_as_float(pk << 16)),
+                           silu_fast(__uint_as_float(pk & 0xffff0000u)));
+      }
+      *(u32x2*)(C + (int64_t)(row0 + lr) * ldc + col0 + c_col) = o;
+    }
+    // rows 13-15 of the block carry into the next (a wave's LDS accesses
+    // complete in order, so the block's reads above are done first)
+    if (lane < 48) {
+      const int cr = lane >> 4, cc = (lane & 15) * 4;
+      *(u32x2*)(carry + cr * kLd + cc) = *(const u32x2*)(ep + (13 + cr) * kLd + cc);
+    }
+  }
+}
+
+// Rows 0-2 of every 128-row sub-tile of the fused conv projection (their
+// taps are rows 125-127 of the sub-tile before, zeros at a sequence start),
+// with conv_prefill_bf16's arithmetic, and the decode's conv state: the last
+// 4 inputs of each sequence, [B, cols, 4].  One thread per (sub-tile, 8
+// channels).
+__global__ __launch_bounds__(256) void conv_fixup_kernel(const bf16_t* __restrict__ side,
+                                                         const bf16_t* __restrict__ w,
+                                                         bf16_t* __restrict__ C, int64_t ldc,
+                                                         bf16_t* __restrict__ state, int nsub,
+                                                         int sub_per_seq, int cols) {
+  const int C8 = cols / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)nsub * C8) return;
+  const int c0 = (int)(idx % C8) * 8;
+  const int sb = (int)(idx / C8);
+  float wt[8][4];
+  {
+    const u32x4* wp = (const u32x4*)(w + (int64_t)c0 * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 r = wp[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int flat = j * 8 + e * 2;
+        wt[flat / 4][flat % 4] = __uint_as_float(r[e] << 16);
+        wt[(flat + 1) / 4][(flat + 1) % 4] = __uint_as_float(r[e] & 0xffff0000u);
+      }
+    }
+  }
+  // xv[0..2]: the taps (rows 125-127 before), xv[3..5]: rows 0-2
+  u32x4 xv[6];
+  const bool seq_start = sb % sub_per_seq == 0;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    xv[k] = seq_start ? u32x4{0u, 0u, 0u, 0u}
+                      : *(const u32x4*)(side + ((int64_t)(sb - 1) * 7 + 4 + k) * cols + c0);
+    xv[3 + k] = *(const u32x4*)(side + ((int64_t)sb * 7 + k) * cols + c0);
+  }
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int ch = e * 2 + hh;
+        float sacc = 0.f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          sacc += wt[ch][d] *
+                  __uint_as_float(hh ? (xv[t + d][e] & 0xffff0000u) : (xv[t + d][e] << 16));
+        a[hh] = sacc;
+      }
+      const uint32_t pk = pack_bf16x2(a[0], a[1]);
+      o[e] = pack_bf16x2(silu_fast(__uint_as_float(pk << 16)),
+                         silu_fast(__uint_as_float(pk & 0xffff0000u)));
+    }
+    *(u32x4*)(C + ((int64_t)sb * 128 + t) * ldc + c0) = o;
+  }
+  if (state && sb % sub_per_seq == sub_per_seq - 1) {
+    const int64_t b = sb / sub_per_seq;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 r = *(const u32x4*)(side + ((int64_t)sb * 7 + 3 + j) * cols + c0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        state[(b * cols + c0 + 2 * e) * 4 + j] = (bf16_t)(r[e] & 0xffffu);
+        state[(b * cols + c0 + 2 * e + 1) * 4 + j] = (bf16_t)(r[e] >> 16);
+      }
+    }
+  }
+}
+
 template <int EPI, int BN>
 __global__ __launch_bounds__(512, 1) void gemm_x16p_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
@@ -865,14 +1036,15 @@ template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_ppp_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
     bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N, int K, int n_major,
-    int group, int ntiles) {
+    int group, int ntiles, ConvEpi ce) {
   using TX = Tile256;
   constexpr int BM = TX::BM, BN = TX::BN;
   constexpr int NW = TX::NW, WN = TX::WN, NI = TX::NI, NJ = TX::NJ;
   constexpr int kStage = TX::Stage, AG = TX::AG, WGW = TX::WGW;
   constexpr int kLoads = AG + WGW;
   constexpr int kEpiChunk = 16 * ((EPI == KAD_EPI_SWIGLU ? NJ * 8 : NJ * 16) + 8);
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[2 * kStage + NW * kEpiChunk];
+  constexpr int kCarry = EPI == kEpiConv ? 3 * (NJ * 16 + 8) : 0;   // per wave
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[2 * kStage + NW * (kEpiChunk + kCarry)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -988,8 +1160,17 @@ __global__ __launch_bounds__(512, 1) void gemm_ppp_kernel(
     int m0, n0;
     origin(r, m0, n0);
     const int col0 = EPI == KAD_EPI_SWIGLU ? (n0 + wn * NJ * 16) / 2 : n0 + wn * NJ * 16;
-    epilogue_x16_chunked<EPI, NI, NJ>(acc, ep, lane, m0 + wm * NI * 16, col0, C, ldc, R, ldr, M,
-                                      N);
+    if constexpr (EPI == kEpiConv) {
+      if (n0 < ce.cols)
+        epilogue_conv_chunked<NI, NJ>(acc, ep, smem + 2 * kStage + NW * kEpiChunk + swave * kCarry,
+                                      lane, m0 + wm * NI * 16, col0, C, ldc, ce);
+      else
+        epilogue_x16_chunked<KAD_EPI_STORE, NI, NJ>(acc, ep, lane, m0 + wm * NI * 16, col0, C,
+                                                    ldc, R, ldr, M, N);
+    } else {
+      epilogue_x16_chunked<EPI, NI, NJ>(acc, ep, lane, m0 + wm * NI * 16, col0, C, ldc, R, ldr,
+                                        M, N);
+    }
   };
 
   zero();
@@ -1010,6 +1191,9 @@ __global__ __launch_bounds__(512, 1) void gemm_ppp_kernel(
       if (kt == 0 && g > 0) {
         epilogue(g / KT - 1);
         zero();
+        // the conv epilogue needs the registers that the next slice's
+        // fragments would hold if their reads were hoisted above it
+        if constexpr (EPI == kEpiConv) __builtin_amdgcn_sched_barrier(0);
       }
       read_slice(g);
       if (g >= 1) issue();
@@ -1036,6 +1220,7 @@ __global__ __launch_bounds__(512, 1) void gemm_ppp_kernel(
         __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
         epilogue(g / KT - 1);
         zero();
+        if constexpr (EPI == kEpiConv) __builtin_amdgcn_sched_barrier(0);
       }
       issue();
       read_slice(g);
@@ -1061,7 +1246,8 @@ __global__ __launch_bounds__(512, 1) void gemm_ppp_kernel(
 
 template <int EPI>
 int launch_ppp(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
-               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s,
+               const ConvEpi& ce = ConvEpi{}) {
   const int64_t ntiles = kad_cdiv(M, 256) * kad_cdiv(N, 256);
   if (ntiles > 0x7fffffff / 2 || ntiles * (K / kBK) > 0x7fffffff)
     KAD_UNSUPPORTED("gemm grid too large");
@@ -1075,7 +1261,7 @@ int launch_ppp(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, 
   const int n_major = (int64_t)N >= (int64_t)M ? 1 : 0;
   hipLaunchKernelGGL((gemm_ppp_kernel<EPI>), dim3((unsigned)grid), dim3(512), 0, s,
                      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
-                     (const bf16_t*)R, ldr, M, N, K, n_major, 8, (int)ntiles);
+                     (const bf16_t*)R, ldr, M, N, K, n_major, 8, (int)ntiles, ce);
   return kad_launch_status("gemm_ppp_kernel");
 }
 
@@ -1670,4 +1856,46 @@ extern "C" int kad_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t 
                              int64_t ldc, const void* R, int64_t ldr, int M, int N, int K,
                              int epilogue, kad_stream_t stream) {
   return kad_gemm_bf16_tiled(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, epilogue, 0, stream);
+}
+
+extern "C" int kad_gemm_bf16_conv_workspace_bytes(int M, int conv_cols, int64_t* bytes) {
+  KAD_REQUIRE(bytes, "null pointer argument");
+  KAD_REQUIRE(M > 0 && conv_cols > 0, "dimensions must be positive");
+  *bytes = (int64_t)((M + 127) / 128) * 7 * conv_cols * 2;
+  return KAD_OK;
+}
+
+extern "C" int kad_gemm_bf16_conv(const void* A, int64_t lda, const void* W, int64_t ldw, void* C,
+                                  int64_t ldc, int M, int N, int K, int conv_cols,
+                                  const void* conv_weight, int seq_len, void* conv_state,
+                                  void* workspace, int64_t workspace_bytes, kad_stream_t stream) {
+  KAD_REQUIRE(A && W && C && conv_weight && workspace, "null pointer argument");
+  KAD_REQUIRE(M > 0 && N > 0 && K > 0 && conv_cols > 0 && seq_len > 0,
+              "dimensions must be positive");
+  KAD_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0,
+              "lda/ldw must be >= K and multiples of 8");
+  KAD_REQUIRE(((uintptr_t)A | (uintptr_t)W) % 16 == 0, "A and W must be 16-byte aligned");
+  KAD_REQUIRE(ldc >= N && ldc % 8 == 0 && ((uintptr_t)C % 16) == 0,
+              "C rows must be 16-byte aligned with ldc >= N");
+  KAD_REQUIRE(((uintptr_t)conv_weight % 16) == 0, "the conv weight must be 16-byte aligned");
+  KAD_REQUIRE(M % seq_len == 0, "M must be a whole number of sequences");
+  int64_t need = 0;
+  kad_gemm_bf16_conv_workspace_bytes(M, conv_cols, &need);
+  KAD_REQUIRE(workspace_bytes >= need, "workspace of %lld bytes is smaller than %lld",
+              (long long)workspace_bytes, (long long)need);
+  KAD_REQUIRE(((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
+  if (K % kBK || M % 256 || N % 256 || conv_cols % 256 || conv_cols > N || seq_len % 128)
+    KAD_UNSUPPORTED("the conv projection takes M, N, conv_cols multiples of 256 (conv_cols <= N), "
+                    "K %% %d == 0 and sequences of a multiple of 128 rows (got M=%d N=%d K=%d "
+                    "conv_cols=%d seq_len=%d)", kBK, M, N, K, conv_cols, seq_len);
+  hipStream_t s = (hipStream_t)stream;
+  const ConvEpi ce{(const bf16_t*)conv_weight, (bf16_t*)workspace, conv_cols};
+  if (const int rc = launch_ppp<kEpiConv>(A, lda, W, ldw, C, ldc, nullptr, 0, M, N, K, s, ce))
+    return rc;
+  const int nsub = M / 128;
+  const int64_t threads = (int64_t)nsub * (conv_cols / 8);
+  hipLaunchKernelGGL(conv_fixup_kernel, dim3((unsigned)kad_cdiv(threads, 256)), dim3(256), 0, s,
+                     (const bf16_t*)workspace, (const bf16_t*)conv_weight, (bf16_t*)C, ldc,
+                     (bf16_t*)conv_state, nsub, seq_len / 128, conv_cols);
+  return kad_launch_status("conv_fixup_kernel");
 }

@@ -20,6 +20,7 @@ bf16 with the reference's rounding points.  Nothing here falls back to a
 non-HIP implementation: every numeric step is a libkadllm_hip entry point.
 """
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -205,6 +206,40 @@ class Qwen35Runner:
         layers.gemm(n, lyr.w_ab, out=out[:, c:c + lyr.w_ab.shape[0]])
         return out
 
+    def _gdn_proj_conv(self, lyr, n, B, L, conv_state):
+        """The prefill's projection rows and the causal conv (+ SiLU) of their
+        q | k | v channels: (proj [rows, gdn_cols], conv) with conv the rows
+        holding the conv outputs in columns [0, conv_dim).  Where the shape
+        allows, one call (kad_gemm_bf16_conv) writes the conv outputs straight
+        into proj's q | k | v columns (the same bits), and conv is proj;
+        otherwise the plain projection and kad_causal_conv_prefill into a
+        buffer of its own.  conv_state receives each prompt's last 4 inputs."""
+        rows = n.shape[0]
+        C = self.conv_dim
+        c = C + self.vd
+        dev = n.device
+        stream = _lib.stream_of(n)
+        w_in = lyr.w_in
+        if (L % 128 == 0 and rows % 256 == 0 and c % 256 == 0 and C % 256 == 0
+                and n.shape[1] % 64 == 0 and lyr.conv_w.is_contiguous()
+                and lyr.conv_w.data_ptr() % 16 == 0):
+            proj = torch.empty(rows, self.gdn_cols, dtype=torch.bfloat16, device=dev)
+            nb = ctypes.c_int64(0)
+            _lib.call("kad_gemm_bf16_conv_workspace_bytes", rows, C, ctypes.byref(nb))
+            ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+            _lib.call("kad_gemm_bf16_conv", _lib.ptr(n), n.stride(0), _lib.ptr(w_in),
+                      w_in.stride(0), _lib.ptr(proj), proj.stride(0), rows, c, n.shape[1], C,
+                      _lib.ptr(lyr.conv_w), L, _lib.ptr(conv_state), _lib.ptr(ws), ws.numel(),
+                      stream)
+            layers.gemm(n, lyr.w_ab, out=proj[:, c:c + lyr.w_ab.shape[0]])
+            return proj, proj
+        proj = self._gdn_proj(lyr, n)
+        conv = torch.empty(rows, C, dtype=torch.bfloat16, device=dev)
+        _lib.call("kad_causal_conv_prefill", _lib.ptr(proj), proj.stride(0), _lib.ptr(lyr.conv_w),
+                  _lib.ptr(conv), conv.stride(0), _lib.ptr(conv_state), n.shape[0] // L, L, C, 1,
+                  stream)
+        return proj, conv
+
     def _gdn_gates(self, lyr, proj):
         hv = self.cfg.linear_num_value_heads
         o = self.conv_dim + self.vd
@@ -330,20 +365,17 @@ class Qwen35Runner:
             terminal = li == len(self.layers) - 1
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
-                proj = self._gdn_proj(lyr, n)
-                conv = torch.empty(rows, self.conv_dim, dtype=torch.bfloat16, device=dev)
                 conv_state = torch.empty(B, self.conv_dim, 4, dtype=torch.bfloat16, device=dev)
-                _lib.call("kad_causal_conv_prefill", _lib.ptr(proj), proj.stride(0),
-                          _lib.ptr(lyr.conv_w), _lib.ptr(conv), conv.stride(0),
-                          _lib.ptr(conv_state), B, L, self.conv_dim, 1, _lib.stream_of(x))
+                proj, conv = self._gdn_proj_conv(lyr, n, B, L, conv_state)
                 g, beta = self._gdn_gates(lyr, proj)
                 o = torch.empty(rows, self.vd, dtype=torch.bfloat16, device=dev)
                 S = torch.empty(B, HV, dk, dv, dtype=torch.float32, device=dev)
                 base = conv.data_ptr()
                 es = conv.element_size()
                 ws = _lib.gdn_chunk_workspace(B, L, HV, dk, dev)
+                ldc = conv.stride(0)
                 args = (_lib.ptr(conv), _lib.ptr_at(base + self.kd * es),
-                        _lib.ptr_at(base + 2 * self.kd * es), self.conv_dim, self.conv_dim, 0,
+                        _lib.ptr_at(base + 2 * self.kd * es), ldc, ldc, 0,
                         _lib.ptr(g), 2, _lib.ptr(beta), 0, HV, None, 2, 1, _lib.ptr(o), self.vd,
                         _lib.ptr(S), _lib.ptr(ws), ws.numel(), B, L, H_, HV, dk, dv,
                         float(dk ** -0.5))

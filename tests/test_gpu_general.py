@@ -2,10 +2,12 @@
 fp32/fp16 selection, beams above 1024) and the reference's toy model on them,
 against the oracle and the reference's own outputs."""
 
+import ctypes
+
 import pytest
 import torch
 
-from kadllm_amd import grbeam_search, ops
+from kadllm_amd import _lib, grbeam_search, ops
 from kadllm_amd.attention import prefix_attention_decode
 from kadllm_amd.grbeam import select_level
 from _fixtures import gdn_inputs
@@ -270,3 +272,54 @@ def test_reference_hybrid_lm_matches_reference_outputs(device, ci):
     assert torch.equal(result.tokens.cpu(), c["tokens"])
     torch.testing.assert_close(result.scores.cpu(), c["scores"], atol=1e-4, rtol=1e-5)
     assert torch.equal(result.valid.cpu(), c["valid"])
+
+
+@pytest.mark.parametrize("B,L,N,C,K", [(2, 128, 1024, 768, 256), (3, 256, 512, 256, 128),
+                                       (1, 1024, 1024, 512, 64), (2, 256, 8192, 6144, 1024)])
+def test_gemm_conv_prefill_equals_gemm_then_conv(device, B, L, N, C, K):
+    """kad_gemm_bf16_conv against kad_gemm_bf16 followed by
+    kad_causal_conv_prefill, bit for bit: the conv columns, the plain columns
+    past them, and the conv state; sequences of one and of several 128-row
+    blocks per tile, a wider output row stride (the last case is the GDN
+    input projection of the 0.8B model)."""
+    M = B * L
+    g = torch.Generator().manual_seed(M + N + C + K)
+    a = (torch.randn(M, K, generator=g) * 0.5).bfloat16().to(device)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).bfloat16().to(device)
+    cw = (torch.rand(C, 4, generator=g) - 0.5).bfloat16().to(device)
+    ldc = N + 64
+    stream = _lib.stream_of(a)
+    plain = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_gemm_bf16", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(plain), N, None, 0, M, N, K,
+              0, stream)
+    conv = torch.empty(M, C, dtype=torch.bfloat16, device=device)
+    st1 = torch.empty(B, C, 4, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_causal_conv_prefill", _lib.ptr(plain), N, _lib.ptr(cw), _lib.ptr(conv), C,
+              _lib.ptr(st1), B, L, C, 1, stream)
+    nb = ctypes.c_int64(0)
+    _lib.call("kad_gemm_bf16_conv_workspace_bytes", M, C, ctypes.byref(nb))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=device)
+    out = torch.full((M, ldc), 9.0, dtype=torch.bfloat16, device=device)
+    st2 = torch.empty(B, C, 4, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_gemm_bf16_conv", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(out), ldc, M, N, K, C,
+              _lib.ptr(cw), L, _lib.ptr(st2), _lib.ptr(ws), ws.numel(), stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :C], conv), "fused conv columns differ"
+    assert torch.equal(out[:, C:N], plain[:, C:]), "plain columns differ"
+    assert torch.equal(st2, st1), "conv state differs"
+    assert (out[:, N:].float() == 9.0).all(), "wrote past N"
+
+
+def test_gemm_conv_prefill_rejects_unsupported(device):
+    """Shapes off the fused form are refused (the model then makes the two calls)."""
+    a = torch.zeros(256, 64, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(512, 64, dtype=torch.bfloat16, device=device)
+    cw = torch.zeros(256, 4, dtype=torch.bfloat16, device=device)
+    out = torch.empty(256, 512, dtype=torch.bfloat16, device=device)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=device)
+    # sequences of 64 rows; conv columns not a multiple of 256
+    for L, C in ((64, 256), (128, 128)):
+        with pytest.raises(_lib.KadLibraryError, match="unsupported"):
+            _lib.call("kad_gemm_bf16_conv", _lib.ptr(a), 64, _lib.ptr(w), 64, _lib.ptr(out), 512,
+                      256, 512, 64, C, _lib.ptr(cw), L, None, _lib.ptr(ws), ws.numel(),
+                      _lib.stream_of(a))
