@@ -717,9 +717,10 @@ __device__ __forceinline__ void epilogue_conv_chunked(f32x4 (&acc)[NI][NJ], bf16
   static_assert(NI * 16 == 128 && NJ * 16 == 64, "128 x 64 wave sub-tiles");
   constexpr int kCols = NJ * 16, kLd = kCols + 8;
   const int e_row = lane & 15, e_col = (lane >> 4) * 4;
-  // 4 channels per lane (few registers beside the accumulators): rows
-  // c_row + 4 k of a block, channels col0 + c_col .. + 3
-  const int c_row = lane >> 4, c_col = (lane & 15) * 4;
+  // 4 channels x 4 consecutive rows per lane (rows 4 rg .. 4 rg + 3 of a
+  // block, channels col0 + c_col .. + 3): the 7 input rows of its window are
+  // read and widened once
+  const int rg = lane >> 4, c_col = (lane & 15) * 4;
   // this lane's 4 channels' taps, packed: word j of wpk[h] holds channel
   // 2h + j/2, taps 2 (j%2) and 2 (j%2) + 1
   u32x4 wpk[2];
@@ -744,40 +745,51 @@ __device__ __forceinline__ void epilogue_conv_chunked(f32x4 (&acc)[NI][NJ], bf16
         packed[h] = (uint32_t)f2bf(acc[i][j][h * 2]) | ((uint32_t)f2bf(acc[i][j][h * 2 + 1]) << 16);
       *(u32x2*)(ep + e_row * kLd + j * 16 + e_col) = packed;
     }
+    // window rows 4 rg - 3 .. 4 rg + 3 (negative: the carry of the block before)
+    u32x2 xw[7];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int r = c_row + rr * 4, lr = i * 16 + r;   // row in the block, in the sub-tile
-      auto row_at = [&](int src) {   // block row src (-3 .. 15; negative: the carry)
-        return src >= 0 ? *(const u32x2*)(ep + src * kLd + c_col)
-                        : *(const u32x2*)(carry + (src + 3) * kLd + c_col);
-      };
-      u32x2 xw[4];   // rows r-3 .. r
+    for (int d = 0; d < 7; ++d) {
+      const int src = rg * 4 - 3 + d;
+      xw[d] = src >= 0 ? *(const u32x2*)(ep + src * kLd + c_col)
+                       : *(const u32x2*)(carry + (src + 3) * kLd + c_col);
+    }
+    if (i == 0 && rg == 0) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) xw[d] = row_at(r - 3 + d);
-      if (i == 0 && r < 3) {
-        *(u32x2*)(side + (int64_t)r * ce.cols) = xw[3];
-        continue;
+      for (int r = 0; r < 3; ++r) *(u32x2*)(side + (int64_t)r * ce.cols) = xw[3 + r];
+    }
+    if (i == NI - 1 && rg == 3) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) *(u32x2*)(side + (int64_t)(3 + r) * ce.cols) = xw[3 + r];
+    }
+    u32x2 o[4];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {   // channel pair 2e, 2e + 1
+      float xf[2][7];
+#pragma unroll
+      for (int d = 0; d < 7; ++d) {
+        xf[0][d] = __uint_as_float(xw[d][e] << 16);
+        xf[1][d] = __uint_as_float(xw[d][e] & 0xffff0000u);
       }
-      if (i == NI - 1 && r >= 12) *(u32x2*)(side + (int64_t)(3 + r - 12) * ce.cols) = xw[3];
-      u32x2 o;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
+      for (int q = 0; q < 4; ++q) {   // row 4 rg + q: inputs xf[.][q .. q + 3]
         float a[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const int ch = e * 2 + hh;
           float sacc = 0.f;
 #pragma unroll
-          for (int d = 0; d < 4; ++d)
-            sacc += wtap(ch, d) *
-                    __uint_as_float(hh ? (xw[d][e] & 0xffff0000u) : (xw[d][e] << 16));
+          for (int d = 0; d < 4; ++d) sacc += wtap(e * 2 + hh, d) * xf[hh][q + d];
           a[hh] = sacc;
         }
         const uint32_t pk = pack_bf16x2(a[0], a[1]);
-        o[e] = pack_bf16x2(silu_fast(__uint_as_float(pk << 16)),
-                           silu_fast(__uint_as_float(pk & 0xffff0000u)));
+        o[q][e] = pack_bf16x2(silu_fast(__uint_as_float(pk << 16)),
+                              silu_fast(__uint_as_float(pk & 0xffff0000u)));
       }
-      *(u32x2*)(C + (int64_t)(row0 + lr) * ldc + col0 + c_col) = o;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = rg * 4 + q;
+      if (i == 0 && r < 3) continue;   // finished by conv_fixup_kernel
+      *(u32x2*)(C + (int64_t)(row0 + i * 16 + r) * ldc + col0 + c_col) = o[q];
     }
     // rows 13-15 of the block carry into the next (a wave's LDS accesses
     // complete in order, so the block's reads above are done first)
