@@ -202,8 +202,10 @@ class Qwen35Runner:
         if out is None:
             out = torch.empty(n.shape[0], self.gdn_cols, dtype=torch.bfloat16, device=n.device)
         c = self.conv_dim + self.vd
-        layers.gemm(n, lyr.w_in, out=out[:, :c])
+        # the 32-column gate projection first, while n is still in the caches
+        # the large projection's output then sweeps out
         layers.gemm(n, lyr.w_ab, out=out[:, c:c + lyr.w_ab.shape[0]])
+        layers.gemm(n, lyr.w_in, out=out[:, :c])
         return out
 
     def _gdn_proj_conv(self, lyr, n, B, L, conv_state):
@@ -224,6 +226,7 @@ class Qwen35Runner:
                 and n.shape[1] % 64 == 0 and lyr.conv_w.is_contiguous()
                 and lyr.conv_w.data_ptr() % 16 == 0):
             proj = torch.empty(rows, self.gdn_cols, dtype=torch.bfloat16, device=dev)
+            layers.gemm(n, lyr.w_ab, out=proj[:, c:c + lyr.w_ab.shape[0]])
             nb = ctypes.c_int64(0)
             _lib.call("kad_gemm_bf16_conv_workspace_bytes", rows, C, ctypes.byref(nb))
             ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
@@ -231,7 +234,6 @@ class Qwen35Runner:
                       w_in.stride(0), _lib.ptr(proj), proj.stride(0), rows, c, n.shape[1], C,
                       _lib.ptr(lyr.conv_w), L, _lib.ptr(conv_state), _lib.ptr(ws), ws.numel(),
                       stream)
-            layers.gemm(n, lyr.w_ab, out=proj[:, c:c + lyr.w_ab.shape[0]])
             return proj, proj
         proj = self._gdn_proj(lyr, n)
         conv = torch.empty(rows, C, dtype=torch.bfloat16, device=dev)
