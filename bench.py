@@ -64,12 +64,13 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 T975 = {1: 12.706, 2: 4.303, 3: 3.182, 4: 2.776, 5: 2.571, 6: 2.447, 7: 2.365, 9: 2.262}
 
-# HBM bytes per GEMM call of the default workload: rocprofv3 FETCH_SIZE and
-# WRITE_SIZE over the GEMM dispatches of one search, each scaled by its reading
-# for a 1 GiB device copy (reads x2.0, writes x1.0), divided by the number of
-# GEMM calls (346; a call that splits its last round launches two kernels).
-# Re-measured with the commands in profiles/hbm_traffic_and_busy_b32_p1024_w256.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 378.8e6
+# HBM bytes per plain GEMM call of the default workload: rocprofv3 FETCH_SIZE
+# and WRITE_SIZE over the GEMM dispatches of one search (the fused conv
+# projection apart), each scaled by its reading for a 1 GiB device copy (reads
+# x2.0, writes x1.0), divided by the number of GEMM calls (328; a call that
+# splits its last round launches two kernels).  Re-measured with the commands
+# in profiles/hbm_traffic_and_busy_b32_p1024_w256.md.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 326.0e6
 
 
 def repeat_stability(outputs, first):
@@ -137,10 +138,12 @@ def kernel_work(name, a):
         label = "gdn_replay" if name == "kad_gdn_suffix_replay" else "gdn_recurrent"
         return label, "hbm", nbytes, BW * HV * 2 * T * 2 * K * V
     if name == "kad_gemm_bf16_conv":
-        # the GDN input projection with the prefill conv in its epilogue: A, W
-        # and the output once (the conv's inputs stay on chip), the conv state
+        # the prefill's GDN input projection with the depthwise conv in its
+        # epilogue (a class of its own: its time includes the conv's VALU
+        # work): A, W and the output once (the conv's inputs stay on chip),
+        # the conv state
         M, N, K, Cc, L = a[6], a[7], a[8], a[9], a[11]
-        return "gemm", "mfma", 2 * (M * K + N * K + M * N) + (M // L) * Cc * 4 * 2, \
+        return "gemm_conv", "mfma", 2 * (M * K + N * K + M * N) + (M // L) * Cc * 4 * 2, \
             2 * M * N * K
     if name in ("kad_gdn_suffix_replay_conv", "kad_gdn_suffix_replay_conv_gated"):
         # pre-conv q|k|v rows in, replay output out (the conv output stays on
