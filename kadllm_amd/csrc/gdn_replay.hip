@@ -402,7 +402,9 @@ struct GateOutArgs {
   int t_first;
 };
 
-template <int T, int NS, bool CONV, bool GATED = false>
+// LAST (with GATED, last token only): the earlier tokens' q, whose outputs
+// nothing reads, enter no product (their k and v still update the state)
+template <int T, int NS, bool CONV, bool GATED = false, bool LAST = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 1 ? 3 : (T == 4 ? 1 : 2), 8)))
 void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                            const bf16_t* __restrict__ v, int64_t ld_qk, int64_t ld_v,
@@ -421,6 +423,8 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
   constexpr int STAGE = 3 * BLK + 512;      // + the gates: 64 fp32 decays, 64 beta words
   static_assert(!CONV || T <= 2, "the fused conv takes one- and two-token suffixes");
   static_assert(!GATED || CONV, "the gated output comes with the fused conv");
+  static_assert(!LAST || GATED, "the last-token form is a gated form");
+  constexpr int TQ = LAST ? T - 1 : 0;   // the first token whose q is used
   constexpr int TAB = CONV ? ConvTab<T>::bytes : 0;
   constexpr int PSUM = GATED ? T * 16 * 16 * 4 : 0;   // [token][beam][piece] row-sum pieces
   __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE + TAB + PSUM];
@@ -672,34 +676,36 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
       for (int t = 0; t < T; ++t) {
         const int r = col * T + t;
         const int off = r * 256 + (((ks * 4 + quad) ^ (col & 15)) * 16);
-        fq[t] = *(const bf16x8*)(sq + off);
+        if (t >= TQ) fq[t] = *(const bf16x8*)(sq + off);
         fk[t] = *(const bf16x8*)(sk + off);
       }
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        qq[t] = dot8_bf16(fq[t], fq[t], qq[t]);
+        if (t >= TQ) qq[t] = dot8_bf16(fq[t], fq[t], qq[t]);
         kk[t] = dot8_bf16(fk[t], fk[t], kk[t]);
 #pragma unroll
         for (int j = 0; j <= t; ++j) {
-          kqx[j][t] = dot8_bf16(fk[j], fq[t], kqx[j][t]);
+          if (t >= TQ) kqx[j][t] = dot8_bf16(fk[j], fq[t], kqx[j][t]);
           if (j < t) kkx[j][t] = dot8_bf16(fk[j], fk[t], kkx[j][t]);
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc_k[t][mt] = mfma16x16x32(a_hi[mt][ks], fk[t], acc_k[t][mt]);
           acc_k[t][mt] = mfma16x16x32(a_lo[mt][ks], fk[t], acc_k[t][mt]);
-          acc_q[t][mt] = mfma16x16x32(a_hi[mt][ks], fq[t], acc_q[t][mt]);
-          acc_q[t][mt] = mfma16x16x32(a_lo[mt][ks], fq[t], acc_q[t][mt]);
+          if (t >= TQ) {
+            acc_q[t][mt] = mfma16x16x32(a_hi[mt][ks], fq[t], acc_q[t][mt]);
+            acc_q[t][mt] = mfma16x16x32(a_lo[mt][ks], fq[t], acc_q[t][mt]);
+          }
         }
       }
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      qq[t] = add_xor32(add_xor16(qq[t]));
+      if (t >= TQ) qq[t] = add_xor32(add_xor16(qq[t]));
       kk[t] = add_xor32(add_xor16(kk[t]));
 #pragma unroll
       for (int j = 0; j <= t; ++j) {
-        kqx[j][t] = add_xor32(add_xor16(kqx[j][t]));
+        if (t >= TQ) kqx[j][t] = add_xor32(add_xor16(kqx[j][t]));
         if (j < t) kkx[j][t] = add_xor32(add_xor16(kkx[j][t]));
       }
     }
@@ -708,7 +714,7 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       rk[t] = 1.0f / sqrtf(kk[t] + 1e-6f);
-      rq[t] = scale / sqrtf(qq[t] + 1e-6f);
+      rq[t] = t >= TQ ? scale / sqrtf(qq[t] + 1e-6f) : 0.f;
       const uint8_t* sg = stage_buf + s * STAGE + 3 * BLK;
       et[t] = expf(((const float*)sg)[col * T + t]);
       const uint32_t bw = ((const uint32_t*)(sg + 256))[col * T + t];
@@ -799,12 +805,14 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
           for (int j = 0; j < t; ++j) recall += c[j] * (kkx[j][t] * rk[j] * rk[t]) * u[j][mt][i];
           const float ut = btf[t] * (vt[i] - recall);
           u[t][mt][i] = ut;
+          if (t < TQ) continue;   // an output nothing reads
           float o = gam * (acc_q[t][mt][i] * rq[t]);
 #pragma unroll
           for (int j = 0; j < t; ++j) o += c[j] * (kqx[j][t] * rk[j] * rq[t]) * u[j][mt][i];
           o += (kqx[t][t] * rk[t] * rq[t]) * ut;
           ov[i] = o;
         }
+        if (t < TQ) continue;
         if constexpr (GATED) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) og[mt][i] = ov[i];
@@ -912,18 +920,20 @@ int launch_replay_conv(const bf16_t* proj, int64_t ld, const ConvArgs& cv, const
   const bf16_t* q = proj;
   const bf16_t* k = proj + (int64_t)H * 128;
   const bf16_t* v = proj + (int64_t)2 * H * 128;
-#define KAD_REPLAY_CONV(TT, GV)                                                                \
-  if (T == TT && (go != nullptr) == GV) {                                                      \
-    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, 3, true, GV>), dim3((unsigned)nblocks),      \
+  const bool last = go != nullptr && go->t_first == T - 1 && T > 1;
+#define KAD_REPLAY_CONV(TT, GV, LV)                                                            \
+  if (T == TT && (go != nullptr) == GV && last == LV) {                                        \
+    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, 3, true, GV, LV>), dim3((unsigned)nblocks),  \
                        dim3(256), 0, stream, q, k, v, ld, ld, g, KAD_DTYPE_F32, beta,          \
                        KAD_DTYPE_BF16, ld_gate, state, sdt, (bf16_t*)out, ld_out, W, H, HV,    \
                        scale, bpb, nbb, cv, go ? *go : GateOutArgs{});                         \
     return kad_launch_status("gdn_replay_lds_kernel");                                         \
   }
-  KAD_REPLAY_CONV(1, false)
-  KAD_REPLAY_CONV(2, false)
-  KAD_REPLAY_CONV(1, true)
-  KAD_REPLAY_CONV(2, true)
+  KAD_REPLAY_CONV(1, false, false)
+  KAD_REPLAY_CONV(2, false, false)
+  KAD_REPLAY_CONV(1, true, false)
+  KAD_REPLAY_CONV(2, true, false)
+  KAD_REPLAY_CONV(2, true, true)
 #undef KAD_REPLAY_CONV
   KAD_UNSUPPORTED("the fused conv replay takes 1 or 2 suffix tokens, got %d", T);
 }
