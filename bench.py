@@ -145,6 +145,15 @@ def kernel_work(name, a):
         M, N, K, Cc, L = a[6], a[7], a[8], a[9], a[11]
         return "gemm_conv", "mfma", 2 * (M * K + N * K + M * N) + (M // L) * Cc * 4 * 2, \
             2 * M * N * K
+    if name == "kad_gdn_suffix_replay_conv_gated_parents":
+        # the last level's mixer: the earlier token's pre-conv rows read in
+        # place from the parents' cache, the new token's rows and gate rows,
+        # the state and the gates in, each beam's normed last-token row out
+        B, W, T, H, HV, K, V = a[25:32]
+        BW, C = B * W, 2 * H * K + HV * V
+        nbytes = BW * T * C * 2 + BW * HV * V * 2 * 2 + B * HV * K * V * _es(a[18]) \
+            + BW * T * HV * 6 + B * C * 3 * 2 + C * 4 * 2
+        return "gdn_replay", "hbm", nbytes, BW * HV * 2 * T * 2 * K * V + 8 * BW * C * T
     if name in ("kad_gdn_suffix_replay_conv", "kad_gdn_suffix_replay_conv_gated"):
         # pre-conv q|k|v rows in, replay output out (the conv output stays on
         # chip); gated: the gate rows of the normed tokens in, normed rows out

@@ -101,6 +101,24 @@ int kad_gdn_suffix_replay_conv_gated(const void* proj, int64_t ld_proj, const vo
                                      int last_token_only, void* out, int64_t ld_out, int B,
                                      int W, int T, int H, int HV, int K, int V, float scale,
                                      kad_stream_t stream);
+/* kad_gdn_suffix_replay_conv_gated (last token only, T = 2) reading each
+ * beam's earlier token from its parent's cached projection row in place:
+ * prev holds the parent level's rows, (b*Wp + p)*(T-1) + t at stride ld_prev
+ * (bf16, 16-byte aligned, ld_prev a multiple of 8); parents [B, W] (int64,
+ * clamped to [0, Wp)); cur one row per beam of the new token (b*W + w, stride
+ * ld_cur); z the new token's gate rows (one per beam); the gates log_decay /
+ * beta still in (n*T + t) rows.  The same bits as gathering the parents'
+ * rows (kad_gather_beam_rows) into one [B*W*T] buffer and calling
+ * kad_gdn_suffix_replay_conv_gated on it.  No counterpart in the reference:
+ * it saves the search's last level the copy of the cached rows that the
+ * reference's full replay recomputes (src/kadllm/adapters/qwen3_5.py:216). */
+int kad_gdn_suffix_replay_conv_gated_parents(
+    const void* prev, int64_t ld_prev, const int64_t* parents, int Wp, const void* cur,
+    int64_t ld_cur, const void* conv_state, int64_t ss_b, int64_t ss_c, int64_t ss_t,
+    int history, const void* conv_weight, const void* log_decay, int gate_dtype,
+    const void* beta, int beta_dtype, int64_t ld_gate, const void* state, int state_dtype,
+    const void* z, int64_t ldz, const void* norm_w, float eps, void* out, int64_t ld_out, int B,
+    int W, int T, int H, int HV, int K, int V, float scale, kad_stream_t stream);
 
 /* --------------------------------------------------------------------------
  * Depthwise causal short convolution over [prefix taps || suffix].

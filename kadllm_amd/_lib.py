@@ -31,6 +31,8 @@ SIGNATURES = {
     "kad_gdn_suffix_replay_conv": "pl" "plllip" "pipil" "pi" "pl" "iiiiiii" "f" "s",
     "kad_gdn_suffix_replay_conv_gated": "pl" "plllip" "pipil" "pi" "plpfi" "pl" "iiiiiii" "f"
                                         "s",
+    "kad_gdn_suffix_replay_conv_gated_parents": "plpipl" "plllip" "pipil" "pi" "plpf" "pl"
+                                                "iiiiiii" "f" "s",
     "kad_causal_conv_suffix": "plll" "pllli" "pip" "plll" "iiiiii" "s",
     "kad_gemm_bf16": "plplplpl" "iiii" "s",
     "kad_gemm_bf16_tiled": "plplplpl" "iiiii" "s",

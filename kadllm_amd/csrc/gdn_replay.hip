@@ -402,9 +402,22 @@ struct GateOutArgs {
   int t_first;
 };
 
+// Parent-row form (PAR, with LAST): the earlier tokens' rows are read in
+// place from the parent level's cached projection rows, through each beam's
+// parent index, and the new token's from a compact buffer of one row per
+// beam, so the search's last level gathers no rows.
+struct ParentRows {
+  const bf16_t* prev;       // parent rows: (b*Wp + parent)*(T-1) + t, stride ld_prev
+  int64_t ld_prev;
+  const int64_t* parents;   // [B, W], clamped to [0, Wp)
+  int Wp;
+  const bf16_t* cur;        // new rows: b*W + beam, stride ld_cur
+  int64_t ld_cur;
+};
+
 // LAST (with GATED, last token only): the earlier tokens' q, whose outputs
 // nothing reads, enter no product (their k and v still update the state)
-template <int T, int NS, bool CONV, bool GATED = false, bool LAST = false>
+template <int T, int NS, bool CONV, bool GATED = false, bool LAST = false, bool PAR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 1 ? 3 : (T == 4 ? 1 : 2), 8)))
 void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                            const bf16_t* __restrict__ v, int64_t ld_qk, int64_t ld_v,
@@ -413,7 +426,7 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
                            const void* __restrict__ state, int state_dtype,
                            bf16_t* __restrict__ out, int64_t ld_out, int W, int H, int HV,
                            float scale, int beams_per_block, int nbb, ConvArgs cv,
-                           GateOutArgs go) {
+                           GateOutArgs go, ParentRows pr) {
   constexpr int KD = 128, VD = 128;
   constexpr int KSTEPS = KD / 32;
   constexpr int VROWS = VD / 4;
@@ -424,12 +437,16 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
   static_assert(!CONV || T <= 2, "the fused conv takes one- and two-token suffixes");
   static_assert(!GATED || CONV, "the gated output comes with the fused conv");
   static_assert(!LAST || GATED, "the last-token form is a gated form");
+  static_assert(!PAR || (LAST && T >= 2), "the parent-row form is a last-token form");
   constexpr int TQ = LAST ? T - 1 : 0;   // the first token whose q is used
   constexpr int TAB = CONV ? ConvTab<T>::bytes : 0;
-  constexpr int PSUM = GATED ? T * 16 * 16 * 4 : 0;   // [token][beam][piece] row-sum pieces
-  __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE + TAB + PSUM];
+  // [normed token][beam][piece] row-sum pieces (one token in the last-token form)
+  constexpr int PSUM = GATED ? (LAST ? 1 : T) * 16 * 16 * 4 : 0;
+  constexpr int PARB = PAR ? 256 * 4 : 0;   // the block's parent indices
+  __shared__ __attribute__((aligned(16))) uint8_t stage_buf[NS * STAGE + TAB + PSUM + PARB];
   uint8_t* const tab = stage_buf + NS * STAGE;
   float* const psum = (float*)(stage_buf + NS * STAGE + TAB);
+  int* const par_lds = (int*)(stage_buf + NS * STAGE + TAB + PSUM);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -458,13 +475,29 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
       const int I = w * T + j;
       const int r = 4 * I + (lane >> 4);
       const int c = (lane & 15) ^ ((r / T) & 15);
-      const int64_t qrow = (row0 + r) * ld_qk + (int64_t)h * KD + c * 8;
-      const int64_t vrow = (row0 + r) * ld_v + (int64_t)hv * VD + c * 8;
-      __builtin_amdgcn_global_load_lds((replay_global_t*)(q + qrow),
-                                       (replay_lds_t*)(sb + I * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((replay_global_t*)(k + qrow),
+      const bf16_t *qs, *ks, *vs;
+      if constexpr (PAR) {
+        // (beam, token) of row r: an earlier token from the parent's cached
+        // row, the new token from the compact buffer
+        const int beam = gi * 16 + r / T, t = r % T;
+        const bf16_t* base =
+            t < T - 1 ? pr.prev + ((int64_t)(b * pr.Wp + par_lds[beam]) * (T - 1) + t) * pr.ld_prev
+                      : pr.cur + ((int64_t)b * W + n_begin + beam) * pr.ld_cur;
+        qs = base + (int64_t)h * KD + c * 8;
+        ks = base + (int64_t)(H + h) * KD + c * 8;
+        vs = base + (int64_t)2 * H * KD + (int64_t)hv * VD + c * 8;
+      } else {
+        const int64_t qrow = (row0 + r) * ld_qk + (int64_t)h * KD + c * 8;
+        const int64_t vrow = (row0 + r) * ld_v + (int64_t)hv * VD + c * 8;
+        qs = q + qrow;
+        ks = k + qrow;
+        vs = v + vrow;
+      }
+      __builtin_amdgcn_global_load_lds((replay_global_t*)qs, (replay_lds_t*)(sb + I * 1024), 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds((replay_global_t*)ks,
                                        (replay_lds_t*)(sb + BLK + I * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((replay_global_t*)(v + vrow),
+      __builtin_amdgcn_global_load_lds((replay_global_t*)vs,
                                        (replay_lds_t*)(sb + 2 * BLK + I * 1024), 16, 0, 0);
     }
     // the group's gates, lane r = (beam, token) row: wave 0 the fp32 log
@@ -500,6 +533,14 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
         for (int i = 0; i < 3; ++i) tab_tap[j][i] = bf2f(sp[(int64_t)(cv.hist - 3 + i) * cv.ss_t]);
       }
     }
+  }
+  if constexpr (PAR) {
+    // the block's parent indices, clamped (their loads precede every DMA)
+    for (int i = threadIdx.x; i < n_end - n_begin; i += 256) {
+      const int64_t p0 = pr.parents[(int64_t)b * W + n_begin + i];
+      par_lds[i] = (int)(p0 < 0 ? 0 : (p0 >= pr.Wp ? pr.Wp - 1 : p0));
+    }
+    __syncthreads();
   }
   // the first NS - 1 groups' loads go out before the state's, so they land
   // meanwhile
@@ -592,8 +633,8 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
         if (t >= go.t_first) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
-            zg[t][mt] = *(const u32x2*)(go.z + (nz * T + t) * go.ldz + (int64_t)hv * VD + v0 +
-                                        mt * 16 + quad * 4);
+            zg[t][mt] = *(const u32x2*)(go.z + (PAR ? nz : nz * T + t) * go.ldz +
+                                        (int64_t)hv * VD + v0 + mt * 16 + quad * 4);
         }
     }
     if (gi + NS - 1 < ngroups) dma_group(gi + NS - 1, (gi + NS - 1) % NS);
@@ -725,7 +766,8 @@ void gdn_replay_lds_kernel(const bf16_t* __restrict__ q, const bf16_t* __restric
     // gated RMSNorm of token t's rows and their store (see GateOutArgs)
     auto gated_out = [&](int t, const float (&o)[MT][4], const u32x2 (&zt)[MT], int64_t nrow) {
       float f[MT][4];
-      float* ps = psum + t * 256;   // one buffer per token: no barrier between tokens
+      // one buffer per normed token: no barrier between tokens
+      float* ps = psum + (LAST ? 0 : t * 256);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         // o rounded to bf16 as the unfused path stores it; this lane's four
@@ -859,7 +901,7 @@ int launch_replay(const void* q, const void* k, const void* v, int64_t ld_qk, in
                        dim3(256), 0, stream, (const bf16_t*)q, (const bf16_t*)k,              \
                        (const bf16_t*)v, ld_qk, ld_v, g, gdt, beta, bdt, ld_gate, state, sdt, \
                        (bf16_t*)out, ld_out, W, H, HV, scale, bpb, nbb, ConvArgs{},           \
-                       GateOutArgs{});                                                        \
+                       GateOutArgs{}, ParentRows{});                                          \
     return kad_launch_status("gdn_replay_lds_kernel");                                        \
   }
       KAD_REPLAY_LDS(1, 3)
@@ -912,7 +954,7 @@ int dispatch_dims(int K, int V, const void* q, const void* k, const void* v, int
 int launch_replay_conv(const bf16_t* proj, int64_t ld, const ConvArgs& cv, const void* g,
                        const void* beta, int64_t ld_gate, const void* state, int sdt, void* out,
                        int64_t ld_out, int B, int W, int T, int H, int HV, float scale,
-                       const GateOutArgs* go, hipStream_t stream) {
+                       const GateOutArgs* go, const ParentRows* par, hipStream_t stream) {
   const int bpb = W <= 256 ? W : 128;
   const int nbb = (int)kad_cdiv(W, bpb);
   const int64_t nblocks = (int64_t)B * HV * nbb;
@@ -921,19 +963,22 @@ int launch_replay_conv(const bf16_t* proj, int64_t ld, const ConvArgs& cv, const
   const bf16_t* k = proj + (int64_t)H * 128;
   const bf16_t* v = proj + (int64_t)2 * H * 128;
   const bool last = go != nullptr && go->t_first == T - 1 && T > 1;
-#define KAD_REPLAY_CONV(TT, GV, LV)                                                            \
-  if (T == TT && (go != nullptr) == GV && last == LV) {                                        \
-    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, 3, true, GV, LV>), dim3((unsigned)nblocks),  \
-                       dim3(256), 0, stream, q, k, v, ld, ld, g, KAD_DTYPE_F32, beta,          \
-                       KAD_DTYPE_BF16, ld_gate, state, sdt, (bf16_t*)out, ld_out, W, H, HV,    \
-                       scale, bpb, nbb, cv, go ? *go : GateOutArgs{});                         \
+  const bool pv = par != nullptr;
+#define KAD_REPLAY_CONV(TT, GV, LV, PV)                                                        \
+  if (T == TT && (go != nullptr) == GV && last == LV && pv == PV) {                            \
+    hipLaunchKernelGGL((gdn_replay_lds_kernel<TT, 3, true, GV, LV, PV>),                       \
+                       dim3((unsigned)nblocks), dim3(256), 0, stream, q, k, v, ld, ld, g,      \
+                       KAD_DTYPE_F32, beta, KAD_DTYPE_BF16, ld_gate, state, sdt, (bf16_t*)out, \
+                       ld_out, W, H, HV, scale, bpb, nbb, cv, go ? *go : GateOutArgs{},        \
+                       par ? *par : ParentRows{});                                             \
     return kad_launch_status("gdn_replay_lds_kernel");                                         \
   }
-  KAD_REPLAY_CONV(1, false, false)
-  KAD_REPLAY_CONV(2, false, false)
-  KAD_REPLAY_CONV(1, true, false)
-  KAD_REPLAY_CONV(2, true, false)
-  KAD_REPLAY_CONV(2, true, true)
+  KAD_REPLAY_CONV(1, false, false, false)
+  KAD_REPLAY_CONV(2, false, false, false)
+  KAD_REPLAY_CONV(1, true, false, false)
+  KAD_REPLAY_CONV(2, true, false, false)
+  KAD_REPLAY_CONV(2, true, true, false)
+  KAD_REPLAY_CONV(2, true, true, true)
 #undef KAD_REPLAY_CONV
   KAD_UNSUPPORTED("the fused conv replay takes 1 or 2 suffix tokens, got %d", T);
 }
@@ -946,7 +991,7 @@ int replay_conv_common(
     int64_t ss_t, int history, const void* conv_weight, const void* log_decay, int gate_dtype,
     const void* beta, int beta_dtype, int64_t ld_gate, const void* state, int state_dtype,
     void* out, int64_t ld_out, int B, int W, int T, int H, int HV, int K, int V, float scale,
-    const GateOutArgs* go, kad_stream_t stream) {
+    const GateOutArgs* go, kad_stream_t stream, const ParentRows* par = nullptr) {
   KAD_REQUIRE(proj && conv_state && conv_weight && log_decay && beta && state && out,
               "null pointer argument");
   KAD_REQUIRE(B > 0 && W > 0 && T > 0 && H > 0 && HV > 0 && K > 0 && V > 0,
@@ -974,7 +1019,7 @@ int replay_conv_common(
   const ConvArgs cv{(const bf16_t*)conv_state, ss_b, ss_c, ss_t, history,
                     (const bf16_t*)conv_weight};
   return launch_replay_conv((const bf16_t*)proj, ld_proj, cv, log_decay, beta, ld_gate, state,
-                            state_dtype, out, ld_out, B, W, T, H, HV, scale, go,
+                            state_dtype, out, ld_out, B, W, T, H, HV, scale, go, par,
                             (hipStream_t)stream);
 }
 }  // namespace
@@ -1006,6 +1051,29 @@ extern "C" int kad_gdn_suffix_replay_conv_gated(
   return replay_conv_common(proj, ld_proj, conv_state, ss_b, ss_c, ss_t, history, conv_weight,
                             log_decay, gate_dtype, beta, beta_dtype, ld_gate, state, state_dtype,
                             out, ld_out, B, W, T, H, HV, K, V, scale, &go, stream);
+}
+
+extern "C" int kad_gdn_suffix_replay_conv_gated_parents(
+    const void* prev, int64_t ld_prev, const int64_t* parents, int Wp, const void* cur,
+    int64_t ld_cur, const void* conv_state, int64_t ss_b, int64_t ss_c, int64_t ss_t,
+    int history, const void* conv_weight, const void* log_decay, int gate_dtype,
+    const void* beta, int beta_dtype, int64_t ld_gate, const void* state, int state_dtype,
+    const void* z, int64_t ldz, const void* norm_w, float eps, void* out, int64_t ld_out, int B,
+    int W, int T, int H, int HV, int K, int V, float scale, kad_stream_t stream) {
+  KAD_REQUIRE(prev && parents && cur && z && norm_w, "null pointer argument");
+  KAD_REQUIRE(Wp > 0, "Wp must be positive");
+  KAD_REQUIRE(ldz % 4 == 0 && ((uintptr_t)z % 8) == 0 && ((uintptr_t)norm_w % 8) == 0,
+              "z rows and the norm weight must be 8-byte aligned (ldz a multiple of 4)");
+  KAD_REQUIRE(ldz >= (int64_t)HV * V, "ldz smaller than a row");
+  KAD_REQUIRE(ld_prev >= (int64_t)2 * H * K + (int64_t)HV * V, "ld_prev smaller than a row");
+  if (T != 2) KAD_UNSUPPORTED("the parent-row conv replay takes two-token suffixes, got %d", T);
+  if (!(ld_prev % 8 == 0 && ((uintptr_t)prev % 16) == 0))
+    KAD_UNSUPPORTED("the parent-row conv replay takes 16-byte aligned parent rows");
+  const GateOutArgs go{(const bf16_t*)z, ldz, (const bf16_t*)norm_w, eps, T - 1};
+  const ParentRows pr{(const bf16_t*)prev, ld_prev, parents, Wp, (const bf16_t*)cur, ld_cur};
+  return replay_conv_common(cur, ld_cur, conv_state, ss_b, ss_c, ss_t, history, conv_weight,
+                            log_decay, gate_dtype, beta, beta_dtype, ld_gate, state, state_dtype,
+                            out, ld_out, B, W, T, H, HV, K, V, scale, &go, stream, &pr);
 }
 
 extern "C" int kad_gdn_suffix_replay(const void* q, const void* k, const void* v,

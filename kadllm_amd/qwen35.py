@@ -270,6 +270,50 @@ class Qwen35Runner:
             _lib.call("kad_gdn_recurrent", *args, W, _lib.ptr(o), self.vd, None, B * W, T, H_, HV,
                       dk, dv, float(dk ** -0.5), _lib.stream_of(conv))
 
+    def _mixer_fusable(self, lyr, W):
+        """Whether the fused decode mixer takes this layer's shapes (besides
+        the suffix length and row alignment, checked where it is called)."""
+        cfg = self.cfg
+        return (W % 16 == 0 and cfg.linear_key_head_dim == 128
+                and cfg.linear_value_head_dim == 128 and self.gdn_cols % 8 == 0
+                and lyr.conv_w.is_contiguous() and lyr.conv_w.data_ptr() % 8 == 0
+                and lyr.norm_w.data_ptr() % 8 == 0
+                and cfg.linear_num_value_heads % 2 == 0)
+
+    def _gdn_mix_parents(self, lyr, n, prev, parents, cached, B, W, Wp, T):
+        """_gdn_mix for the search's last level (last token only, T = 2) with
+        the earlier token's projection rows read in place from the parent
+        level's cache (kad_gdn_suffix_replay_conv_gated_parents): only the new
+        token's rows are projected, and only the parents' gate inputs (a | b,
+        64 bytes a row) are gathered.  The same bits as gathering the rows."""
+        cfg = self.cfg
+        H_, HV = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+        dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+        C = self.conv_dim
+        c = C + self.vd
+        cols = self.gdn_cols
+        BW = B * W
+        dev = n.device
+        stream = _lib.stream_of(n)
+        nab = lyr.w_ab.shape[0]
+        ab = torch.empty(BW * T, nab, dtype=torch.bfloat16, device=dev)
+        _lib.call("kad_gather_beam_rows", _lib.ptr_at(prev.data_ptr() + c * 2), cols * 2, T - 1,
+                  _lib.ptr(ab), nab * 2, T, T - 1, nab * 2, _lib.ptr(parents), B, W, Wp, stream)
+        cur = torch.empty(BW, cols, dtype=torch.bfloat16, device=dev)
+        layers.gemm(n, lyr.w_ab, out=ab.view(BW, T, nab)[:, T - 1])
+        layers.gemm(n, lyr.w_in, out=cur[:, :c])
+        g, beta = layers.gdn_gates(ab[:, :HV], ab[:, HV:2 * HV], lyr.A_log, lyr.dt_bias)
+        cs, S = cached
+        z = cur[:, C:C + self.vd]
+        y = torch.empty(BW, self.vd, dtype=torch.bfloat16, device=dev)
+        _lib.call("kad_gdn_suffix_replay_conv_gated_parents", _lib.ptr(prev), cols,
+                  _lib.ptr(parents), Wp, _lib.ptr(cur), cols, _lib.ptr(cs), *cs.stride(),
+                  cs.shape[-1], _lib.ptr(lyr.conv_w), _lib.ptr(g), 2, _lib.ptr(beta), 0,
+                  g.stride(0), _lib.ptr(S), _lib.dtype_code(S.dtype), _lib.ptr(z), cols,
+                  _lib.ptr(lyr.norm_w), cfg.rms_norm_eps, _lib.ptr(y), self.vd, B, W, T, H_, HV,
+                  dk, dv, float(dk ** -0.5), stream)
+        return y
+
     def _gdn_mix(self, lyr, proj, T, cached, B, W, last_only):
         """A GDN layer's suffix mixer up to out_proj: conv of the projection
         rows' q | k | v channels, replay against the prefix state, gated
@@ -560,15 +604,21 @@ class Qwen35Runner:
             n = layers.rmsnorm(x, lyr.input_norm, cfg.rms_norm_eps)
             if isinstance(lyr, _GdnLayer):
                 cols = self.gdn_cols
-                proj = torch.empty(BW * T, cols, dtype=torch.bfloat16, device=dev)
-                pv = proj.view(BW, T, cols)
-                if T > 1:
-                    follow(cache.layers[li], proj, T - 1, cols * 2, cols * 2, cols * 2)
-                self._gdn_proj(lyr, n, out=pv[:, T - 1])
-                y = self._gdn_mix(lyr, proj, T, cached, B, W, last_only=True)
+                if T == 2 and not keep_cache and self._mixer_fusable(lyr, W):
+                    # the last level reads the earlier token's rows from the
+                    # parents' cache in place: no row gather
+                    y = self._gdn_mix_parents(lyr, n, cache.layers[li], parents, cached, B, W,
+                                              Wp, T)
+                else:
+                    proj = torch.empty(BW * T, cols, dtype=torch.bfloat16, device=dev)
+                    pv = proj.view(BW, T, cols)
+                    if T > 1:
+                        follow(cache.layers[li], proj, T - 1, cols * 2, cols * 2, cols * 2)
+                    self._gdn_proj(lyr, n, out=pv[:, T - 1])
+                    y = self._gdn_mix(lyr, proj, T, cached, B, W, last_only=True)
+                    if keep_cache:
+                        new_layers.append(proj)
                 layers.gemm(y, lyr.w_out, out=x, epilogue=layers.EPI_RESIDUAL, residual=x)
-                if keep_cache:
-                    new_layers.append(proj)
             else:
                 proj = layers.gemm(n, lyr.w_qkv)
                 ld = proj.stride(0)

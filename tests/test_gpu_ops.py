@@ -354,3 +354,45 @@ def test_gdn_replay_conv_rejects_what_it_does_not_fuse(device):
             _lib.call("kad_gdn_suffix_replay_conv", _lib.ptr(proj), C, _lib.ptr(cs), *cs.stride(),
                       4, _lib.ptr(cw), _lib.ptr(gd), 2, _lib.ptr(bd), 0, HV, _lib.ptr(Sd), 2,
                       _lib.ptr(o), HV * K, B, W, T, H, HV, K, K, K ** -0.5, _lib.stream_of(proj))
+
+
+@pytest.mark.parametrize("W,Wp,H,HV", [(16, 16, 2, 2), (48, 32, 4, 8), (256, 256, 2, 4)])
+def test_gdn_replay_conv_gated_parents_equals_gather(device, W, Wp, H, HV):
+    """kad_gdn_suffix_replay_conv_gated_parents (the earlier token read through
+    each beam's parent from the parent level's rows) against
+    kad_gather_beam_rows of those rows followed by
+    kad_gdn_suffix_replay_conv_gated on the gathered buffer, bit for bit,
+    including a parent index past Wp (both clamp it)."""
+    B, T, K, hist = 2, 2, 128, 4
+    C = 2 * H * K + HV * K
+    ld = C + HV * K + 40                 # q | k | v | z | more columns
+    g = torch.Generator().manual_seed(W + Wp + H + HV)
+    prev = (torch.randn(B * Wp * (T - 1), ld, generator=g) * 0.7).bfloat16().to(device)
+    cur = (torch.randn(B * W, ld, generator=g) * 0.7).bfloat16().to(device)
+    parents = torch.randint(0, Wp, (B, W), generator=g)
+    parents[0, 3] = Wp + 5
+    parents = parents.to(device)
+    cs = (torch.randn(B, C, hist, generator=g) * 0.7).bfloat16().to(device)
+    cw = (torch.rand(C, 4, generator=g) - 0.5).bfloat16().to(device)
+    logd = (-torch.rand(B * W * T, HV, generator=g) * 0.3).to(device)
+    beta = torch.rand(B * W * T, HV, generator=g).bfloat16().to(device)
+    S = (torch.randn(B, HV, K, K, generator=g) * 0.05).to(device)
+    nw = (1.0 + 0.1 * torch.randn(K, generator=g)).bfloat16().to(device)
+    stream = _lib.stream_of(cur)
+    # reference: the rows gathered into one [B*W*T] buffer
+    full = torch.empty(B * W * T, ld, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_gather_beam_rows", _lib.ptr(prev), ld * 2, T - 1, _lib.ptr(full), ld * 2, T,
+              T - 1, ld * 2, _lib.ptr(parents), B, W, Wp, stream)
+    full.view(B * W, T, ld)[:, T - 1].copy_(cur)
+    y1 = torch.empty(B * W, HV * K, dtype=torch.bfloat16, device=device)
+    _lib.call("kad_gdn_suffix_replay_conv_gated", _lib.ptr(full), ld, _lib.ptr(cs), *cs.stride(),
+              hist, _lib.ptr(cw), _lib.ptr(logd), 2, _lib.ptr(beta), 0, HV, _lib.ptr(S), 2,
+              _lib.ptr(full[:, C:]), ld, _lib.ptr(nw), 1e-6, 1, _lib.ptr(y1), HV * K, B, W, T, H,
+              HV, K, K, K ** -0.5, stream)
+    y2 = torch.full_like(y1, 2.0)
+    _lib.call("kad_gdn_suffix_replay_conv_gated_parents", _lib.ptr(prev), ld, _lib.ptr(parents), Wp,
+              _lib.ptr(cur), ld, _lib.ptr(cs), *cs.stride(), hist, _lib.ptr(cw), _lib.ptr(logd), 2,
+              _lib.ptr(beta), 0, HV, _lib.ptr(S), 2, _lib.ptr(cur[:, C:]), ld, _lib.ptr(nw), 1e-6,
+              _lib.ptr(y2), HV * K, B, W, T, H, HV, K, K, K ** -0.5, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y1), "parent-row fused replay differs from gather + fused replay"
