@@ -180,7 +180,10 @@ int kad_gemm_bf16_conv(const void* A, int64_t lda, const void* W, int64_t ldw, v
 /* Same with an explicit tile configuration, the forms the automatic choice
  * picks from (0 = automatic choice as kad_gemm_bf16; 1 = 32x256 with 4 waves;
  * 2 = 128x128 with 4 waves; 5 = 256x256 with 8 waves; 11 = 64x32 with 2
- * waves, no SwiGLU epilogue; 12 = 32x64 with 2 waves, no SwiGLU epilogue; 16 = 256x256 with 8 waves on 16x16x32 MFMAs,
+ * waves, no SwiGLU epilogue; 12 = 32x64 with 2 waves, no SwiGLU epilogue;
+ * 13 = outputs of at most 32 columns, one wave per 32 rows over the whole
+ * of K with the weight in LDS, K a multiple of 256 up to 2,048, 16-byte
+ * aligned A and W rows, no SwiGLU epilogue; 16 = 256x256 with 8 waves on 16x16x32 MFMAs,
  * direct-to-LDS loads and a 16-byte store epilogue, which needs 16-byte
  * aligned C (and R) with ldc, ldr and the output width multiples of 8;
  * 18 = 16 persistent, one workgroup per CU walking the tiles; 19 = 16's

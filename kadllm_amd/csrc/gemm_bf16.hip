@@ -1707,10 +1707,130 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int6
   return kad_launch_status("gemm_bf16_kernel");
 }
 
+// Outputs of at most 32 columns (the GDN gate projection, N = 2 x value
+// heads), read-bound on A.  The generic 64 x 32 tiles leave half the chip
+// idle at M = 8,192 and wait for HBM once per 64-deep K tile.  Here a wave
+// owns 32 rows and walks the whole of K after one barrier: the weight is
+// copied into LDS once per workgroup, step-major (each 16-deep K step's
+// 32 x 16 elements form 1 KB, which a wave's fragment read takes whole, free
+// of bank conflicts), and the wave's rows of A stream through registers in slices of
+// 256 of K, three slices in flight.  The MFMA chain is the generic kernel's
+// 32x32x16 one in the same K order, so the results are the same bits.  One
+// wave per workgroup when the waves number fewer than two per CU (M =
+// 8,192: every CU then holds a wave, 11.4 -> 8.9 us in the search), else four sharing
+// the weight's copy.
+constexpr int kN32Steps = 16;  // 16-deep MFMA steps per slice
+
+template <int EPI, int NSL, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemm_n32_kernel(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ Wt, int64_t ldw,
+    bf16_t* C, int64_t ldc, const bf16_t* R, int64_t ldr, int M, int N) {
+  constexpr int K = NSL * kN32Steps * 16;
+  extern __shared__ __attribute__((aligned(16))) bf16_t wsm[];  // [K / 16][32 rows][16]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = (blockIdx.x * WAVES + wave) * 32;
+  const int r = lane & 31, kq = (lane >> 5) * 8;
+  // rows past M read row M - 1 (their results are not stored)
+  const bf16_t* a = A + (int64_t)min(m0 + r, M - 1) * lda + kq;
+  u32x4 ar[3][kN32Steps];
+  auto fetch = [&](u32x4 (&dst)[kN32Steps], int sl) {
+#pragma unroll
+    for (int i = 0; i < kN32Steps; ++i) dst[i] = *(const u32x4*)(a + (sl * kN32Steps + i) * 16);
+  };
+#pragma unroll
+  for (int sl = 0; sl < 3; ++sl)
+    if (sl < NSL) fetch(ar[sl], sl);
+  // the weight into LDS by direct loads, one 16-deep K step (32 rows x 32
+  // bytes, 1 KB) per instruction, all in flight at once: lane l fetches row
+  // l / 2 (rows past N read row N - 1), bytes 16 (l % 2) .. +15 of the step
+  {
+    const bf16_t* wg = Wt + (int64_t)min(lane >> 1, N - 1) * ldw + (lane & 1) * 8;
+    for (int kt = wave; kt < K / 16; kt += WAVES) dma16(wg + kt * 16, wsm + kt * 512);
+  }
+  __syncthreads();
+  // fragment of step kt: row lane % 32, elements 8 (lane / 32) .. +7
+  const bf16_t* wl = wsm + r * 16 + kq;
+  f32x16 acc = {};
+#pragma unroll
+  for (int sl = 0; sl < NSL; ++sl) {
+#pragma unroll
+    for (int i = 0; i < kN32Steps; ++i) {
+      const bf16x8 wf = as_bf16x8(*(const u32x4*)(wl + (sl * kN32Steps + i) * 512));
+      acc = mfma32x32x16(as_bf16x8(ar[sl % 3][i]), wf, acc);
+    }
+    if (sl + 3 < NSL) fetch(ar[sl % 3], sl + 3);
+  }
+  // lane holds column lane % 32 and rows (e/4)*8 + (lane/32)*4 + e%4
+  const int col = lane & 31, row_q = (lane >> 5) * 4;
+  if (m0 >= M || col >= N) return;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = m0 + row_q + (e / 4) * 8 + (e % 4);
+    if (row < M) {
+      float v = acc[e];
+      if constexpr (EPI == KAD_EPI_RESIDUAL) v = bf2f(R[(int64_t)row * ldr + col]) + round_bf(v);
+      C[(int64_t)row * ldc + col] = f2bf(v);
+    }
+  }
+}
+
+// whole-K rows of A and the weight in 16-byte units, K a multiple of 256 up
+// to 2,048 (the weight's LDS copy at most 128 KB)
+bool n32_ok(const void* A, int64_t lda, const void* W, int64_t ldw, int N, int K, int epi) {
+  return epi != KAD_EPI_SWIGLU && N <= 32 && K % 256 == 0 && K >= 256 && K <= 2048 &&
+         ((uintptr_t)A % 16) == 0 && ((uintptr_t)W % 16) == 0 && lda % 8 == 0 && ldw % 8 == 0;
+}
+
+template <int EPI, int NSL, int WAVES>
+int launch_n32_w(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+                 const void* R, int64_t ldr, int M, int N, hipStream_t s) {
+  const size_t lds = (size_t)32 * NSL * kN32Steps * 16 * 2;
+  static bool configured = false;
+  if (!configured) {
+    if (hipFuncSetAttribute((const void*)gemm_n32_kernel<EPI, NSL, WAVES>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+      kad_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
+      return KAD_ERR_HIP;
+    }
+    configured = true;
+  }
+  const int64_t nblocks = kad_cdiv(M, 32 * WAVES);
+  hipLaunchKernelGGL((gemm_n32_kernel<EPI, NSL, WAVES>), dim3((unsigned)nblocks), dim3(64 * WAVES),
+                     lds, s, (const bf16_t*)A, lda, (const bf16_t*)W, ldw, (bf16_t*)C, ldc,
+                     (const bf16_t*)R, ldr, M, N);
+  return kad_launch_status("gemm_n32_kernel");
+}
+
+template <int EPI, int NSL>
+int launch_n32_at(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+                  const void* R, int64_t ldr, int M, int N, hipStream_t s) {
+  if (kad_cdiv(M, 32) < 2 * (int64_t)device_cu_count())
+    return launch_n32_w<EPI, NSL, 1>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+  return launch_n32_w<EPI, NSL, 4>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+}
+
+template <int EPI>
+int launch_n32(const void* A, int64_t lda, const void* W, int64_t ldw, void* C, int64_t ldc,
+               const void* R, int64_t ldr, int M, int N, int K, hipStream_t s) {
+  if (!n32_ok(A, lda, W, ldw, N, K, EPI))
+    KAD_UNSUPPORTED("tile configuration 13 needs N <= 32, K a multiple of 256 up to 2,048, "
+                    "16-byte aligned A and W rows and no SwiGLU epilogue");
+  switch (K / 256) {
+    case 1: return launch_n32_at<EPI, 1>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+    case 2: return launch_n32_at<EPI, 2>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+    case 3: return launch_n32_at<EPI, 3>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+    case 4: return launch_n32_at<EPI, 4>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+    case 5: return launch_n32_at<EPI, 5>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+    case 6: return launch_n32_at<EPI, 6>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+    case 7: return launch_n32_at<EPI, 7>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+    default: return launch_n32_at<EPI, 8>(A, lda, W, ldw, C, ldc, R, ldr, M, N, s);
+  }
+}
+
 // tile configurations (tile_config argument of kad_gemm_bf16_tiled): the
 // forms the automatic choice uses; the numbers are part of the C ABI
 enum { CFG_AUTO = 0, CFG_32x256 = 1, CFG_128x128 = 2, CFG_256x256_8W = 5, CFG_64x32 = 11,
-       CFG_32x64 = 12,
+       CFG_32x64 = 12, CFG_N32 = 13,
        CFG_256x256_X16 = 16, CFG_256x256_X16P = 18, CFG_128x128_X16 = 19,
        CFG_256x256_S3 = 20, CFG_256x256_PPP = 22, CFG_256x256_W4E = 24 };
 
@@ -1738,7 +1858,9 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
     if (M <= 64)
       cfg = N <= 2048 && EPI != KAD_EPI_SWIGLU ? CFG_32x64 : CFG_32x256;
     else if (N <= 32)
-      cfg = CFG_64x32;
+      // whole-K waves of 32 rows (the GDN gate projection at M = 8,192 and
+      // 32,768), else 64x32 tiles
+      cfg = n32_ok(A, lda, W, ldw, N, K, EPI) ? CFG_N32 : CFG_64x32;
     else if (tiles256 >= 256 && !vec)
       cfg = CFG_256x256_8W;
     else if (EPI == KAD_EPI_STORE && M % 256 == 0 && N % 256 == 0 && K <= 2048 &&
@@ -1802,6 +1924,10 @@ int pick(int cfg, const void* A, int64_t lda, const void* W, int64_t ldw, void* 
       return launch<32, 64, 1, 2, EPI == KAD_EPI_SWIGLU ? KAD_EPI_STORE : EPI>(
           A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
     case CFG_128x128: return launch<128, 128, 2, 2, EPI>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, s);
+    case CFG_N32:
+      if (EPI == KAD_EPI_SWIGLU) KAD_UNSUPPORTED("tile configuration 13 has no SwiGLU epilogue");
+      return launch_n32<EPI == KAD_EPI_SWIGLU ? KAD_EPI_STORE : EPI>(A, lda, W, ldw, C, ldc, R, ldr,
+                                                                     M, N, K, s);
     case CFG_64x32:
       // two waves of 32x32: twice the workgroups of 128x32 tiles for this
       // read-bound shape (12.1 against 14.0 us at M = 32,768, N = 32)

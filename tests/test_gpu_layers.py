@@ -182,6 +182,59 @@ def test_gemm_last_round_column_split_is_bitwise(device, N, epi):
         _bf16_ulp_close(outs[0][rows], prod, "split gemm store")
 
 
+@pytest.mark.parametrize("M,N,K,epi", [(8192, 32, 1024, layers.EPI_STORE),
+                                       (600, 20, 256, layers.EPI_STORE),
+                                       (1000, 32, 768, layers.EPI_RESIDUAL),
+                                       (333, 7, 2048, layers.EPI_STORE),
+                                       (20000, 32, 512, layers.EPI_RESIDUAL)])
+def test_gemm_narrow_output_whole_k_waves_agree(device, M, N, K, epi):
+    """Outputs of at most 32 columns (the GDN gate projection): the whole-K
+    32-row waves (configuration 13, which the automatic choice takes for
+    them) against 64x32 and 32x256 tiles, on ragged M, strided A and C and
+    K from one to eight 256-deep slices, with one wave per workgroup and
+    (M = 20,000) four: the same bits, within 1 ulp of the fp32 product."""
+    from kadllm_amd import _lib
+    g = torch.Generator().manual_seed(M + N + K + epi)
+    a_full = torch.randn(M, K + 64, generator=g).bfloat16().to(device)
+    a = a_full[:, 32:32 + K]                       # lda = K + 64, 64-byte offset
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16().to(device)
+    x = torch.randn(M, N, generator=g).bfloat16().to(device)
+    outs = {}
+    for cfg in (0, 1, 11, 13):
+        c = torch.zeros(M, N + 8, dtype=torch.bfloat16, device=device)
+        cv = c[:, :N]
+        if epi == layers.EPI_RESIDUAL:
+            cv.copy_(x)
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), a.stride(0), _lib.ptr(w), K, _lib.ptr(cv),
+                  c.stride(0), _lib.ptr(cv) if epi == layers.EPI_RESIDUAL else None,
+                  c.stride(0) if epi == layers.EPI_RESIDUAL else 0, M, N, K, epi, cfg,
+                  _lib.stream_of(a))
+        torch.cuda.synchronize()
+        assert (c[:, N:] == 0).all(), f"config {cfg} wrote past the output width"
+        outs[cfg] = cv.cpu()
+    for cfg in (0, 1, 11):
+        assert torch.equal(outs[cfg], outs[13]), f"config {cfg} differs from configuration 13"
+    prod = (a.float().cpu() @ w.float().cpu().T).bfloat16()
+    if epi == layers.EPI_STORE:
+        _bf16_ulp_close(outs[13], prod, "narrow gemm store")
+    else:
+        ref = (x.float().cpu() + prod.float()).bfloat16().float()
+        tol = (ref.abs() + prod.float().abs()) * 2 ** -7 + 1e-30
+        assert ((outs[13].float() - ref).abs() <= tol).all(), "narrow gemm residual"
+
+
+@pytest.mark.parametrize("N,K", [(33, 1024), (32, 448), (32, 2304)])
+def test_gemm_narrow_output_configuration_rejects(device, N, K):
+    """Configuration 13 takes N <= 32 and K a multiple of 256 up to 2,048 only."""
+    from kadllm_amd import _lib
+    a = torch.zeros(64, K, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(N, K, dtype=torch.bfloat16, device=device)
+    c = torch.zeros(64, N, dtype=torch.bfloat16, device=device)
+    with pytest.raises(_lib.KadLibraryError, match="tile configuration 13 needs"):
+        _lib.call("kad_gemm_bf16_tiled", _lib.ptr(a), K, _lib.ptr(w), K, _lib.ptr(c), N, None, 0,
+                  64, N, K, layers.EPI_STORE, 13, _lib.stream_of(a))
+
+
 @pytest.mark.parametrize("K", [64, 128, 192])
 def test_gemm_short_k_pipelines_agree(device, K):
     """The 16x16x32 configurations at K of one to three 64-deep tiles, where
@@ -311,7 +364,7 @@ def test_gemm_pipelined_tile_rejects_unaligned_output(device):
                   0, 256, 256, 64, layers.EPI_STORE, 16, _lib.stream_of(a))
 
 
-@pytest.mark.parametrize("cfg", [11, 12])
+@pytest.mark.parametrize("cfg", [11, 12, 13])
 def test_gemm_skinny_tiles_reject_swiglu(device, cfg):
     """The 64x32 and 32x64 register-staged tiles carry no SwiGLU epilogue (a
     wave's 32 columns cannot hold a [gate 32 | up 32] block) and say so."""
